@@ -1,0 +1,270 @@
+"""Benchmark: fwd+bwd attention TFLOPS and % of MI355X fp16 dense MFMA peak.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu]
+
+Workload (BASELINE.json metric, quoted on the headline shape): config C3,
+causal MHA, B=1, Hq=Hkv=8, N=4096, D=128, fp16 inputs from one seeded CPU
+generator (q, k, v, dO in that order, N(0,1)), resident in HBM before timing.
+
+One step = the hot path through the C ABI on torch's current stream:
+fa_fwd, then fa_bwd_preprocess (Dv, dQ := 0), then fa_bwd_main, into
+preallocated buffers. K steps are timed between two device synchronisations;
+HIP events recorded on the same stream between the launches give each
+kernel's average duration. The same step through the public autograd op
+(`flash_attn(...).backward(g)`, which adds output allocation and the dQ
+fp32->fp16 cast) is timed as `api_ms_per_step`.
+
+FLOPs follow the reference's convention (attention.cu:219, bwd.cu:246):
+fwd = 4*B*Hq*N^2*D, halved for causal; bwd = 2.5x fwd.
+
+cpu_baseline: the float64-pinned oracle's float32 restatement (numpy, the
+"port") timed on the host cores over a bounded sample of the same workload;
+torch's CPU scaled_dot_product_attention fwd+bwd (fp32) on the same sample is
+reported beside it.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "flash-attention-p100_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, AMD published (no sparsity)
+P100_HEADLINE_TFLOPS = 120.259e9 / 45.485e-3 / 1e12  # 45.485 ms on P100
+
+CONFIGS = {
+    "C2": dict(B=1, Hq=16, Hkv=16, N=2048, D=64, causal=True, s=1.0,
+               desc="causal MHA fwd+bwd fp16 B=1 Hq=Hkv=16 N=2048 D=64"),
+    "C3": dict(B=1, Hq=8, Hkv=8, N=4096, D=128, causal=True, s=1.0,
+               desc="causal MHA fwd+bwd fp16 B=1 Hq=Hkv=8 N=4096 D=128 (headline)"),
+    "C4": dict(B=2, Hq=32, Hkv=8, N=3001, D=128, causal=False, s=0.5,
+               desc="non-causal GQA fwd+bwd fp16 B=2 Hq=32 Hkv=8 N=3001 D=128"),
+}
+
+
+def flops(c):
+    f = 4.0 * c["B"] * c["Hq"] * c["N"] ** 2 * c["D"]
+    if c["causal"]:
+        f /= 2
+    return f, 2.5 * f
+
+
+def make_inputs(c, torch):
+    g = torch.Generator().manual_seed(0)
+    shp_q = (c["B"], c["Hq"], c["N"], c["D"])
+    shp_k = (c["B"], c["Hkv"], c["N"], c["D"])
+    out = []
+    for shp in (shp_q, shp_k, shp_k, shp_q):
+        out.append((torch.randn(*shp, generator=g) * c["s"]).half())
+    return out
+
+
+def load_capi():
+    lib = ctypes.CDLL(os.path.join(PKG, "libfa_mi355x.so"))
+    vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    lib.fa_fwd.argtypes = [vp] * 5 + [i] * 7 + [vp]
+    lib.fa_bwd_preprocess.argtypes = [vp] * 4 + [i] * 4 + [vp]
+    lib.fa_bwd_main.argtypes = [vp] * 9 + [i] * 6 + [vp]
+    lib.fa_bwd_workspace_bytes.argtypes = [i] * 5
+    lib.fa_bwd_workspace_bytes.restype = sz
+    lib.fa_error_string.restype = ctypes.c_char_p
+    return lib
+
+
+def gpu_bench(c, steps, warmup):
+    import torch
+    import fa_p100  # noqa: F401  (fails loudly if the binding is not built)
+
+    lib = load_capi()
+    dev = torch.device("cuda:0")
+    q, k, v, do = (t.to(dev) for t in make_inputs(c, torch))
+    B, Hq, Hkv, N, D, causal = c["B"], c["Hq"], c["Hkv"], c["N"], c["D"], int(c["causal"])
+    o = torch.empty_like(q)
+    lse = torch.empty(B, Hq, N, device=dev)
+    dvec = torch.empty(lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D) // 4, device=dev)
+    dq = torch.empty(B, Hq, N, D, device=dev)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    pq, pk, pv, pdo, po, plse, pdvec, pdq, pdk, pdv = map(P, (q, k, v, do, o, lse, dvec, dq, dk, dv))
+    stream = torch.cuda.current_stream(dev)
+    s = ctypes.c_void_p(stream.cuda_stream)
+
+    def check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {lib.fa_error_string(rc).decode()}")
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        check(lib.fa_fwd(pq, pk, pv, po, plse, B, Hq, Hkv, N, D, causal, 0, s), "fa_fwd")
+        if ev is not None:
+            ev[1].record(stream)
+        check(lib.fa_bwd_preprocess(pdo, po, pdvec, pdq, B, Hq, N, D, s), "fa_bwd_preprocess")
+        if ev is not None:
+            ev[2].record(stream)
+        check(lib.fa_bwd_main(pq, pk, pv, pdo, plse, pdvec, pdq, pdk, pdv, B, Hq, Hkv, N, D,
+                              causal, s), "fa_bwd_main")
+        if ev is not None:
+            ev[3].record(stream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(evs[i])
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    pre_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    main_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / steps
+
+    # Same step through the public autograd op.
+    import fa_p100 as fa
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+
+    def api_step():
+        for t in (qa, ka, va):
+            t.grad = None
+        fa.flash_attn(qa, ka, va, bool(causal)).backward(do)
+
+    for _ in range(warmup):
+        api_step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        api_step()
+    torch.cuda.synchronize()
+    api_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return dict(wall_ms=wall_ms, fwd_ms=fwd_ms, pre_ms=pre_ms, main_ms=main_ms, api_ms=api_ms,
+                device=torch.cuda.get_device_name(0))
+
+
+def cpu_baseline(c, budget_s=20.0):
+    """Oracle (numpy fp32) fwd+bwd on host cores over a bounded sample of the workload."""
+    import numpy as np
+    import torch
+    from oracle import attention as ora
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max((x.get("num_threads", 1) for x in threadpool_info()), default=1)
+    except Exception:
+        cores = os.cpu_count() or 1
+    # Sample: one (batch, head) slice of the workload, repeated within the budget.
+    q, k, v, do = make_inputs(dict(c, B=1, Hq=1, Hkv=1), torch)
+    qn, kn, vn, don = (t.float().numpy() for t in (q, k, v, do))
+    one = dict(c, B=1, Hq=1, Hkv=1)
+    f_fwd, f_bwd = flops(one)
+
+    def run():
+        o, lse = ora.attention_fwd(qn, kn, vn, c["causal"], dtype=np.float32)
+        ora.attention_bwd(qn, kn, vn, don, c["causal"], o=o, lse=lse, dtype=np.float32)
+
+    run()
+    reps, t_tot = 0, 0.0
+    while t_tot < budget_s / 2 and reps < 50:
+        t0 = time.perf_counter()
+        run()
+        t_tot += time.perf_counter() - t0
+        reps += 1
+    port = (f_fwd + f_bwd) * reps / t_tot / 1e12
+
+    # torch CPU SDPA fp32 fwd+bwd on the same sample (BASELINE.md's CPU plan).
+    torch.set_num_threads(os.cpu_count() or 1)
+    tq, tk, tv = (t.float().requires_grad_(True) for t in (q, k, v))
+    tdo = do.float()
+
+    def sdpa():
+        for t in (tq, tk, tv):
+            t.grad = None
+        torch.nn.functional.scaled_dot_product_attention(
+            tq, tk, tv, is_causal=c["causal"], enable_gqa=c["Hq"] != c["Hkv"]).backward(tdo)
+
+    sdpa()
+    sreps, s_tot = 0, 0.0
+    while s_tot < budget_s / 2 and sreps < 50:
+        t0 = time.perf_counter()
+        sdpa()
+        s_tot += time.perf_counter() - t0
+        sreps += 1
+    sdpa_tf = (f_fwd + f_bwd) * sreps / s_tot / 1e12
+    return {
+        "value": round(port, 4), "unit": "TFLOPS", "cores": int(cores), "kind": "port",
+        "sample": (f"1 of {c['B'] * c['Hq']} (batch, head) slices of {c['desc']}: numpy fp32 "
+                   f"oracle fwd+bwd x{reps} in {t_tot:.1f} s, FLOPs by the same convention"),
+        "torch_sdpa_cpu_fp32": {"value": round(sdpa_tf, 4), "unit": "TFLOPS",
+                                "threads": torch.get_num_threads(), "reps": sreps},
+    }
+
+
+def read_traffic(workload):
+    path = os.path.join(ROOT, "profiles", f"traffic_bwd_main_{workload}.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("hbm_bytes_per_dispatch")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
+              "(the attention kernel at its single-GPU shape); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    c = CONFIGS[args.config]
+    f_fwd, f_bwd = flops(c)
+    r = gpu_bench(c, args.steps, args.warmup)
+    step_ms = r["wall_ms"]
+    value = (f_fwd + f_bwd) / (step_ms * 1e-3) / 1e12
+    main_tf = f_bwd / (r["main_ms"] * 1e-3) / 1e12
+    traffic = read_traffic(args.config)
+    out = {
+        "metric": "fwd+bwd attention TFLOPS & % fp16 MFMA peak, causal N=4096 D=64/128",
+        "value": round(value, 2),
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(value / P100_HEADLINE_TFLOPS, 1) if args.config == "C3" else None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: {c['desc']}", "B": c["B"], "Hq": c["Hq"],
+                   "Hkv": c["Hkv"], "N": c["N"], "D": c["D"], "causal": c["causal"]},
+        "pct_peak": round(100 * value / PEAK_FP16_TFLOPS, 2),
+        "fwd_tflops": round(f_fwd / (r["fwd_ms"] * 1e-3) / 1e12, 2),
+        "bwd_tflops": round(f_bwd / ((r["pre_ms"] + r["main_ms"]) * 1e-3) / 1e12, 2),
+        "kernel_ms": {"fwd": round(r["fwd_ms"], 4), "bwd_preprocess": round(r["pre_ms"], 4),
+                      "bwd_main": round(r["main_ms"], 4)},
+        "api_ms_per_step": round(r["api_ms"], 4),
+        "device": r["device"],
+        "roofline": {"kernel": "bwd_main (fa_bwd_main)", "bound": "mfma",
+                     "achieved": round(main_tf, 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(main_tf / PEAK_FP16_TFLOPS, 4),
+                     "traffic": traffic},
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(c)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

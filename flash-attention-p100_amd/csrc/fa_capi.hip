@@ -1,0 +1,108 @@
+// C ABI entry points (declared in include/fa_mi355x.h).
+//
+// Validation here mirrors the reference binding's checks that do not need
+// torch (fa_p100_ext.cu:59-65, 111-113): head dim, positive N, the head
+// grouping. Tensor-type checks ("must be a CUDA tensor", "must be fp16") live
+// in the torch extension, where tensors exist. Nothing here allocates or keeps
+// state beyond each kernel's one-time LDS-limit attribute.
+#include <limits.h>
+
+#include "../../include/fa_mi355x.h"
+#include "fa_launch.h"
+
+namespace {
+
+int check_shape(int B, int Hq, int Hkv, int N, int D) {
+  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (N <= 0) return FA_ERR_SEQLEN;
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return FA_ERR_HEADS;
+  if (B <= 0) return FA_ERR_BATCH;
+  // Kernels index rows of one (b, h) slice with 32-bit ints and whole tensors
+  // with 64-bit offsets; grid.y is B*H (limit 65535 on the launch).
+  if ((long long)B * Hq > 65535 || (long long)N * D > INT_MAX) return FA_ERR_TOO_LARGE;
+  return FA_OK;
+}
+
+int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }
+
+}  // namespace
+
+extern "C" {
+
+const char* fa_error_string(int err) {
+  switch (err) {
+    case FA_OK: return "success";
+    case FA_ERR_HEAD_DIM: return "head dim must be 64 or 128";
+    case FA_ERR_SEQLEN: return "N must be positive";
+    case FA_ERR_HEADS: return "query heads (H) must be a multiple of key/value heads (Hkv)";
+    case FA_ERR_BATCH: return "B must be positive";
+    case FA_ERR_NULL: return "a required pointer is NULL";
+    case FA_ERR_WORKSPACE: return "workspace is smaller than fa_bwd_workspace_bytes()";
+    case FA_ERR_TOO_LARGE: return "shape exceeds the kernels' index range";
+    default: return hipGetErrorString((hipError_t)err);
+  }
+}
+
+const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
+
+int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
+           int Hkv, int N, int D, int causal, int full_precision, void* stream) {
+  (void)full_precision;  // fp16 products are exact in the fp32 accumulator
+  const int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc != FA_OK) return rc;
+  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream};
+  return to_code(fa::launch_fwd(a));
+}
+
+size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
+  if (check_shape(B, Hq, Hkv, N, D) != FA_OK) return 0;
+  const size_t bytes = (size_t)B * Hq * N * sizeof(float);
+  return (bytes + 255) & ~(size_t)255;
+}
+
+int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, float* dq, int B, int Hq,
+                      int N, int D, void* stream) {
+  const int rc = check_shape(B, Hq, Hq, N, D);
+  if (rc != FA_OK) return rc;
+  if (!dO || !o || !dvec || !dq) return FA_ERR_NULL;
+  fa::BwdArgs a{};
+  a.dO = dO;
+  a.o = o;
+  a.dvec = dvec;
+  a.dq = dq;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hq;
+  a.N = N;
+  a.D = D;
+  a.stream = stream;
+  return to_code(fa::launch_bwd_preprocess(a));
+}
+
+int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const float* lse,
+                const float* dvec, float* dq, void* dk, void* dv, int B, int Hq, int Hkv, int N,
+                int D, int causal, void* stream) {
+  const int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc != FA_OK) return rc;
+  if (!q || !k || !v || !dO || !lse || !dvec || !dq || !dk || !dv) return FA_ERR_NULL;
+  fa::BwdArgs a{q, k, v, dO, nullptr, lse, const_cast<float*>(dvec), dq, dk, dv,
+                B, Hq, Hkv, N, D, causal != 0, stream};
+  return to_code(fa::launch_bwd_main(a));
+}
+
+int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,
+           const float* lse, float* dq, void* dk, void* dv, void* workspace,
+           size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+           void* stream) {
+  const int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc != FA_OK) return rc;
+  if (!workspace) return FA_ERR_NULL;
+  if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
+  float* dvec = static_cast<float*>(workspace);
+  int e = fa_bwd_preprocess(dO, o, dvec, dq, B, Hq, N, D, stream);
+  if (e != FA_OK) return e;
+  return fa_bwd_main(q, k, v, dO, lse, dvec, dq, dk, dv, B, Hq, Hkv, N, D, causal, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,78 @@
+// Device-side building blocks shared by the forward and backward kernels.
+//
+// Everything here targets gfx950 (CDNA4) directly: wave64, the
+// v_mfma_f32_32x32x16_f16 matrix instruction, and LDS tiles with padded rows.
+//
+// MFMA 32x32x16 (fp16 in, fp32 accumulate) register layout, per lane l of 64,
+// h = l / 32:
+//   A (32x16, M x K): 8 halves, A[l % 32][8h + e],  e = 0..7
+//   B (16x32, K x N): 8 halves, B[8h + e][l % 32]
+//   C (32x32)       : 16 floats, C[8*(r/4) + 4h + (r%4)][l % 32], r = 0..15
+// Because only the products along K are summed, A and B may enumerate the K
+// index in any order as long as both use the same order; the kernels use
+// this to feed an accumulator straight back in as the next product's operand.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16 zero16() {
+  floatx16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// 16-byte global load; returns zeros when `ok` is false.
+__device__ __forceinline__ u32x4 load16(const half_t* p, bool ok) {
+  u32x4 r = {0u, 0u, 0u, 0u};
+  if (ok) r = *reinterpret_cast<const u32x4*>(p);
+  return r;
+}
+
+__device__ __forceinline__ half8 as_half8(u32x4 v) {
+  return __builtin_bit_cast(half8, v);
+}
+
+// Low halves of x and y packed as (x.lo, y.lo); likewise for high halves.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+// Transposes a 4-row x 8-column block of halves held as four 16-byte rows
+// into eight 4-element columns: col[c] = (r0[c], r1[c], r2[c], r3[c]).
+__device__ __forceinline__ void transpose_4x8(const u32x4 (&rows)[4], u32x2 (&cols)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    cols[2 * w][0] = pack_lo(rows[0][w], rows[1][w]);
+    cols[2 * w][1] = pack_lo(rows[2][w], rows[3][w]);
+    cols[2 * w + 1][0] = pack_hi(rows[0][w], rows[1][w]);
+    cols[2 * w + 1][1] = pack_hi(rows[2][w], rows[3][w]);
+  }
+}
+
+// Swap with the lane 32 positions away (the other half of the wave).
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+}  // namespace fa

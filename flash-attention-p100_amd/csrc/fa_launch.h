@@ -1,0 +1,46 @@
+// Host-side launch descriptors shared by the kernels and the C ABI layer.
+// Arguments are validated by the C ABI (fa_capi.hip) before these are called.
+#pragma once
+#include <hip/hip_runtime.h>
+
+namespace fa {
+
+struct FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  int B, Hq, Hkv, N, D;
+  bool causal;
+  void* stream;
+};
+
+struct BwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* dO;
+  const void* o;
+  const float* lse;
+  float* dvec;
+  float* dq;
+  void* dk;
+  void* dv;
+  int B, Hq, Hkv, N, D;
+  bool causal;
+  void* stream;
+};
+
+hipError_t launch_fwd(const FwdArgs& a);
+hipError_t launch_bwd_preprocess(const BwdArgs& a);
+hipError_t launch_bwd_main(const BwdArgs& a);
+
+// Raises the kernel's dynamic-LDS limit to `bytes` once per process.
+template <typename Kernel>
+inline hipError_t allow_lds(Kernel k, size_t bytes) {
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
+}  // namespace fa

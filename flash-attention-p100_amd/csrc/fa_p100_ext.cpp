@@ -1,0 +1,118 @@
+// Torch binding `fa_p100_ext`: the drop-in for the reference's pybind module
+// (fa_p100_ext.cu:144-147), with the same two functions, argument lists,
+// checks, error messages, allocations and return dtypes:
+//
+//   forward(q, k, v, causal, full_precision) -> [o fp16 (B,Hq,N,D), lse fp32 (B,Hq,N)]
+//       fa_p100_ext.cu:53-83
+//   backward(q, k, v, dO, o, lse, causal)    -> [dq fp32 (B,Hq,N,D), dk fp16, dv fp16]
+//       fa_p100_ext.cu:103-142
+//
+// Plain C++ (no device code): every launch goes through the C ABI of
+// libfa_mi355x.so (include/fa_mi355x.h). Unlike the reference, which uses the
+// legacy default stream without a device guard (flash_fwd.cuh:351,
+// flash_bwd.cuh:475-483), launches go to torch's current stream on the
+// tensors' device.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <cmath>
+#include <vector>
+
+#include "fa_mi355x.h"
+
+namespace {
+
+void check_in(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.scalar_type() == at::kHalf, name, " must be fp16");
+  TORCH_CHECK(t.dim() == 4, name, " must be (B, H, N, D)");
+}
+
+void check_rc(int rc, const char* what) {
+  TORCH_CHECK(rc == FA_OK, what, " failed: ", fa_error_string(rc));
+}
+
+void* current_stream(const at::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+}  // namespace
+
+std::vector<at::Tensor> fa_forward(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
+                                   bool full_precision) {
+  check_in(q, "q");
+  check_in(k, "k");
+  check_in(v, "v");
+  q = q.contiguous();
+  k = k.contiguous();
+  v = v.contiguous();
+  const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  const int Hkv = k.size(1);
+  TORCH_CHECK(D == 64 || D == 128, "head dim must be 64 or 128, got ", D);
+  TORCH_CHECK(N > 0, "N must be positive");
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
+              ") must be a multiple of key/value heads (", Hkv, ")");
+  TORCH_CHECK(k.sizes() == v.sizes(), "k and v must match");
+  TORCH_CHECK(k.size(0) == B && k.size(2) == N && k.size(3) == D,
+              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
+              "q, k and v must be on the same device");
+
+  c10::DeviceGuard guard(q.device());
+  auto o = at::empty_like(q);
+  auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
+  check_rc(fa_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr<float>(),
+                  B, H, Hkv, N, D, causal ? 1 : 0, full_precision ? 1 : 0, current_stream(q)),
+           "fa_fwd");
+  return {o, lse};
+}
+
+std::vector<at::Tensor> fa_backward(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
+                                    at::Tensor o, at::Tensor lse, bool causal) {
+  check_in(q, "q");
+  check_in(dO, "dO");
+  q = q.contiguous();
+  k = k.contiguous();
+  v = v.contiguous();
+  dO = dO.contiguous();
+  o = o.contiguous();
+  lse = lse.contiguous();
+  const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  const int Hkv = k.size(1);
+  TORCH_CHECK(D == 64 || D == 128, "head dim must be 64 or 128, got ", D);
+  TORCH_CHECK(N > 0, "N must be positive");
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
+  // The reference checks only q and dO here (fa_p100_ext.cu:106); the kernels
+  // would read out of bounds on anything else, so the rest is checked too.
+  TORCH_CHECK(k.scalar_type() == at::kHalf && v.scalar_type() == at::kHalf &&
+                  o.scalar_type() == at::kHalf,
+              "k, v and o must be fp16");
+  TORCH_CHECK(lse.scalar_type() == at::kFloat, "lse must be fp32");
+  TORCH_CHECK(k.sizes() == v.sizes() && k.dim() == 4 && k.size(0) == B && k.size(2) == N &&
+                  k.size(3) == D,
+              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(dO.sizes() == q.sizes() && o.sizes() == q.sizes(), "dO and o must match q");
+  TORCH_CHECK(lse.dim() == 3 && lse.size(0) == B && lse.size(1) == H && lse.size(2) == N,
+              "lse must be (B, H, N)");
+
+  c10::DeviceGuard guard(q.device());
+  auto f32 = q.options().dtype(at::kFloat);
+  // dq is fp32: it is accumulated across key tiles. dk/dv leave as fp16.
+  auto dq = at::empty({B, H, N, D}, f32);
+  auto dk = at::empty_like(k);
+  auto dv = at::empty_like(k);
+  const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
+  auto dvec = at::empty({(int64_t)(ws_bytes / sizeof(float))}, f32);  // rowsum(dO * O)
+  check_rc(fa_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                  lse.data_ptr<float>(), dq.data_ptr<float>(), dk.data_ptr(), dv.data_ptr(),
+                  dvec.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
+                  current_stream(q)),
+           "fa_bwd");
+  return {dq, dk, dv};
+}
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("forward", &fa_forward, "FlashAttention forward (gfx950)");
+  m.def("backward", &fa_backward, "FlashAttention backward (gfx950)");
+}

@@ -1,0 +1,99 @@
+"""FlashAttention-2 for the AMD Instinct MI355X (gfx950) as a torch autograd Function.
+
+Drop-in for the reference module of the same name (fa_p100.py): same public
+names, arguments and return values.
+
+    from fa_p100 import flash_attn
+    o = flash_attn(q, k, v, causal=True)   # q: (B, Hq, N, D) fp16 on the GPU
+                                           # k, v: (B, Hkv, N, D), Hq % Hkv == 0
+
+D is 64 or 128; N is arbitrary; Hkv == Hq is multi-head, Hkv == 1 multi-query,
+anything between grouped-query. The kernels are hand-written HIP for gfx950
+(fp16 MFMA with fp32 accumulation), built in-tree by build.py into
+libfa_mi355x.so, and reached through the `fa_p100_ext` torch binding. Unlike
+the reference (fa_p100.py:21-28), importing does not compile anything: the
+binding must already be built, and importing fails loudly if it is not.
+
+`full_precision` is accepted for API compatibility (fa_p100.py:48). The
+reference used it to switch its forward from fp16 to fp32 multiply-adds; on
+MFMA every fp16 product is exact in the fp32 accumulator, so both settings run
+the same kernel.
+"""
+import importlib.machinery
+import importlib.util
+import math
+import os
+import sysconfig
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_EXT_NAME = "fa_p100_ext"
+
+
+def _load_ext():
+    """Load the in-tree torch binding; raise ImportError if it is not built."""
+    path = os.path.join(_HERE, _EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
+    if not os.path.exists(path):
+        raise ImportError(
+            f"{path} is not built. Run `python {os.path.join(_HERE, 'build.py')}` "
+            "(or __graft_entry__.build()) first; there is no fallback path.")
+    loader = importlib.machinery.ExtensionFileLoader(_EXT_NAME, path)
+    spec = importlib.util.spec_from_file_location(_EXT_NAME, path, loader=loader)
+    mod = importlib.util.module_from_spec(spec)
+    loader.exec_module(mod)
+    return mod
+
+
+_ext = _load_ext()
+
+
+class _FlashAttnP100(torch.autograd.Function):
+    """Autograd wrapper; same saved state and return types as fa_p100.py:31-45."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, full_precision):
+        o, lse = _ext.forward(q, k, v, causal, full_precision)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.causal = causal
+        return o
+
+    @staticmethod
+    def backward(ctx, grad_o):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = _ext.backward(q, k, v, grad_o.contiguous(), o, lse, ctx.causal)
+        # dq is accumulated in fp32; hand every gradient back in its input's dtype.
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
+
+
+def flash_attn(q, k, v, causal=False, full_precision=False):
+    """Attention over fp16 GPU tensors (fa_p100.py:48-55).
+
+    q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
+    and D in {64, 128}. scale = 1/sqrt(D). Causal masking is top-left aligned
+    (key j is hidden from query i when j > i).
+    """
+    return _FlashAttnP100.apply(q, k, v, causal, full_precision)
+
+
+def _expand_kv(k, n_head):
+    """Repeat each K/V head across the query heads that share it (fa_p100.py:58-62)."""
+    if k.size(1) == n_head:
+        return k
+    return k.repeat_interleave(n_head // k.size(1), dim=1)
+
+
+def reference(q, k, v, causal=False):
+    """Plain-torch attention for comparison, as the reference ships (fa_p100.py:65-75).
+
+    A helper for users' own checks; `flash_attn` never calls it.
+    """
+    k = _expand_kv(k, q.size(1))
+    v = _expand_kv(v, q.size(1))
+    scale = 1.0 / math.sqrt(q.size(-1))
+    s = (q.float() @ k.float().transpose(-1, -2).contiguous()) * scale
+    if causal:
+        n = q.size(-2)
+        mask = torch.triu(torch.ones(n, n, device=q.device, dtype=torch.bool), 1)
+        s = s.masked_fill(mask, float("-inf"))
+    return (s.softmax(-1) @ v.float()).to(q.dtype)

@@ -1,0 +1,158 @@
+"""HuggingFace transformers attention hook for the gfx950 FlashAttention kernels.
+
+Drop-in for the reference module of the same name (fa_p100_hf.py): registers
+the kernels under the attention-implementation name "fa_p100", so a supported
+model (Qwen3, Llama-style decoders) runs on them with
+
+    from fa_p100_hf import enable_fa_p100
+    model = AutoModelForCausalLM.from_config(cfg).half().cuda()
+    enable_fa_p100(model)
+
+Checked against transformers 5.15: `ALL_ATTENTION_FUNCTIONS` is a mapping whose
+`__setitem__` registers a local implementation, `config._attn_implementation`
+is a recursive setter, and masking_utils returns no mask at all for an
+implementation that is not in the mask registry (masking_utils.py:819-820).
+That last point is relied on: the kernel applies causality itself, so no
+(B, H, N, N) mask is ever built. The price is that a padding mask would be
+dropped without a word, which is why `enable_fa_p100` wraps `model.forward`
+to reject one (fa_p100_hf.py:13-22, 183-211).
+
+Every unsupported request raises NotImplementedError instead of degrading
+(fa_p100_hf.py:24-32): attention / padding masks, output_attentions,
+head_mask, sliding windows, dropout, head_dim other than 64/128, a scale other
+than 1/sqrt(D), q_len != kv_len (KV-cache decoding).
+"""
+import warnings
+
+import torch
+
+from fa_p100 import flash_attn
+
+_IMPL_NAME = "fa_p100"
+_warned_cast = False
+
+
+def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout=0.0,
+                              scaling=None, is_causal=None, **kwargs):
+    """transformers attention-interface entry point (fa_p100_hf.py:46-142).
+
+    query is (B, Hq, N, D) and key/value (B, Hkv, N, D); returns
+    (out (B, N, Hq, D) in query's dtype, None), the contract of
+    transformers' sdpa_attention_forward.
+    """
+    global _warned_cast
+
+    if attention_mask is not None:
+        raise NotImplementedError(
+            "fa_p100 got an attention mask, but the kernel has no mask input. "
+            "Pack sequences to one fixed length so no padding is needed.")
+    if kwargs.get("output_attentions", False):
+        raise NotImplementedError(
+            "fa_p100 never forms the attention probabilities, so "
+            "output_attentions=True is not available; use attn_implementation='eager'.")
+    if kwargs.get("head_mask") is not None:
+        raise NotImplementedError("fa_p100 does not support head_mask.")
+    if kwargs.get("sliding_window") is not None:
+        raise NotImplementedError(
+            f"fa_p100 is dense or causal only; this layer asks for a sliding window "
+            f"of {kwargs['sliding_window']}.")
+    if dropout:
+        raise NotImplementedError(f"fa_p100 has no attention dropout (got {dropout}).")
+
+    head_dim = query.size(-1)
+    if head_dim not in (64, 128):
+        raise NotImplementedError(f"fa_p100 supports head_dim 64 or 128, got {head_dim}.")
+    # The kernels fix scale = 1/sqrt(D); any other request would be mis-scaled.
+    if scaling is not None and abs(scaling - head_dim ** -0.5) > 1e-6:
+        raise NotImplementedError(
+            f"fa_p100 fixes the scale at 1/sqrt(D) = {head_dim ** -0.5:.6g}; "
+            f"the model asked for {scaling:.6g}.")
+    if key.size(2) != query.size(2):
+        raise NotImplementedError(
+            f"fa_p100 needs q_len == kv_len (got q={query.size(2)}, kv={key.size(2)}); "
+            "incremental decoding with a KV cache is not supported.")
+
+    if is_causal is None:
+        is_causal = getattr(module, "is_causal", True) and query.size(2) > 1
+
+    # The kernels take fp16. Under fp16 autocast, Qwen3's fp32 q_norm/k_norm
+    # weights and rotary tables hand q and k over in fp32 while v is fp16, so
+    # casting here is the normal path; outside autocast it is worth a warning.
+    orig_dtype = query.dtype
+    if query.dtype != torch.float16 or key.dtype != torch.float16 \
+            or value.dtype != torch.float16:
+        sanctioned = (torch.is_autocast_enabled("cuda")
+                      and torch.get_autocast_dtype("cuda") == torch.float16)
+        if not sanctioned and not _warned_cast:
+            warnings.warn(
+                f"fa_p100 casts q={query.dtype} k={key.dtype} v={value.dtype} to float16 "
+                "outside fp16 autocast; the kernels are fp16 only. Run the step under "
+                "torch.autocast('cuda', torch.float16).", stacklevel=2)
+            _warned_cast = True
+        query, key, value = query.half(), key.half(), value.half()
+
+    # GQA/MQA go to the kernel as they are: no repeat_kv copies.
+    full_precision = getattr(module, "_fa_p100_full_precision", False)
+    out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision)
+    return out.transpose(1, 2).contiguous().to(orig_dtype), None
+
+
+def register():
+    """Add "fa_p100" to transformers' attention registry (idempotent)."""
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+
+    ALL_ATTENTION_FUNCTIONS[_IMPL_NAME] = fa_p100_attention_forward
+    return _IMPL_NAME
+
+
+def _set_impl(config, name):
+    config._attn_implementation = name
+    for sub in getattr(config, "sub_configs", {}) or {}:
+        child = getattr(config, sub, None)
+        if child is not None:
+            _set_impl(child, name)
+
+
+def enable_fa_p100(model, full_precision=False):
+    """Switch `model` onto the kernels and guard the paths they cannot serve.
+
+    Mirrors fa_p100_hf.py:161-213: registers the implementation, points every
+    config at it, records `full_precision` on every module, turns the KV cache
+    off, and wraps `model.forward` once so a padding mask or use_cache=True
+    raises instead of being silently ignored.
+    """
+    register()
+    _set_impl(model.config, _IMPL_NAME)
+    for mod in model.modules():
+        if hasattr(mod, "config") and hasattr(mod.config, "_attn_implementation"):
+            _set_impl(mod.config, _IMPL_NAME)
+        mod._fa_p100_full_precision = full_precision
+
+    # q_len must equal kv_len, so a cache could never be used.
+    model.config.use_cache = False
+    if getattr(model, "generation_config", None) is not None:
+        model.generation_config.use_cache = False
+
+    if not getattr(model, "_fa_p100_guarded", False):
+        inner = model.forward
+
+        def guarded(*args, attention_mask=None, use_cache=None, **kwargs):
+            # transformers drops the mask before the attention interface sees it
+            # for unregistered implementations: this is the last place to catch it.
+            if attention_mask is not None and not bool(attention_mask.all()):
+                raise NotImplementedError(
+                    "fa_p100 cannot apply a padding mask, and transformers would "
+                    "discard it silently. Pack the batch so every position is real.")
+            # Rejected up front rather than at the first decode step, after a
+            # prefill that would have succeeded.
+            if use_cache:
+                raise NotImplementedError(
+                    "fa_p100 needs q_len == kv_len, so it cannot serve a KV cache; it "
+                    "is a training kernel. Set generation_config.use_cache = False for "
+                    "cache-free generation.")
+            return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
+
+        model.forward = guarded
+        model._fa_p100_guarded = True
+
+    return model

@@ -1,0 +1,108 @@
+/*
+ * fa_mi355x.h -- C ABI of the MI355X (gfx950) FlashAttention-2 library.
+ *
+ * The reference exposes this path only as a pybind torch extension named
+ * `fa_p100_ext` with two functions, `forward` and `backward`
+ * (fa_p100_ext.cu:53-83, 103-142, 144-147), which call straight into
+ * `flash::launch` (flash_fwd.cuh:342-355) and `flash_bwd::launch`
+ * (flash_bwd.cuh:466-484). This header is the layer beneath that binding:
+ * plain pointers and sizes, no torch types, no allocation inside, no global
+ * state. The torch extension built beside it (`fa_p100_ext`) and any other
+ * host (ctypes, a C++ driver) call these entry points.
+ *
+ * Conventions shared by every entry point
+ *   - Tensors are dense row-major (B, H, N, D): element (b,h,n,d) sits at
+ *     ((b*H + h)*N + n)*D + d. q, o, dO, dq are (B, Hq, N, D); k, v, dk, dv
+ *     are (B, Hkv, N, D); lse and the Dv workspace are (B, Hq, N) float32.
+ *   - fp16 buffers hold IEEE binary16 (`_Float16` / `__half` / torch.half).
+ *   - Query head h reads key/value head h / (Hq/Hkv), which is
+ *     `repeat_interleave` over the head axis (fa_p100.py:58-62).
+ *   - scale = 1/sqrt(D) is fixed (fa_p100_ext.cu:71, 117).
+ *   - `stream` is a hipStream_t (NULL = the null stream). Every launch is
+ *     asynchronous on it; the call returns after enqueueing.
+ *   - Return value: FA_OK (0), an FA_ERR_* validation code (nothing was
+ *     launched), or a hipError_t value reported by the HIP runtime.
+ *   - Entry points are reentrant and thread-safe: they keep no state.
+ */
+#ifndef FA_MI355X_H_
+#define FA_MI355X_H_
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FA_OK = 0,
+  FA_ERR_HEAD_DIM = 10001,   /* D not in {64, 128} (fa_p100_ext.cu:59, 111) */
+  FA_ERR_SEQLEN = 10002,     /* N <= 0 (fa_p100_ext.cu:60, 112) */
+  FA_ERR_HEADS = 10003,      /* Hkv <= 0 or Hq % Hkv != 0 (fa_p100_ext.cu:61, 113) */
+  FA_ERR_BATCH = 10004,      /* B <= 0 */
+  FA_ERR_NULL = 10005,       /* a required pointer is NULL */
+  FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
+  FA_ERR_TOO_LARGE = 10007   /* an index would overflow the kernels' 32-bit row counters */
+};
+
+/* Human-readable text for any value returned by this library. */
+const char* fa_error_string(int err);
+
+/* Library version string, e.g. "fa_mi355x 1.0 gfx950". */
+const char* fa_version(void);
+
+/*
+ * Forward pass. Replaces fa_forward (fa_p100_ext.cu:53-83) below its torch
+ * checks: writes o (fp16, B,Hq,N,D) and lse (fp32, B,Hq,N; natural log of
+ * the row sum of exp(scaled logits), flash_fwd.cuh:324-329).
+ * `full_precision` is accepted for the reference's API (fa_p100_ext.cu:44-50);
+ * fp16 products are exact in the fp32 MFMA accumulator, so both tiers run the
+ * same kernel.
+ */
+int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+           int B, int Hq, int Hkv, int N, int D, int causal,
+           int full_precision, void* stream);
+
+/*
+ * Bytes of device workspace fa_bwd needs: the (B, Hq, N) float32 Dv vector,
+ * the `dvec` allocation of fa_p100_ext.cu:124, rounded up to 256 bytes.
+ */
+size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D);
+
+/*
+ * Backward pass. Replaces fa_backward (fa_p100_ext.cu:103-142) below its torch
+ * checks. Inputs q, k, v, dO, o (fp16) and lse (fp32) are the forward's
+ * inputs/outputs. Writes dq (fp32, B,Hq,N,D), dk and dv (fp16, B,Hkv,N,D).
+ * dq is produced by accumulation, so it is cleared first by this call.
+ * `workspace` must hold fa_bwd_workspace_bytes() bytes. Equivalent to
+ * fa_bwd_preprocess() followed by fa_bwd_main().
+ */
+int fa_bwd(const void* q, const void* k, const void* v, const void* dO,
+           const void* o, const float* lse, float* dq, void* dk, void* dv,
+           void* workspace, size_t workspace_bytes,
+           int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
+
+/*
+ * First phase of fa_bwd, the counterpart of bwd_preprocess plus the dQ memset
+ * (flash_bwd.cuh:65-78, 475-476): dvec = rowsum(dO * o) in fp32 (B,Hq,N) and
+ * dq = 0. Exposed so a host can time or schedule the phases separately.
+ */
+int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, float* dq,
+                      int B, int Hq, int N, int D, void* stream);
+
+/*
+ * Second phase of fa_bwd, the counterpart of bwd_kernel
+ * (flash_bwd.cuh:95-464, launched at 479-483): K/V-stationary dK, dV and
+ * dQ (+=, fp32) from the saved lse and the dvec written by
+ * fa_bwd_preprocess. dq must hold the preprocess phase's zeros (or any
+ * partial sum to add to).
+ */
+int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
+                const float* lse, const float* dvec, float* dq, void* dk,
+                void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
+                void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* FA_MI355X_H_ */

@@ -1,0 +1,167 @@
+"""CPU oracle for the FlashAttention-2 forward and backward (test infrastructure).
+
+This module is TEST INFRASTRUCTURE ONLY. It is imported by `tests/`, by
+`__graft_entry__.smoke()` (as the checker) and by `bench.py`'s `cpu_baseline`
+leg (as the timed CPU restatement). The product path (`fa_p100.flash_attn`, the
+torch extension and the C-ABI library) never imports or calls it.
+
+It restates the reference's algorithm in numpy, in float64 by default:
+
+  forward   O = softmax(Q K^T * scale) V, scale = 1/sqrt(D), causal mask col > row
+            (fa_p100.py:65-75, attention.cu:72-102); LSE = logsumexp of the
+            SCALED logits per row, natural log (flash_fwd.cuh:321-329)
+  GQA       query head h reads key/value head h // (Hq/Hkv), i.e.
+            repeat_interleave over the head axis (fa_p100.py:58-62,
+            flash_fwd.cuh:90)
+  preprocess Dv = rowsum(dO * O) (flash_bwd.cuh:65-78)
+  backward  P = exp(S*scale - LSE), dV = P^T dO, dP = dO V^T,
+            dS = P (dP - Dv), dQ = dS K * scale, dK = dS^T Q * scale
+            (bwd.cu:20-69, flash_bwd.cuh:11-16, 267-282, 434-463);
+            GQA dK/dV sum over the query heads of a group
+  loss      sum(dO * O), whose gradient is exactly the backward above
+            (bwd.cu:73-105); used by the finite-difference pin
+  metrics   rel = max|got-ref| / RMS(ref) (test_fa_p100.py:35-37), relative
+            L2, max-abs
+
+How each function is pinned (tests/test_oracle.py): the backward against
+central finite differences of `loss` (bwd.cu:136-160); forward and backward
+against torch's own scaled_dot_product_attention + autograd in float64 (an
+independent library routine); closed forms (N=1 gives O=V, causal row 0 gives
+V_0, Q=0 gives the (prefix) mean of V and LSE=log(count)); GQA equals MHA on
+repeat_interleave'd K/V with group-summed dK/dV; permutation equivariance over
+heads and key-permutation invariance (dense); causal tail independence.
+"""
+import math
+
+import numpy as np
+
+__all__ = [
+    "expand_kv", "attention_fwd", "bwd_preprocess", "attention_bwd",
+    "attention_loss", "rel_max_rms", "rel_l2", "max_abs", "fwd_flops",
+    "bwd_flops",
+]
+
+
+def expand_kv(k, n_head):
+    """Repeat each K/V head across the query heads sharing it (fa_p100.py:58-62)."""
+    hkv = k.shape[1]
+    if hkv == n_head:
+        return k
+    if n_head % hkv:
+        raise ValueError("query heads must be a multiple of kv heads")
+    return np.repeat(k, n_head // hkv, axis=1)
+
+
+def _group_sum(g, hkv):
+    """Sum gradients over the query heads that share one K/V head."""
+    b, hq, n, d = g.shape
+    if hq == hkv:
+        return g
+    return g.reshape(b, hkv, hq // hkv, n, d).sum(axis=2)
+
+
+def _scores(q, k, causal, dtype):
+    """Scaled logits S*scale with the causal upper triangle set to -inf.
+
+    The scale is applied to the logit after the product, never to Q
+    (flash_fwd.cuh:94-101, 220-224). Causal is top-left aligned with
+    q_len == kv_len: key col is masked for query row when col > row
+    (flash_fwd.cuh:239).
+    """
+    d = q.shape[-1]
+    scale = 1.0 / math.sqrt(d)
+    s = np.matmul(q.astype(dtype), np.swapaxes(k.astype(dtype), -1, -2)) * dtype(scale)
+    if causal:
+        n = q.shape[-2]
+        mask = np.triu(np.ones((n, n), dtype=bool), 1)
+        s = np.where(mask, -np.inf, s).astype(dtype)
+    return s
+
+
+def attention_fwd(q, k, v, causal=False, dtype=np.float64):
+    """Forward: returns (O, LSE) computed in `dtype`.
+
+    q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
+    both in `dtype`. LSE is in natural-log units of the scaled logits
+    (flash_fwd.cuh:324-329).
+    """
+    hq = q.shape[1]
+    k = expand_kv(np.asarray(k), hq)
+    v = expand_kv(np.asarray(v), hq)
+    s = _scores(np.asarray(q), k, causal, dtype)
+    m = s.max(axis=-1, keepdims=True)
+    p = np.exp(s - m)
+    l = p.sum(axis=-1, keepdims=True)
+    o = np.matmul(p / l, v.astype(dtype))
+    lse = (m + np.log(l))[..., 0]
+    return o, lse
+
+
+def bwd_preprocess(o, do, dtype=np.float64):
+    """Dv = rowsum(dO * O) per query row (flash_bwd.cuh:65-78)."""
+    return (np.asarray(o).astype(dtype) * np.asarray(do).astype(dtype)).sum(axis=-1)
+
+
+def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64):
+    """Analytic backward: returns (dQ, dK, dV) in `dtype`.
+
+    When `o`/`lse` are given they are used as the saved forward state (as the
+    kernels do, flash_bwd.cuh:278); otherwise they are recomputed here.
+    dK and dQ carry the scale; dV does not (flash_bwd.cuh:442, 457).
+    """
+    q = np.asarray(q)
+    hq, hkv = q.shape[1], np.asarray(k).shape[1]
+    d = q.shape[-1]
+    scale = dtype(1.0 / math.sqrt(d))
+    ke = expand_kv(np.asarray(k), hq).astype(dtype)
+    ve = expand_kv(np.asarray(v), hq).astype(dtype)
+    qd = q.astype(dtype)
+    dod = np.asarray(do).astype(dtype)
+    if o is None or lse is None:
+        o, lse = attention_fwd(q, k, v, causal, dtype)
+    s = _scores(q, ke, causal, dtype)
+    p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
+    dv = np.matmul(np.swapaxes(p, -1, -2), dod)
+    dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
+    dvec = bwd_preprocess(o, dod, dtype)
+    ds = p * (dp - dvec[..., None])
+    dq = np.matmul(ds, ke) * scale
+    dk = np.matmul(np.swapaxes(ds, -1, -2), qd) * scale
+    return dq, _group_sum(dk, hkv), _group_sum(dv, hkv)
+
+
+def attention_loss(q, k, v, do, causal=False, dtype=np.float64):
+    """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
+    o, _ = attention_fwd(q, k, v, causal, dtype)
+    return float((o * np.asarray(do).astype(dtype)).sum())
+
+
+def rel_max_rms(got, ref):
+    """max|got - ref| / RMS(ref), the reference suite's metric (test_fa_p100.py:35-37)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(got - ref).max() / math.sqrt(float((ref * ref).mean())))
+
+
+def rel_l2(got, ref):
+    """||got - ref||_2 / ||ref||_2."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.linalg.norm((got - ref).ravel()) / np.linalg.norm(ref.ravel()))
+
+
+def max_abs(got, ref):
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    return float(np.abs(got - ref).max())
+
+
+def fwd_flops(b, hq, n, d, causal):
+    """Algorithmic forward FLOPs 4*B*Hq*N^2*D, halved for causal (attention.cu:219)."""
+    f = 4.0 * b * hq * n * n * d
+    return f / 2 if causal else f
+
+
+def bwd_flops(b, hq, n, d, causal):
+    """Backward FLOPs = 2.5x the forward (bwd.cu:246)."""
+    return 2.5 * fwd_flops(b, hq, n, d, causal)

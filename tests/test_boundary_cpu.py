@@ -1,0 +1,76 @@
+"""Boundary checks that need no GPU: the C-ABI library and the torch binding.
+
+No kernel is launched here: only symbol lookup, host-side helpers and the
+argument checks that reject before any device work.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from helpers import LIB, header_functions, load_capi
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    declared = header_functions()
+    assert {"fa_fwd", "fa_bwd", "fa_bwd_workspace_bytes", "fa_bwd_preprocess",
+            "fa_bwd_main", "fa_error_string", "fa_version"} <= set(declared)
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/fa_mi355x.h but not exported"
+
+
+def test_host_only_helpers():
+    lib = load_capi()
+    assert lib.fa_version().decode().startswith("fa_mi355x")
+    assert lib.fa_error_string(0) == b"success"
+    assert b"64 or 128" in lib.fa_error_string(10001)
+    assert b"multiple" in lib.fa_error_string(10003)
+    # (B, Hq, N) float32 rounded up to 256 bytes; 0 for an invalid shape.
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 128) == 8 * 4096 * 4
+    assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 256
+    assert lib.fa_bwd_workspace_bytes(1, 8, 3, 4096, 128) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 80) == 0
+
+
+def test_capi_validation_returns_before_any_launch():
+    lib = load_capi()
+    s = ctypes.c_void_p(0)
+    z = ctypes.c_void_p(0)
+    # head dim, sequence length, heads, batch, null pointers
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 96, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 0, 64, 0, 0, s) == 10002
+    assert lib.fa_fwd(z, z, z, z, z, 1, 4, 3, 8, 64, 0, 0, s) == 10003
+    assert lib.fa_fwd(z, z, z, z, z, 0, 2, 2, 8, 64, 0, 0, s) == 10004
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 64, 0, 0, s) == 10005
+    assert lib.fa_bwd_main(*([z] * 9), 1, 2, 2, 8, 64, 1, s) == 10005
+    assert lib.fa_bwd_preprocess(z, z, z, z, 1, 2, 8, 128, s) == 10005
+    one = ctypes.c_void_p(1)
+    assert lib.fa_bwd(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, s) == 10006
+
+
+def test_binding_rejects_host_tensors_with_reference_messages():
+    import fa_p100
+    x = torch.zeros(1, 2, 8, 64, dtype=torch.half)
+    with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
+        fa_p100._ext.forward(x, x, x, False, False)
+    with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
+        fa_p100._ext.backward(x, x, x, x, x, torch.zeros(1, 2, 8), True)
+    with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
+        fa_p100.flash_attn(x, x, x, True)
+
+
+def test_public_api_surface_matches_reference():
+    import inspect
+
+    import fa_p100
+    import fa_p100_hf
+    sig = inspect.signature(fa_p100.flash_attn)
+    assert list(sig.parameters) == ["q", "k", "v", "causal", "full_precision"]
+    assert sig.parameters["causal"].default is False
+    assert sig.parameters["full_precision"].default is False
+    for name in ("_FlashAttnP100", "reference", "_expand_kv", "_ext"):
+        assert hasattr(fa_p100, name)
+    for name in ("fa_p100_attention_forward", "register", "enable_fa_p100", "_set_impl"):
+        assert hasattr(fa_p100_hf, name)
+    assert callable(fa_p100._ext.forward) and callable(fa_p100._ext.backward)

@@ -1,0 +1,219 @@
+"""GPU parity of the gfx950 kernels against the float64 CPU oracle.
+
+Restates the reference's regression matrix (test_fa_p100.py:56-139) as pytest:
+forward over D x (Hq, Hkv) x N x causal x precision tier, gradients over
+D x (Hq, Hkv) x N x causal, and the four input regimes, plus the committed
+golden fixtures, each through the public `flash_attn` op and through the C ABI.
+
+Bars: forward max-abs <= 4e-3 and LSE max-abs <= 1e-3; dQ/dK/dV relative L2
+<= 1e-2; the reference's max|err|/RMS(ref) < 6e-2 on everything.
+"""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (FWD_MAX_ABS, GRAD_REL_L2, LSE_MAX_ABS, REF_REL, ROOT, load_capi,
+                     make_inputs, np64)
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _fa():
+    import fa_p100
+    return fa_p100
+
+
+def run_flash(q, k, v, do, causal, full_precision=False):
+    """Forward + backward through flash_attn; returns numpy o, dq, dk, dv."""
+    fa = _fa()
+    qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    o = fa.flash_attn(qg, kg, vg, causal, full_precision)
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    return np64(o), np64(qg.grad), np64(kg.grad), np64(vg.grad)
+
+
+def check_fwd(o, ref_o, what):
+    err = ora.max_abs(o, ref_o)
+    rel = ora.rel_max_rms(o, ref_o)
+    assert err <= FWD_MAX_ABS and rel < REF_REL, f"{what}: max-abs {err:.3e} rel {rel:.3e}"
+
+
+def check_grads(got, ref, what):
+    for name, g, r in zip(("dQ", "dK", "dV"), got, ref):
+        assert np.isfinite(g).all(), f"{what} {name}: non-finite"
+        if not np.any(r):
+            # e.g. N=1: softmax over one key is constant, so dQ is exactly 0.
+            assert np.abs(g).max() <= 1e-6, f"{what} {name}: expected zeros, max {np.abs(g).max():.3e}"
+            continue
+        l2 = ora.rel_l2(g, r)
+        rel = ora.rel_max_rms(g, r)
+        assert l2 <= GRAD_REL_L2 and rel < REF_REL, f"{what} {name}: rel-L2 {l2:.3e} rel {rel:.3e}"
+
+
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (8, 2), (8, 1)])
+@pytest.mark.parametrize("N", [1, 7, 63, 64, 65, 333, 1023])
+def test_forward_matrix(D, Hq, Hkv, N):
+    """test_fa_p100.py:56-78: both causalities, both precision tiers, plus LSE."""
+    fa = _fa()
+    q, k, v, _ = make_inputs(1, Hq, Hkv, N, D, seed=N * 7 + D + Hkv)
+    for causal in (False, True):
+        ref_o, ref_lse = ora.attention_fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+        for fp in (False, True):
+            o = fa.flash_attn(q.to(DEV), k.to(DEV), v.to(DEV), causal, fp)
+            check_fwd(np64(o), ref_o, f"fwd D{D} {Hq}/{Hkv} N{N} causal={causal} fp32={fp}")
+        o, lse = fa._ext.forward(q.to(DEV), k.to(DEV), v.to(DEV), causal, False)
+        assert lse.dtype == torch.float32 and tuple(lse.shape) == (1, Hq, N)
+        err = ora.max_abs(np64(lse), ref_lse)
+        assert err <= LSE_MAX_ABS, f"lse D{D} {Hq}/{Hkv} N{N} causal={causal}: {err:.3e}"
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 2), (8, 1)])
+@pytest.mark.parametrize("N", [7, 64, 129, 333])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gradient_matrix(D, Hq, Hkv, N, causal):
+    """test_fa_p100.py:82-103, against the float64 analytic backward."""
+    q, k, v, do = make_inputs(1, Hq, Hkv, N, D, seed=N * 13 + D + Hkv + causal)
+    got = run_flash(q, k, v, do, causal, True)
+    ref_o, _ = ora.attention_fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    ref = ora.attention_bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal)
+    check_fwd(got[0], ref_o, "fwd")
+    check_grads(got[1:], ref, f"grad D{D} {Hq}/{Hkv} N{N} causal={causal}")
+
+
+@pytest.mark.parametrize("regime,scale", [("1 N(0,1)", 1.0), ("2 large x10", 10.0),
+                                          ("3 near-uniform", 0.05), ("4 near-one-hot", 3.0)])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_input_regimes(regime, scale, D, causal):
+    """test_fa_p100.py:107-139: q, k scaled, v and dO N(0,1), (1,4,256,D).
+
+    The max-abs forward bar is stated for N(0,1)-scale inputs; every regime
+    must still meet the relative bars.
+    """
+    q, k, v, do = make_inputs(1, 4, 4, 256, D, seed=int(scale * 100) + D + causal,
+                              scale_qk=scale)
+    got = run_flash(q, k, v, do, causal, True)
+    ref_o, _ = ora.attention_fwd(q.numpy(), k.numpy(), v.numpy(), causal)
+    ref = ora.attention_bwd(q.numpy(), k.numpy(), v.numpy(), do.numpy(), causal)
+    check_fwd(got[0], ref_o, f"regime {regime} D{D} causal={causal}")
+    check_grads(got[1:], ref, f"regime {regime} D{D} causal={causal}")
+
+
+# ---------------------------------------------------------------------------
+def _golden_cases():
+    path = os.path.join(ROOT, "tests", "golden", "attention_cases.npz")
+    z = np.load(path)
+    n = len([k for k in z.files if k.endswith("_meta")])
+    return [(i, {k[len(f"c{i}_"):]: z[k] for k in z.files if k.startswith(f"c{i}_")})
+            for i in range(n)]
+
+
+@pytest.mark.parametrize("idx,case", _golden_cases(), ids=lambda x: str(x) if isinstance(x, int) else "")
+def test_golden_fixtures_via_op(idx, case):
+    b, hq, hkv, n, d, causal = (int(x) for x in case["meta"])
+    q, k, v, do = (torch.from_numpy(case[x]) for x in ("q", "k", "v", "do"))
+    got = run_flash(q, k, v, do, bool(causal))
+    check_fwd(got[0], case["o"], f"golden {idx}")
+    check_grads(got[1:], (case["dq"], case["dk"], case["dv"]), f"golden {idx}")
+
+
+@pytest.mark.parametrize("idx,case", _golden_cases(), ids=lambda x: str(x) if isinstance(x, int) else "")
+def test_golden_fixtures_via_capi(idx, case):
+    """Same fixtures through the C ABI (ctypes), with caller-owned buffers."""
+    lib = load_capi()
+    b, hq, hkv, n, d, causal = (int(x) for x in case["meta"])
+    q, k, v, do = (torch.from_numpy(case[x]).to(DEV) for x in ("q", "k", "v", "do"))
+    o = torch.empty_like(q)
+    lse = torch.empty(b, hq, n, device=DEV, dtype=torch.float32)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    rc = lib.fa_fwd(p(q), p(k), p(v), p(o), p(lse), b, hq, hkv, n, d, causal, 0, stream)
+    assert rc == 0, lib.fa_error_string(rc)
+    ws_bytes = lib.fa_bwd_workspace_bytes(b, hq, hkv, n, d)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq = torch.full((b, hq, n, d), 7.0, device=DEV)   # fa_bwd must clear it itself
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    rc = lib.fa_bwd(p(q), p(k), p(v), p(do), p(o), p(lse), p(dq), p(dk), p(dv), p(ws),
+                    ws_bytes, b, hq, hkv, n, d, causal, stream)
+    assert rc == 0, lib.fa_error_string(rc)
+    torch.cuda.synchronize()
+    check_fwd(np64(o), case["o"], f"capi golden {idx}")
+    assert ora.max_abs(np64(lse), case["lse"]) <= LSE_MAX_ABS
+    check_grads((np64(dq), np64(dk), np64(dv)), (case["dq"], case["dk"], case["dv"]),
+                f"capi golden {idx}")
+
+
+def test_capi_rejects_bad_arguments_without_launching():
+    lib = load_capi()
+    x = torch.zeros(1, 2, 8, 64, device=DEV, dtype=torch.half)
+    lse = torch.zeros(1, 2, 8, device=DEV)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(0)
+    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 96, 0, 0, s) == 10001
+    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 0, 64, 0, 0, s) == 10002
+    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 3, 2, 8, 64, 0, 0, s) == 10003
+    assert lib.fa_fwd(None, p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 64, 0, 0, s) == 10005
+    ws = torch.zeros(16, device=DEV, dtype=torch.uint8)
+    assert lib.fa_bwd(p(x), p(x), p(x), p(x), p(x), p(lse), p(lse), p(x), p(x), p(ws), 16,
+                      1, 2, 2, 8, 64, 0, s) == 10006
+
+
+def test_reference_error_messages_on_device():
+    """The binding's TORCH_CHECKs that need device tensors (fa_p100_ext.cu:31-65, 106-113)."""
+    fa = _fa()
+    h = lambda *s: torch.zeros(*s, device=DEV, dtype=torch.half)
+    with pytest.raises(RuntimeError, match="q must be fp16"):
+        fa._ext.forward(h(1, 2, 8, 64).float(), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
+    with pytest.raises(RuntimeError, match=r"q must be \(B, H, N, D\)"):
+        fa._ext.forward(h(2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
+    with pytest.raises(RuntimeError, match="head dim must be 64 or 128, got 96"):
+        fa._ext.forward(h(1, 2, 8, 96), h(1, 2, 8, 96), h(1, 2, 8, 96), False, False)
+    with pytest.raises(RuntimeError, match="N must be positive"):
+        fa._ext.forward(h(1, 2, 0, 64), h(1, 2, 0, 64), h(1, 2, 0, 64), False, False)
+    with pytest.raises(RuntimeError, match=r"query heads \(3\) must be a multiple of key/value heads \(2\)"):
+        fa._ext.forward(h(1, 3, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
+    with pytest.raises(RuntimeError, match="k and v must match"):
+        fa._ext.forward(h(1, 2, 8, 64), h(1, 2, 8, 64), h(1, 1, 8, 64), False, False)
+    with pytest.raises(RuntimeError, match="k/v must be"):
+        fa._ext.forward(h(1, 2, 8, 64), h(1, 2, 9, 64), h(1, 2, 9, 64), False, False)
+    with pytest.raises(RuntimeError, match="query heads must be a multiple of kv heads"):
+        fa._ext.backward(h(1, 3, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), h(1, 3, 8, 64),
+                         h(1, 3, 8, 64), torch.zeros(1, 3, 8, device=DEV), False)
+    with pytest.raises(RuntimeError, match="dO must be fp16"):
+        fa._ext.backward(h(1, 2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64).float(),
+                         h(1, 2, 8, 64), torch.zeros(1, 2, 8, device=DEV), False)
+
+
+def test_noncontiguous_inputs_and_current_stream():
+    """Transposed-view inputs (what HF passes) and launches on a side stream."""
+    fa = _fa()
+    q, k, v, do = make_inputs(2, 4, 2, 77, 64, seed=5)
+    ref_o, _ = ora.attention_fwd(q.numpy(), k.numpy(), v.numpy(), True)
+    qv = q.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    kv = k.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    vv = v.transpose(1, 2).contiguous().to(DEV).transpose(1, 2)
+    assert not qv.is_contiguous()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        o = fa.flash_attn(qv, kv, vv, True)
+    side.synchronize()
+    check_fwd(np64(o), ref_o, "strided inputs on a side stream")
+
+
+def test_backward_is_repeatable():
+    """dQ uses fp32 atomics: repeated runs must agree to fp32 reordering noise."""
+    q, k, v, do = make_inputs(1, 4, 4, 300, 128, seed=17)
+    a = run_flash(q, k, v, do, True)
+    b = run_flash(q, k, v, do, True)
+    assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])  # dK, dV deterministic
+    assert ora.rel_l2(a[1], b[1]) < 1e-6

@@ -1,0 +1,95 @@
+"""The HF hook's raise-on-unsupported guards (fa_p100_hf.py:64-105, 186-206).
+
+All guards fire before any kernel runs, so they are checked on the CPU with
+host tensors and a stub module; registration and enable_fa_p100 are checked on
+a tiny random-init Qwen3 built on the CPU.
+"""
+import types
+import warnings
+
+import pytest
+import torch
+
+import fa_p100_hf as hf
+
+
+def qkv(n=4, d=64, hq=4, hkv=2, dtype=torch.half, kv_len=None):
+    kv_len = n if kv_len is None else kv_len
+    return (torch.zeros(1, hq, n, d, dtype=dtype), torch.zeros(1, hkv, kv_len, d, dtype=dtype),
+            torch.zeros(1, hkv, kv_len, d, dtype=dtype))
+
+
+MOD = types.SimpleNamespace(is_causal=True)
+
+
+@pytest.mark.parametrize("kwargs,match", [
+    (dict(attention_mask=torch.ones(1, 1, 4, 4)), "attention mask"),
+    (dict(attention_mask=None, output_attentions=True), "output_attentions"),
+    (dict(attention_mask=None, head_mask=torch.ones(4)), "head_mask"),
+    (dict(attention_mask=None, sliding_window=128), "sliding window of 128"),
+    (dict(attention_mask=None, dropout=0.1), "dropout"),
+])
+def test_unsupported_requests_raise(kwargs, match):
+    q, k, v = qkv()
+    with pytest.raises(NotImplementedError, match=match):
+        hf.fa_p100_attention_forward(MOD, q, k, v, **kwargs)
+
+
+def test_head_dim_scale_and_kv_len_guards():
+    q, k, v = qkv(d=96)
+    with pytest.raises(NotImplementedError, match="head_dim 64 or 128, got 96"):
+        hf.fa_p100_attention_forward(MOD, q, k, v, None)
+    q, k, v = qkv(d=128)
+    with pytest.raises(NotImplementedError, match="scale"):
+        hf.fa_p100_attention_forward(MOD, q, k, v, None, scaling=0.1)
+    q, k, v = qkv(n=1, kv_len=9)
+    with pytest.raises(NotImplementedError, match="q_len == kv_len"):
+        hf.fa_p100_attention_forward(MOD, q, k, v, None)
+
+
+def test_valid_call_reaches_the_kernel_and_casts_with_one_warning():
+    # Host tensors pass every hook guard and are stopped by the binding's
+    # device check, i.e. the call really goes to the kernel (no CPU fallback).
+    hf._warned_cast = False
+    q, k, v = qkv(dtype=torch.float32)
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+            hf.fa_p100_attention_forward(MOD, q, k, v, None, scaling=64 ** -0.5)
+        with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+            hf.fa_p100_attention_forward(MOD, q, k, v, None)
+    assert sum("casts" in str(x.message) for x in w) == 1
+
+
+def _tiny_qwen3():
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=128, hidden_size=128, intermediate_size=256,
+                      num_hidden_layers=2, num_attention_heads=2, num_key_value_heads=1,
+                      head_dim=64, max_position_embeddings=256)
+    torch.manual_seed(0)
+    return Qwen3ForCausalLM(cfg)
+
+
+def test_register_and_enable():
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    assert hf.register() == "fa_p100"
+    assert ALL_ATTENTION_FUNCTIONS.get_interface("fa_p100", None) is hf.fa_p100_attention_forward
+    model = _tiny_qwen3()
+    hf.enable_fa_p100(model, full_precision=True)
+    assert model.config._attn_implementation == "fa_p100"
+    assert model.config.use_cache is False
+    assert all(getattr(m, "_fa_p100_full_precision") is True for m in model.modules())
+    inner = model.forward
+    hf.enable_fa_p100(model)          # idempotent: the guard wraps once
+    assert model.forward is inner
+
+    ids = torch.zeros(1, 6, dtype=torch.long)
+    with pytest.raises(NotImplementedError, match="padding mask"):
+        model(ids, attention_mask=torch.tensor([[1, 1, 1, 1, 0, 0]]))
+    with pytest.raises(NotImplementedError, match="KV cache"):
+        model(ids, use_cache=True)
+    # An all-ones mask passes the guard; the attention hook then receives no
+    # mask (transformers' early exit) and the call reaches the binding, whose
+    # device check stops host tensors.
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        model(ids, attention_mask=torch.ones(1, 6, dtype=torch.long))

@@ -1,0 +1,178 @@
+"""Pins the CPU oracle (oracle/attention.py) before anything is checked against it.
+
+Each check is chosen so a plausible slip in the restatement fails it:
+  * finite differences of loss = sum(dO*O) against the analytic backward
+    (bwd.cu:136-160) catch a wrong formula, sign, missing scale or a swapped
+    dK/dQ;
+  * torch's scaled_dot_product_attention + autograd in float64 (an independent
+    library implementation) catches a wrong scale, mask orientation, GQA head
+    map or LSE convention;
+  * closed forms (N=1, causal row 0, Q=0, LSE=log(count)) and invariants
+    (GQA == MHA on repeat_interleave'd K/V with group-summed grads, head
+    permutation equivariance, key permutation invariance, causal tail
+    independence) catch indexing slips that happen to cancel elsewhere.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as ora
+
+
+def rnd(rng, *shape, scale=1.0):
+    return rng.standard_normal(shape) * scale
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("hq,hkv", [(2, 2), (4, 2), (3, 1)])
+def test_backward_matches_finite_differences(causal, hq, hkv):
+    # bwd.cu:136-160: central differences with h = 1e-4, 12 probes cycling
+    # over Q, K, V, pass if the relative error is < 1e-4 (published 4e-10).
+    rng = np.random.default_rng(4242)
+    n, d = 19, 16
+    q, do = rnd(rng, 1, hq, n, d), rnd(rng, 1, hq, n, d)
+    k, v = rnd(rng, 1, hkv, n, d), rnd(rng, 1, hkv, n, d)
+    grads = ora.attention_bwd(q, k, v, do, causal)
+    h, worst = 1e-4, 0.0
+    for trial in range(12):
+        which = trial % 3
+        base = [q, k, v]
+        idx = int(rng.integers(base[which].size))
+        plus = [t.copy() for t in base]
+        minus = [t.copy() for t in base]
+        plus[which].flat[idx] += h
+        minus[which].flat[idx] -= h
+        fd = (ora.attention_loss(*plus, do, causal) - ora.attention_loss(*minus, do, causal)) / (2 * h)
+        an = grads[which].flat[idx]
+        worst = max(worst, abs(fd - an) / max(abs(an), 1e-3))
+    assert worst < 1e-4, worst
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("b,hq,hkv,n,d", [(1, 2, 2, 1, 64), (2, 4, 2, 37, 64),
+                                          (1, 4, 1, 65, 128), (1, 3, 3, 130, 32)])
+def test_matches_torch_sdpa_float64(causal, b, hq, hkv, n, d):
+    rng = np.random.default_rng(7)
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    o, lse = ora.attention_fwd(q, k, v, causal)
+    dq, dk, dv = ora.attention_bwd(q, k, v, do, causal)
+
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    to = F.scaled_dot_product_attention(tq, tk, tv, is_causal=causal, enable_gqa=hq != hkv)
+    to.backward(torch.tensor(do))
+    assert np.allclose(o, to.detach().numpy(), atol=1e-12, rtol=1e-10)
+    for mine, theirs in ((dq, tq.grad), (dk, tk.grad), (dv, tv.grad)):
+        assert np.allclose(mine, theirs.numpy(), atol=1e-11, rtol=1e-9)
+
+    # LSE: natural-log logsumexp of the scaled logits, computed independently.
+    ke = np.repeat(k, hq // hkv, axis=1)
+    s = torch.tensor(q @ np.swapaxes(ke, -1, -2) / math.sqrt(d))
+    if causal:
+        s = s.masked_fill(torch.triu(torch.ones(n, n, dtype=torch.bool), 1), float("-inf"))
+    assert np.allclose(lse, torch.logsumexp(s, -1).numpy(), atol=1e-12)
+
+
+def test_closed_forms():
+    rng = np.random.default_rng(1)
+    d = 64
+    # N = 1: the only key is the row itself, O = V and LSE = q.k * scale.
+    q, k, v = rnd(rng, 1, 2, 1, d), rnd(rng, 1, 2, 1, d), rnd(rng, 1, 2, 1, d)
+    for causal in (False, True):
+        o, lse = ora.attention_fwd(q, k, v, causal)
+        assert np.allclose(o, v)
+        assert np.allclose(lse, (q * k).sum(-1) / math.sqrt(d))
+    # Causal row 0 sees only key 0.
+    n = 9
+    q, k, v = rnd(rng, 1, 2, n, d), rnd(rng, 1, 2, n, d), rnd(rng, 1, 2, n, d)
+    o, _ = ora.attention_fwd(q, k, v, True)
+    assert np.allclose(o[:, :, 0], v[:, :, 0])
+    # Q = 0: uniform weights, O = (prefix) mean of V, LSE = log(count).
+    z = np.zeros_like(q)
+    o, lse = ora.attention_fwd(z, k, v, False)
+    assert np.allclose(o, np.broadcast_to(v.mean(axis=2, keepdims=True), o.shape))
+    assert np.allclose(lse, math.log(n))
+    o, lse = ora.attention_fwd(z, k, v, True)
+    counts = np.arange(1, n + 1)
+    assert np.allclose(o, np.cumsum(v, axis=2) / counts[:, None])
+    assert np.allclose(lse, np.log(counts))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_equals_mha_on_expanded_kv(causal):
+    rng = np.random.default_rng(3)
+    b, hq, hkv, n, d = 2, 6, 2, 23, 64
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    ke, ve = np.repeat(k, 3, axis=1), np.repeat(v, 3, axis=1)
+    o1, l1 = ora.attention_fwd(q, k, v, causal)
+    o2, l2 = ora.attention_fwd(q, ke, ve, causal)
+    assert np.allclose(o1, o2) and np.allclose(l1, l2)
+    dq1, dk1, dv1 = ora.attention_bwd(q, k, v, do, causal)
+    dq2, dk2, dv2 = ora.attention_bwd(q, ke, ve, do, causal)
+    assert np.allclose(dq1, dq2)
+    assert np.allclose(dk1, dk2.reshape(b, hkv, 3, n, d).sum(2))
+    assert np.allclose(dv1, dv2.reshape(b, hkv, 3, n, d).sum(2))
+    # head h uses kv head h // 3 (repeat_interleave), not h % hkv
+    o_h4, _ = ora.attention_fwd(q[:, 4:5], k[:, 1:2], v[:, 1:2], causal)
+    assert np.allclose(o1[:, 4:5], o_h4)
+
+
+def test_permutations_and_tail_independence():
+    rng = np.random.default_rng(5)
+    b, h, n, d = 1, 3, 17, 64
+    q, k, v, do = (rnd(rng, b, h, n, d) for _ in range(4))
+    # Head permutation equivariance.
+    perm = np.array([2, 0, 1])
+    o, _ = ora.attention_fwd(q, k, v, True)
+    op, _ = ora.attention_fwd(q[:, perm], k[:, perm], v[:, perm], True)
+    assert np.allclose(op, o[:, perm])
+    # Dense attention is invariant to permuting keys together with values;
+    # dK/dV permute along.
+    kp = rng.permutation(n)
+    o, _ = ora.attention_fwd(q, k, v, False)
+    o2, _ = ora.attention_fwd(q, k[:, :, kp], v[:, :, kp], False)
+    assert np.allclose(o, o2)
+    _, dk, dv = ora.attention_bwd(q, k, v, do, False)
+    _, dk2, dv2 = ora.attention_bwd(q, k[:, :, kp], v[:, :, kp], do, False)
+    assert np.allclose(dk[:, :, kp], dk2) and np.allclose(dv[:, :, kp], dv2)
+    # Causal: rows < m do not depend on anything at positions >= m.
+    m = 11
+    o_full, l_full = ora.attention_fwd(q, k, v, True)
+    o_cut, l_cut = ora.attention_fwd(q[:, :, :m], k[:, :, :m], v[:, :, :m], True)
+    assert np.allclose(o_full[:, :, :m], o_cut) and np.allclose(l_full[:, :, :m], l_cut)
+
+
+def test_preprocess_and_metrics():
+    rng = np.random.default_rng(9)
+    o, do = rnd(rng, 1, 2, 5, 8), rnd(rng, 1, 2, 5, 8)
+    assert np.allclose(ora.bwd_preprocess(o, do), np.einsum("bhnd,bhnd->bhn", o, do))
+    ref = np.array([3.0, -4.0])                   # RMS = sqrt(12.5)
+    got = np.array([3.5, -4.0])
+    assert ora.rel_max_rms(got, ref) == pytest.approx(0.5 / math.sqrt(12.5))
+    assert ora.rel_l2(got, ref) == pytest.approx(0.5 / 5.0)
+    assert ora.max_abs(got, ref) == pytest.approx(0.5)
+    # FLOP convention (attention.cu:219, bwd.cu:246) at the headline shape.
+    assert ora.fwd_flops(1, 8, 4096, 128, True) == pytest.approx(34.36e9, rel=1e-3)
+    assert ora.bwd_flops(1, 8, 4096, 128, True) == pytest.approx(85.90e9, rel=1e-3)
+
+
+def test_planted_mistakes_are_caught():
+    """A wrong scale placement or a transposed GQA map must fail the pins above."""
+    rng = np.random.default_rng(11)
+    b, hq, hkv, n, d = 1, 4, 2, 12, 64
+    q, k, v = rnd(rng, b, hq, n, d), rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    tq, tk, tv = (torch.tensor(x) for x in (q, k, v))
+    good = F.scaled_dot_product_attention(tq, tk, tv, is_causal=True, enable_gqa=True).numpy()
+    o, _ = ora.attention_fwd(q, k, v, True)
+    assert np.allclose(o, good)
+    # Planted: kv head chosen by h % hkv (tile) instead of h // G (interleave).
+    bad_k, bad_v = np.tile(k, (1, 2, 1, 1)), np.tile(v, (1, 2, 1, 1))
+    bad, _ = ora.attention_fwd(q, bad_k, bad_v, True)
+    assert not np.allclose(bad, good)
+    # Planted: mask orientation flipped (future visible, past hidden).
+    bad, _ = ora.attention_fwd(q[:, :, ::-1], k[:, :, ::-1], v[:, :, ::-1], True)
+    assert not np.allclose(bad[:, :, ::-1], good)
