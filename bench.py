@@ -7,7 +7,7 @@ causal MHA, B=1, Hq=Hkv=8, N=4096, D=128, fp16 inputs from one seeded CPU
 generator (q, k, v, dO in that order, N(0,1)), resident in HBM before timing.
 
 One step = the hot path through the C ABI on torch's current stream:
-fa_fwd, then fa_bwd_preprocess (Dv, dQ := 0), then fa_bwd_main, into
+fa_fwd, then fa_bwd_preprocess (Dv), then fa_bwd_main (dK, dV, dQ), into
 preallocated buffers. K steps are timed between two device synchronisations;
 HIP events recorded on the same stream between the launches give each
 kernel's average duration. The same step through the public autograd op
@@ -69,7 +69,7 @@ def load_capi():
     lib = ctypes.CDLL(os.path.join(PKG, "libfa_mi355x.so"))
     vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
     lib.fa_fwd.argtypes = [vp] * 5 + [i] * 7 + [vp]
-    lib.fa_bwd_preprocess.argtypes = [vp] * 4 + [i] * 4 + [vp]
+    lib.fa_bwd_preprocess.argtypes = [vp] * 3 + [i] * 4 + [vp]
     lib.fa_bwd_main.argtypes = [vp] * 9 + [i] * 6 + [vp]
     lib.fa_bwd_workspace_bytes.argtypes = [i] * 5
     lib.fa_bwd_workspace_bytes.restype = sz
@@ -105,7 +105,7 @@ def gpu_bench(c, steps, warmup):
         check(lib.fa_fwd(pq, pk, pv, po, plse, B, Hq, Hkv, N, D, causal, 0, s), "fa_fwd")
         if ev is not None:
             ev[1].record(stream)
-        check(lib.fa_bwd_preprocess(pdo, po, pdvec, pdq, B, Hq, N, D, s), "fa_bwd_preprocess")
+        check(lib.fa_bwd_preprocess(pdo, po, pdvec, B, Hq, N, D, s), "fa_bwd_preprocess")
         if ev is not None:
             ev[2].record(stream)
         check(lib.fa_bwd_main(pq, pk, pv, pdo, plse, pdvec, pdq, pdk, pdv, B, Hq, Hkv, N, D,

@@ -1,31 +1,39 @@
 // FlashAttention-2 backward for gfx950 (MI355X).
 //
 // Counterpart of the reference's flash_bwd::bwd_preprocess and
-// flash_bwd::bwd_kernel (flash_bwd.cuh:65-78, 95-464), redesigned around
-// MFMA. Per (query tile i, key tile j), with L = LSE and Dv = rowsum(dO*O):
+// flash_bwd::bwd_kernel (flash_bwd.cuh:65-78, 95-464). Per (query tile i,
+// key tile j), with L = LSE and Dv = rowsum(dO*O) (flash_bwd.cuh:11-16):
 //   S = Q K^T            P = exp(S*scale - L)
 //   dV += P^T dO         dP = dO V^T
 //   dS = P (dP - Dv)     dK += dS^T Q * scale     dQ += dS K * scale
-// (flash_bwd.cuh:11-16).
 //
-// Main kernel layout (K/V stationary, FA2 loop order):
-//   * a workgroup owns kBC = 128 key rows; each of its 4 waves owns 32 of
-//     them and keeps its K and V rows in registers as MFMA B operands and its
-//     dK^T / dV^T blocks in fp32 accumulators for the whole kernel;
-//   * it walks the query rows in tiles of kBR = 32 (from the diagonal on,
-//     for causal, flash_bwd.cuh:158-161), looping over the query heads of its
-//     key/value head for GQA/MQA (flash_bwd.cuh:120-131, 163);
-//   * S and dP come out of v_mfma_f32_32x32x16_f16 with lane l holding key
-//     column l % 32, so P and dS feed dV^T += dO^T P and dK^T += Q^T dS
-//     straight from the accumulators (the product's K index order is chosen
-//     to match), with Q^T / dO^T staged transposed in LDS;
-//   * dS is also written to LDS (fp16) so the four waves can form
-//     dQ = dS K over all 128 keys, one 32-column slice of the head dim per
-//     wave, added to the fp32 dQ with atomics (flash_bwd.cuh:434-443);
-//   * dead lanes (causal col > row, ragged row/col >= N) contribute exactly
-//     zero (flash_bwd.cuh:267-282).
-// P and dS are rounded to fp16 only as MFMA operands; S, dP, P and dS are
-// computed in fp32.
+// The reference accumulates dQ with fp32 atomicAdd from its key-stationary
+// blocks (flash_bwd.cuh:434-443). Measured on MI355X, fp32 atomics sustain
+// ~1.3 TB/s whatever their scope or locality, about 1/5 of plain stores, and
+// at the headline shape that stream alone would outlast the whole backward.
+// So dQ gets its own query-stationary pass that recomputes S and dP (7
+// products per tile pair instead of 5, but no atomics, no dQ clearing, and a
+// deterministic result), and both passes run in ONE launch:
+//
+//   workgroup (t, b*Hkv + hkv), 4 waves:
+//     phase 1: dK, dV for key rows [128t, 128t+128) of kv head hkv,
+//              over all query heads of its group and all query tiles
+//              (from the diagonal on when causal, flash_bwd.cuh:158-161)
+//     phase 2: dQ for query rows [128t, 128t+128) of each query head of the
+//              group, over all key tiles (up to the diagonal when causal)
+//
+// Under causal masking phase 1 shrinks with t while phase 2 grows with t, so
+// the workgroups' total work is nearly equal without giving up parallelism.
+//
+// Both phases run on v_mfma_f32_32x32x16_f16 with 32 rows per wave. Phase 1
+// keeps the wave's K and V rows in registers (B operands) and dK^T/dV^T in
+// accumulators; P and dS come out of the S/dP accumulators and feed
+// dV^T += dO^T P and dK^T += Q^T dS directly, with the dO^T/Q^T operands read
+// from the row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the
+// forward kernel: S^T = K Q^T and dP^T = V dO^T with Q, dO held as B
+// operands, then dQ^T += K^T dS^T. Dead lanes (causal col > row, ragged
+// rows/cols >= N) contribute exactly zero (flash_bwd.cuh:267-282). P and dS
+// are rounded to fp16 only as MFMA operands.
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -34,34 +42,25 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBC = 32 * kWaves;  // key rows per workgroup
-constexpr int kBR = 32;           // query rows per inner tile
+constexpr int kTile = 32 * kWaves;  // rows a workgroup owns (keys in phase 1, queries in phase 2)
+constexpr int kSub = 64;            // rows per streamed tile (queries in 1, keys in 2)
 
 template <int D>
-struct BwdSmem {
-  static constexpr int kKtRow = kBC + 8;   // K^T  [D][kKtRow]
-  static constexpr int kQRow = D + 8;      // Q, dO row-major [kBR][kQRow]
-  static constexpr int kQtRow = kBR + 4;   // Q^T, dO^T [D][kQtRow]
-  static constexpr int kSRow = kBC + 8;    // dS   [kBR][kSRow]
-  static constexpr int kKt = 0;
-  static constexpr int kQs = kKt + D * kKtRow;
-  static constexpr int kQt = kQs + kBR * kQRow;
-  static constexpr int kOs = kQt + D * kQtRow;
-  static constexpr int kOt = kOs + kBR * kQRow;
-  static constexpr int kSs = kOt + D * kQtRow;
-  static constexpr int kHalves = kSs + kBR * kSRow;
-  static constexpr int kBytes = kHalves * 2 + 2 * kBR * 4;  // + lse2, dvec
+struct BwdLds {
+  static constexpr int kRow = D + 8;
+  static constexpr int kTileHalves = kSub * kRow;
+  static constexpr int kStageHalves = 2 * kTileHalves;      // two tensors per stage
+  static constexpr int kFloatOff = 2 * kStageHalves * 2;    // bytes: after both stages
+  static constexpr int kBytes = kFloatOff + 2 * 2 * kSub * 4;  // per stage: lse2[64], dvec[64]
 };
 
 // ---------------------------------------------------------------------------
 // Preprocess: dvec[row] = sum_d float(O[row,d]) * float(dO[row,d]) from the
-// fp16-rounded O (flash_bwd.cuh:65-78), fused with clearing dq (the
-// reference's cudaMemsetAsync, flash_bwd.cuh:476).
+// fp16-rounded O (flash_bwd.cuh:65-78).
 template <int D>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__ O,
                                                       const half_t* __restrict__ dO,
-                                                      float* __restrict__ dvec,
-                                                      float* __restrict__ dq, long rows) {
+                                                      float* __restrict__ dvec, long rows) {
   constexpr int kLanesPerRow = D / 8;
   constexpr int kRowsPerBlock = 256 / kLanesPerRow;
   const int tid = threadIdx.x;
@@ -73,9 +72,6 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
     const half8 g = as_half8(*reinterpret_cast<const u32x4*>(dO + row * D + c8));
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += (float)o[e] * (float)g[e];
-    floatx4 z = {0.f, 0.f, 0.f, 0.f};
-    *reinterpret_cast<floatx4*>(dq + row * D + c8) = z;
-    *reinterpret_cast<floatx4*>(dq + row * D + c8 + 4) = z;
   }
 #pragma unroll
   for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
@@ -83,47 +79,6 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
 }
 
 // ---------------------------------------------------------------------------
-// Stages one query tile: Q and dO both row-major and transposed, plus the
-// tile's LSE (converted to the log2 domain) and dvec.
-template <int D>
-__device__ __forceinline__ void stage_q_tile(half_t* smem, float* lse2s, float* dvs,
-                                             const half_t* Qg, const half_t* dOg,
-                                             const float* Lg, const float* Dg, int i0,
-                                             int N, int tid, bool bounds) {
-  using S = BwdSmem<D>;
-  constexpr int kTasks = (kBR / 4) * (D / 8);  // per tensor
-#pragma unroll
-  for (int t = tid; t < 2 * kTasks; t += kThreads) {
-    const int which = t / kTasks;  // 0: Q, 1: dO
-    const int idx = t % kTasks;
-    const int rg = idx % (kBR / 4), dg = idx / (kBR / 4);
-    const half_t* src = which ? dOg : Qg;
-    u32x4 rows[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + rg * 4 + r;
-      rows[r] = load16(src + (size_t)i * D + dg * 8, !bounds || i < N);
-    }
-    half_t* rm = smem + (which ? S::kOs : S::kQs);
-    half_t* tr = smem + (which ? S::kOt : S::kQt);
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      *reinterpret_cast<u32x4*>(rm + (rg * 4 + r) * S::kQRow + dg * 8) = rows[r];
-    u32x2 cols[8];
-    transpose_4x8(rows, cols);
-#pragma unroll
-    for (int c = 0; c < 8; ++c)
-      *reinterpret_cast<u32x2*>(tr + (dg * 8 + c) * S::kQtRow + rg * 4) = cols[c];
-  }
-  if (tid < kBR) {
-    const int i = i0 + tid;
-    lse2s[tid] = (!bounds || i < N) ? Lg[i] * kLog2e : 0.f;
-  } else if (tid < 2 * kBR) {
-    const int i = i0 + tid - kBR;
-    dvs[tid - kBR] = (!bounds || i < N) ? Dg[i] : 0.f;
-  }
-}
-
 template <int D, bool CAUSAL, bool BOUNDS>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
@@ -131,10 +86,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const float* __restrict__ Lse, const float* __restrict__ Dvec,
     float* __restrict__ dQ, half_t* __restrict__ dK, half_t* __restrict__ dV,
     int N, int Hq, int group, float scale, float scale_log2) {
-  using S = BwdSmem<D>;
+  using L = BwdLds<D>;
+  constexpr int kRow = L::kRow;
   extern __shared__ __align__(16) half_t smem[];
-  float* lse2s = reinterpret_cast<float*>(smem + S::kHalves);
-  float* dvs = lse2s + kBR;
+  float* fl = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kFloatOff);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -142,165 +97,246 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
-  const int j0 = blockIdx.x * kBC;
-  const int bkv = blockIdx.y;  // over B*Hkv
+  const int t0 = blockIdx.x * kTile;  // first row this workgroup owns
+  const int bkv = blockIdx.y;         // over B*Hkv
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
   const size_t kv_off = (size_t)bkv * N * D;
-  K += kv_off;
-  V += kv_off;
-  dK += kv_off;
-  dV += kv_off;
+  const half_t* Kh = K + kv_off;
+  const half_t* Vh = V + kv_off;
 
-  // Stationary K^T in LDS for the dQ product.
+  // =========================== phase 1: dK, dV ===========================
   {
-    constexpr int kTasks = (kBC / 4) * (D / 8);
+    const int jw = t0 + wave * 32;  // this wave's key rows
+    const int j_col = jw + l32;
+    half8 kb[D / 16], vb[D / 16];
 #pragma unroll
-    for (int t = tid; t < kTasks; t += kThreads) {
-      const int rg = t % (kBC / 4), dg = t / (kBC / 4);
-      u32x4 rows[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = j0 + rg * 4 + r;
-        rows[r] = load16(K + (size_t)j * D + dg * 8, !BOUNDS || j < N);
-      }
-      u32x2 cols[8];
-      transpose_4x8(rows, cols);
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        *reinterpret_cast<u32x2*>(smem + S::kKt + (dg * 8 + c) * S::kKtRow + rg * 4) = cols[c];
+    for (int kk = 0; kk < D / 16; ++kk) {
+      const bool ok = !BOUNDS || j_col < N;
+      kb[kk] = as_half8(load16(Kh + (size_t)j_col * D + kk * 16 + h * 8, ok));
+      vb[kk] = as_half8(load16(Vh + (size_t)j_col * D + kk * 16 + h * 8, ok));
     }
-  }
-
-  // This wave's key rows as B operands (K^T for S, V^T for dP).
-  const int jw = j0 + wave * 32;
-  const int j_col = jw + l32;
-  half8 kb[D / 16], vb[D / 16];
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk) {
-    const bool ok = !BOUNDS || j_col < N;
-    kb[kk] = as_half8(load16(K + (size_t)j_col * D + kk * 16 + h * 8, ok));
-    vb[kk] = as_half8(load16(V + (size_t)j_col * D + kk * 16 + h * 8, ok));
-  }
-
-  floatx16 dvacc[D / 32], dkacc[D / 32];
-#pragma unroll
-  for (int c = 0; c < D / 32; ++c) {
-    dvacc[c] = zero16();
-    dkacc[c] = zero16();
-  }
-
-  const int i_start = CAUSAL ? j0 : 0;  // j0 is a multiple of kBR
-  for (int g = 0; g < group; ++g) {
-    const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
-    const half_t* Qg = Q + bhq * N * D;
-    const half_t* dOg = dO + bhq * N * D;
-    const float* Lg = Lse + bhq * N;
-    const float* Dg = Dvec + bhq * N;
-    float* dQg = dQ + bhq * N * D;
-
-    for (int i0 = i_start; i0 < N; i0 += kBR) {
-      stage_q_tile<D>(smem, lse2s, dvs, Qg, dOg, Lg, Dg, i0, N, tid, BOUNDS);
-      __syncthreads();
-
-      half_t* dSs = smem + S::kSs;
-      const bool active = !CAUSAL || (i0 + kBR - 1 >= jw);
-      if (active) {
-        floatx16 sacc = zero16(), pacc = zero16();
-        const half_t* qrow = smem + S::kQs + l32 * S::kQRow + h * 8;
-        const half_t* orow = smem + S::kOs + l32 * S::kQRow + h * 8;
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          sacc = mfma32(*reinterpret_cast<const half8*>(qrow + kk * 16), kb[kk], sacc);
-          pacc = mfma32(*reinterpret_cast<const half8*>(orow + kk * 16), vb[kk], pacc);
-        }
-        // P and dS; row i = i0 + 8*(r/4) + 4h + r%4, column j_col.
-        const bool need_mask = (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kBR > N || jw + 32 > N));
-        half8 pb[2], sb[2];
-#pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 8 * g4 + 4 * h);
-          const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 8 * g4 + 4 * h);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g4 + e;
-            float p = fast_exp2(sacc[r] * scale_log2 - l4[e]);
-            if (need_mask) {
-              const int i = i0 + 8 * g4 + 4 * h + e;
-              const bool dead = (CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N));
-              if (dead) p = 0.f;
-            }
-            const float ds = p * (pacc[r] - d4[e]);
-            pb[r >> 3][r & 7] = (half_t)p;
-            sb[r >> 3][r & 7] = (half_t)ds;
-            dSs[(8 * g4 + 4 * h + e) * S::kSRow + wave * 32 + l32] = (half_t)ds;
-          }
-        }
-        // dV^T += dO^T P and dK^T += Q^T dS. K-step q covers query rows
-        // 16q .. 16q+15; slot (h, e) is row 16q + 8*(e/4) + 4h + e%4.
-#pragma unroll
-        for (int c = 0; c < D / 32; ++c) {
-          const half_t* ot = smem + S::kOt + (c * 32 + l32) * S::kQtRow + 4 * h;
-          const half_t* qt = smem + S::kQt + (c * 32 + l32) * S::kQtRow + 4 * h;
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            const half4 olo = *reinterpret_cast<const half4*>(ot + 16 * q);
-            const half4 ohi = *reinterpret_cast<const half4*>(ot + 16 * q + 8);
-            const half4 qlo = *reinterpret_cast<const half4*>(qt + 16 * q);
-            const half4 qhi = *reinterpret_cast<const half4*>(qt + 16 * q + 8);
-            const half8 ao = {olo[0], olo[1], olo[2], olo[3], ohi[0], ohi[1], ohi[2], ohi[3]};
-            const half8 aq = {qlo[0], qlo[1], qlo[2], qlo[3], qhi[0], qhi[1], qhi[2], qhi[3]};
-            dvacc[c] = mfma32(ao, pb[q], dvacc[c]);
-            dkacc[c] = mfma32(aq, sb[q], dkacc[c]);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          dSs[(8 * (r >> 2) + 4 * h + (r & 3)) * S::kSRow + wave * 32 + l32] = (half_t)0.f;
-      }
-      __syncthreads();
-
-      // dQ[i, d] += scale * sum_j dS[i, j] K[j, d] over the workgroup's keys.
-      {
-        constexpr int kDBlocks = D / 32;                 // 32-column slices
-        constexpr int kJSplit = kWaves / kDBlocks;       // waves sharing a slice
-        constexpr int kJSteps = kBC / 16 / kJSplit;      // 16-key steps per wave
-        const int c = wave % kDBlocks;
-        const int js = wave / kDBlocks;
-        floatx16 qacc = zero16();
-        const half_t* srow = dSs + l32 * S::kSRow + h * 8 + js * kJSteps * 16;
-        const half_t* krow = smem + S::kKt + (c * 32 + l32) * S::kKtRow + h * 8 + js * kJSteps * 16;
-#pragma unroll
-        for (int t = 0; t < kJSteps; ++t)
-          qacc = mfma32(*reinterpret_cast<const half8*>(srow + t * 16),
-                        *reinterpret_cast<const half8*>(krow + t * 16), qacc);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int i = i0 + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (!BOUNDS || i < N)
-            unsafeAtomicAdd(dQg + (size_t)i * D + c * 32 + l32, qacc[r] * scale);
-        }
-      }
-    }
-  }
-
-  // dK (scaled) and dV leave once, from the accumulators, as fp16.
-  if (!BOUNDS || j_col < N) {
-    half_t* dkrow = dK + (size_t)j_col * D;
-    half_t* dvrow = dV + (size_t)j_col * D;
+    floatx16 dvacc[D / 32], dkacc[D / 32];
 #pragma unroll
     for (int c = 0; c < D / 32; ++c) {
+      dvacc[c] = zero16();
+      dkacc[c] = zero16();
+    }
+
+    const int i_start = CAUSAL ? t0 : 0;  // t0 is a multiple of kSub
+    const int n_qt = (N - i_start + kSub - 1) / kSub;
+    const int n_it = group * n_qt;  // (query head, query tile) pairs, flattened
+
+    RowStage<D, kSub> sq, so;
+    float pf_l = 0.f, pf_d = 0.f;  // prefetched lse2 / dvec (threads 0..63)
+    auto fetch = [&](int it) {
+      const int g = it / n_qt;
+      const int i0 = i_start + (it % n_qt) * kSub;
+      const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
+      sq.load(Q + bhq * N * D, i0, N, tid, BOUNDS);
+      so.load(dO + bhq * N * D, i0, N, tid, BOUNDS);
+      if (tid < kSub) {
+        const int i = i0 + tid;
+        const bool ok = !BOUNDS || i < N;
+        pf_l = ok ? Lse[bhq * N + i] * kLog2e : 0.f;
+        pf_d = ok ? Dvec[bhq * N + i] : 0.f;
+      }
+    };
+    auto put = [&](int stage) {
+      half_t* base = smem + stage * L::kStageHalves;
+      sq.store(base, tid);
+      so.store(base + L::kTileHalves, tid);
+      if (tid < kSub) {
+        fl[stage * 2 * kSub + tid] = pf_l;
+        fl[stage * 2 * kSub + kSub + tid] = pf_d;
+      }
+    };
+
+    fetch(0);
+    put(0);
+    __syncthreads();
+    for (int it = 0; it < n_it; ++it) {
+      const int i0 = i_start + (it % n_qt) * kSub;
+      const bool has_next = it + 1 < n_it;
+      if (has_next) fetch(it + 1);
+
+      const half_t* Qs = smem + (it & 1) * L::kStageHalves;
+      const half_t* Os = Qs + L::kTileHalves;
+      const float* lse2s = fl + (it & 1) * 2 * kSub;
+      const float* dvs = lse2s + kSub;
+
+      const bool active = !CAUSAL || (i0 + kSub - 1 >= jw);
+      if (active) {
+        floatx16 sacc[2], pacc[2];
 #pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        half4 k4, v4;
+        for (int m = 0; m < 2; ++m) {
+          sacc[m] = zero16();
+          pacc[m] = zero16();
+          const half_t* qrow = Qs + (m * 32 + l32) * kRow + h * 8;
+          const half_t* orow = Os + (m * 32 + l32) * kRow + h * 8;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          k4[e] = (half_t)(dkacc[c][4 * g4 + e] * scale);
-          v4[e] = (half_t)dvacc[c][4 * g4 + e];
+          for (int kk = 0; kk < D / 16; ++kk) {
+            sacc[m] = mfma32(*reinterpret_cast<const half8*>(qrow + kk * 16), kb[kk], sacc[m]);
+            pacc[m] = mfma32(*reinterpret_cast<const half8*>(orow + kk * 16), vb[kk], pacc[m]);
+          }
         }
-        *reinterpret_cast<half4*>(dkrow + c * 32 + 8 * g4 + 4 * h) = k4;
-        *reinterpret_cast<half4*>(dvrow + c * 32 + 8 * g4 + 4 * h) = v4;
+        const bool need_mask =
+            (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kSub > N || jw + 32 > N));
+        half8 pb[2][2], sb[2][2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
+            const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 32 * m + 8 * g4 + 4 * h);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int r = 4 * g4 + e;
+              float p = fast_exp2(sacc[m][r] * scale_log2 - l4[e]);
+              if (need_mask) {
+                const int i = i0 + 32 * m + 8 * g4 + 4 * h + e;
+                if ((CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N))) p = 0.f;
+              }
+              pb[m][r >> 3][r & 7] = (half_t)p;
+              sb[m][r >> 3][r & 7] = (half_t)(p * (pacc[m][r] - d4[e]));
+            }
+          }
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS; k-step (m, q) = query rows 32m+16q .. +15.
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+          for (int m = 0; m < 2; ++m) {
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              const half8 ao = tr_operand(Os, kRow, 32 * m + 16 * q, 32 * c, lane);
+              const half8 aq = tr_operand(Qs, kRow, 32 * m + 16 * q, 32 * c, lane);
+              dvacc[c] = mfma32(ao, pb[m][q], dvacc[c]);
+              dkacc[c] = mfma32(aq, sb[m][q], dkacc[c]);
+            }
+          }
+        }
+      }
+      if (has_next) put((it + 1) & 1);
+      __syncthreads();
+    }
+
+    if (!BOUNDS || j_col < N) {
+      half_t* dkrow = dK + kv_off + (size_t)j_col * D;
+      half_t* dvrow = dV + kv_off + (size_t)j_col * D;
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          half4 k4, v4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            k4[e] = (half_t)(dkacc[c][4 * g4 + e] * scale);
+            v4[e] = (half_t)dvacc[c][4 * g4 + e];
+          }
+          *reinterpret_cast<half4*>(dkrow + c * 32 + 8 * g4 + 4 * h) = k4;
+          *reinterpret_cast<half4*>(dvrow + c * 32 + 8 * g4 + 4 * h) = v4;
+        }
+      }
+    }
+  }
+
+  // ============================== phase 2: dQ ==============================
+  {
+    const int iw = t0 + wave * 32;  // this wave's query rows
+    const int i_row = iw + l32;
+    const bool row_ok = !BOUNDS || i_row < N;
+    const int kv_end = CAUSAL ? min(N, t0 + kTile) : N;
+    const int n_kt = (kv_end + kSub - 1) / kSub;
+
+    for (int g = 0; g < group; ++g) {
+      const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
+      const half_t* Qg = Q + bhq * N * D;
+      const half_t* dOg = dO + bhq * N * D;
+      half8 qb[D / 16], ob[D / 16];
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+        qb[kk] = as_half8(load16(Qg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+        ob[kk] = as_half8(load16(dOg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+      }
+      const float lse2 = row_ok ? Lse[bhq * N + i_row] * kLog2e : 0.f;
+      const float dvv = row_ok ? Dvec[bhq * N + i_row] : 0.f;
+      floatx16 qacc[D / 32];
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) qacc[c] = zero16();
+
+      RowStage<D, kSub> sk, sv;
+      sk.load(Kh, 0, N, tid, BOUNDS);
+      sv.load(Vh, 0, N, tid, BOUNDS);
+      sk.store(smem, tid);
+      sv.store(smem + L::kTileHalves, tid);
+      __syncthreads();
+      for (int t = 0; t < n_kt; ++t) {
+        const int j0 = t * kSub;
+        const bool has_next = t + 1 < n_kt;
+        if (has_next) {
+          sk.load(Kh, j0 + kSub, N, tid, BOUNDS);
+          sv.load(Vh, j0 + kSub, N, tid, BOUNDS);
+        }
+        const half_t* Ks = smem + (t & 1) * L::kStageHalves;
+        const half_t* Vs = Ks + L::kTileHalves;
+        const bool active = !CAUSAL || j0 <= iw + 31;
+        if (active) {
+          half8 sb[2][2];
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            floatx16 st = zero16(), pt = zero16();
+            const half_t* krow = Ks + (s * 32 + l32) * kRow + h * 8;
+            const half_t* vrow = Vs + (s * 32 + l32) * kRow + h * 8;
+#pragma unroll
+            for (int kk = 0; kk < D / 16; ++kk) {
+              st = mfma32(*reinterpret_cast<const half8*>(krow + kk * 16), qb[kk], st);
+              pt = mfma32(*reinterpret_cast<const half8*>(vrow + kk * 16), ob[kk], pt);
+            }
+            const bool need_mask =
+                (CAUSAL && j0 + 32 * s + 31 > iw) || (BOUNDS && j0 + 32 * s + 32 > N);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              float p = fast_exp2(st[r] * scale_log2 - lse2);
+              if (need_mask) {
+                const int j = j0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
+                if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) p = 0.f;
+              }
+              sb[s][r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
+            }
+          }
+          // dQ^T += K^T dS^T; k-step (s, q) = key rows 32s+16q .. +15.
+#pragma unroll
+          for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+#pragma unroll
+              for (int q = 0; q < 2; ++q)
+                qacc[c] = mfma32(tr_operand(Ks, kRow, 32 * s + 16 * q, 32 * c, lane), sb[s][q],
+                                 qacc[c]);
+            }
+          }
+        }
+        if (has_next) {
+          half_t* nb = smem + ((t + 1) & 1) * L::kStageHalves;
+          sk.store(nb, tid);
+          sv.store(nb + L::kTileHalves, tid);
+        }
+        __syncthreads();
+      }
+
+      if (row_ok) {
+        float* qrow = dQ + bhq * N * D + (size_t)i_row * D;
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) {
+#pragma unroll
+          for (int g4 = 0; g4 < 4; ++g4) {
+            floatx4 v4;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v4[e] = qacc[c][4 * g4 + e] * scale;
+            *reinterpret_cast<floatx4*>(qrow + c * 32 + 8 * g4 + 4 * h) = v4;
+          }
+        }
       }
     }
   }
@@ -312,14 +348,14 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   const long rows = (long)a.B * a.Hq * a.N;
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   hipLaunchKernelGGL((bwd_pre_kernel<D>), grid, dim3(256), 0, (hipStream_t)a.stream,
-                     (const half_t*)a.o, (const half_t*)a.dO, a.dvec, a.dq, rows);
+                     (const half_t*)a.o, (const half_t*)a.dO, a.dvec, rows);
   return hipGetLastError();
 }
 
 template <int D, bool CAUSAL, bool BOUNDS>
 hipError_t launch_main_t(const BwdArgs& a) {
-  const dim3 grid((a.N + kBC - 1) / kBC, a.B * a.Hkv);
-  const size_t smem = BwdSmem<D>::kBytes;
+  const dim3 grid((a.N + kTile - 1) / kTile, a.B * a.Hkv);
+  const size_t smem = BwdLds<D>::kBytes;
   static const hipError_t attr = allow_lds(bwd_kernel<D, CAUSAL, BOUNDS>, smem);
   if (attr != hipSuccess) return attr;
   const float scale = 1.f / sqrtf((float)D);
@@ -333,7 +369,7 @@ hipError_t launch_main_t(const BwdArgs& a) {
 
 template <int D>
 hipError_t launch_main_d(const BwdArgs& a) {
-  const bool bounds = (a.N % kBC) != 0;  // kBC is a multiple of kBR
+  const bool bounds = (a.N % kTile) != 0;  // kTile is a multiple of kSub
   if (a.causal) return bounds ? launch_main_t<D, true, true>(a) : launch_main_t<D, true, false>(a);
   return bounds ? launch_main_t<D, false, true>(a) : launch_main_t<D, false, false>(a);
 }

@@ -61,16 +61,15 @@ size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
   return (bytes + 255) & ~(size_t)255;
 }
 
-int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, float* dq, int B, int Hq,
-                      int N, int D, void* stream) {
+int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, int B, int Hq, int N, int D,
+                      void* stream) {
   const int rc = check_shape(B, Hq, Hq, N, D);
   if (rc != FA_OK) return rc;
-  if (!dO || !o || !dvec || !dq) return FA_ERR_NULL;
+  if (!dO || !o || !dvec) return FA_ERR_NULL;
   fa::BwdArgs a{};
   a.dO = dO;
   a.o = o;
   a.dvec = dvec;
-  a.dq = dq;
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hq;
@@ -100,7 +99,7 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const vo
   if (!workspace) return FA_ERR_NULL;
   if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
   float* dvec = static_cast<float*>(workspace);
-  int e = fa_bwd_preprocess(dO, o, dvec, dq, B, Hq, N, D, stream);
+  int e = fa_bwd_preprocess(dO, o, dvec, B, Hq, N, D, stream);
   if (e != FA_OK) return e;
   return fa_bwd_main(q, k, v, dO, lse, dvec, dq, dk, dv, B, Hq, Hkv, N, D, causal, stream);
 }

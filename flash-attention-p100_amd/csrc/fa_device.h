@@ -75,4 +75,61 @@ __device__ __forceinline__ void transpose_4x8(const u32x4 (&rows)[4], u32x2 (&co
 // Swap with the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
+// ds_read_b64_tr_b16 (gfx950 LDS transpose read). Within each group of 16
+// lanes, lane a + 4t supplies the address of 4 halves at (row t, columns
+// 4a .. 4a+3) of a 4 x 16 block; lane n of the group receives column n of
+// that block, i.e. the 4 rows of one column.
+__device__ __forceinline__ half4 lds_read_tr(const half_t* p) {
+  const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p));
+  return __builtin_bit_cast(half4, v);
+}
+
+// MFMA A operand of a product whose K index runs over the ROWS of a row-major
+// LDS tile (row stride `stride` halves): lane (l32, h) receives column
+// c0 + l32 at the 8 rows rbase + 8*(e/4) + 4h + e%4, e = 0..7. That row order
+// is the one in which a 32x32 accumulator's registers r = 8q..8q+7 enumerate
+// their rows (rbase = 16q), so such an accumulator, converted to fp16, is the
+// matching B operand without any data movement.
+__device__ __forceinline__ half8 tr_operand(const half_t* tile, int stride, int rbase, int c0,
+                                            int lane) {
+  const int n = lane & 15, grp = lane >> 4;
+  const int row = rbase + 4 * (grp >> 1) + (n >> 2);
+  const int col = c0 + 16 * (grp & 1) + 4 * (n & 3);
+  const half4 lo = lds_read_tr(tile + row * stride + col);
+  const half4 hi = lds_read_tr(tile + (row + 8) * stride + col);
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Global -> register -> LDS staging of a block of ROWS rows x D halves by a
+// 256-thread workgroup, 16 bytes per chunk; rows >= N load as zeros. The LDS
+// copy is row-major with `kRow` = D + 8 halves per row.
+template <int D, int ROWS, int THREADS = 256>
+struct RowStage {
+  static constexpr int kRow = D + 8;
+  static constexpr int kPer = ROWS * D / 8 / THREADS;
+  static_assert(kPer * THREADS * 8 == ROWS * D, "tile must split evenly over the threads");
+  u32x4 v[kPer];
+
+  __device__ __forceinline__ void load(const half_t* src, int r0, int N, int tid, bool bounds) {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int c = tid + u * THREADS;
+      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
+      const int r = r0 + row;
+      v[u] = load16(src + (size_t)r * D + col, !bounds || r < N);
+    }
+  }
+  __device__ __forceinline__ void store(half_t* dst, int tid) const {
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int c = tid + u * THREADS;
+      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
+      *reinterpret_cast<u32x4*>(dst + row * kRow + col) = v[u];
+    }
+  }
+};
+
 }  // namespace fa

@@ -98,7 +98,7 @@ std::vector<at::Tensor> fa_backward(at::Tensor q, at::Tensor k, at::Tensor v, at
 
   c10::DeviceGuard guard(q.device());
   auto f32 = q.options().dtype(at::kFloat);
-  // dq is fp32: it is accumulated across key tiles. dk/dv leave as fp16.
+  // Same dtypes as the reference: dq fp32, dk/dv fp16 (fa_p100_ext.cu:118-123).
   auto dq = at::empty({B, H, N, D}, f32);
   auto dk = at::empty_like(k);
   auto dv = at::empty_like(k);

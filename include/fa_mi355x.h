@@ -71,10 +71,10 @@ size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D);
 /*
  * Backward pass. Replaces fa_backward (fa_p100_ext.cu:103-142) below its torch
  * checks. Inputs q, k, v, dO, o (fp16) and lse (fp32) are the forward's
- * inputs/outputs. Writes dq (fp32, B,Hq,N,D), dk and dv (fp16, B,Hkv,N,D).
- * dq is produced by accumulation, so it is cleared first by this call.
- * `workspace` must hold fa_bwd_workspace_bytes() bytes. Equivalent to
- * fa_bwd_preprocess() followed by fa_bwd_main().
+ * inputs/outputs. Writes dq (fp32, B,Hq,N,D), dk and dv (fp16, B,Hkv,N,D);
+ * every element of the three outputs is overwritten. `workspace` must hold
+ * fa_bwd_workspace_bytes() bytes. Equivalent to fa_bwd_preprocess() followed
+ * by fa_bwd_main(). Deterministic: no atomics are used.
  */
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO,
            const void* o, const float* lse, float* dq, void* dk, void* dv,
@@ -82,19 +82,19 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO,
            int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
 
 /*
- * First phase of fa_bwd, the counterpart of bwd_preprocess plus the dQ memset
- * (flash_bwd.cuh:65-78, 475-476): dvec = rowsum(dO * o) in fp32 (B,Hq,N) and
- * dq = 0. Exposed so a host can time or schedule the phases separately.
+ * First phase of fa_bwd, the counterpart of bwd_preprocess
+ * (flash_bwd.cuh:65-78): dvec = rowsum(dO * o) in fp32, shape (B,Hq,N).
+ * Exposed so a host can time or schedule the phases separately.
  */
-int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, float* dq,
+int fa_bwd_preprocess(const void* dO, const void* o, float* dvec,
                       int B, int Hq, int N, int D, void* stream);
 
 /*
  * Second phase of fa_bwd, the counterpart of bwd_kernel
- * (flash_bwd.cuh:95-464, launched at 479-483): K/V-stationary dK, dV and
- * dQ (+=, fp32) from the saved lse and the dvec written by
- * fa_bwd_preprocess. dq must hold the preprocess phase's zeros (or any
- * partial sum to add to).
+ * (flash_bwd.cuh:95-464, launched at 479-483): dK, dV (key/value-stationary)
+ * and dQ (query-stationary, recomputing S and dP instead of the reference's
+ * fp32 atomicAdd) in one launch, from the saved lse and the dvec written by
+ * fa_bwd_preprocess. Overwrites dq, dk and dv.
  */
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
                 const float* lse, const float* dvec, float* dq, void* dk,

@@ -44,7 +44,7 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd(z, z, z, z, z, 0, 2, 2, 8, 64, 0, 0, s) == 10004
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 64, 0, 0, s) == 10005
     assert lib.fa_bwd_main(*([z] * 9), 1, 2, 2, 8, 64, 1, s) == 10005
-    assert lib.fa_bwd_preprocess(z, z, z, z, 1, 2, 8, 128, s) == 10005
+    assert lib.fa_bwd_preprocess(z, z, z, 1, 2, 8, 128, s) == 10005
     one = ctypes.c_void_p(1)
     assert lib.fa_bwd(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, s) == 10006
 

@@ -210,10 +210,10 @@ def test_noncontiguous_inputs_and_current_stream():
     check_fwd(np64(o), ref_o, "strided inputs on a side stream")
 
 
-def test_backward_is_repeatable():
-    """dQ uses fp32 atomics: repeated runs must agree to fp32 reordering noise."""
-    q, k, v, do = make_inputs(1, 4, 4, 300, 128, seed=17)
+def test_backward_is_deterministic():
+    """No atomics anywhere: repeated runs give bit-identical gradients."""
+    q, k, v, do = make_inputs(1, 8, 2, 300, 128, seed=17)
     a = run_flash(q, k, v, do, True)
     b = run_flash(q, k, v, do, True)
-    assert np.array_equal(a[2], b[2]) and np.array_equal(a[3], b[3])  # dK, dV deterministic
-    assert ora.rel_l2(a[1], b[1]) < 1e-6
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
