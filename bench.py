@@ -69,8 +69,8 @@ def load_capi():
     lib = ctypes.CDLL(os.path.join(PKG, "libfa_mi355x.so"))
     vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
     lib.fa_fwd.argtypes = [vp] * 5 + [i] * 7 + [vp]
-    lib.fa_bwd_preprocess.argtypes = [vp] * 3 + [i] * 4 + [vp]
-    lib.fa_bwd_main.argtypes = [vp] * 9 + [i] * 6 + [vp]
+    lib.fa_bwd_preprocess.argtypes = [vp] * 4 + [sz] + [i] * 4 + [vp]
+    lib.fa_bwd_main.argtypes = [vp] * 5 + [sz] + [vp] * 3 + [i] * 6 + [vp]
     lib.fa_bwd_workspace_bytes.argtypes = [i] * 5
     lib.fa_bwd_workspace_bytes.restype = sz
     lib.fa_error_string.restype = ctypes.c_char_p
@@ -87,11 +87,12 @@ def gpu_bench(c, steps, warmup):
     B, Hq, Hkv, N, D, causal = c["B"], c["Hq"], c["Hkv"], c["N"], c["D"], int(c["causal"])
     o = torch.empty_like(q)
     lse = torch.empty(B, Hq, N, device=dev)
-    dvec = torch.empty(lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D) // 4, device=dev)
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
     dq = torch.empty(B, Hq, N, D, device=dev)
     dk, dv = torch.empty_like(k), torch.empty_like(v)
     P = lambda t: ctypes.c_void_p(t.data_ptr())
-    pq, pk, pv, pdo, po, plse, pdvec, pdq, pdk, pdv = map(P, (q, k, v, do, o, lse, dvec, dq, dk, dv))
+    pq, pk, pv, pdo, po, plse, pws, pdq, pdk, pdv = map(P, (q, k, v, do, o, lse, ws, dq, dk, dv))
     stream = torch.cuda.current_stream(dev)
     s = ctypes.c_void_p(stream.cuda_stream)
 
@@ -105,10 +106,11 @@ def gpu_bench(c, steps, warmup):
         check(lib.fa_fwd(pq, pk, pv, po, plse, B, Hq, Hkv, N, D, causal, 0, s), "fa_fwd")
         if ev is not None:
             ev[1].record(stream)
-        check(lib.fa_bwd_preprocess(pdo, po, pdvec, B, Hq, N, D, s), "fa_bwd_preprocess")
+        check(lib.fa_bwd_preprocess(pdo, po, plse, pws, ws_bytes, B, Hq, N, D, s),
+              "fa_bwd_preprocess")
         if ev is not None:
             ev[2].record(stream)
-        check(lib.fa_bwd_main(pq, pk, pv, pdo, plse, pdvec, pdq, pdk, pdv, B, Hq, Hkv, N, D,
+        check(lib.fa_bwd_main(pq, pk, pv, pdo, pws, ws_bytes, pdq, pdk, pdv, B, Hq, Hkv, N, D,
                               causal, s), "fa_bwd_main")
         if ev is not None:
             ev[3].record(stream)

@@ -31,9 +31,12 @@
 // dV^T += dO^T P and dK^T += Q^T dS directly, with the dO^T/Q^T operands read
 // from the row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the
 // forward kernel: S^T = K Q^T and dP^T = V dO^T with Q, dO held as B
-// operands, then dQ^T += K^T dS^T. Dead lanes (causal col > row, ragged
-// rows/cols >= N) contribute exactly zero (flash_bwd.cuh:267-282). P and dS
-// are rounded to fp16 only as MFMA operands.
+// operands, then dQ^T += K^T dS^T. Streamed tiles go from global memory
+// straight into double-buffered, XOR-swizzled LDS tiles
+// (global_load_lds_dwordx4). Dead lanes (causal col > row, ragged rows/cols
+// >= N) contribute exactly zero (flash_bwd.cuh:267-282); tiles that contain
+// any take a separate masked path. P and dS are rounded to fp16 only as MFMA
+// operands.
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -47,20 +50,21 @@ constexpr int kSub = 64;            // rows per streamed tile (queries in 1, key
 
 template <int D>
 struct BwdLds {
-  static constexpr int kRow = D + 8;
-  static constexpr int kTileHalves = kSub * kRow;
-  static constexpr int kStageHalves = 2 * kTileHalves;      // two tensors per stage
-  static constexpr int kFloatOff = 2 * kStageHalves * 2;    // bytes: after both stages
-  static constexpr int kBytes = kFloatOff + 2 * 2 * kSub * 4;  // per stage: lse2[64], dvec[64]
+  static constexpr int kTileHalves = kSub * D;
+  static constexpr int kStageHalves = 2 * kTileHalves + 2 * kSub * 2;  // 2 tiles + lse2, dvec
+  static constexpr int kBytes = 2 * kStageHalves * 2;
 };
 
 // ---------------------------------------------------------------------------
 // Preprocess: dvec[row] = sum_d float(O[row,d]) * float(dO[row,d]) from the
-// fp16-rounded O (flash_bwd.cuh:65-78).
+// fp16-rounded O (flash_bwd.cuh:65-78), and lse2[row] = LSE[row] * log2(e),
+// the form in which the main kernel consumes the saved LSE.
 template <int D>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__ O,
                                                       const half_t* __restrict__ dO,
-                                                      float* __restrict__ dvec, long rows) {
+                                                      const float* __restrict__ Lse,
+                                                      float* __restrict__ dvec,
+                                                      float* __restrict__ lse2, long rows) {
   constexpr int kLanesPerRow = D / 8;
   constexpr int kRowsPerBlock = 256 / kLanesPerRow;
   const int tid = threadIdx.x;
@@ -75,21 +79,121 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
   }
 #pragma unroll
   for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (row < rows && (tid % kLanesPerRow) == 0) dvec[row] = acc;
+  if (row < rows && (tid % kLanesPerRow) == 0) {
+    dvec[row] = acc;
+    lse2[row] = Lse[row] * kLog2e;
+  }
 }
+
+// Direct load of 64 consecutive floats (rows r0 .. r0+63, clamped to N-1).
+__device__ __forceinline__ void vec_load64(float* lds, const float* g, int r0, int N, int lane) {
+  const int r = min(r0 + lane, N - 1);
+  __builtin_amdgcn_global_load_lds((const void*)(g + r),
+                                   (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+}
+
+// ------------------------------- phase 1 -----------------------------------
+template <int D, bool CAUSAL, bool BOUNDS>
+struct KVWave {
+  half8 kb[D / 16], vb[D / 16];      // this wave's K, V rows as B operands
+  floatx16 dvacc[D / 32], dkacc[D / 32];
+
+  // One 64-row query tile staged at (Qs, Os, lse2s, dvs), rows i0 .. i0+63.
+  template <bool MASK>
+  __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
+                                       const float* dvs, int i0, int j_col, int N, int lane,
+                                       float c) {
+    const int h = lane >> 5, l32 = lane & 31;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      floatx16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+        sacc = mfma32(tile_read16<D>(Qs, m * 32 + l32, 2 * kk + h), kb[kk], sacc);
+        pacc = mfma32(tile_read16<D>(Os, m * 32 + l32, 2 * kk + h), vb[kk], pacc);
+      }
+      half8 pb[2], sb[2];
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
+        const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 32 * m + 8 * g4 + 4 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g4 + e;
+          float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
+          if constexpr (MASK) {
+            const int i = i0 + 32 * m + 8 * g4 + 4 * h + e;
+            if ((CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N))) p = 0.f;
+          }
+          pb[r >> 3][r & 7] = (half_t)p;
+          sb[r >> 3][r & 7] = (half_t)(p * (pacc[r] - d4[e]));
+        }
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS; k-step q = query rows 32m+16q .. +15.
+#pragma unroll
+      for (int cb = 0; cb < D / 32; ++cb) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          dvacc[cb] = mfma32(tile_tr_operand<D>(Os, 32 * m + 16 * q, 32 * cb, lane), pb[q], dvacc[cb]);
+          dkacc[cb] = mfma32(tile_tr_operand<D>(Qs, 32 * m + 16 * q, 32 * cb, lane), sb[q], dkacc[cb]);
+        }
+      }
+    }
+  }
+};
+
+// ------------------------------- phase 2 -----------------------------------
+template <int D, bool CAUSAL, bool BOUNDS>
+struct QWave {
+  half8 qb[D / 16], ob[D / 16];  // this wave's Q, dO rows as B operands
+  floatx16 qacc[D / 32];
+  float lse2, dvv;
+
+  // One 64-row key tile staged at (Ks, Vs), keys j0 .. j0+63.
+  template <bool MASK>
+  __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int j0, int i_row,
+                                       int N, int lane, float c) {
+    const int h = lane >> 5, l32 = lane & 31;
+    half8 sb[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      floatx16 st = zero16(), pt = zero16();
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk) {
+        st = mfma32(tile_read16<D>(Ks, s * 32 + l32, 2 * kk + h), qb[kk], st);
+        pt = mfma32(tile_read16<D>(Vs, s * 32 + l32, 2 * kk + h), ob[kk], pt);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(fmaf(st[r], c, -lse2));
+        if constexpr (MASK) {
+          const int j = j0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
+          if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) p = 0.f;
+        }
+        sb[s][r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
+      }
+    }
+    // dQ^T += K^T dS^T; k-step (s, q) = keys 32s+16q .. +15.
+#pragma unroll
+    for (int cb = 0; cb < D / 32; ++cb)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+          qacc[cb] = mfma32(tile_tr_operand<D>(Ks, 32 * s + 16 * q, 32 * cb, lane), sb[s][q], qacc[cb]);
+  }
+};
 
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL, bool BOUNDS>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
-    const float* __restrict__ Lse, const float* __restrict__ Dvec,
+    const float* __restrict__ Lse2, const float* __restrict__ Dvec,
     float* __restrict__ dQ, half_t* __restrict__ dK, half_t* __restrict__ dV,
     int N, int Hq, int group, float scale, float scale_log2) {
   using L = BwdLds<D>;
-  constexpr int kRow = L::kRow;
   extern __shared__ __align__(16) half_t smem[];
-  float* fl = reinterpret_cast<float*>(reinterpret_cast<char*>(smem) + L::kFloatOff);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -105,137 +209,75 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const half_t* Kh = K + kv_off;
   const half_t* Vh = V + kv_off;
 
+  auto stage_ptr = [&](int st) { return smem + st * L::kStageHalves; };
+
   // =========================== phase 1: dK, dV ===========================
   {
     const int jw = t0 + wave * 32;  // this wave's key rows
     const int j_col = jw + l32;
-    half8 kb[D / 16], vb[D / 16];
+    const bool col_ok = !BOUNDS || j_col < N;
+    KVWave<D, CAUSAL, BOUNDS> w;
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      const bool ok = !BOUNDS || j_col < N;
-      kb[kk] = as_half8(load16(Kh + (size_t)j_col * D + kk * 16 + h * 8, ok));
-      vb[kk] = as_half8(load16(Vh + (size_t)j_col * D + kk * 16 + h * 8, ok));
+      w.kb[kk] = as_half8(load16(Kh + (size_t)j_col * D + kk * 16 + h * 8, col_ok));
+      w.vb[kk] = as_half8(load16(Vh + (size_t)j_col * D + kk * 16 + h * 8, col_ok));
     }
-    floatx16 dvacc[D / 32], dkacc[D / 32];
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-      dvacc[c] = zero16();
-      dkacc[c] = zero16();
+    for (int cb = 0; cb < D / 32; ++cb) {
+      w.dvacc[cb] = zero16();
+      w.dkacc[cb] = zero16();
     }
 
     const int i_start = CAUSAL ? t0 : 0;  // t0 is a multiple of kSub
     const int n_qt = (N - i_start + kSub - 1) / kSub;
     const int n_it = group * n_qt;  // (query head, query tile) pairs, flattened
 
-    RowStage<D, kSub> sq, so;
-    float pf_l = 0.f, pf_d = 0.f;  // prefetched lse2 / dvec (threads 0..63)
-    auto fetch = [&](int it) {
+    auto fetch = [&](int it, half_t* st) {
       const int g = it / n_qt;
       const int i0 = i_start + (it % n_qt) * kSub;
       const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
-      sq.load(Q + bhq * N * D, i0, N, tid, BOUNDS);
-      so.load(dO + bhq * N * D, i0, N, tid, BOUNDS);
-      if (tid < kSub) {
-        const int i = i0 + tid;
-        const bool ok = !BOUNDS || i < N;
-        pf_l = ok ? Lse[bhq * N + i] * kLog2e : 0.f;
-        pf_d = ok ? Dvec[bhq * N + i] : 0.f;
-      }
-    };
-    auto put = [&](int stage) {
-      half_t* base = smem + stage * L::kStageHalves;
-      sq.store(base, tid);
-      so.store(base + L::kTileHalves, tid);
-      if (tid < kSub) {
-        fl[stage * 2 * kSub + tid] = pf_l;
-        fl[stage * 2 * kSub + kSub + tid] = pf_d;
-      }
+      tile_load<D, kSub, kWaves>(st, Q + bhq * N * D, i0, N, wave, lane);
+      tile_load<D, kSub, kWaves>(st + L::kTileHalves, dO + bhq * N * D, i0, N, wave, lane);
+      float* fv = reinterpret_cast<float*>(st + 2 * L::kTileHalves);
+      if (wave == 0) vec_load64(fv, Lse2 + bhq * N, i0, N, lane);
+      if (wave == 1) vec_load64(fv + kSub, Dvec + bhq * N, i0, N, lane);
     };
 
-    fetch(0);
-    put(0);
+    fetch(0, stage_ptr(0));
+    wait_vmem();
     __syncthreads();
     for (int it = 0; it < n_it; ++it) {
       const int i0 = i_start + (it % n_qt) * kSub;
-      const bool has_next = it + 1 < n_it;
-      if (has_next) fetch(it + 1);
-
-      const half_t* Qs = smem + (it & 1) * L::kStageHalves;
+      if (it + 1 < n_it) fetch(it + 1, stage_ptr((it + 1) & 1));
+      const half_t* Qs = stage_ptr(it & 1);
       const half_t* Os = Qs + L::kTileHalves;
-      const float* lse2s = fl + (it & 1) * 2 * kSub;
+      const float* lse2s = reinterpret_cast<const float*>(Os + L::kTileHalves);
       const float* dvs = lse2s + kSub;
-
       const bool active = !CAUSAL || (i0 + kSub - 1 >= jw);
       if (active) {
-        floatx16 sacc[2], pacc[2];
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          sacc[m] = zero16();
-          pacc[m] = zero16();
-          const half_t* qrow = Qs + (m * 32 + l32) * kRow + h * 8;
-          const half_t* orow = Os + (m * 32 + l32) * kRow + h * 8;
-#pragma unroll
-          for (int kk = 0; kk < D / 16; ++kk) {
-            sacc[m] = mfma32(*reinterpret_cast<const half8*>(qrow + kk * 16), kb[kk], sacc[m]);
-            pacc[m] = mfma32(*reinterpret_cast<const half8*>(orow + kk * 16), vb[kk], pacc[m]);
-          }
-        }
-        const bool need_mask =
-            (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kSub > N || jw + 32 > N));
-        half8 pb[2][2], sb[2][2];
-#pragma unroll
-        for (int m = 0; m < 2; ++m) {
-#pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
-            const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 32 * m + 8 * g4 + 4 * h);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int r = 4 * g4 + e;
-              float p = fast_exp2(sacc[m][r] * scale_log2 - l4[e]);
-              if (need_mask) {
-                const int i = i0 + 32 * m + 8 * g4 + 4 * h + e;
-                if ((CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N))) p = 0.f;
-              }
-              pb[m][r >> 3][r & 7] = (half_t)p;
-              sb[m][r >> 3][r & 7] = (half_t)(p * (pacc[m][r] - d4[e]));
-            }
-          }
-        }
-        // dV^T += dO^T P, dK^T += Q^T dS; k-step (m, q) = query rows 32m+16q .. +15.
-#pragma unroll
-        for (int c = 0; c < D / 32; ++c) {
-#pragma unroll
-          for (int m = 0; m < 2; ++m) {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              const half8 ao = tr_operand(Os, kRow, 32 * m + 16 * q, 32 * c, lane);
-              const half8 aq = tr_operand(Qs, kRow, 32 * m + 16 * q, 32 * c, lane);
-              dvacc[c] = mfma32(ao, pb[m][q], dvacc[c]);
-              dkacc[c] = mfma32(aq, sb[m][q], dkacc[c]);
-            }
-          }
-        }
+        const bool mask = (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kSub > N || jw + 32 > N));
+        if (mask) w.template step<true>(Qs, Os, lse2s, dvs, i0, j_col, N, lane, scale_log2);
+        else w.template step<false>(Qs, Os, lse2s, dvs, i0, j_col, N, lane, scale_log2);
       }
-      if (has_next) put((it + 1) & 1);
+      wait_vmem();
       __syncthreads();
     }
 
-    if (!BOUNDS || j_col < N) {
+    if (col_ok) {
       half_t* dkrow = dK + kv_off + (size_t)j_col * D;
       half_t* dvrow = dV + kv_off + (size_t)j_col * D;
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
+      for (int cb = 0; cb < D / 32; ++cb) {
 #pragma unroll
         for (int g4 = 0; g4 < 4; ++g4) {
           half4 k4, v4;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            k4[e] = (half_t)(dkacc[c][4 * g4 + e] * scale);
-            v4[e] = (half_t)dvacc[c][4 * g4 + e];
+            k4[e] = (half_t)(w.dkacc[cb][4 * g4 + e] * scale);
+            v4[e] = (half_t)w.dvacc[cb][4 * g4 + e];
           }
-          *reinterpret_cast<half4*>(dkrow + c * 32 + 8 * g4 + 4 * h) = k4;
-          *reinterpret_cast<half4*>(dvrow + c * 32 + 8 * g4 + 4 * h) = v4;
+          *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
+          *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
         }
       }
     }
@@ -253,88 +295,50 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
       const half_t* Qg = Q + bhq * N * D;
       const half_t* dOg = dO + bhq * N * D;
-      half8 qb[D / 16], ob[D / 16];
+      QWave<D, CAUSAL, BOUNDS> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        qb[kk] = as_half8(load16(Qg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
-        ob[kk] = as_half8(load16(dOg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+        w.qb[kk] = as_half8(load16(Qg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+        w.ob[kk] = as_half8(load16(dOg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
       }
-      const float lse2 = row_ok ? Lse[bhq * N + i_row] * kLog2e : 0.f;
-      const float dvv = row_ok ? Dvec[bhq * N + i_row] : 0.f;
-      floatx16 qacc[D / 32];
+      w.lse2 = row_ok ? Lse2[bhq * N + i_row] : 0.f;
+      w.dvv = row_ok ? Dvec[bhq * N + i_row] : 0.f;
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) qacc[c] = zero16();
+      for (int cb = 0; cb < D / 32; ++cb) w.qacc[cb] = zero16();
 
-      RowStage<D, kSub> sk, sv;
-      sk.load(Kh, 0, N, tid, BOUNDS);
-      sv.load(Vh, 0, N, tid, BOUNDS);
-      sk.store(smem, tid);
-      sv.store(smem + L::kTileHalves, tid);
+      tile_load<D, kSub, kWaves>(stage_ptr(0), Kh, 0, N, wave, lane);
+      tile_load<D, kSub, kWaves>(stage_ptr(0) + L::kTileHalves, Vh, 0, N, wave, lane);
+      wait_vmem();
       __syncthreads();
       for (int t = 0; t < n_kt; ++t) {
         const int j0 = t * kSub;
-        const bool has_next = t + 1 < n_kt;
-        if (has_next) {
-          sk.load(Kh, j0 + kSub, N, tid, BOUNDS);
-          sv.load(Vh, j0 + kSub, N, tid, BOUNDS);
+        if (t + 1 < n_kt) {
+          half_t* nb = stage_ptr((t + 1) & 1);
+          tile_load<D, kSub, kWaves>(nb, Kh, j0 + kSub, N, wave, lane);
+          tile_load<D, kSub, kWaves>(nb + L::kTileHalves, Vh, j0 + kSub, N, wave, lane);
         }
-        const half_t* Ks = smem + (t & 1) * L::kStageHalves;
+        const half_t* Ks = stage_ptr(t & 1);
         const half_t* Vs = Ks + L::kTileHalves;
         const bool active = !CAUSAL || j0 <= iw + 31;
         if (active) {
-          half8 sb[2][2];
-#pragma unroll
-          for (int s = 0; s < 2; ++s) {
-            floatx16 st = zero16(), pt = zero16();
-            const half_t* krow = Ks + (s * 32 + l32) * kRow + h * 8;
-            const half_t* vrow = Vs + (s * 32 + l32) * kRow + h * 8;
-#pragma unroll
-            for (int kk = 0; kk < D / 16; ++kk) {
-              st = mfma32(*reinterpret_cast<const half8*>(krow + kk * 16), qb[kk], st);
-              pt = mfma32(*reinterpret_cast<const half8*>(vrow + kk * 16), ob[kk], pt);
-            }
-            const bool need_mask =
-                (CAUSAL && j0 + 32 * s + 31 > iw) || (BOUNDS && j0 + 32 * s + 32 > N);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              float p = fast_exp2(st[r] * scale_log2 - lse2);
-              if (need_mask) {
-                const int j = j0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
-                if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) p = 0.f;
-              }
-              sb[s][r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
-            }
-          }
-          // dQ^T += K^T dS^T; k-step (s, q) = key rows 32s+16q .. +15.
-#pragma unroll
-          for (int c = 0; c < D / 32; ++c) {
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-#pragma unroll
-              for (int q = 0; q < 2; ++q)
-                qacc[c] = mfma32(tr_operand(Ks, kRow, 32 * s + 16 * q, 32 * c, lane), sb[s][q],
-                                 qacc[c]);
-            }
-          }
+          const bool mask = (CAUSAL && j0 + kSub - 1 > iw) || (BOUNDS && j0 + kSub > N);
+          if (mask) w.template step<true>(Ks, Vs, j0, i_row, N, lane, scale_log2);
+          else w.template step<false>(Ks, Vs, j0, i_row, N, lane, scale_log2);
         }
-        if (has_next) {
-          half_t* nb = smem + ((t + 1) & 1) * L::kStageHalves;
-          sk.store(nb, tid);
-          sv.store(nb + L::kTileHalves, tid);
-        }
+        wait_vmem();
         __syncthreads();
       }
 
       if (row_ok) {
         float* qrow = dQ + bhq * N * D + (size_t)i_row * D;
 #pragma unroll
-        for (int c = 0; c < D / 32; ++c) {
+        for (int cb = 0; cb < D / 32; ++cb) {
 #pragma unroll
           for (int g4 = 0; g4 < 4; ++g4) {
             floatx4 v4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v4[e] = qacc[c][4 * g4 + e] * scale;
-            *reinterpret_cast<floatx4*>(qrow + c * 32 + 8 * g4 + 4 * h) = v4;
+            for (int e = 0; e < 4; ++e) v4[e] = w.qacc[cb][4 * g4 + e] * scale;
+            *reinterpret_cast<floatx4*>(qrow + cb * 32 + 8 * g4 + 4 * h) = v4;
           }
         }
       }
@@ -348,7 +352,7 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   const long rows = (long)a.B * a.Hq * a.N;
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   hipLaunchKernelGGL((bwd_pre_kernel<D>), grid, dim3(256), 0, (hipStream_t)a.stream,
-                     (const half_t*)a.o, (const half_t*)a.dO, a.dvec, rows);
+                     (const half_t*)a.o, (const half_t*)a.dO, a.lse, a.dvec, a.lse2, rows);
   return hipGetLastError();
 }
 
@@ -361,7 +365,7 @@ hipError_t launch_main_t(const BwdArgs& a) {
   const float scale = 1.f / sqrtf((float)D);
   hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), smem,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
-                     (const half_t*)a.v, (const half_t*)a.dO, a.lse, a.dvec, a.dq,
+                     (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, scale,
                      scale * kLog2e);
   return hipGetLastError();

@@ -25,6 +25,11 @@ int check_shape(int B, int Hq, int Hkv, int N, int D) {
 
 int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }
 
+// One (B, Hq, N) float32 vector, rounded up to 256 bytes.
+size_t vec_bytes(int B, int Hq, int N) {
+  return ((size_t)B * Hq * N * sizeof(float) + 255) & ~(size_t)255;
+}
+
 }  // namespace
 
 extern "C" {
@@ -57,19 +62,21 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int
 
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
   if (check_shape(B, Hq, Hkv, N, D) != FA_OK) return 0;
-  const size_t bytes = (size_t)B * Hq * N * sizeof(float);
-  return (bytes + 255) & ~(size_t)255;
+  return 2 * vec_bytes(B, Hq, N);
 }
 
-int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, int B, int Hq, int N, int D,
-                      void* stream) {
+int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* workspace,
+                      size_t workspace_bytes, int B, int Hq, int N, int D, void* stream) {
   const int rc = check_shape(B, Hq, Hq, N, D);
   if (rc != FA_OK) return rc;
-  if (!dO || !o || !dvec) return FA_ERR_NULL;
+  if (!dO || !o || !lse || !workspace) return FA_ERR_NULL;
+  if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
   fa::BwdArgs a{};
   a.dO = dO;
   a.o = o;
-  a.dvec = dvec;
+  a.lse = lse;
+  a.dvec = static_cast<float*>(workspace);
+  a.lse2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vec_bytes(B, Hq, N));
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hq;
@@ -79,14 +86,31 @@ int fa_bwd_preprocess(const void* dO, const void* o, float* dvec, int B, int Hq,
   return to_code(fa::launch_bwd_preprocess(a));
 }
 
-int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const float* lse,
-                const float* dvec, float* dq, void* dk, void* dv, int B, int Hq, int Hkv, int N,
-                int D, int causal, void* stream) {
+int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+                size_t workspace_bytes, float* dq, void* dk, void* dv, int B, int Hq, int Hkv,
+                int N, int D, int causal, void* stream) {
   const int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
-  if (!q || !k || !v || !dO || !lse || !dvec || !dq || !dk || !dv) return FA_ERR_NULL;
-  fa::BwdArgs a{q, k, v, dO, nullptr, lse, const_cast<float*>(dvec), dq, dk, dv,
-                B, Hq, Hkv, N, D, causal != 0, stream};
+  if (!q || !k || !v || !dO || !workspace || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
+  fa::BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dO = dO;
+  a.dvec = const_cast<float*>(static_cast<const float*>(workspace));
+  a.lse2 = reinterpret_cast<float*>(const_cast<char*>(static_cast<const char*>(workspace)) +
+                                    vec_bytes(B, Hq, N));
+  a.dq = dq;
+  a.dk = dk;
+  a.dv = dv;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.N = N;
+  a.D = D;
+  a.causal = causal != 0;
+  a.stream = stream;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -98,10 +122,10 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const vo
   if (rc != FA_OK) return rc;
   if (!workspace) return FA_ERR_NULL;
   if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
-  float* dvec = static_cast<float*>(workspace);
-  int e = fa_bwd_preprocess(dO, o, dvec, B, Hq, N, D, stream);
+  int e = fa_bwd_preprocess(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, stream);
   if (e != FA_OK) return e;
-  return fa_bwd_main(q, k, v, dO, lse, dvec, dq, dk, dv, B, Hq, Hkv, N, D, causal, stream);
+  return fa_bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, dk, dv, B, Hq, Hkv, N, D,
+                     causal, stream);
 }
 
 }  // extern "C"

@@ -103,6 +103,76 @@ __device__ __forceinline__ half8 tr_operand(const half_t* tile, int stride, int 
   return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// ---------------------------------------------------------------------------
+// Swizzled row-major LDS tiles filled by direct global -> LDS loads.
+//
+// A tile holds rows of D halves (2D bytes) with no padding. Row r keeps its
+// logical 16-byte chunk c at physical chunk c ^ swz(r). swz spreads
+//   * eight consecutive rows read at one logical chunk (the 16-byte MFMA
+//     operand reads, one row per lane) over eight distinct chunks, and
+//   * four consecutive rows read at one aligned chunk pair (the transpose
+//     reads) over four distinct chunk pairs,
+// so neither access pattern piles onto one group of LDS banks.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) return (r & 7) << 1;
+  else return ((r & 3) << 1) | ((r >> 2) & 1);
+}
+
+template <int D>
+__device__ __forceinline__ const half_t* tile_chunk(const half_t* tile, int r, int c) {
+  return tile + r * D + ((c ^ swz<D>(r)) << 3);
+}
+
+// 16-byte MFMA operand: row r, logical chunk c (halves 8c .. 8c+7).
+template <int D>
+__device__ __forceinline__ half8 tile_read16(const half_t* tile, int r, int c) {
+  return *reinterpret_cast<const half8*>(tile_chunk<D>(tile, r, c));
+}
+
+// The transpose-read operand of tr_operand() for a swizzled tile.
+template <int D>
+__device__ __forceinline__ half8 tile_tr_operand(const half_t* tile, int rbase, int c0, int lane) {
+  const int n = lane & 15, grp = lane >> 4;
+  const int row = rbase + 4 * (grp >> 1) + (n >> 2);
+  const int col = c0 + 16 * (grp & 1) + 4 * (n & 3);
+  const half_t* p0 = tile_chunk<D>(tile, row, col >> 3) + (col & 7);
+  const half_t* p1 = tile_chunk<D>(tile, row + 8, col >> 3) + (col & 7);
+  const half4 lo = lds_read_tr(p0);
+  const half4 hi = lds_read_tr(p1);
+  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// One wave copies 1 KB (64 lanes x 16 B) from global memory straight into LDS
+// at `lds` (wave-uniform), lane l landing at lds + 16*l bytes.
+__device__ __forceinline__ void lds_direct16(half_t* lds, const half_t* src) {
+  __builtin_amdgcn_global_load_lds(
+      (const void*)src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
+}
+
+// Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Loads rows [r0, r0 + ROWS) of a row-major (N, D) fp16 matrix into a swizzled
+// LDS tile, using the NW waves of the workgroup. Rows >= N are clamped to row
+// N - 1 (finite data); the kernels mask them before they can contribute.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void tile_load(half_t* tile, const half_t* g, int r0, int N,
+                                          int wave, int lane) {
+  constexpr int kRowsPerInst = 512 / D;              // 1 KB per wave instruction
+  constexpr int kInsts = ROWS / kRowsPerInst;
+  static_assert(kInsts % NW == 0, "tile must split evenly over the waves");
+  const int rl = lane / (D / 8);                      // row within the instruction
+  const int pc = lane % (D / 8);                      // physical chunk
+#pragma unroll
+  for (int u = 0; u < kInsts / NW; ++u) {
+    const int inst = u * NW + wave;
+    const int r = inst * kRowsPerInst + rl;
+    const int gr = min(r0 + r, N - 1);
+    lds_direct16(tile + inst * 512, g + (size_t)gr * D + ((pc ^ swz<D>(r)) << 3));
+  }
+}
+
 // Global -> register -> LDS staging of a block of ROWS rows x D halves by a
 // 256-thread workgroup, 16 bytes per chunk; rows >= N load as zeros. The LDS
 // copy is row-major with `kRow` = D + 8 halves per row.

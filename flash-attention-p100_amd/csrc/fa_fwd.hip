@@ -1,263 +1,254 @@
 // FlashAttention-2 forward for gfx950 (MI355X).
 //
 // Counterpart of the reference's flash::fwd_kernel (flash_fwd.cuh:68-340),
-// redesigned around MFMA:
-//   * a workgroup is 4 waves; each wave owns 32 query rows (BR = 128 rows per
-//     workgroup) and walks the key/value sequence in tiles of BC = 64 rows;
-//   * S is computed TRANSPOSED, S^T = K Q^T, on v_mfma_f32_32x32x16_f16 with
-//     Q^T held in registers as the B operand for the whole kernel. In the
-//     accumulator layout lane l then owns query row l % 32, so the online
-//     softmax row max / row sum is a per-lane reduction plus one exchange
-//     with the other half of the wave;
-//   * P^T leaves the accumulator as fp16 and is fed back as the B operand of
-//     O^T += V^T P^T without touching LDS (the K index order of the product
-//     is chosen to match the accumulator layout); V is staged transposed
-//     (V^T, rows = head dim) in LDS, K row-major, both double-buffered;
+// redesigned around MFMA, the CDNA4 LDS and the balance of a causal grid:
+//
+// Work split. A workgroup is 8 waves and owns a 64-row query tile: waves are
+// (row block rb in {0,1}) x (key quarter kq in {0..3}). Each wave owns 32
+// query rows and, of every 128 keys staged, the 32 keys of its quarter; the
+// four quarters' partial (max, sum, O) are merged through LDS at the end of
+// the tile. Under causal masking a workgroup takes query tile x and then
+// tile T-1-x, so every workgroup does the same amount of work (the long and
+// the short end of the triangle), and the grid of (T/2) x (B*Hq) workgroups
+// x 8 waves keeps two waves on every SIMD at the headline shape.
+//
+// Per wave and 32-key step, on v_mfma_f32_32x32x16_f16 (fp32 accumulate):
+//   * S^T = K Q^T with this wave's Q^T held in registers as the B operand, so
+//     in the accumulator lane l owns query row l % 32 and the softmax row
+//     max is a per-lane max plus one exchange with the other half-wave;
 //   * the scale is applied to the fp32 logit (never to Q in fp16,
-//     flash_fwd.cuh:94-101) with log2(e) folded in so exp2 is used;
-//   * causal: key tiles past the workgroup's last row are never loaded
-//     (flash_fwd.cuh:127-130) and a wave skips tiles entirely above its own
-//     rows; ragged N is handled by zero-filled loads plus -inf masking of
-//     key columns >= N (flash_fwd.cuh:226-243).
-// Outputs: O (fp16) and LSE = m + log(l) in natural-log units of the scaled
-// logits (flash_fwd.cuh:321-339).
+//     flash_fwd.cuh:94-101), folded with log2(e) into one FMA before exp2;
+//   * the running max is refreshed lazily: O and the row sum are rescaled
+//     only when some row's max grows by more than 2^8, so P stays <= 256 and
+//     the rescale (a pass over all O accumulators) is rare;
+//   * P^T leaves the accumulator as fp16 and feeds O^T += V^T P^T directly,
+//     with V^T read from the row-major V tile by the LDS transpose read.
+// K and V tiles move from global memory straight into double-buffered,
+// XOR-swizzled LDS tiles (global_load_lds_dwordx4), so staging costs no
+// registers and no LDS store instructions.
+//
+// Causal tiles past the diagonal are never loaded (flash_fwd.cuh:127-130);
+// diagonal and ragged tiles take a separate masked path (flash_fwd.cuh:
+// 226-243). Outputs: O (fp16) and LSE = m + log(l) in natural-log units of
+// the scaled logits (flash_fwd.cuh:321-339).
 #include "fa_device.h"
 #include "fa_launch.h"
 
 namespace fa {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBR = 32 * kWaves;  // query rows per workgroup
-constexpr int kBC = 64;           // key rows per tile
-constexpr int kKPad = 8;          // halves of padding per K row in LDS
-constexpr int kVPad = 4;          // halves of padding per V^T row in LDS
+constexpr int kBR = 64;    // query rows per tile (2 row blocks of 32)
+constexpr int kKV = 128;   // keys staged per step (4 quarters of 32)
+constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold, log2 units
 
 template <int D>
-struct FwdSmem {
-  static constexpr int kKRow = D + kKPad;    // K tile  [kBC][kKRow]
-  static constexpr int kVRow = kBC + kVPad;  // V^T tile [D][kVRow]
-  static constexpr int kKElems = kBC * kKRow;
-  static constexpr int kVElems = D * kVRow;
-  static constexpr int kStage = kKElems + kVElems;
-  static constexpr int kBytes = 2 * kStage * 2;
+struct FwdLds {
+  static constexpr int kTileHalves = kKV * D;          // one K or V tile
+  static constexpr int kStageHalves = 2 * kTileHalves; // K + V
+  static constexpr int kStageBytes = 2 * kStageHalves * 2;
+  // Merge area (reuses the stages): per wave, D/32 x 16 floats per lane.
+  static constexpr int kPartBytes = kWaves * 64 * D * 2;  // D/32*16 = D/2 floats/lane
+  static constexpr int kMLBytes = kWaves * 64 * 8;        // (m, l) per lane
+  static constexpr int kBytes =
+      (kStageBytes > kPartBytes ? kStageBytes : kPartBytes) + kMLBytes;
 };
 
-// Global -> register staging of one K/V tile (rows j0 .. j0+kBC-1).
-template <int D>
-struct KVStage {
-  static constexpr int kKChunks = kBC * D / 8;             // 16-byte chunks of K
-  static constexpr int kKPerThread = kKChunks / kThreads;  // 2 (D=64) or 4 (D=128)
-  static constexpr int kVTasks = (kBC / 4) * (D / 8);      // 4x8 blocks of V
-  static constexpr int kVPerThread = (kVTasks + kThreads - 1) / kThreads;  // 1
-  u32x4 k[kKPerThread];
-  u32x4 v[kVPerThread][4];
+template <int D, bool CAUSAL, bool BOUNDS>
+struct FwdWave {
+  // Per-wave state for one 32-row query block.
+  half8 qb[D / 16];
+  floatx16 oacc[D / 32];
+  float m_raw;  // running max of the raw (unscaled) logits; -inf before any key
+  float l;      // this lane's partial row sum of p (its 16 of every 32 keys)
 
-  __device__ __forceinline__ void load(const half_t* K, const half_t* V, int j0, int N,
-                                       int tid, bool bounds) {
+  template <bool MASK>
+  __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int kq, int j0,
+                                       int i_row, int N, int lane, float c, float thr_raw) {
+    const int h = lane >> 5, l32 = lane & 31;
+    floatx16 s = zero16();
 #pragma unroll
-    for (int u = 0; u < kKPerThread; ++u) {
-      const int c = tid + u * kThreads;
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-      const int j = j0 + row;
-      k[u] = load16(K + (size_t)j * D + col, !bounds || j < N);
-    }
+    for (int kk = 0; kk < D / 16; ++kk)
+      s = mfma32(tile_read16<D>(Ks, kq * 32 + l32, 2 * kk + h), qb[kk], s);
+    if constexpr (MASK) {
 #pragma unroll
-    for (int u = 0; u < kVPerThread; ++u) {
-      const int t = tid + u * kThreads;
-      // j-groups vary fastest across lanes so the transposed LDS writes of a
-      // wave land in distinct banks.
-      const int jg = t % (kBC / 4), dg = t / (kBC / 4);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = j0 + jg * 4 + r;
-        v[u][r] = load16(V + (size_t)j * D + dg * 8, t < kVTasks && (!bounds || j < N));
+      for (int r = 0; r < 16; ++r) {
+        const int j = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) s[r] = -INFINITY;
       }
     }
-  }
-
-  __device__ __forceinline__ void store(half_t* Ks, half_t* Vt, int tid) const {
-    using S = FwdSmem<D>;
+    float mloc = s[0];
 #pragma unroll
-    for (int u = 0; u < kKPerThread; ++u) {
-      const int c = tid + u * kThreads;
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(Ks + row * S::kKRow + col) = k[u];
+    for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
+    mloc = fmaxf(mloc, xor32(mloc));
+    // Lazy rescale: only when some row's max grew by more than 2^8.
+    if (__builtin_expect(__any(mloc > m_raw + thr_raw), 0)) {
+      const float m_new = fmaxf(m_raw, mloc);
+      const float corr = (m_raw == -INFINITY) ? 0.f : fast_exp2((m_raw - m_new) * c);
+      l *= corr;
+#pragma unroll
+      for (int cb = 0; cb < D / 32; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[cb][r] *= corr;
+      m_raw = m_new;
     }
+    const float neg = (m_raw == -INFINITY) ? 0.f : -m_raw * c;
+    half8 pb[2];
 #pragma unroll
-    for (int u = 0; u < kVPerThread; ++u) {
-      const int t = tid + u * kThreads;
-      if (t < kVTasks) {
-        const int jg = t % (kBC / 4), dg = t / (kBC / 4);
-        u32x2 cols[8];
-        transpose_4x8(v[u], cols);
-#pragma unroll
-        for (int c = 0; c < 8; ++c)
-          *reinterpret_cast<u32x2*>(Vt + (dg * 8 + c) * S::kVRow + jg * 4) = cols[c];
-      }
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(fmaf(s[r], c, neg));
+      l += p;
+      pb[r >> 3][r & 7] = (half_t)p;
     }
+    // O^T += V^T P^T; k-step q covers keys 16q .. 16q+15 of this quarter.
+#pragma unroll
+    for (int cb = 0; cb < D / 32; ++cb)
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+        oacc[cb] = mfma32(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, lane), pb[q], oacc[cb]);
   }
 };
+
+template <int D, bool CAUSAL, bool BOUNDS>
+__device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
+                                         const half_t* __restrict__ V, half_t* __restrict__ O,
+                                         float* __restrict__ Lse, int N, int qtile,
+                                         float c, float thr_raw, half_t* smem) {
+  using L = FwdLds<D>;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int rb = wave & 1, kq = wave >> 1;
+  const int q0 = qtile * kBR;
+  const int i_base = q0 + rb * 32;
+  const int i_row = i_base + l32;
+
+  FwdWave<D, CAUSAL, BOUNDS> w;
+  const bool row_ok = !BOUNDS || i_row < N;
+#pragma unroll
+  for (int kk = 0; kk < D / 16; ++kk)
+    w.qb[kk] = as_half8(load16(Q + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+#pragma unroll
+  for (int cb = 0; cb < D / 32; ++cb) w.oacc[cb] = zero16();
+  w.m_raw = -INFINITY;
+  w.l = 0.f;
+
+  const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
+  const int n_it = (kv_end + kKV - 1) / kKV;
+
+  tile_load<D, kKV, kWaves>(smem, K, 0, N, wave, lane);
+  tile_load<D, kKV, kWaves>(smem + L::kTileHalves, V, 0, N, wave, lane);
+  wait_vmem();
+  __syncthreads();
+  for (int it = 0; it < n_it; ++it) {
+    if (it + 1 < n_it) {
+      half_t* nb = smem + ((it + 1) & 1) * L::kStageHalves;
+      tile_load<D, kKV, kWaves>(nb, K, (it + 1) * kKV, N, wave, lane);
+      tile_load<D, kKV, kWaves>(nb + L::kTileHalves, V, (it + 1) * kKV, N, wave, lane);
+    }
+    const half_t* Ks = smem + (it & 1) * L::kStageHalves;
+    const half_t* Vs = Ks + L::kTileHalves;
+    const int j0 = it * kKV + kq * 32;
+    const bool active = j0 < kv_end && (!CAUSAL || j0 <= i_base + 31);
+    if (active) {
+      const bool mask = (CAUSAL && j0 + 31 > i_base) || (BOUNDS && j0 + 32 > N);
+      if (mask) w.template step<true>(Ks, Vs, kq, j0, i_row, N, lane, c, thr_raw);
+      else w.template step<false>(Ks, Vs, kq, j0, i_row, N, lane, c, thr_raw);
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+
+  // Merge the four key quarters of each row block through LDS.
+  float* part = reinterpret_cast<float*>(smem);
+  float2* ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(smem) +
+                                         (L::kStageBytes > L::kPartBytes ? L::kStageBytes
+                                                                         : L::kPartBytes));
+#pragma unroll
+  for (int cb = 0; cb < D / 32; ++cb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      floatx4 v = {w.oacc[cb][4 * g], w.oacc[cb][4 * g + 1], w.oacc[cb][4 * g + 2],
+                   w.oacc[cb][4 * g + 3]};
+      *reinterpret_cast<floatx4*>(part + ((wave * (D / 8) + cb * 4 + g) * 64 + lane) * 4) = v;
+    }
+  ml[wave * 64 + lane] = make_float2(w.m_raw, w.l);
+  __syncthreads();
+
+  // Wave (rb, kq) finishes d-block kq of row block rb (D=64: kq < 2 only).
+  if (kq < D / 32) {
+    const int cb = kq;
+    float mk[4], lk[4];
+    float m_star = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int src = k * 2 + rb;  // wave index of quarter k in this row block
+      const float2 a = ml[src * 64 + lane];
+      const float2 bb = ml[src * 64 + (lane ^ 32)];
+      mk[k] = a.x;
+      lk[k] = a.y + bb.y;
+      m_star = fmaxf(m_star, mk[k]);
+    }
+    float wk[4], l_star = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      wk[k] = (mk[k] == -INFINITY) ? 0.f : fast_exp2((mk[k] - m_star) * c);
+      l_star += wk[k] * lk[k];
+    }
+    const float inv_l = 1.f / l_star;
+    if (row_ok) {
+      half_t* orow = O + (size_t)i_row * D + cb * 32;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int src = k * 2 + rb;
+          const floatx4 v =
+              *reinterpret_cast<const floatx4*>(part + ((src * (D / 8) + cb * 4 + g) * 64 + lane) * 4);
+          acc += v * wk[k];
+        }
+        half4 o4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o4[e] = (half_t)(acc[e] * inv_l);
+        *reinterpret_cast<half4*>(orow + 8 * g + 4 * h) = o4;
+      }
+      if (cb == 0 && h == 0) Lse[i_row] = (m_star * c + __log2f(l_star)) * kLn2;
+    }
+  }
+  __syncthreads();  // the LDS is reused by the next tile
+}
 
 template <int D, bool CAUSAL, bool BOUNDS>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, float scale_log2) {
-  using S = FwdSmem<D>;
   extern __shared__ __align__(16) half_t smem[];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int h = lane >> 5;     // which half of the wave
-  const int l32 = lane & 31;
-
-  // Longest causal tiles first: they start before the short ones.
-  const int qtile = CAUSAL ? (n_qtiles - 1 - (int)blockIdx.x) : (int)blockIdx.x;
-  const int q0 = qtile * kBR;
-  const int bh = blockIdx.y;                   // over B*Hq
+  const int bh = blockIdx.y;  // over B*Hq
   const int b = bh / Hq, hq = bh % Hq;
-  const int hkv = hq / group;                  // repeat_interleave head map
   const int Hkv = Hq / group;
+  const int hkv = hq / group;  // repeat_interleave head map (flash_fwd.cuh:90)
   const size_t q_off = (size_t)bh * N * D;
   const size_t kv_off = ((size_t)b * Hkv + hkv) * N * D;
-  Q += q_off;
-  O += q_off;
-  K += kv_off;
-  V += kv_off;
-  Lse += (size_t)bh * N;
-
-  // This wave's query rows and its Q^T operands (B of S^T = K Q^T).
-  const int i_base = q0 + wave * 32;
-  const int i_row = i_base + l32;
-  half8 qb[D / 16];
-#pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk)
-    qb[kk] = as_half8(load16(Q + (size_t)i_row * D + kk * 16 + h * 8, !BOUNDS || i_row < N));
-
-  floatx16 oacc[D / 32];
-#pragma unroll
-  for (int c = 0; c < D / 32; ++c) oacc[c] = zero16();
-  float m_run = -INFINITY;  // running max, log2 domain
-  float l_run = 0.f;        // running sum of exp2(x - m_run)
-
-  const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
-  const int n_tiles = (kv_end + kBC - 1) / kBC;
-
-  KVStage<D> st;
-  st.load(K, V, 0, N, tid, BOUNDS);
-  st.store(smem, smem + S::kKElems, tid);
-  __syncthreads();
-
-  for (int t = 0; t < n_tiles; ++t) {
-    const int j0 = t * kBC;
-    const bool has_next = t + 1 < n_tiles;
-    if (has_next) st.load(K, V, j0 + kBC, N, tid, BOUNDS);
-
-    half_t* Ks = smem + (t & 1) * S::kStage;
-    half_t* Vt = Ks + S::kKElems;
-
-    // A wave whose rows all precede this tile sees only masked keys.
-    const bool active = !CAUSAL || j0 <= i_base + 31;
-    if (active) {
-      floatx16 sacc[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        sacc[s] = zero16();
-        const half_t* krow = Ks + (s * 32 + l32) * S::kKRow + h * 8;
-#pragma unroll
-        for (int kk = 0; kk < D / 16; ++kk) {
-          const half8 a = *reinterpret_cast<const half8*>(krow + kk * 16);
-          sacc[s] = mfma32(a, qb[kk], sacc[s]);
-        }
-      }
-
-      // Scale into the log2 domain and mask.
-      const bool need_mask = (CAUSAL && j0 + kBC - 1 > i_base) || (BOUNDS && j0 + kBC > N);
-      float mloc = -INFINITY;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = sacc[s][r] * scale_log2;
-          if (need_mask) {
-            const int j = j0 + s * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) x = -INFINITY;
-          }
-          sacc[s][r] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      }
-      mloc = fmaxf(mloc, xor32(mloc));
-      const float m_new = fmaxf(m_run, mloc);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float corr = fast_exp2(m_run - m_use);
-      float lloc = 0.f;
-      half8 pb[4];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(sacc[s][r] - m_use);
-          lloc += p;
-          pb[2 * s + (r >> 3)][r & 7] = (half_t)p;
-        }
-      }
-      lloc += xor32(lloc);
-      l_run = l_run * corr + lloc;
-      m_run = m_new;
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[c][r] *= corr;
-
-      // O^T += V^T P^T. K-step (s, q) covers keys 32s+16q .. +15; slot (h, e)
-      // is key 32s + 16q + 8*(e/4) + 4h + e%4, matching the accumulator.
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        const half_t* vrow = Vt + (c * 32 + l32) * S::kVRow + 4 * h;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const half4 lo = *reinterpret_cast<const half4*>(vrow + ks * 16);
-          const half4 hi = *reinterpret_cast<const half4*>(vrow + ks * 16 + 8);
-          const half8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          oacc[c] = mfma32(a, pb[ks], oacc[c]);
-        }
-      }
-    }
-
-    if (has_next) {
-      half_t* Kn = smem + ((t + 1) & 1) * S::kStage;
-      st.store(Kn, Kn + S::kKElems, tid);
-    }
-    __syncthreads();
-  }
-
-  // Epilogue: O = acc / l (fp16), LSE = (m + log2 l) * ln 2.
-  if (!BOUNDS || i_row < N) {
-    const float inv_l = 1.f / l_run;
-    half_t* orow = O + (size_t)i_row * D;
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        half4 o4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = (half_t)(oacc[c][4 * g + e] * inv_l);
-        *reinterpret_cast<half4*>(orow + c * 32 + 8 * g + 4 * h) = o4;
-      }
-    }
-    if (h == 0) Lse[i_row] = (m_run + __log2f(l_run)) * kLn2;
+  const float thr_raw = kRescaleLog2 / scale_log2;
+  const int first = blockIdx.x;
+  fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off, Lse + (size_t)bh * N,
+                              N, first, scale_log2, thr_raw, smem);
+  if (CAUSAL) {
+    const int second = n_qtiles - 1 - first;
+    if (second > first)
+      fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
+                                  Lse + (size_t)bh * N, N, second, scale_log2, thr_raw, smem);
   }
 }
 
 template <int D, bool CAUSAL, bool BOUNDS>
 hipError_t launch_fwd_t(const FwdArgs& a) {
   const int n_qtiles = (a.N + kBR - 1) / kBR;
-  dim3 grid(n_qtiles, a.B * a.Hq);
-  const size_t smem = FwdSmem<D>::kBytes;
+  const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
+  dim3 grid(gx, a.B * a.Hq);
+  const size_t smem = FwdLds<D>::kBytes;
   const float scale_log2 = kLog2e / sqrtf((float)D);
   // One-time, idempotent: lift the dynamic-LDS cap above the 64 KB default.
   static const hipError_t attr = allow_lds(fwd_kernel<D, CAUSAL, BOUNDS>, smem);
@@ -271,7 +262,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
 
 template <int D>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  const bool bounds = (a.N % kBR) != 0;  // kBR is a multiple of kBC
+  const bool bounds = (a.N % kKV) != 0;  // kKV is a multiple of kBR
   if (a.causal) return bounds ? launch_fwd_t<D, true, true>(a) : launch_fwd_t<D, true, false>(a);
   return bounds ? launch_fwd_t<D, false, true>(a) : launch_fwd_t<D, false, false>(a);
 }

@@ -23,7 +23,8 @@ struct BwdArgs {
   const void* dO;
   const void* o;
   const float* lse;
-  float* dvec;
+  float* dvec;   // workspace: rowsum(dO * O), (B, Hq, N)
+  float* lse2;   // workspace: LSE * log2(e), (B, Hq, N)
   float* dq;
   void* dk;
   void* dv;

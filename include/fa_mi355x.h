@@ -63,8 +63,9 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
            int full_precision, void* stream);
 
 /*
- * Bytes of device workspace fa_bwd needs: the (B, Hq, N) float32 Dv vector,
- * the `dvec` allocation of fa_p100_ext.cu:124, rounded up to 256 bytes.
+ * Bytes of device workspace fa_bwd needs: two (B, Hq, N) float32 vectors, the
+ * reference's `dvec` (fa_p100_ext.cu:124) and the saved LSE pre-multiplied by
+ * log2(e), each rounded up to 256 bytes. 0 for an invalid shape.
  */
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D);
 
@@ -83,23 +84,25 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO,
 
 /*
  * First phase of fa_bwd, the counterpart of bwd_preprocess
- * (flash_bwd.cuh:65-78): dvec = rowsum(dO * o) in fp32, shape (B,Hq,N).
- * Exposed so a host can time or schedule the phases separately.
+ * (flash_bwd.cuh:65-78): fills `workspace` with dvec = rowsum(dO * o) and
+ * lse * log2(e), both fp32 (B,Hq,N). Exposed so a host can time or schedule
+ * the phases separately.
  */
-int fa_bwd_preprocess(const void* dO, const void* o, float* dvec,
+int fa_bwd_preprocess(const void* dO, const void* o, const float* lse,
+                      void* workspace, size_t workspace_bytes,
                       int B, int Hq, int N, int D, void* stream);
 
 /*
  * Second phase of fa_bwd, the counterpart of bwd_kernel
  * (flash_bwd.cuh:95-464, launched at 479-483): dK, dV (key/value-stationary)
  * and dQ (query-stationary, recomputing S and dP instead of the reference's
- * fp32 atomicAdd) in one launch, from the saved lse and the dvec written by
- * fa_bwd_preprocess. Overwrites dq, dk and dv.
+ * fp32 atomicAdd) in one launch, from the workspace fa_bwd_preprocess filled.
+ * Overwrites dq, dk and dv.
  */
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
-                const float* lse, const float* dvec, float* dq, void* dk,
-                void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
-                void* stream);
+                const void* workspace, size_t workspace_bytes, float* dq,
+                void* dk, void* dv, int B, int Hq, int Hkv, int N, int D,
+                int causal, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

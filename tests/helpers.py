@@ -50,9 +50,9 @@ def load_capi():
     lib.fa_bwd_workspace_bytes.restype = sz
     lib.fa_bwd.argtypes = [vp] * 10 + [sz] + [i] * 6 + [vp]
     lib.fa_bwd.restype = i
-    lib.fa_bwd_preprocess.argtypes = [vp] * 3 + [i] * 4 + [vp]
+    lib.fa_bwd_preprocess.argtypes = [vp] * 4 + [sz] + [i] * 4 + [vp]
     lib.fa_bwd_preprocess.restype = i
-    lib.fa_bwd_main.argtypes = [vp] * 9 + [i] * 6 + [vp]
+    lib.fa_bwd_main.argtypes = [vp] * 5 + [sz] + [vp] * 3 + [i] * 6 + [vp]
     lib.fa_bwd_main.restype = i
     return lib
 

@@ -26,9 +26,9 @@ def test_host_only_helpers():
     assert lib.fa_error_string(0) == b"success"
     assert b"64 or 128" in lib.fa_error_string(10001)
     assert b"multiple" in lib.fa_error_string(10003)
-    # (B, Hq, N) float32 rounded up to 256 bytes; 0 for an invalid shape.
-    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 128) == 8 * 4096 * 4
-    assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 256
+    # two (B, Hq, N) float32 vectors, each rounded up to 256 bytes; 0 if invalid.
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 128) == 2 * 8 * 4096 * 4
+    assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 512
     assert lib.fa_bwd_workspace_bytes(1, 8, 3, 4096, 128) == 0
     assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 80) == 0
 
@@ -43,8 +43,8 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd(z, z, z, z, z, 1, 4, 3, 8, 64, 0, 0, s) == 10003
     assert lib.fa_fwd(z, z, z, z, z, 0, 2, 2, 8, 64, 0, 0, s) == 10004
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 64, 0, 0, s) == 10005
-    assert lib.fa_bwd_main(*([z] * 9), 1, 2, 2, 8, 64, 1, s) == 10005
-    assert lib.fa_bwd_preprocess(z, z, z, 1, 2, 8, 128, s) == 10005
+    assert lib.fa_bwd_main(*([z] * 5), 0, *([z] * 3), 1, 2, 2, 8, 64, 1, s) == 10005
+    assert lib.fa_bwd_preprocess(z, z, z, z, 0, 1, 2, 8, 128, s) == 10005
     one = ctypes.c_void_p(1)
     assert lib.fa_bwd(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, s) == 10006
 
