@@ -15,7 +15,8 @@
 // products per tile pair instead of 5, but no atomics, no dQ clearing, and a
 // deterministic result), and both passes run in ONE launch:
 //
-//   workgroup (t, b*Hkv + hkv), 4 waves:
+//   workgroup (t, b*Hkv + hkv), 4 waves (numbered so that each kv head's
+//   workgroups share one XCD and its L2):
 //     phase 1: dK, dV for key rows [128t, 128t+128) of kv head hkv,
 //              over all query heads of its group and all query tiles
 //              (from the diagonal on when causal, flash_bwd.cuh:158-161)
@@ -26,8 +27,8 @@
 // the workgroups' total work is nearly equal without giving up parallelism.
 //
 // Both phases run on v_mfma_f32_32x32x16_f16 with 32 rows per wave. Phase 1
-// keeps the wave's K and V rows in registers (B operands) and dK^T/dV^T in
-// accumulators; P and dS come out of the S/dP accumulators and feed
+// keeps the workgroup's K and V rows resident in LDS (B operands) and each
+// wave's dK^T/dV^T in accumulators; P and dS come out of the S/dP accumulators and feed
 // dV^T += dO^T P and dK^T += Q^T dS directly, with the dO^T/Q^T operands read
 // from the row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the
 // forward kernel: S^T = K Q^T and dP^T = V dO^T with Q, dO held as B
@@ -52,7 +53,9 @@ template <int D>
 struct BwdLds {
   static constexpr int kTileHalves = kSub * D;
   static constexpr int kStageHalves = 2 * kTileHalves + 2 * kSub * 2;  // 2 tiles + lse2, dvec
-  static constexpr int kBytes = 2 * kStageHalves * 2;
+  // Phase 1 also keeps the workgroup's K and V rows (kTile each) resident.
+  static constexpr int kKVHalves = 2 * kTile * D;
+  static constexpr int kBytes = (2 * kStageHalves + kKVHalves) * 2;
 };
 
 // ---------------------------------------------------------------------------
@@ -92,43 +95,78 @@ __device__ __forceinline__ void vec_load64(float* lds, const float* g, int r0, i
                                    (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
+// The MFMA parts of every step run on one straight-line path; only the
+// softmax-side VALU branches between its masked and unmasked forms. Keeping
+// branches away from the MFMAs lets the compiler keep the loop-carried
+// accumulators in place instead of copying them between register files on
+// every iteration. Operand reads run one k-step ahead of the MFMAs that
+// consume them, fenced so the scheduler does not hoist every read of the step
+// (which costs more registers than the kernel has).
+
 // ------------------------------- phase 1 -----------------------------------
 template <int D, bool CAUSAL, bool BOUNDS>
 struct KVWave {
-  half8 kb[D / 16], vb[D / 16];      // this wave's K, V rows as B operands
   floatx16 dvacc[D / 32], dkacc[D / 32];
 
-  // One 64-row query tile staged at (Qs, Os, lse2s, dvs), rows i0 .. i0+63.
+  // P and dS for one 32-row block m of the query tile, from the S and dP
+  // accumulators; masked lanes (causal col > row, rows/cols >= N) give 0.
   template <bool MASK>
+  __device__ __forceinline__ void pds(const floatx16& sacc, const floatx16& pacc,
+                                      const float* lse2s, const float* dvs, int m, int i0,
+                                      int j_col, int N, int h, float c, half8 (&pb)[2],
+                                      half8 (&sb)[2]) {
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
+      const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 32 * m + 8 * g4 + 4 * h);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 4 * g4 + e;
+        float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
+        if constexpr (MASK) {
+          const int i = i0 + 32 * m + 8 * g4 + 4 * h + e;
+          if ((CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N))) p = 0.f;
+        }
+        pb[r >> 3][r & 7] = (half_t)p;
+        sb[r >> 3][r & 7] = (half_t)(p * (pacc[r] - d4[e]));
+      }
+    }
+  }
+
+  // One 64-row query tile staged at (Qs, Os, lse2s, dvs), rows i0 .. i0+63,
+  // against this wave's 32 key rows kr0 .. kr0+31 of the resident LDS tiles
+  // (Kt, Vt). K and V are re-read from LDS rather than held in registers, so
+  // the whole kernel stays within the MFMA's reach of VGPR accumulators.
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
-                                       const float* dvs, int i0, int j_col, int N, int lane,
-                                       float c) {
+                                       const float* dvs, const half_t* Kt, const half_t* Vt,
+                                       int kr0, int i0, int j_col, int N, int lane, float c,
+                                       bool mask) {
     const int h = lane >> 5, l32 = lane & 31;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       floatx16 sacc = zero16(), pacc = zero16();
+      half8 aq = tile_read16<D>(Qs, m * 32 + l32, h), ao = tile_read16<D>(Os, m * 32 + l32, h);
+      half8 bk = tile_read16<D>(Kt, kr0 + l32, h), bv = tile_read16<D>(Vt, kr0 + l32, h);
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        sacc = mfma32(tile_read16<D>(Qs, m * 32 + l32, 2 * kk + h), kb[kk], sacc);
-        pacc = mfma32(tile_read16<D>(Os, m * 32 + l32, 2 * kk + h), vb[kk], pacc);
+        half8 nq = aq, no = ao, nk = bk, nv = bv;
+        if (kk + 1 < D / 16) {
+          nq = tile_read16<D>(Qs, m * 32 + l32, 2 * kk + 2 + h);
+          no = tile_read16<D>(Os, m * 32 + l32, 2 * kk + 2 + h);
+          nk = tile_read16<D>(Kt, kr0 + l32, 2 * kk + 2 + h);
+          nv = tile_read16<D>(Vt, kr0 + l32, 2 * kk + 2 + h);
+        }
+        sacc = mfma32(aq, bk, sacc);
+        pacc = mfma32(ao, bv, pacc);
+        __builtin_amdgcn_sched_barrier(0);
+        aq = nq;
+        ao = no;
+        bk = nk;
+        bv = nv;
       }
       half8 pb[2], sb[2];
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
-        const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 32 * m + 8 * g4 + 4 * h);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g4 + e;
-          float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
-          if constexpr (MASK) {
-            const int i = i0 + 32 * m + 8 * g4 + 4 * h + e;
-            if ((CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N))) p = 0.f;
-          }
-          pb[r >> 3][r & 7] = (half_t)p;
-          sb[r >> 3][r & 7] = (half_t)(p * (pacc[r] - d4[e]));
-        }
-      }
+      if (mask) pds<true>(sacc, pacc, lse2s, dvs, m, i0, j_col, N, h, c, pb, sb);
+      else pds<false>(sacc, pacc, lse2s, dvs, m, i0, j_col, N, h, c, pb, sb);
       // dV^T += dO^T P, dK^T += Q^T dS; k-step q = query rows 32m+16q .. +15.
 #pragma unroll
       for (int cb = 0; cb < D / 32; ++cb) {
@@ -136,6 +174,7 @@ struct KVWave {
         for (int q = 0; q < 2; ++q) {
           dvacc[cb] = mfma32(tile_tr_operand<D>(Os, 32 * m + 16 * q, 32 * cb, lane), pb[q], dvacc[cb]);
           dkacc[cb] = mfma32(tile_tr_operand<D>(Qs, 32 * m + 16 * q, 32 * cb, lane), sb[q], dkacc[cb]);
+          __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
@@ -149,38 +188,55 @@ struct QWave {
   floatx16 qacc[D / 32];
   float lse2, dvv;
 
-  // One 64-row key tile staged at (Ks, Vs), keys j0 .. j0+63.
   template <bool MASK>
+  __device__ __forceinline__ void ds(const floatx16& st, const floatx16& pt, int j0, int s,
+                                     int i_row, int N, int h, float c, half8 (&sb)[2]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float p = fast_exp2(fmaf(st[r], c, -lse2));
+      if constexpr (MASK) {
+        const int j = j0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
+        if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) p = 0.f;
+      }
+      sb[r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
+    }
+  }
+
+  // One 64-row key tile staged at (Ks, Vs), keys j0 .. j0+63.
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int j0, int i_row,
-                                       int N, int lane, float c) {
+                                       int N, int lane, float c, bool mask) {
     const int h = lane >> 5, l32 = lane & 31;
     half8 sb[2][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       floatx16 st = zero16(), pt = zero16();
+      half8 ak = tile_read16<D>(Ks, s * 32 + l32, h), av = tile_read16<D>(Vs, s * 32 + l32, h);
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        st = mfma32(tile_read16<D>(Ks, s * 32 + l32, 2 * kk + h), qb[kk], st);
-        pt = mfma32(tile_read16<D>(Vs, s * 32 + l32, 2 * kk + h), ob[kk], pt);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(fmaf(st[r], c, -lse2));
-        if constexpr (MASK) {
-          const int j = j0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
-          if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) p = 0.f;
+        half8 nk = ak, nv = av;
+        if (kk + 1 < D / 16) {
+          nk = tile_read16<D>(Ks, s * 32 + l32, 2 * kk + 2 + h);
+          nv = tile_read16<D>(Vs, s * 32 + l32, 2 * kk + 2 + h);
         }
-        sb[s][r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
+        st = mfma32(ak, qb[kk], st);
+        pt = mfma32(av, ob[kk], pt);
+        __builtin_amdgcn_sched_barrier(0);
+        ak = nk;
+        av = nv;
       }
+      if (mask) ds<true>(st, pt, j0, s, i_row, N, h, c, sb[s]);
+      else ds<false>(st, pt, j0, s, i_row, N, h, c, sb[s]);
     }
     // dQ^T += K^T dS^T; k-step (s, q) = keys 32s+16q .. +15.
 #pragma unroll
-    for (int cb = 0; cb < D / 32; ++cb)
+    for (int cb = 0; cb < D / 32; ++cb) {
 #pragma unroll
       for (int s = 0; s < 2; ++s)
 #pragma unroll
         for (int q = 0; q < 2; ++q)
           qacc[cb] = mfma32(tile_tr_operand<D>(Ks, 32 * s + 16 * q, 32 * cb, lane), sb[s][q], qacc[cb]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
 };
 
@@ -191,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
     const float* __restrict__ Lse2, const float* __restrict__ Dvec,
     float* __restrict__ dQ, half_t* __restrict__ dK, half_t* __restrict__ dV,
-    int N, int Hq, int group, float scale, float scale_log2) {
+    int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2) {
   using L = BwdLds<D>;
   extern __shared__ __align__(16) half_t smem[];
 
@@ -201,8 +257,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
-  const int t0 = blockIdx.x * kTile;  // first row this workgroup owns
-  const int bkv = blockIdx.y;         // over B*Hkv
+  const int wi = xcd_work_index(n_tiles * BHkv);
+  if (wi < 0) return;
+  const int bkv = wi / n_tiles;             // over B*Hkv
+  const int t0 = (wi % n_tiles) * kTile;    // first row this workgroup owns
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
   const size_t kv_off = (size_t)bkv * N * D;
@@ -217,11 +275,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int j_col = jw + l32;
     const bool col_ok = !BOUNDS || j_col < N;
     KVWave<D, CAUSAL, BOUNDS> w;
-#pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      w.kb[kk] = as_half8(load16(Kh + (size_t)j_col * D + kk * 16 + h * 8, col_ok));
-      w.vb[kk] = as_half8(load16(Vh + (size_t)j_col * D + kk * 16 + h * 8, col_ok));
-    }
+    half_t* Kt = smem + 2 * L::kStageHalves;  // stationary K, V rows t0 .. t0+kTile-1
+    half_t* Vt = Kt + kTile * D;
+    tile_load<D, kTile, kWaves>(Kt, Kh, t0, N, wave, lane);
+    tile_load<D, kTile, kWaves>(Vt, Vh, t0, N, wave, lane);
 #pragma unroll
     for (int cb = 0; cb < D / 32; ++cb) {
       w.dvacc[cb] = zero16();
@@ -253,12 +310,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const half_t* Os = Qs + L::kTileHalves;
       const float* lse2s = reinterpret_cast<const float*>(Os + L::kTileHalves);
       const float* dvs = lse2s + kSub;
-      const bool active = !CAUSAL || (i0 + kSub - 1 >= jw);
-      if (active) {
-        const bool mask = (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kSub > N || jw + 32 > N));
-        if (mask) w.template step<true>(Qs, Os, lse2s, dvs, i0, j_col, N, lane, scale_log2);
-        else w.template step<false>(Qs, Os, lse2s, dvs, i0, j_col, N, lane, scale_log2);
-      }
+      // Causal tiles wholly above a wave's keys give exact zeros through the
+      // masked path; they occur only on the diagonal, so they are not skipped.
+      const bool mask = (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kSub > N || jw + 32 > N));
+      w.step(Qs, Os, lse2s, dvs, Kt, Vt, wave * 32, i0, j_col, N, lane, scale_log2, mask);
       wait_vmem();
       __syncthreads();
     }
@@ -319,12 +374,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         }
         const half_t* Ks = stage_ptr(t & 1);
         const half_t* Vs = Ks + L::kTileHalves;
-        const bool active = !CAUSAL || j0 <= iw + 31;
-        if (active) {
-          const bool mask = (CAUSAL && j0 + kSub - 1 > iw) || (BOUNDS && j0 + kSub > N);
-          if (mask) w.template step<true>(Ks, Vs, j0, i_row, N, lane, scale_log2);
-          else w.template step<false>(Ks, Vs, j0, i_row, N, lane, scale_log2);
-        }
+        const bool mask = (CAUSAL && j0 + kSub - 1 > iw) || (BOUNDS && j0 + kSub > N);
+        w.step(Ks, Vs, j0, i_row, N, lane, scale_log2, mask);
         wait_vmem();
         __syncthreads();
       }
@@ -358,7 +409,8 @@ hipError_t launch_pre_d(const BwdArgs& a) {
 
 template <int D, bool CAUSAL, bool BOUNDS>
 hipError_t launch_main_t(const BwdArgs& a) {
-  const dim3 grid((a.N + kTile - 1) / kTile, a.B * a.Hkv);
+  const int n_tiles = (a.N + kTile - 1) / kTile;
+  const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
   const size_t smem = BwdLds<D>::kBytes;
   static const hipError_t attr = allow_lds(bwd_kernel<D, CAUSAL, BOUNDS>, smem);
   if (attr != hipSuccess) return attr;
@@ -366,8 +418,8 @@ hipError_t launch_main_t(const BwdArgs& a) {
   hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), smem,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
-                     (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, scale,
-                     scale * kLog2e);
+                     (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
+                     a.B * a.Hkv, scale, scale * kLog2e);
   return hipGetLastError();
 }
 

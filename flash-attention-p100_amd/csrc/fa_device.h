@@ -104,18 +104,41 @@ __device__ __forceinline__ half8 tr_operand(const half_t* tile, int stride, int 
 }
 
 // ---------------------------------------------------------------------------
+// XCD-aware work numbering. MI355X dispatches consecutive workgroups of a
+// launch round-robin over its 8 XCDs, each with its own L2. Workgroup L thus
+// runs on XCD L % 8; giving that XCD the contiguous work range
+// [xcd * per, (xcd + 1) * per) keeps all workgroups of a head (which re-read
+// the same K/V or Q/dO tiles) behind one L2. Returns -1 for the few padding
+// workgroups when `total` is not a multiple of 8. Only locality depends on the
+// dispatch order; correctness does not.
+constexpr int kXcds = 8;
+__host__ __device__ __forceinline__ int xcd_grid(int total) {
+  return ((total + kXcds - 1) / kXcds) * kXcds;
+}
+__device__ __forceinline__ int xcd_work_index(int total) {
+  const int per = (total + kXcds - 1) / kXcds;
+  const int L = blockIdx.x;
+  const int w = (L % kXcds) * per + L / kXcds;
+  return w < total ? w : -1;
+}
+
+// ---------------------------------------------------------------------------
 // Swizzled row-major LDS tiles filled by direct global -> LDS loads.
 //
 // A tile holds rows of D halves (2D bytes) with no padding. Row r keeps its
-// logical 16-byte chunk c at physical chunk c ^ swz(r). swz spreads
-//   * eight consecutive rows read at one logical chunk (the 16-byte MFMA
-//     operand reads, one row per lane) over eight distinct chunks, and
-//   * four consecutive rows read at one aligned chunk pair (the transpose
-//     reads) over four distinct chunk pairs,
-// so neither access pattern piles onto one group of LDS banks.
+// logical 16-byte chunk c at physical chunk c ^ swz(r). The LDS has 64 banks
+// of 4 bytes (256 bytes per bank row, measured with SQ_LDS_BANK_CONFLICT), so
+// for D = 128 a tile row is one bank row and swz must spread
+//   * sixteen consecutive rows read at one logical chunk (the 16-byte MFMA
+//     operand reads, one row per lane, 16 lanes per LDS cycle) over all 16
+//     chunk positions, and
+//   * four consecutive rows read at two neighbouring chunk pairs (the
+//     transpose reads of lanes 0-31) over all 8 chunk-pair positions;
+// ((r & 3) << 2) | ((r >> 2) & 3) does both. For D = 64 two tile rows share a
+// bank row and ((r & 3) << 1) | ((r >> 2) & 1) does the same job.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128) return (r & 7) << 1;
+  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
   else return ((r & 3) << 1) | ((r >> 2) & 1);
 }
 

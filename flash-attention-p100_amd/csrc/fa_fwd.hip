@@ -10,7 +10,9 @@
 // the tile. Under causal masking a workgroup takes query tile x and then
 // tile T-1-x, so every workgroup does the same amount of work (the long and
 // the short end of the triangle), and the grid of (T/2) x (B*Hq) workgroups
-// x 8 waves keeps two waves on every SIMD at the headline shape.
+// x 8 waves keeps two waves on every SIMD at the headline shape. Workgroups
+// are numbered so that each head's tiles run on one XCD and its K/V stay in
+// that XCD's L2.
 //
 // Per wave and 32-key step, on v_mfma_f32_32x32x16_f16 (fp32 accumulate):
 //   * S^T = K Q^T with this wave's Q^T held in registers as the B operand, so
@@ -223,16 +225,18 @@ template <int D, bool CAUSAL, bool BOUNDS>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
-    int N, int Hq, int group, int n_qtiles, float scale_log2) {
+    int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2) {
   extern __shared__ __align__(16) half_t smem[];
-  const int bh = blockIdx.y;  // over B*Hq
+  const int w = xcd_work_index(gx * BH);
+  if (w < 0) return;
+  const int bh = w / gx;       // over B*Hq
+  const int first = w % gx;    // query tile (and, causal, its partner)
   const int b = bh / Hq, hq = bh % Hq;
   const int Hkv = Hq / group;
   const int hkv = hq / group;  // repeat_interleave head map (flash_fwd.cuh:90)
   const size_t q_off = (size_t)bh * N * D;
   const size_t kv_off = ((size_t)b * Hkv + hkv) * N * D;
   const float thr_raw = kRescaleLog2 / scale_log2;
-  const int first = blockIdx.x;
   fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off, Lse + (size_t)bh * N,
                               N, first, scale_log2, thr_raw, smem);
   if (CAUSAL) {
@@ -247,7 +251,8 @@ template <int D, bool CAUSAL, bool BOUNDS>
 hipError_t launch_fwd_t(const FwdArgs& a) {
   const int n_qtiles = (a.N + kBR - 1) / kBR;
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
-  dim3 grid(gx, a.B * a.Hq);
+  const int BH = a.B * a.Hq;
+  dim3 grid(xcd_grid(gx * BH));
   const size_t smem = FwdLds<D>::kBytes;
   const float scale_log2 = kLog2e / sqrtf((float)D);
   // One-time, idempotent: lift the dynamic-LDS cap above the 64 KB default.
@@ -256,7 +261,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), smem,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
-                     n_qtiles, scale_log2);
+                     n_qtiles, gx, BH, scale_log2);
   return hipGetLastError();
 }
 
