@@ -77,12 +77,20 @@ def load_capi():
     return lib
 
 
-def gpu_bench(c, steps, warmup):
+def gpu_bench(c, steps, warmup, copy_mib=0):
     import torch
     import fa_p100  # noqa: F401  (fails loudly if the binding is not built)
 
     lib = load_capi()
     dev = torch.device("cuda:0")
+    if copy_mib:
+        # A plain device copy of known size, so a counter run (FETCH_SIZE,
+        # WRITE_SIZE) of this same command can calibrate the counters' scale.
+        src = torch.ones(copy_mib * 2**20 // 4, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v, do = (t.to(dev) for t in make_inputs(c, torch))
     B, Hq, Hkv, N, D, causal = c["B"], c["Hq"], c["Hkv"], c["N"], c["D"], int(c["causal"])
     o = torch.empty_like(q)
@@ -172,7 +180,7 @@ def cpu_baseline(c, budget_s=20.0):
 
     run()
     reps, t_tot = 0, 0.0
-    while t_tot < budget_s / 2 and reps < 50:
+    while t_tot < budget_s / 2 and reps < 500:
         t0 = time.perf_counter()
         run()
         t_tot += time.perf_counter() - t0
@@ -222,6 +230,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="first run one device copy of MIB MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -231,7 +241,7 @@ def main():
 
     c = CONFIGS[args.config]
     f_fwd, f_bwd = flops(c)
-    r = gpu_bench(c, args.steps, args.warmup)
+    r = gpu_bench(c, args.steps, args.warmup, args.copy_calibration)
     step_ms = r["wall_ms"]
     value = (f_fwd + f_bwd) / (step_ms * 1e-3) / 1e12
     main_tf = f_bwd / (r["main_ms"] * 1e-3) / 1e12

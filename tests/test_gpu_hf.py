@@ -1,0 +1,110 @@
+"""The HuggingFace hook on the GPU: envelope parity and the Qwen3-0.6B-shaped step.
+
+The reference's only result-level test of its hook is verify_hf.py, which needs
+a hub checkpoint (verify_hf.py:23, 61-64) and is therefore not runnable here;
+parity of the hook is pinned by this test's own method instead, following
+verify_hf.py:78-154: on one set of random-init weights, logits through
+fa_p100 are compared with the eager implementation, and the gap must stay
+within a small multiple of the eager-vs-sdpa gap (both fp16 on the GPU).
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def qwen3(layers, hidden, heads, kv_heads, head_dim, inter, vocab, seed=0):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=vocab, hidden_size=hidden, intermediate_size=inter,
+                      num_hidden_layers=layers, num_attention_heads=heads,
+                      num_key_value_heads=kv_heads, head_dim=head_dim,
+                      max_position_embeddings=8192, use_cache=False)
+    torch.manual_seed(seed)
+    with torch.device("cuda"):
+        model = Qwen3ForCausalLM(cfg)
+    return model
+
+
+def logits_with(model, impl, ids):
+    model.config._attn_implementation = impl
+    with torch.no_grad(), torch.autocast("cuda", torch.float16):
+        return model(ids).logits.float()
+
+
+@pytest.mark.parametrize("head_dim,heads,kv", [(64, 8, 2), (128, 4, 4)])
+def test_hook_logits_within_eager_sdpa_envelope(head_dim, heads, kv):
+    import fa_p100_hf
+    model = qwen3(2, 512, heads, kv, head_dim, 1024, 1000).eval()
+    ids = torch.randint(0, 1000, (2, 384), device="cuda", generator=torch.Generator("cuda").manual_seed(1))
+    eager = logits_with(model, "eager", ids)
+    sdpa = logits_with(model, "sdpa", ids)
+    calls = {"n": 0}
+    inner = fa_p100_hf.fa_p100_attention_forward
+
+    def counted(*a, **k):
+        calls["n"] += 1
+        return inner(*a, **k)
+
+    from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
+    fa_p100_hf.enable_fa_p100(model)
+    ALL_ATTENTION_FUNCTIONS["fa_p100"] = counted
+    try:
+        fa = logits_with(model, "fa_p100", ids)
+    finally:
+        ALL_ATTENTION_FUNCTIONS["fa_p100"] = inner
+    assert calls["n"] == 2          # one call per layer: the kernel really ran
+    env = (sdpa - eager).abs()
+    gap = (fa - eager).abs()
+    assert gap.mean() <= 2 * env.mean() + 1e-4, (gap.mean().item(), env.mean().item())
+    q = torch.quantile(gap.flatten()[:2_000_000], 0.9999)
+    qe = torch.quantile(env.flatten()[:2_000_000], 0.9999)
+    assert q <= 4 * qe + 1e-3, (q.item(), qe.item())
+    top1 = (fa.argmax(-1) == eager.argmax(-1)).float().mean()
+    top1_env = (sdpa.argmax(-1) == eager.argmax(-1)).float().mean()
+    assert top1 >= top1_env - 0.01
+
+
+def test_hook_training_step_grads_match_eager():
+    """fwd+bwd through the hook vs eager: loss and parameter gradients agree."""
+    import fa_p100_hf
+    losses, grads = {}, {}
+    for impl in ("eager", "fa_p100"):
+        model = qwen3(2, 256, 4, 2, 64, 512, 500, seed=3)
+        if impl == "fa_p100":
+            fa_p100_hf.enable_fa_p100(model)
+        else:
+            model.config._attn_implementation = "eager"
+        ids = torch.randint(0, 500, (1, 300), device="cuda", generator=torch.Generator("cuda").manual_seed(2))
+        with torch.autocast("cuda", torch.float16):
+            out = model(ids, labels=ids)
+        out.loss.backward()
+        losses[impl] = out.loss.item()
+        grads[impl] = {n: p.grad.float().clone() for n, p in model.named_parameters()
+                       if "self_attn" in n and p.grad is not None}
+    assert abs(losses["fa_p100"] - losses["eager"]) <= 1e-3 * abs(losses["eager"])
+    for n, g in grads["eager"].items():
+        h = grads["fa_p100"][n]
+        assert torch.isfinite(h).all(), n
+        rel = ((h - g).norm() / g.norm()).item()
+        assert rel < 5e-2, (n, rel)
+
+
+def test_qwen3_0p6b_shaped_training_step_through_hook():
+    """Qwen3-0.6B-shaped decoder, random init, B=1, seq 8192,
+    token ids uniform over the vocab, one fwd+bwd step (fp16 autocast) with
+    attention through the hook, unmodified transformers code."""
+    import fa_p100_hf
+    model = qwen3(28, 1024, 16, 8, 128, 3072, 151936)
+    model.train()
+    fa_p100_hf.enable_fa_p100(model)
+    g = torch.Generator("cuda").manual_seed(0)
+    ids = torch.randint(0, 151936, (1, 8192), device="cuda", generator=g)
+    with torch.autocast("cuda", torch.float16):
+        out = model(ids, labels=ids)
+    out.loss.backward()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.loss)
+    # Random init predicts ~uniformly: the loss sits near log(vocab).
+    assert abs(out.loss.item() - torch.log(torch.tensor(151936.0)).item()) < 1.0
+    q_grad = model.model.layers[0].self_attn.q_proj.weight.grad
+    assert q_grad is not None and torch.isfinite(q_grad).all() and q_grad.abs().sum() > 0
