@@ -15,47 +15,59 @@
 // products per tile pair instead of 5, but no atomics, no dQ clearing, and a
 // deterministic result), and both passes run in ONE launch:
 //
-//   workgroup (t, b*Hkv + hkv), 4 waves (numbered so that each kv head's
+//   workgroup (t, b*Hkv + hkv), 8 waves (numbered so that each kv head's
 //   workgroups share one XCD and its L2):
-//     phase 1: dK, dV for key rows [128t, 128t+128) of kv head hkv,
-//              over all query heads of its group and all query tiles
-//              (from the diagonal on when causal, flash_bwd.cuh:158-161)
+//     phase 1: dK, dV for key rows [128t, 128t+128) of kv head hkv, over all
+//              query heads of its group and all query tiles (from the
+//              diagonal on when causal, flash_bwd.cuh:158-161). Wave w owns
+//              key rows 32*(w%4) .. +31 and, of each staged 64-row query
+//              tile, the 32-row half w/4; the two halves' dK/dV partials are
+//              summed through LDS at the end.
 //     phase 2: dQ for query rows [128t, 128t+128) of each query head of the
-//              group, over all key tiles (up to the diagonal when causal)
+//              group, over all key tiles (up to the diagonal when causal).
+//              Wave w owns query rows 32*(w%4) .. +31 and, of each staged
+//              64-key tile, the 32-key half w/4; partials summed through LDS.
 //
 // Under causal masking phase 1 shrinks with t while phase 2 grows with t, so
-// the workgroups' total work is nearly equal without giving up parallelism.
+// the workgroups' total work is nearly equal without giving up parallelism;
+// 8 waves keep two waves on every SIMD at the headline shape, so one wave's
+// softmax arithmetic overlaps the other's matrix products.
 //
-// Both phases run on v_mfma_f32_32x32x16_f16 with 32 rows per wave. Phase 1
-// keeps the workgroup's K and V rows resident in LDS (B operands) and each
-// wave's dK^T/dV^T in accumulators; P and dS come out of the S/dP accumulators and feed
-// dV^T += dO^T P and dK^T += Q^T dS directly, with the dO^T/Q^T operands read
-// from the row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the
-// forward kernel: S^T = K Q^T and dP^T = V dO^T with Q, dO held as B
-// operands, then dQ^T += K^T dS^T. Streamed tiles go from global memory
-// straight into double-buffered, XOR-swizzled LDS tiles
-// (global_load_lds_dwordx4). Dead lanes (causal col > row, ragged rows/cols
-// >= N) contribute exactly zero (flash_bwd.cuh:267-282); tiles that contain
-// any take a separate masked path. P and dS are rounded to fp16 only as MFMA
-// operands.
+// Both phases run on v_mfma_f32_32x32x16_f16. Phase 1 keeps the workgroup's
+// K and V rows resident in LDS and each wave's dK^T/dV^T in accumulators;
+// P and dS come out of the S/dP accumulators and feed dV^T += dO^T P and
+// dK^T += Q^T dS directly, with the dO^T/Q^T operands read from the
+// row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the forward
+// kernel: S^T = K Q^T and dP^T = V dO^T with Q, dO held as B operands, then
+// dQ^T += K^T dS^T. Streamed tiles go from global memory straight into
+// double-buffered, padded, row-permuted LDS tiles (global_load_lds_dwordx4).
+// Steps are straight-line code (masking is index arithmetic, compiled in only
+// for causal / ragged instantiations): a branch around the MFMAs makes the
+// compiler copy the loop-carried accumulators between register files on
+// every iteration. Dead lanes (causal col > row, ragged rows/cols >= N)
+// contribute exactly zero (flash_bwd.cuh:267-282). P and dS are rounded to
+// fp16 only as MFMA operands.
 #include "fa_device.h"
 #include "fa_launch.h"
 
 namespace fa {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kTile = 32 * kWaves;  // rows a workgroup owns (keys in phase 1, queries in phase 2)
-constexpr int kSub = 64;            // rows per streamed tile (queries in 1, keys in 2)
+constexpr int kTile = 128;  // rows a workgroup owns (keys in phase 1, queries in phase 2)
+constexpr int kSub = 64;    // rows per streamed tile (queries in 1, keys in 2)
 
 template <int D>
 struct BwdLds {
-  static constexpr int kTileHalves = kSub * D;
+  static constexpr int kTileHalves = Tile<D>::template halves<kSub>();
   static constexpr int kStageHalves = 2 * kTileHalves + 2 * kSub * 2;  // 2 tiles + lse2, dvec
   // Phase 1 also keeps the workgroup's K and V rows (kTile each) resident.
-  static constexpr int kKVHalves = 2 * kTile * D;
-  static constexpr int kBytes = (2 * kStageHalves + kKVHalves) * 2;
+  static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();
+  static constexpr int kBytes = (2 * kStageHalves + 2 * kKVTileHalves) * 2;
+  // Partial-sum exchange (reuses the stages and the K/V area): 4 waves x
+  // 2*D/32 accumulators of 16 floats per lane.
+  static_assert(4 * 2 * (D / 32) * 16 * 64 * 4 <= kBytes, "merge area exceeds the LDS budget");
 };
 
 // ---------------------------------------------------------------------------
@@ -95,89 +107,83 @@ __device__ __forceinline__ void vec_load64(float* lds, const float* g, int r0, i
                                    (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
 }
 
-// The MFMA parts of every step run on one straight-line path; only the
-// softmax-side VALU branches between its masked and unmasked forms. Keeping
-// branches away from the MFMAs lets the compiler keep the loop-carried
-// accumulators in place instead of copying them between register files on
-// every iteration. Operand reads run one k-step ahead of the MFMAs that
-// consume them, fenced so the scheduler does not hoist every read of the step
-// (which costs more registers than the kernel has).
+// Exchange of per-wave accumulators: waves of the upper half (w >= 4) store
+// theirs, waves w-4 add them. `acc` holds n accumulators; layout
+// [w % 4][k][g4][lane] x 4 floats, bank-conflict-free 16-byte accesses.
+template <int n>
+__device__ __forceinline__ void partial_store(float* buf, const floatx16 (&acc)[n], int w4,
+                                              int lane) {
+#pragma unroll
+  for (int k = 0; k < n; ++k)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const floatx4 v = {acc[k][4 * g4], acc[k][4 * g4 + 1], acc[k][4 * g4 + 2], acc[k][4 * g4 + 3]};
+      *reinterpret_cast<floatx4*>(buf + (((w4 * n + k) * 4 + g4) * 64 + lane) * 4) = v;
+    }
+}
+template <int n>
+__device__ __forceinline__ void partial_add(const float* buf, floatx16 (&acc)[n], int w4,
+                                            int lane) {
+#pragma unroll
+  for (int k = 0; k < n; ++k)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const floatx4 v =
+          *reinterpret_cast<const floatx4*>(buf + (((w4 * n + k) * 4 + g4) * 64 + lane) * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[k][4 * g4 + e] += v[e];
+    }
+}
 
 // ------------------------------- phase 1 -----------------------------------
+// acc[0 .. D/32) = dV^T blocks, acc[D/32 .. 2D/32) = dK^T blocks.
 template <int D, bool CAUSAL, bool BOUNDS>
 struct KVWave {
-  floatx16 dvacc[D / 32], dkacc[D / 32];
+  floatx16 acc[2 * (D / 32)];
 
-  // P and dS for one 32-row block m of the query tile, from the S and dP
-  // accumulators; masked lanes (causal col > row, rows/cols >= N) give 0.
-  template <bool MASK>
-  __device__ __forceinline__ void pds(const floatx16& sacc, const floatx16& pacc,
-                                      const float* lse2s, const float* dvs, int m, int i0,
-                                      int j_col, int N, int h, float c, half8 (&pb)[2],
-                                      half8 (&sb)[2]) {
+  // Query rows i0 + 32m .. +31 (m = this wave's half of the staged tile)
+  // against key rows kr0 .. kr0+31 of the resident tiles (Kt, Vt).
+  __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
+                                       const float* dvs, const half_t* Kt, const half_t* Vt,
+                                       int m, int kr0, int i0, int j_col, int N, int lane,
+                                       int roff, int troff, float c) {
+    const int h = lane >> 5;
+    floatx16 sacc = zero16(), pacc = zero16();
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      sacc = mfma32(tile_read16<D>(Qs, m * 32, kk, roff), tile_read16<D>(Kt, kr0, kk, roff), sacc);
+      pacc = mfma32(tile_read16<D>(Os, m * 32, kk, roff), tile_read16<D>(Vt, kr0, kk, roff), pacc);
+    }
+    // P and dS. A lane holds key column j_col and the 16 query rows
+    // i = i0 + 32m + 8*g4 + 4h + e. Dead key columns j >= N need no mask:
+    // they feed only dK/dV rows that are never stored.
+    const int base = i0 + 32 * m + 4 * h;
+    const int lo = j_col - base;  // alive when 8*g4 + e >= lo (causal)
+    const int hi = N - base;      // alive when 8*g4 + e <  hi (ragged)
+    half8 pb[2], sb[2];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
       const floatx4 d4 = *reinterpret_cast<const floatx4*>(dvs + 32 * m + 8 * g4 + 4 * h);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int r = 4 * g4 + e;
+        const int r = 4 * g4 + e, idx = 8 * g4 + e;
         float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
-        if constexpr (MASK) {
-          const int i = i0 + 32 * m + 8 * g4 + 4 * h + e;
-          if ((CAUSAL && j_col > i) || (BOUNDS && (i >= N || j_col >= N))) p = 0.f;
-        }
+        if (CAUSAL) p = (idx >= lo) ? p : 0.f;
+        if (BOUNDS) p = (idx < hi) ? p : 0.f;
         pb[r >> 3][r & 7] = (half_t)p;
         sb[r >> 3][r & 7] = (half_t)(p * (pacc[r] - d4[e]));
       }
     }
-  }
-
-  // One 64-row query tile staged at (Qs, Os, lse2s, dvs), rows i0 .. i0+63,
-  // against this wave's 32 key rows kr0 .. kr0+31 of the resident LDS tiles
-  // (Kt, Vt). K and V are re-read from LDS rather than held in registers, so
-  // the whole kernel stays within the MFMA's reach of VGPR accumulators.
-  __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
-                                       const float* dvs, const half_t* Kt, const half_t* Vt,
-                                       int kr0, int i0, int j_col, int N, int lane, float c,
-                                       bool mask) {
-    const int h = lane >> 5, l32 = lane & 31;
+    // dV^T += dO^T P, dK^T += Q^T dS; k-step q = query rows 32m+16q .. +15.
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      floatx16 sacc = zero16(), pacc = zero16();
-      half8 aq = tile_read16<D>(Qs, m * 32 + l32, h), ao = tile_read16<D>(Os, m * 32 + l32, h);
-      half8 bk = tile_read16<D>(Kt, kr0 + l32, h), bv = tile_read16<D>(Vt, kr0 + l32, h);
+    for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-        half8 nq = aq, no = ao, nk = bk, nv = bv;
-        if (kk + 1 < D / 16) {
-          nq = tile_read16<D>(Qs, m * 32 + l32, 2 * kk + 2 + h);
-          no = tile_read16<D>(Os, m * 32 + l32, 2 * kk + 2 + h);
-          nk = tile_read16<D>(Kt, kr0 + l32, 2 * kk + 2 + h);
-          nv = tile_read16<D>(Vt, kr0 + l32, 2 * kk + 2 + h);
-        }
-        sacc = mfma32(aq, bk, sacc);
-        pacc = mfma32(ao, bv, pacc);
-        __builtin_amdgcn_sched_barrier(0);
-        aq = nq;
-        ao = no;
-        bk = nk;
-        bv = nv;
+      for (int q = 0; q < 2; ++q) {
+        acc[cb] = mfma32(tile_tr_operand<D>(Os, 32 * m + 16 * q, 32 * cb, troff), pb[q], acc[cb]);
+        acc[D / 32 + cb] =
+            mfma32(tile_tr_operand<D>(Qs, 32 * m + 16 * q, 32 * cb, troff), sb[q], acc[D / 32 + cb]);
       }
-      half8 pb[2], sb[2];
-      if (mask) pds<true>(sacc, pacc, lse2s, dvs, m, i0, j_col, N, h, c, pb, sb);
-      else pds<false>(sacc, pacc, lse2s, dvs, m, i0, j_col, N, h, c, pb, sb);
-      // dV^T += dO^T P, dK^T += Q^T dS; k-step q = query rows 32m+16q .. +15.
-#pragma unroll
-      for (int cb = 0; cb < D / 32; ++cb) {
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          dvacc[cb] = mfma32(tile_tr_operand<D>(Os, 32 * m + 16 * q, 32 * cb, lane), pb[q], dvacc[cb]);
-          dkacc[cb] = mfma32(tile_tr_operand<D>(Qs, 32 * m + 16 * q, 32 * cb, lane), sb[q], dkacc[cb]);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      }
-    }
   }
 };
 
@@ -185,58 +191,39 @@ struct KVWave {
 template <int D, bool CAUSAL, bool BOUNDS>
 struct QWave {
   half8 qb[D / 16], ob[D / 16];  // this wave's Q, dO rows as B operands
-  floatx16 qacc[D / 32];
+  floatx16 acc[D / 32];          // dQ^T blocks
   float lse2, dvv;
 
-  template <bool MASK>
-  __device__ __forceinline__ void ds(const floatx16& st, const floatx16& pt, int j0, int s,
-                                     int i_row, int N, int h, float c, half8 (&sb)[2]) {
+  // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
+  __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
+                                       int i_row, int N, int lane, int roff, int troff, float c) {
+    const int h = lane >> 5;
+    floatx16 st = zero16(), pt = zero16();
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) {
+      st = mfma32(tile_read16<D>(Ks, s * 32, kk, roff), qb[kk], st);
+      pt = mfma32(tile_read16<D>(Vs, s * 32, kk, roff), ob[kk], pt);
+    }
+    // dS^T. A lane holds query row i_row and the 16 keys
+    // j = j0 + 32s + 8*g4 + 4h + e. Rows i_row >= N are never stored.
+    const int base = j0 + 32 * s + 4 * h;
+    const int lo = i_row - base;  // alive when 8*g4 + e <= lo (causal)
+    const int hi = N - base;      // alive when 8*g4 + e <  hi (ragged)
+    half8 sb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
+      const int idx = 8 * (r >> 2) + (r & 3);
       float p = fast_exp2(fmaf(st[r], c, -lse2));
-      if constexpr (MASK) {
-        const int j = j0 + 32 * s + 8 * (r >> 2) + 4 * h + (r & 3);
-        if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) p = 0.f;
-      }
+      if (CAUSAL) p = (idx <= lo) ? p : 0.f;
+      if (BOUNDS) p = (idx < hi) ? p : 0.f;
       sb[r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
     }
-  }
-
-  // One 64-row key tile staged at (Ks, Vs), keys j0 .. j0+63.
-  __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int j0, int i_row,
-                                       int N, int lane, float c, bool mask) {
-    const int h = lane >> 5, l32 = lane & 31;
-    half8 sb[2][2];
+    // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15.
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      floatx16 st = zero16(), pt = zero16();
-      half8 ak = tile_read16<D>(Ks, s * 32 + l32, h), av = tile_read16<D>(Vs, s * 32 + l32, h);
+    for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
-      for (int kk = 0; kk < D / 16; ++kk) {
-        half8 nk = ak, nv = av;
-        if (kk + 1 < D / 16) {
-          nk = tile_read16<D>(Ks, s * 32 + l32, 2 * kk + 2 + h);
-          nv = tile_read16<D>(Vs, s * 32 + l32, 2 * kk + 2 + h);
-        }
-        st = mfma32(ak, qb[kk], st);
-        pt = mfma32(av, ob[kk], pt);
-        __builtin_amdgcn_sched_barrier(0);
-        ak = nk;
-        av = nv;
-      }
-      if (mask) ds<true>(st, pt, j0, s, i_row, N, h, c, sb[s]);
-      else ds<false>(st, pt, j0, s, i_row, N, h, c, sb[s]);
-    }
-    // dQ^T += K^T dS^T; k-step (s, q) = keys 32s+16q .. +15.
-#pragma unroll
-    for (int cb = 0; cb < D / 32; ++cb) {
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int q = 0; q < 2; ++q)
-          qacc[cb] = mfma32(tile_tr_operand<D>(Ks, 32 * s + 16 * q, 32 * cb, lane), sb[s][q], qacc[cb]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
+      for (int q = 0; q < 2; ++q)
+        acc[cb] = mfma32(tile_tr_operand<D>(Ks, 32 * s + 16 * q, 32 * cb, troff), sb[q], acc[cb]);
   }
 };
 
@@ -250,17 +237,20 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2) {
   using L = BwdLds<D>;
   extern __shared__ __align__(16) half_t smem[];
+  float* xbuf = reinterpret_cast<float*>(smem);  // partial-sum exchange area
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int w4 = wave & 3;     // row block (keys in phase 1, queries in phase 2)
+  const int half = wave >> 2;  // which 32-row half of each streamed tile
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
   const int wi = xcd_work_index(n_tiles * BHkv);
   if (wi < 0) return;
-  const int bkv = wi / n_tiles;             // over B*Hkv
-  const int t0 = (wi % n_tiles) * kTile;    // first row this workgroup owns
+  const int bkv = wi / n_tiles;            // over B*Hkv
+  const int t0 = (wi % n_tiles) * kTile;   // first row this workgroup owns
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
   const size_t kv_off = (size_t)bkv * N * D;
@@ -268,22 +258,19 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const half_t* Vh = V + kv_off;
 
   auto stage_ptr = [&](int st) { return smem + st * L::kStageHalves; };
+  const int roff = row_lane_off<D>(lane), troff = tr_lane_off<D>(lane);
 
   // =========================== phase 1: dK, dV ===========================
   {
-    const int jw = t0 + wave * 32;  // this wave's key rows
+    const int jw = t0 + w4 * 32;  // this wave's key rows
     const int j_col = jw + l32;
-    const bool col_ok = !BOUNDS || j_col < N;
     KVWave<D, CAUSAL, BOUNDS> w;
-    half_t* Kt = smem + 2 * L::kStageHalves;  // stationary K, V rows t0 .. t0+kTile-1
-    half_t* Vt = Kt + kTile * D;
+    half_t* Kt = smem + 2 * L::kStageHalves;  // resident K, V rows t0 .. t0+kTile-1
+    half_t* Vt = Kt + L::kKVTileHalves;
     tile_load<D, kTile, kWaves>(Kt, Kh, t0, N, wave, lane);
     tile_load<D, kTile, kWaves>(Vt, Vh, t0, N, wave, lane);
 #pragma unroll
-    for (int cb = 0; cb < D / 32; ++cb) {
-      w.dvacc[cb] = zero16();
-      w.dkacc[cb] = zero16();
-    }
+    for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
 
     const int i_start = CAUSAL ? t0 : 0;  // t0 is a multiple of kSub
     const int n_qt = (N - i_start + kSub - 1) / kSub;
@@ -305,42 +292,51 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     __syncthreads();
     for (int it = 0; it < n_it; ++it) {
       const int i0 = i_start + (it % n_qt) * kSub;
-      if (it + 1 < n_it) fetch(it + 1, stage_ptr((it + 1) & 1));
+      // The last iteration re-fetches its own tile into the idle buffer, so the
+      // loop body stays free of branches around the products.
+      fetch(min(it + 1, n_it - 1), stage_ptr((it + 1) & 1));
       const half_t* Qs = stage_ptr(it & 1);
       const half_t* Os = Qs + L::kTileHalves;
       const float* lse2s = reinterpret_cast<const float*>(Os + L::kTileHalves);
       const float* dvs = lse2s + kSub;
       // Causal tiles wholly above a wave's keys give exact zeros through the
-      // masked path; they occur only on the diagonal, so they are not skipped.
-      const bool mask = (CAUSAL && i0 < jw + 31) || (BOUNDS && (i0 + kSub > N || jw + 32 > N));
-      w.step(Qs, Os, lse2s, dvs, Kt, Vt, wave * 32, i0, j_col, N, lane, scale_log2, mask);
+      // mask; they occur only on the diagonal, so they are not skipped.
+      w.step(Qs, Os, lse2s, dvs, Kt, Vt, half, w4 * 32, i0, j_col, N, lane, roff, troff,
+             scale_log2);
       wait_vmem();
       __syncthreads();
     }
 
-    if (col_ok) {
-      half_t* dkrow = dK + kv_off + (size_t)j_col * D;
-      half_t* dvrow = dV + kv_off + (size_t)j_col * D;
+    // Sum the two halves' partials, then dK (scaled) and dV leave as fp16.
+    if (half) partial_store(xbuf, w.acc, w4, lane);
+    __syncthreads();
+    if (!half) {
+      partial_add(xbuf, w.acc, w4, lane);
+      if (!BOUNDS || j_col < N) {
+        half_t* dkrow = dK + kv_off + (size_t)j_col * D;
+        half_t* dvrow = dV + kv_off + (size_t)j_col * D;
 #pragma unroll
-      for (int cb = 0; cb < D / 32; ++cb) {
+        for (int cb = 0; cb < D / 32; ++cb) {
 #pragma unroll
-        for (int g4 = 0; g4 < 4; ++g4) {
-          half4 k4, v4;
+          for (int g4 = 0; g4 < 4; ++g4) {
+            half4 k4, v4;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            k4[e] = (half_t)(w.dkacc[cb][4 * g4 + e] * scale);
-            v4[e] = (half_t)w.dvacc[cb][4 * g4 + e];
+            for (int e = 0; e < 4; ++e) {
+              k4[e] = (half_t)(w.acc[D / 32 + cb][4 * g4 + e] * scale);
+              v4[e] = (half_t)w.acc[cb][4 * g4 + e];
+            }
+            *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
+            *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
           }
-          *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
-          *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
         }
       }
     }
+    __syncthreads();  // the exchange area is the next phase's staging memory
   }
 
   // ============================== phase 2: dQ ==============================
   {
-    const int iw = t0 + wave * 32;  // this wave's query rows
+    const int iw = t0 + w4 * 32;  // this wave's query rows
     const int i_row = iw + l32;
     const bool row_ok = !BOUNDS || i_row < N;
     const int kv_end = CAUSAL ? min(N, t0 + kTile) : N;
@@ -359,7 +355,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       w.lse2 = row_ok ? Lse2[bhq * N + i_row] : 0.f;
       w.dvv = row_ok ? Dvec[bhq * N + i_row] : 0.f;
 #pragma unroll
-      for (int cb = 0; cb < D / 32; ++cb) w.qacc[cb] = zero16();
+      for (int cb = 0; cb < D / 32; ++cb) w.acc[cb] = zero16();
 
       tile_load<D, kSub, kWaves>(stage_ptr(0), Kh, 0, N, wave, lane);
       tile_load<D, kSub, kWaves>(stage_ptr(0) + L::kTileHalves, Vh, 0, N, wave, lane);
@@ -367,20 +363,23 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       __syncthreads();
       for (int t = 0; t < n_kt; ++t) {
         const int j0 = t * kSub;
-        if (t + 1 < n_kt) {
+        {
           half_t* nb = stage_ptr((t + 1) & 1);
-          tile_load<D, kSub, kWaves>(nb, Kh, j0 + kSub, N, wave, lane);
-          tile_load<D, kSub, kWaves>(nb + L::kTileHalves, Vh, j0 + kSub, N, wave, lane);
+          const int jn = min(t + 1, n_kt - 1) * kSub;  // last step: idle-buffer refetch
+          tile_load<D, kSub, kWaves>(nb, Kh, jn, N, wave, lane);
+          tile_load<D, kSub, kWaves>(nb + L::kTileHalves, Vh, jn, N, wave, lane);
         }
         const half_t* Ks = stage_ptr(t & 1);
         const half_t* Vs = Ks + L::kTileHalves;
-        const bool mask = (CAUSAL && j0 + kSub - 1 > iw) || (BOUNDS && j0 + kSub > N);
-        w.step(Ks, Vs, j0, i_row, N, lane, scale_log2, mask);
+        w.step(Ks, Vs, half, j0, i_row, N, lane, roff, troff, scale_log2);
         wait_vmem();
         __syncthreads();
       }
 
-      if (row_ok) {
+      if (half) partial_store(xbuf, w.acc, w4, lane);
+      __syncthreads();
+      if (!half && row_ok) {
+        partial_add(xbuf, w.acc, w4, lane);
         float* qrow = dQ + bhq * N * D + (size_t)i_row * D;
 #pragma unroll
         for (int cb = 0; cb < D / 32; ++cb) {
@@ -388,11 +387,12 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           for (int g4 = 0; g4 < 4; ++g4) {
             floatx4 v4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v4[e] = w.qacc[cb][4 * g4 + e] * scale;
+            for (int e = 0; e < 4; ++e) v4[e] = w.acc[cb][4 * g4 + e] * scale;
             *reinterpret_cast<floatx4*>(qrow + cb * 32 + 8 * g4 + 4 * h) = v4;
           }
         }
       }
+      __syncthreads();  // the exchange area is the next head's staging memory
     }
   }
 }

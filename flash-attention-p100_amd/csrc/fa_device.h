@@ -123,46 +123,62 @@ __device__ __forceinline__ int xcd_work_index(int total) {
 }
 
 // ---------------------------------------------------------------------------
-// Swizzled row-major LDS tiles filled by direct global -> LDS loads.
+// LDS tiles filled by direct global -> LDS loads.
 //
-// A tile holds rows of D halves (2D bytes) with no padding. Row r keeps its
-// logical 16-byte chunk c at physical chunk c ^ swz(r). The LDS has 64 banks
-// of 4 bytes (256 bytes per bank row, measured with SQ_LDS_BANK_CONFLICT), so
-// for D = 128 a tile row is one bank row and swz must spread
-//   * sixteen consecutive rows read at one logical chunk (the 16-byte MFMA
-//     operand reads, one row per lane, 16 lanes per LDS cycle) over all 16
-//     chunk positions, and
-//   * four consecutive rows read at two neighbouring chunk pairs (the
-//     transpose reads of lanes 0-31) over all 8 chunk-pair positions;
-// ((r & 3) << 2) | ((r >> 2) & 3) does both. For D = 64 two tile rows share a
-// bank row and ((r & 3) << 1) | ((r >> 2) & 1) does the same job.
+// A tile stores rows of D halves padded to S = D/8 + 1 sixteen-byte chunks,
+// and keeps logical row R at LDS row perm16(R), which swaps the two low 2-bit
+// fields of R (an involution that fixes R's 16-row group). The LDS has 64
+// banks of 4 bytes (measured with SQ_LDS_BANK_CONFLICT), i.e. 16 bank groups
+// of 16 bytes, and chunk c of LDS row rho sits in group (rho*S + c) mod 16:
+//   * the 16-byte MFMA operand reads (16 lanes = 16 consecutive logical rows
+//     at one chunk per LDS cycle) hit 16 distinct groups because perm16 (and,
+//     for D = 64, the odd factor S = 9) is a bijection mod 16;
+//   * the transpose reads (per half-wave: 4 logical rows 4h+t, t = 0..3, at 4
+//     consecutive chunks) land on LDS rows 4t+h, spaced by 4, so they also
+//     hit 16 distinct groups.
+// Every read address is then one per-lane base plus a compile-time offset.
 template <int D>
-__device__ __forceinline__ int swz(int r) {
-  if constexpr (D == 128) return ((r & 3) << 2) | ((r >> 2) & 3);
-  else return ((r & 3) << 1) | ((r >> 2) & 1);
+struct Tile {
+  static constexpr int kChunks = D / 8;         // data chunks per row
+  static constexpr int kStride = kChunks + 1;   // chunks per padded row
+  static constexpr int kRowHalves = kStride * 8;
+  template <int ROWS>
+  static constexpr int insts() { return (ROWS * kStride + 63) / 64; }  // 1 KB wave loads
+  template <int ROWS>
+  static constexpr int halves() { return insts<ROWS>() * 512; }
+};
+
+__host__ __device__ __forceinline__ constexpr int perm16(int r) {
+  return (r & ~15) | ((r & 3) << 2) | ((r >> 2) & 3);
 }
 
+// Per-lane offset (halves) of the 16-byte operand read of logical row
+// rowbase + (lane % 32), rowbase a multiple of 16.
 template <int D>
-__device__ __forceinline__ const half_t* tile_chunk(const half_t* tile, int r, int c) {
-  return tile + r * D + ((c ^ swz<D>(r)) << 3);
+__device__ __forceinline__ int row_lane_off(int lane) {
+  return perm16(lane & 31) * Tile<D>::kRowHalves + 8 * (lane >> 5);
 }
 
-// 16-byte MFMA operand: row r, logical chunk c (halves 8c .. 8c+7).
+// Per-lane offset (halves) of the transpose read (see tr_operand()).
 template <int D>
-__device__ __forceinline__ half8 tile_read16(const half_t* tile, int r, int c) {
-  return *reinterpret_cast<const half8*>(tile_chunk<D>(tile, r, c));
-}
-
-// The transpose-read operand of tr_operand() for a swizzled tile.
-template <int D>
-__device__ __forceinline__ half8 tile_tr_operand(const half_t* tile, int rbase, int c0, int lane) {
+__device__ __forceinline__ int tr_lane_off(int lane) {
   const int n = lane & 15, grp = lane >> 4;
-  const int row = rbase + 4 * (grp >> 1) + (n >> 2);
-  const int col = c0 + 16 * (grp & 1) + 4 * (n & 3);
-  const half_t* p0 = tile_chunk<D>(tile, row, col >> 3) + (col & 7);
-  const half_t* p1 = tile_chunk<D>(tile, row + 8, col >> 3) + (col & 7);
-  const half4 lo = lds_read_tr(p0);
-  const half4 hi = lds_read_tr(p1);
+  return (4 * (n >> 2) + (grp >> 1)) * Tile<D>::kRowHalves + 16 * (grp & 1) + 4 * (n & 3);
+}
+
+// 16-byte MFMA operand: logical row rowbase + lane%32, halves 16*kk + 8*(lane/32) ...+7.
+template <int D>
+__device__ __forceinline__ half8 tile_read16(const half_t* tile, int rowbase, int kk, int lane_off) {
+  return *reinterpret_cast<const half8*>(tile + rowbase * Tile<D>::kRowHalves + 16 * kk + lane_off);
+}
+
+// Transpose-read A operand of tr_operand() on a tile: column c0 + lane%32 at
+// logical rows rbase + 8*(e/4) + 4*(lane/32) + e%4 (rbase a multiple of 16).
+template <int D>
+__device__ __forceinline__ half8 tile_tr_operand(const half_t* tile, int rbase, int c0, int tr_off) {
+  const half_t* p = tile + rbase * Tile<D>::kRowHalves + c0 + tr_off;
+  const half4 lo = lds_read_tr(p);
+  const half4 hi = lds_read_tr(p + 2 * Tile<D>::kRowHalves);
   return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -176,23 +192,26 @@ __device__ __forceinline__ void lds_direct16(half_t* lds, const half_t* src) {
 // Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-// Loads rows [r0, r0 + ROWS) of a row-major (N, D) fp16 matrix into a swizzled
-// LDS tile, using the NW waves of the workgroup. Rows >= N are clamped to row
-// N - 1 (finite data); the kernels mask them before they can contribute.
+// Loads logical rows [r0, r0 + ROWS) of a row-major (N, D) fp16 matrix into a
+// tile, using the NW waves of the workgroup. Rows >= N are clamped to row N-1
+// (finite data; the kernels mask them before they can contribute); padding
+// slots receive a copy of their row's first chunk.
 template <int D, int ROWS, int NW>
 __device__ __forceinline__ void tile_load(half_t* tile, const half_t* g, int r0, int N,
                                           int wave, int lane) {
-  constexpr int kRowsPerInst = 512 / D;              // 1 KB per wave instruction
-  constexpr int kInsts = ROWS / kRowsPerInst;
-  static_assert(kInsts % NW == 0, "tile must split evenly over the waves");
-  const int rl = lane / (D / 8);                      // row within the instruction
-  const int pc = lane % (D / 8);                      // physical chunk
+  using T = Tile<D>;
+  constexpr int kInsts = T::template insts<ROWS>();
+  constexpr int kPer = (kInsts + NW - 1) / NW;
 #pragma unroll
-  for (int u = 0; u < kInsts / NW; ++u) {
+  for (int u = 0; u < kPer; ++u) {
     const int inst = u * NW + wave;
-    const int r = inst * kRowsPerInst + rl;
-    const int gr = min(r0 + r, N - 1);
-    lds_direct16(tile + inst * 512, g + (size_t)gr * D + ((pc ^ swz<D>(r)) << 3));
+    if (kInsts % NW == 0 || inst < kInsts) {
+      const int p = inst * 64 + lane;
+      const int rho = p / T::kStride;
+      const int c = p - rho * T::kStride;
+      const int gr = min(r0 + perm16(rho), N - 1);
+      lds_direct16(tile + inst * 512, g + (size_t)gr * D + (c < T::kChunks ? c * 8 : 0));
+    }
   }
 }
 

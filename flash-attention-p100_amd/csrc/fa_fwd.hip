@@ -26,8 +26,9 @@
 //   * P^T leaves the accumulator as fp16 and feeds O^T += V^T P^T directly,
 //     with V^T read from the row-major V tile by the LDS transpose read.
 // K and V tiles move from global memory straight into double-buffered,
-// XOR-swizzled LDS tiles (global_load_lds_dwordx4), so staging costs no
-// registers and no LDS store instructions.
+// padded, row-permuted LDS tiles (global_load_lds_dwordx4), so staging costs
+// no registers and no LDS store instructions, and every LDS read address is a
+// per-lane base plus an immediate.
 //
 // Causal tiles past the diagonal are never loaded (flash_fwd.cuh:127-130);
 // diagonal and ragged tiles take a separate masked path (flash_fwd.cuh:
@@ -47,7 +48,7 @@ constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold, log2 units
 
 template <int D>
 struct FwdLds {
-  static constexpr int kTileHalves = kKV * D;          // one K or V tile
+  static constexpr int kTileHalves = Tile<D>::template halves<kKV>();  // one K or V tile
   static constexpr int kStageHalves = 2 * kTileHalves; // K + V
   static constexpr int kStageBytes = 2 * kStageHalves * 2;
   // Merge area (reuses the stages): per wave, D/32 x 16 floats per lane.
@@ -67,12 +68,13 @@ struct FwdWave {
 
   template <bool MASK>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int kq, int j0,
-                                       int i_row, int N, int lane, float c, float thr_raw) {
-    const int h = lane >> 5, l32 = lane & 31;
+                                       int i_row, int N, int lane, int roff, int troff, float c,
+                                       float thr_raw) {
+    const int h = lane >> 5;
     floatx16 s = zero16();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk)
-      s = mfma32(tile_read16<D>(Ks, kq * 32 + l32, 2 * kk + h), qb[kk], s);
+      s = mfma32(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], s);
     if constexpr (MASK) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -108,7 +110,7 @@ struct FwdWave {
     for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
       for (int q = 0; q < 2; ++q)
-        oacc[cb] = mfma32(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, lane), pb[q], oacc[cb]);
+        oacc[cb] = mfma32(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, troff), pb[q], oacc[cb]);
   }
 };
 
@@ -126,6 +128,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int i_row = i_base + l32;
 
   FwdWave<D, CAUSAL, BOUNDS> w;
+  const int roff = row_lane_off<D>(lane), troff = tr_lane_off<D>(lane);
   const bool row_ok = !BOUNDS || i_row < N;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
@@ -154,8 +157,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const bool active = j0 < kv_end && (!CAUSAL || j0 <= i_base + 31);
     if (active) {
       const bool mask = (CAUSAL && j0 + 31 > i_base) || (BOUNDS && j0 + 32 > N);
-      if (mask) w.template step<true>(Ks, Vs, kq, j0, i_row, N, lane, c, thr_raw);
-      else w.template step<false>(Ks, Vs, kq, j0, i_row, N, lane, c, thr_raw);
+      if (mask) w.template step<true>(Ks, Vs, kq, j0, i_row, N, lane, roff, troff, c, thr_raw);
+      else w.template step<false>(Ks, Vs, kq, j0, i_row, N, lane, roff, troff, c, thr_raw);
     }
     wait_vmem();
     __syncthreads();
