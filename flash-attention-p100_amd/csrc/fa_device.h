@@ -196,16 +196,26 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // tile, using the NW waves of the workgroup. Rows >= N are clamped to row N-1
 // (finite data; the kernels mask them before they can contribute); padding
 // slots receive a copy of their row's first chunk.
-template <int D, int ROWS, int NW>
-__device__ __forceinline__ void tile_load(half_t* tile, const half_t* g, int r0, int N,
-                                          int wave, int lane) {
-  using T = Tile<D>;
-  constexpr int kInsts = T::template insts<ROWS>();
-  constexpr int kPer = (kInsts + NW - 1) / NW;
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
+//
+// With EVEN, the tile is padded to a whole number of instructions per wave
+// (kHalves), so every wave issues exactly kParts instructions and the issue
+// needs no wave-dependent branch; the extra slots receive rows past the tile
+// (clamped to N - 1), which no reader addresses.
+template <int D, int ROWS, int NW, bool EVEN = false>
+struct TileLoad {
+  static constexpr int kInsts = Tile<D>::template insts<ROWS>();
+  static constexpr int kParts = (kInsts + NW - 1) / NW;  // instructions per wave (at most)
+  static constexpr int kHalves = (EVEN ? kParts * NW : kInsts) * 512;
+
+  // Issues this wave's instruction number u (0 <= u < kParts) of the load.
+  // Splitting the load lets a kernel spread the issue over its products: a
+  // wave that issues all of them at once stalls until the memory pipeline has
+  // accepted them.
+  __device__ __forceinline__ static void part(half_t* tile, const half_t* g, int r0, int N,
+                                              int wave, int lane, int u) {
+    using T = Tile<D>;
     const int inst = u * NW + wave;
-    if (kInsts % NW == 0 || inst < kInsts) {
+    if (EVEN || kInsts % NW == 0 || inst < kInsts) {
       const int p = inst * 64 + lane;
       const int rho = p / T::kStride;
       const int c = p - rho * T::kStride;
@@ -213,6 +223,53 @@ __device__ __forceinline__ void tile_load(half_t* tile, const half_t* g, int r0,
       lds_direct16(tile + inst * 512, g + (size_t)gr * D + (c < T::kChunks ? c * 8 : 0));
     }
   }
+};
+
+// Per-lane byte offsets of a wave's TileLoad instructions relative to the
+// tile's first row. They do not depend on the stage, so a kernel computes
+// them once and each load is then a scalar base plus one VGPR offset.
+// Padding instructions (EVEN) read the tile's first row. With CLAMP, offsets
+// past `lim` (the last chunk of row N - 1) are clamped to it, so rows >= N
+// hold finite copies of that chunk, which the kernels mask.
+template <int D, int ROWS, int NW, bool EVEN>
+struct TilePlan {
+  using TL = TileLoad<D, ROWS, NW, EVEN>;
+  uint32_t off[TL::kParts];
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+    using T = Tile<D>;
+#pragma unroll
+    for (int u = 0; u < TL::kParts; ++u) {
+      const int p = (u * NW + wave) * 64 + lane;
+      const int rho = p / T::kStride;
+      const int c = p - rho * T::kStride;
+      const int row = rho < ROWS ? perm16(rho) : 0;
+      off[u] = (uint32_t)(row * D + (c < T::kChunks ? c * 8 : 0)) * 2u;
+    }
+  }
+  // Largest valid offset for a tile starting at row r0 (r0 <= N - 1).
+  __device__ __forceinline__ static uint32_t limit(int r0, int N) {
+    return (uint32_t)((N - 1 - r0) * D + D - 8) * 2u;
+  }
+  template <bool CLAMP>
+  __device__ __forceinline__ void part(half_t* tile, const half_t* g, int r0, uint32_t lim,
+                                       int wave, int u) const {
+    const int inst = u * NW + wave;
+    if (EVEN || TL::kInsts % NW == 0 || inst < TL::kInsts) {
+      const uint32_t o = CLAMP ? min(off[u], lim) : off[u];
+      lds_direct16(tile + inst * 512,
+                   reinterpret_cast<const half_t*>(
+                       reinterpret_cast<const char*>(g + (size_t)r0 * D) + o));
+    }
+  }
+};
+
+template <int D, int ROWS, int NW, bool EVEN = false>
+__device__ __forceinline__ void tile_load(half_t* tile, const half_t* g, int r0, int N,
+                                          int wave, int lane) {
+  using TL = TileLoad<D, ROWS, NW, EVEN>;
+#pragma unroll
+  for (int u = 0; u < TL::kParts; ++u) TL::part(tile, g, r0, N, wave, lane, u);
 }
 
 // Global -> register -> LDS staging of a block of ROWS rows x D halves by a

@@ -28,12 +28,17 @@
 // K and V tiles move from global memory straight into double-buffered,
 // padded, row-permuted LDS tiles (global_load_lds_dwordx4), so staging costs
 // no registers and no LDS store instructions, and every LDS read address is a
-// per-lane base plus an immediate.
+// per-lane base plus an immediate. The next stage's load instructions leave
+// a few at a time between the current stage's products: issued all at once,
+// they stall every wave until the memory pipeline (64 B/clk per CU) has
+// accepted them.
 //
 // Causal tiles past the diagonal are never loaded (flash_fwd.cuh:127-130);
 // diagonal and ragged tiles take a separate masked path (flash_fwd.cuh:
 // 226-243). Outputs: O (fp16) and LSE = m + log(l) in natural-log units of
 // the scaled logits (flash_fwd.cuh:321-339).
+#include <type_traits>
+
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -56,6 +61,12 @@ struct FwdLds {
   static constexpr int kMLBytes = kWaves * 64 * 8;        // (m, l) per lane
   static constexpr int kBytes =
       (kStageBytes > kPartBytes ? kStageBytes : kPartBytes) + kMLBytes;
+  // Load instructions per wave and tile that every wave issues inside the
+  // step; the remaining kInsts % kWaves go out at the start of the step.
+  using TL = TileLoad<D, kKV, kWaves>;
+  static constexpr int kEvenParts = TL::kInsts / kWaves;
+  static constexpr int kIssueSlots = D / 16 + D / 32;
+  static_assert(2 * kEvenParts <= kIssueSlots, "more loads than issue points");
 };
 
 template <int D, bool CAUSAL, bool BOUNDS>
@@ -66,15 +77,18 @@ struct FwdWave {
   float m_raw;  // running max of the raw (unscaled) logits; -inf before any key
   float l;      // this lane's partial row sum of p (its 16 of every 32 keys)
 
-  template <bool MASK>
+  // `issue(s)` is called at issue points s = 0 .. D/16 + D/32 - 1.
+  template <bool MASK, class Issue>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int kq, int j0,
                                        int i_row, int N, int lane, int roff, int troff, float c,
-                                       float thr_raw) {
+                                       float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = zero16();
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk)
+    for (int kk = 0; kk < D / 16; ++kk) {
       s = mfma32(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], s);
+      issue(kk);
+    }
     if constexpr (MASK) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -109,8 +123,10 @@ struct FwdWave {
 #pragma unroll
     for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
+      for (int q = 0; q < 2; ++q) {
         oacc[cb] = mfma32(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, troff), pb[q], oacc[cb]);
+        if (2 * cb + q < D / 32) issue(D / 16 + 2 * cb + q);
+      }
   }
 };
 
@@ -120,7 +136,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          float* __restrict__ Lse, int N, int qtile,
                                          float c, float thr_raw, half_t* smem) {
   using L = FwdLds<D>;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
   const int h = lane >> 5, l32 = lane & 31;
   const int rb = wave & 1, kq = wave >> 1;
   const int q0 = qtile * kBR;
@@ -140,29 +157,55 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
 
   const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
   const int n_it = (kv_end + kKV - 1) / kKV;
+  // Leading steps in which this wave's 32x32 block needs no mask. The later
+  // ones run masked; blocks wholly past the diagonal or past N give exact
+  // zeros there (their few products are not skipped, so every wave issues its
+  // share of the loads inside the same code).
+  int n_full = n_it;
+  if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
+  if (BOUNDS) n_full = min(n_full, N - 32 - kq * 32 >= 0 ? (N - 32 - kq * 32) / kKV + 1 : 0);
 
-  tile_load<D, kKV, kWaves>(smem, K, 0, N, wave, lane);
-  tile_load<D, kKV, kWaves>(smem + L::kTileHalves, V, 0, N, wave, lane);
+  using TL = typename L::TL;
+  TilePlan<D, kKV, kWaves, false> plan;
+  plan.init(wave, lane);
+  {
+    const uint32_t lim = plan.limit(0, N);
+#pragma unroll
+    for (int u = 0; u < TL::kParts; ++u) {
+      plan.template part<BOUNDS>(smem, K, 0, lim, wave, u);
+      plan.template part<BOUNDS>(smem + L::kTileHalves, V, 0, lim, wave, u);
+    }
+  }
   wait_vmem();
   __syncthreads();
-  for (int it = 0; it < n_it; ++it) {
-    if (it + 1 < n_it) {
-      half_t* nb = smem + ((it + 1) & 1) * L::kStageHalves;
-      tile_load<D, kKV, kWaves>(nb, K, (it + 1) * kKV, N, wave, lane);
-      tile_load<D, kKV, kWaves>(nb + L::kTileHalves, V, (it + 1) * kKV, N, wave, lane);
+
+  // One step over stage `it`; the last step re-fetches its own stage into the
+  // idle buffer, so every step issues the same loads.
+  auto run = [&](int it, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    half_t* nb = smem + ((it + 1) & 1) * L::kStageHalves;
+    const int jn = min(it + 1, n_it - 1) * kKV;
+    const uint32_t lim = plan.limit(jn, N);
+    if (L::kEvenParts < TL::kParts && wave < TL::kInsts % kWaves) {
+      plan.template part<BOUNDS>(nb, K, jn, lim, wave, L::kEvenParts);
+      plan.template part<BOUNDS>(nb + L::kTileHalves, V, jn, lim, wave, L::kEvenParts);
     }
+    auto issue = [&](int s) {
+      if (s < 2 * L::kEvenParts) {
+        if (s & 1) plan.template part<BOUNDS>(nb + L::kTileHalves, V, jn, lim, wave, s >> 1);
+        else plan.template part<BOUNDS>(nb, K, jn, lim, wave, s >> 1);
+      }
+    };
     const half_t* Ks = smem + (it & 1) * L::kStageHalves;
     const half_t* Vs = Ks + L::kTileHalves;
-    const int j0 = it * kKV + kq * 32;
-    const bool active = j0 < kv_end && (!CAUSAL || j0 <= i_base + 31);
-    if (active) {
-      const bool mask = (CAUSAL && j0 + 31 > i_base) || (BOUNDS && j0 + 32 > N);
-      if (mask) w.template step<true>(Ks, Vs, kq, j0, i_row, N, lane, roff, troff, c, thr_raw);
-      else w.template step<false>(Ks, Vs, kq, j0, i_row, N, lane, roff, troff, c, thr_raw);
-    }
+    w.template step<MASK>(Ks, Vs, kq, it * kKV + kq * 32, i_row, N, lane, roff, troff, c,
+                          thr_raw, issue);
     wait_vmem();
     __syncthreads();
-  }
+  };
+  int it = 0;
+  for (; it < n_full; ++it) run(it, std::false_type{});
+  for (; it < n_it; ++it) run(it, std::true_type{});
 
   // Merge the four key quarters of each row block through LDS.
   float* part = reinterpret_cast<float*>(smem);
