@@ -47,6 +47,8 @@
 // every iteration. Dead lanes (causal col > row, ragged rows/cols >= N)
 // contribute exactly zero (flash_bwd.cuh:267-282). P and dS are rounded to
 // fp16 only as MFMA operands.
+#include <type_traits>
+
 #include "fa_device.h"
 #include "fa_launch.h"
 
@@ -58,16 +60,18 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 128;  // rows a workgroup owns (keys in phase 1, queries in phase 2)
 constexpr int kSub = 64;    // rows per streamed tile (queries in 1, keys in 2)
 
+// LDS: every tile is its own __shared__ object (declared in bwd_kernel), so
+// the compiler can tell that a step's reads never touch the tiles that the
+// next step's direct loads are filling and does not wait for those loads.
 template <int D>
 struct BwdLds {
-  static constexpr int kTileHalves = Tile<D>::template halves<kSub>();
-  static constexpr int kStageHalves = 2 * kTileHalves + 2 * kSub * 2;  // 2 tiles + lse2, dvec
-  // Phase 1 also keeps the workgroup's K and V rows (kTile each) resident.
-  static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();
-  static constexpr int kBytes = (2 * kStageHalves + 2 * kKVTileHalves) * 2;
-  // Partial-sum exchange (reuses the stages and the K/V area): 4 waves x
-  // 2*D/32 accumulators of 16 floats per lane.
-  static_assert(4 * 2 * (D / 32) * 16 * 64 * 4 <= kBytes, "merge area exceeds the LDS budget");
+  static constexpr int kTileHalves = Tile<D>::template halves<kSub>();     // staged tile
+  static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();  // resident K or V
+  // Partial-sum exchange regions (they reuse the tiles once a phase's loop is
+  // done): D/32 accumulators x 16 floats per lane for one wave.
+  static constexpr int kRegionBytes = (D / 32) * 16 * 64 * 4;
+  static_assert(kRegionBytes <= kTileHalves * 2 && 2 * kRegionBytes <= kKVTileHalves * 2,
+                "exchange regions exceed the tiles");
 };
 
 // ---------------------------------------------------------------------------
@@ -100,38 +104,37 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
   }
 }
 
-// Direct load of 64 consecutive floats (rows r0 .. r0+63, clamped to N-1).
-__device__ __forceinline__ void vec_load64(float* lds, const float* g, int r0, int N, int lane) {
-  const int r = min(r0 + lane, N - 1);
-  __builtin_amdgcn_global_load_lds((const void*)(g + r),
-                                   (__attribute__((address_space(3))) void*)lds, 4, 0, 0);
+// Direct load of 64 consecutive floats (rows r0 .. r0+63 of a per-row
+// vector; rows past its end read as zeros).
+__device__ __forceinline__ void vec_load64(float* lds, rsrc_t r, int r0, int lane) {
+  lds_direct_buf<4>(lds, r, (uint32_t)lane * 4u, (uint32_t)r0 * 4u);
 }
 
 // Exchange of per-wave accumulators: waves of the upper half (w >= 4) store
-// theirs, waves w-4 add them. `acc` holds n accumulators; layout
-// [w % 4][k][g4][lane] x 4 floats, bank-conflict-free 16-byte accesses.
-template <int n>
-__device__ __forceinline__ void partial_store(float* buf, const floatx16 (&acc)[n], int w4,
+// accumulators [k0, k0 + n) into a region, waves w-4 add them. Layout
+// [k][g4][lane] x 4 floats, bank-conflict-free 16-byte accesses.
+template <int n, int N_ACC>
+__device__ __forceinline__ void partial_store(float* region, const floatx16 (&acc)[N_ACC], int k0,
                                               int lane) {
 #pragma unroll
   for (int k = 0; k < n; ++k)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const floatx4 v = {acc[k][4 * g4], acc[k][4 * g4 + 1], acc[k][4 * g4 + 2], acc[k][4 * g4 + 3]};
-      *reinterpret_cast<floatx4*>(buf + (((w4 * n + k) * 4 + g4) * 64 + lane) * 4) = v;
+      const floatx16& a = acc[k0 + k];
+      const floatx4 v = {a[4 * g4], a[4 * g4 + 1], a[4 * g4 + 2], a[4 * g4 + 3]};
+      *reinterpret_cast<floatx4*>(region + ((k * 4 + g4) * 64 + lane) * 4) = v;
     }
 }
-template <int n>
-__device__ __forceinline__ void partial_add(const float* buf, floatx16 (&acc)[n], int w4,
+template <int n, int N_ACC>
+__device__ __forceinline__ void partial_add(const float* region, floatx16 (&acc)[N_ACC], int k0,
                                             int lane) {
 #pragma unroll
   for (int k = 0; k < n; ++k)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
-      const floatx4 v =
-          *reinterpret_cast<const floatx4*>(buf + (((w4 * n + k) * 4 + g4) * 64 + lane) * 4);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(region + ((k * 4 + g4) * 64 + lane) * 4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[k][4 * g4 + e] += v[e];
+      for (int e = 0; e < 4; ++e) acc[k0 + k][4 * g4 + e] += v[e];
     }
 }
 
@@ -236,12 +239,16 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     float* __restrict__ dQ, half_t* __restrict__ dK, half_t* __restrict__ dV,
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2) {
   using L = BwdLds<D>;
-  extern __shared__ __align__(16) half_t smem[];
-  float* xbuf = reinterpret_cast<float*>(smem);  // partial-sum exchange area
+  // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
+  __shared__ __align__(16) half_t ta0[L::kTileHalves], tb0[L::kTileHalves];
+  __shared__ __align__(16) half_t ta1[L::kTileHalves], tb1[L::kTileHalves];
+  __shared__ __align__(16) float vec0[2 * kSub], vec1[2 * kSub];
+  __shared__ __align__(16) half_t kres[L::kKVTileHalves], vres[L::kKVTileHalves];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
+  __builtin_assume(wave >= 0 && wave < kWaves);
   const int w4 = wave & 3;     // row block (keys in phase 1, queries in phase 2)
   const int half = wave >> 2;  // which 32-row half of each streamed tile
   const int h = lane >> 5;
@@ -254,21 +261,37 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
   const size_t kv_off = (size_t)bkv * N * D;
-  const half_t* Kh = K + kv_off;
-  const half_t* Vh = V + kv_off;
-
-  auto stage_ptr = [&](int st) { return smem + st * L::kStageHalves; };
+  const uint32_t head_bytes = (uint32_t)N * D * 2;
+  const rsrc_t rk = make_rsrc(K + kv_off, head_bytes), rv = make_rsrc(V + kv_off, head_bytes);
   const int roff = row_lane_off<D>(lane), troff = tr_lane_off<D>(lane);
+
+  TilePlan<D, kSub, kWaves, false> plan;  // staged 64-row tiles
+  plan.init(wave, lane);
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  // 16 KB-class exchange regions: the four staged tiles, then the halves of
+  // the resident ones.
+  auto region = [&](int i) -> float* {
+    half_t* t = i == 0 ? ta0 : i == 1 ? tb0 : i == 2 ? ta1 : i == 3 ? tb1
+              : i == 4 ? kres : i == 5 ? kres + L::kKVTileHalves / 2
+              : i == 6 ? vres : vres + L::kKVTileHalves / 2;
+    return reinterpret_cast<float*>(t);
+  };
 
   // =========================== phase 1: dK, dV ===========================
   {
     const int jw = t0 + w4 * 32;  // this wave's key rows
     const int j_col = jw + l32;
     KVWave<D, CAUSAL, BOUNDS> w;
-    half_t* Kt = smem + 2 * L::kStageHalves;  // resident K, V rows t0 .. t0+kTile-1
-    half_t* Vt = Kt + L::kKVTileHalves;
-    tile_load<D, kTile, kWaves>(Kt, Kh, t0, N, wave, lane);
-    tile_load<D, kTile, kWaves>(Vt, Vh, t0, N, wave, lane);
+    {
+      TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows t0 .. t0+kTile-1
+      plan_kv.init(wave, lane);
+#pragma unroll
+      for (int u = 0; u < decltype(plan_kv)::TL::kParts; ++u) {
+        plan_kv.part(kres, rk, t0, wave, u);
+        plan_kv.part(vres, rv, t0, wave, u);
+      }
+    }
 #pragma unroll
     for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
 
@@ -276,42 +299,60 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int n_qt = (N - i_start + kSub - 1) / kSub;
     const int n_it = group * n_qt;  // (query head, query tile) pairs, flattened
 
-    auto fetch = [&](int it, half_t* st) {
+    // Q, dO tiles and lse2, dvec of flattened step `it` (clamped to the last
+    // one, so that every step issues the same loads) into one stage.
+    auto fetch = [&](int it, half_t* tq, half_t* to, float* tv) {
+      it = min(it, n_it - 1);
       const int g = it / n_qt;
       const int i0 = i_start + (it % n_qt) * kSub;
       const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
-      tile_load<D, kSub, kWaves>(st, Q + bhq * N * D, i0, N, wave, lane);
-      tile_load<D, kSub, kWaves>(st + L::kTileHalves, dO + bhq * N * D, i0, N, wave, lane);
-      float* fv = reinterpret_cast<float*>(st + 2 * L::kTileHalves);
-      if (wave == 0) vec_load64(fv, Lse2 + bhq * N, i0, N, lane);
-      if (wave == 1) vec_load64(fv + kSub, Dvec + bhq * N, i0, N, lane);
+      const rsrc_t rq = make_rsrc(Q + bhq * N * D, head_bytes);
+      const rsrc_t ro = make_rsrc(dO + bhq * N * D, head_bytes);
+#pragma unroll
+      for (int u = 0; u < decltype(plan)::TL::kParts; ++u) {
+        plan.part(tq, rq, i0, wave, u);
+        plan.part(to, ro, i0, wave, u);
+      }
+      if (wave == 0) vec_load64(tv, make_rsrc(Lse2 + bhq * N, (uint32_t)N * 4), i0, lane);
+      if (wave == 1) vec_load64(tv + kSub, make_rsrc(Dvec + bhq * N, (uint32_t)N * 4), i0, lane);
     };
-
-    fetch(0, stage_ptr(0));
-    wait_vmem();
-    __syncthreads();
-    for (int it = 0; it < n_it; ++it) {
+    // One step over the stage of parity P, while the next step's tiles load
+    // into the other stage.
+    auto step = [&](int it, auto par) {
+      constexpr int P = decltype(par)::value;
+      fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
+      const half_t* Qs = P ? ta1 : ta0;
+      const half_t* Os = P ? tb1 : tb0;
+      const float* lse2s = P ? vec1 : vec0;
       const int i0 = i_start + (it % n_qt) * kSub;
-      // The last iteration re-fetches its own tile into the idle buffer, so the
-      // loop body stays free of branches around the products.
-      fetch(min(it + 1, n_it - 1), stage_ptr((it + 1) & 1));
-      const half_t* Qs = stage_ptr(it & 1);
-      const half_t* Os = Qs + L::kTileHalves;
-      const float* lse2s = reinterpret_cast<const float*>(Os + L::kTileHalves);
-      const float* dvs = lse2s + kSub;
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
-      w.step(Qs, Os, lse2s, dvs, Kt, Vt, half, w4 * 32, i0, j_col, N, lane, roff, troff,
-             scale_log2);
+      w.step(Qs, Os, lse2s, lse2s + kSub, kres, vres, half, w4 * 32, i0, j_col, N, lane, roff,
+             troff, scale_log2);
       wait_vmem();
       __syncthreads();
-    }
+    };
 
-    // Sum the two halves' partials, then dK (scaled) and dV leave as fp16.
-    if (half) partial_store(xbuf, w.acc, w4, lane);
+    fetch(0, ta0, tb0, vec0);
+    wait_vmem();
+    __syncthreads();
+    int it = 0;
+    for (; it + 2 <= n_it; it += 2) {
+      step(it, P0{});
+      step(it + 1, P1{});
+    }
+    if (it < n_it) step(it, P0{});
+
+    // Sum the two halves' partials (dV^T in region 2*w4, dK^T in 2*w4 + 1),
+    // then dK (scaled) and dV leave as fp16.
+    if (half) {
+      partial_store<D / 32>(region(2 * w4), w.acc, 0, lane);
+      partial_store<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
+    }
     __syncthreads();
     if (!half) {
-      partial_add(xbuf, w.acc, w4, lane);
+      partial_add<D / 32>(region(2 * w4), w.acc, 0, lane);
+      partial_add<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
       if (!BOUNDS || j_col < N) {
         half_t* dkrow = dK + kv_off + (size_t)j_col * D;
         half_t* dvrow = dV + kv_off + (size_t)j_col * D;
@@ -331,7 +372,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         }
       }
     }
-    __syncthreads();  // the exchange area is the next phase's staging memory
+    __syncthreads();  // the exchange regions are the next phase's staging memory
   }
 
   // ============================== phase 2: dQ ==============================
@@ -357,29 +398,37 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
 #pragma unroll
       for (int cb = 0; cb < D / 32; ++cb) w.acc[cb] = zero16();
 
-      tile_load<D, kSub, kWaves>(stage_ptr(0), Kh, 0, N, wave, lane);
-      tile_load<D, kSub, kWaves>(stage_ptr(0) + L::kTileHalves, Vh, 0, N, wave, lane);
-      wait_vmem();
-      __syncthreads();
-      for (int t = 0; t < n_kt; ++t) {
-        const int j0 = t * kSub;
-        {
-          half_t* nb = stage_ptr((t + 1) & 1);
-          const int jn = min(t + 1, n_kt - 1) * kSub;  // last step: idle-buffer refetch
-          tile_load<D, kSub, kWaves>(nb, Kh, jn, N, wave, lane);
-          tile_load<D, kSub, kWaves>(nb + L::kTileHalves, Vh, jn, N, wave, lane);
+      // K, V tiles of key step t (clamped to the last one) into a stage.
+      auto fetch = [&](int t, half_t* tk, half_t* tv) {
+        const int jn = min(t, n_kt - 1) * kSub;
+#pragma unroll
+        for (int u = 0; u < decltype(plan)::TL::kParts; ++u) {
+          plan.part(tk, rk, jn, wave, u);
+          plan.part(tv, rv, jn, wave, u);
         }
-        const half_t* Ks = stage_ptr(t & 1);
-        const half_t* Vs = Ks + L::kTileHalves;
-        w.step(Ks, Vs, half, j0, i_row, N, lane, roff, troff, scale_log2);
+      };
+      auto step = [&](int t, auto par) {
+        constexpr int P = decltype(par)::value;
+        fetch(t + 1, P ? ta0 : ta1, P ? tb0 : tb1);
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, N, lane, roff, troff,
+               scale_log2);
         wait_vmem();
         __syncthreads();
+      };
+      fetch(0, ta0, tb0);
+      wait_vmem();
+      __syncthreads();
+      int t = 0;
+      for (; t + 2 <= n_kt; t += 2) {
+        step(t, P0{});
+        step(t + 1, P1{});
       }
+      if (t < n_kt) step(t, P0{});
 
-      if (half) partial_store(xbuf, w.acc, w4, lane);
+      if (half) partial_store<D / 32>(region(4 + w4), w.acc, 0, lane);
       __syncthreads();
       if (!half && row_ok) {
-        partial_add(xbuf, w.acc, w4, lane);
+        partial_add<D / 32>(region(4 + w4), w.acc, 0, lane);
         float* qrow = dQ + bhq * N * D + (size_t)i_row * D;
 #pragma unroll
         for (int cb = 0; cb < D / 32; ++cb) {
@@ -392,7 +441,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           }
         }
       }
-      __syncthreads();  // the exchange area is the next head's staging memory
+      __syncthreads();  // the exchange regions are the next head's staging memory
     }
   }
 }
@@ -411,11 +460,8 @@ template <int D, bool CAUSAL, bool BOUNDS>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
-  const size_t smem = BwdLds<D>::kBytes;
-  static const hipError_t attr = allow_lds(bwd_kernel<D, CAUSAL, BOUNDS>, smem);
-  if (attr != hipSuccess) return attr;
   const float scale = 1.f / sqrtf((float)D);
-  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), smem,
+  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,

@@ -189,6 +189,82 @@ __device__ __forceinline__ void lds_direct16(half_t* lds, const half_t* src) {
       (const void*)src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// Unpadded LDS tiles with an XOR chunk swizzle.
+//
+// Row r of a tile occupies 2*D contiguous bytes and keeps its 16-byte chunk c
+// at position c ^ g(r), where g permutes the low row bits:
+//   D = 128 (a row spans all 16 bank groups): g(r) = perm16(r & 15);
+//   D = 64 (two rows per 256 bytes): g(r) = ((r >> 1) & 1) << 2 | (r >> 2) & 3.
+// Then the 16-byte operand reads (16 consecutive rows at one chunk) and the
+// transpose reads (per half-wave: 4 consecutive rows at 4 consecutive chunks)
+// both hit 16 distinct bank groups, and a direct load covers whole rows
+// (1 KB = 1024 / (2D) rows per instruction, every lane fetching one chunk of
+// its row), which the memory pipeline serves about a quarter faster than the
+// padded pattern. The price is that the swizzle is not additive in the chunk
+// index, so each lane keeps one precomputed LDS offset per operand position.
+template <int D>
+struct Swz {
+  static constexpr int kChunks = D / 8;
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kRowsPerInst = 1024 / kRowBytes;
+  __host__ __device__ static constexpr int g(int r) {
+    return D == 128 ? perm16(r & 15) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+  }
+  template <int ROWS>
+  static constexpr int bytes() { return ROWS * kRowBytes; }
+
+  // Byte offset, within a tile whose rows start at a multiple of 16, of the
+  // 16-byte MFMA operand read of row (lane % 32), halves 16*kk + 8*(lane/32).
+  __device__ __forceinline__ static int rd_off(int lane, int kk) {
+    return (lane & 31) * kRowBytes + (((2 * kk) | (lane >> 5)) ^ g(lane & 15)) * 16;
+  }
+  // Byte offset of this lane's transpose read for the A operand of
+  // tr_operand(): d-block cb (columns 32cb ..), lo (hi = 0) or hi (hi = 1)
+  // row quad.
+  __device__ __forceinline__ static int tr_off(int lane, int cb, int hi) {
+    const int n = lane & 15, grp = lane >> 4, t = n >> 2, a = n & 3;
+    const int r = 4 * (grp >> 1) + t + 8 * hi;
+    const int x = 2 * (grp & 1) + (a >> 1);
+    return r * kRowBytes + ((4 * cb + x) ^ g(r)) * 16 + 8 * (a & 1);
+  }
+};
+
+// Direct-load plan for a swizzled tile of ROWS rows filled by NW waves: every
+// wave issues kParts 1 KB instructions (u = 0 .. kParts-1); the per-lane
+// global offset of part u is base + u * kStride, so one VGPR serves them all.
+template <int D, int ROWS, int NW>
+struct SwzPlan {
+  using S = Swz<D>;
+  static constexpr int kInsts = S::template bytes<ROWS>() / 1024;
+  static_assert(kInsts % NW == 0, "tile must split evenly over the waves");
+  static_assert((S::kRowsPerInst * NW) % 16 == 0, "swizzle must repeat across parts");
+  static constexpr int kParts = kInsts / NW;
+  static constexpr uint32_t kStride = (uint32_t)S::kRowsPerInst * NW * S::kRowBytes;
+  uint32_t base;
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+    const int r = S::kRowsPerInst * wave + lane / S::kChunks;  // row within part 0
+    base = (uint32_t)(r * S::kRowBytes + ((lane % S::kChunks) ^ S::g(r)) * 16);
+  }
+  // Largest valid offset for a tile starting at row r0 (r0 <= N - 1).
+  __device__ __forceinline__ static uint32_t limit(int r0, int N) {
+    return (uint32_t)((N - 1 - r0) * S::kRowBytes + S::kRowBytes - 16);
+  }
+  // Part u of the load of rows r0 .. r0+ROWS-1 of g into `tile`. With CLAMP,
+  // rows >= N receive a copy of row N-1's last chunk (finite data the kernels
+  // mask).
+  template <bool CLAMP>
+  __device__ __forceinline__ void part(char* tile, const half_t* g, int r0, uint32_t lim,
+                                       int wave, int u) const {
+    uint32_t o = base + (uint32_t)u * kStride;
+    if (CLAMP) o = min(o, lim);
+    lds_direct16(reinterpret_cast<half_t*>(tile + (u * NW + wave) * 1024),
+                 reinterpret_cast<const half_t*>(
+                     reinterpret_cast<const char*>(g + (size_t)r0 * D) + o));
+  }
+};
+
 // Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -225,12 +301,37 @@ struct TileLoad {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Direct global -> LDS loads through a buffer resource (buffer_load ... lds).
+// The resource (base, size in bytes) lives in scalar registers; a load is one
+// per-lane 32-bit VGPR offset plus a scalar offset, so a kernel can keep the
+// per-lane offsets in registers that nothing else ever overwrites, and
+// accesses at or past the resource's size return zeros (no clamping needed).
+// Keeping address registers untouched matters: the compiler treats an
+// LDS-DMA instruction's VGPR operands like store data and waits for the load
+// to complete before such a register is reused.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcWord3);
+}
+// Each lane loads `size` bytes (4 or 16) from voff + soff into LDS at
+// lds + size * lane (lds wave-uniform).
+template <int size>
+__device__ __forceinline__ void lds_direct_buf(void* lds, rsrc_t r, uint32_t voff, uint32_t soff) {
+  static_assert(size == 4 || size == 16, "LDS direct loads of 4 or 16 bytes per lane");
+  if constexpr (size == 16)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                             voff, soff, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+                                             voff, soff, 0, 0);
+}
+
 // Per-lane byte offsets of a wave's TileLoad instructions relative to the
 // tile's first row. They do not depend on the stage, so a kernel computes
-// them once and each load is then a scalar base plus one VGPR offset.
-// Padding instructions (EVEN) read the tile's first row. With CLAMP, offsets
-// past `lim` (the last chunk of row N - 1) are clamped to it, so rows >= N
-// hold finite copies of that chunk, which the kernels mask.
+// them once and each load is then a scalar offset plus one VGPR offset.
+// Padding instructions (EVEN) read the tile's first row.
 template <int D, int ROWS, int NW, bool EVEN>
 struct TilePlan {
   using TL = TileLoad<D, ROWS, NW, EVEN>;
@@ -247,20 +348,12 @@ struct TilePlan {
       off[u] = (uint32_t)(row * D + (c < T::kChunks ? c * 8 : 0)) * 2u;
     }
   }
-  // Largest valid offset for a tile starting at row r0 (r0 <= N - 1).
-  __device__ __forceinline__ static uint32_t limit(int r0, int N) {
-    return (uint32_t)((N - 1 - r0) * D + D - 8) * 2u;
-  }
-  template <bool CLAMP>
-  __device__ __forceinline__ void part(half_t* tile, const half_t* g, int r0, uint32_t lim,
-                                       int wave, int u) const {
+  // Loads part u of the tile whose first row is r0 from the (row-major, D
+  // halves per row) buffer `r`; rows past the buffer's end read as zeros.
+  __device__ __forceinline__ void part(half_t* tile, rsrc_t r, int r0, int wave, int u) const {
     const int inst = u * NW + wave;
-    if (EVEN || TL::kInsts % NW == 0 || inst < TL::kInsts) {
-      const uint32_t o = CLAMP ? min(off[u], lim) : off[u];
-      lds_direct16(tile + inst * 512,
-                   reinterpret_cast<const half_t*>(
-                       reinterpret_cast<const char*>(g + (size_t)r0 * D) + o));
-    }
+    if (EVEN || TL::kInsts % NW == 0 || inst < TL::kInsts)
+      lds_direct_buf<16>(tile + inst * 512, r, off[u], (uint32_t)r0 * (uint32_t)(2 * D));
   }
 };
 

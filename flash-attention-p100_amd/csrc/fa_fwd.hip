@@ -55,12 +55,10 @@ template <int D>
 struct FwdLds {
   static constexpr int kTileHalves = Tile<D>::template halves<kKV>();  // one K or V tile
   static constexpr int kStageHalves = 2 * kTileHalves; // K + V
-  static constexpr int kStageBytes = 2 * kStageHalves * 2;
-  // Merge area (reuses the stages): per wave, D/32 x 16 floats per lane.
-  static constexpr int kPartBytes = kWaves * 64 * D * 2;  // D/32*16 = D/2 floats/lane
-  static constexpr int kMLBytes = kWaves * 64 * 8;        // (m, l) per lane
-  static constexpr int kBytes =
-      (kStageBytes > kPartBytes ? kStageBytes : kPartBytes) + kMLBytes;
+  // Merge area (reuses the four tiles, two waves each): per wave, D/32 x 16
+  // floats per lane.
+  static_assert(2 * 64 * D * 2 <= kTileHalves * 2, "merge area exceeds a tile");
+  static constexpr int kMLFloat2 = kWaves * 64;  // (m, l) per lane
   // Load instructions per wave and tile that every wave issues inside the
   // step; the remaining kInsts % kWaves go out at the start of the step.
   using TL = TileLoad<D, kKV, kWaves>;
@@ -134,10 +132,12 @@ template <int D, bool CAUSAL, bool BOUNDS>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int qtile,
-                                         float c, float thr_raw, half_t* smem) {
+                                         float c, float thr_raw, half_t* kt0, half_t* vt0,
+                                         half_t* kt1, half_t* vt1, float2* ml) {
   using L = FwdLds<D>;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
+  __builtin_assume(wave >= 0 && wave < kWaves);
   const int h = lane >> 5, l32 = lane & 31;
   const int rb = wave & 1, kq = wave >> 1;
   const int q0 = qtile * kBR;
@@ -168,57 +168,75 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   using TL = typename L::TL;
   TilePlan<D, kKV, kWaves, false> plan;
   plan.init(wave, lane);
-  {
-    const uint32_t lim = plan.limit(0, N);
+  const rsrc_t rk = make_rsrc(K, (uint32_t)N * D * 2), rv = make_rsrc(V, (uint32_t)N * D * 2);
 #pragma unroll
-    for (int u = 0; u < TL::kParts; ++u) {
-      plan.template part<BOUNDS>(smem, K, 0, lim, wave, u);
-      plan.template part<BOUNDS>(smem + L::kTileHalves, V, 0, lim, wave, u);
-    }
+  for (int u = 0; u < TL::kParts; ++u) {
+    plan.part(kt0, rk, 0, wave, u);
+    plan.part(vt0, rv, 0, wave, u);
   }
   wait_vmem();
   __syncthreads();
 
-  // One step over stage `it`; the last step re-fetches its own stage into the
-  // idle buffer, so every step issues the same loads.
-  auto run = [&](int it, auto mask_tag) {
+  // One step over stage `it` (its buffer parity P is a compile-time constant:
+  // the K and V tiles of both stages are distinct LDS objects, so the
+  // compiler can tell that this step's reads never touch the tiles the next
+  // stage's direct loads are filling, and does not wait for those loads
+  // before them). The last step re-fetches its own stage into the idle
+  // buffers, so every step issues the same loads.
+  auto run = [&](int it, auto par_tag, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
-    half_t* nb = smem + ((it + 1) & 1) * L::kStageHalves;
+    constexpr int P = decltype(par_tag)::value;
+    half_t* nk = P ? kt0 : kt1;
+    half_t* nv = P ? vt0 : vt1;
     const int jn = min(it + 1, n_it - 1) * kKV;
-    const uint32_t lim = plan.limit(jn, N);
     if (L::kEvenParts < TL::kParts && wave < TL::kInsts % kWaves) {
-      plan.template part<BOUNDS>(nb, K, jn, lim, wave, L::kEvenParts);
-      plan.template part<BOUNDS>(nb + L::kTileHalves, V, jn, lim, wave, L::kEvenParts);
+      plan.part(nk, rk, jn, wave, L::kEvenParts);
+      plan.part(nv, rv, jn, wave, L::kEvenParts);
     }
     auto issue = [&](int s) {
       if (s < 2 * L::kEvenParts) {
-        if (s & 1) plan.template part<BOUNDS>(nb + L::kTileHalves, V, jn, lim, wave, s >> 1);
-        else plan.template part<BOUNDS>(nb, K, jn, lim, wave, s >> 1);
+        if (s & 1) plan.part(nv, rv, jn, wave, s >> 1);
+        else plan.part(nk, rk, jn, wave, s >> 1);
       }
     };
-    const half_t* Ks = smem + (it & 1) * L::kStageHalves;
-    const half_t* Vs = Ks + L::kTileHalves;
+    const half_t* Ks = P ? kt1 : kt0;
+    const half_t* Vs = P ? vt1 : vt0;
     w.template step<MASK>(Ks, Vs, kq, it * kKV + kq * 32, i_row, N, lane, roff, troff, c,
                           thr_raw, issue);
     wait_vmem();
     __syncthreads();
   };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   int it = 0;
-  for (; it < n_full; ++it) run(it, std::false_type{});
-  for (; it < n_it; ++it) run(it, std::true_type{});
+  for (; it + 2 <= n_full; it += 2) {
+    run(it, P0{}, std::false_type{});
+    run(it + 1, P1{}, std::false_type{});
+  }
+  for (; it < n_it; ++it) {
+    const bool masked = it >= n_full;
+    if (it & 1) {
+      if (masked) run(it, P1{}, std::true_type{});
+      else run(it, P1{}, std::false_type{});
+    } else {
+      if (masked) run(it, P0{}, std::true_type{});
+      else run(it, P0{}, std::false_type{});
+    }
+  }
 
-  // Merge the four key quarters of each row block through LDS.
-  float* part = reinterpret_cast<float*>(smem);
-  float2* ml = reinterpret_cast<float2*>(reinterpret_cast<char*>(smem) +
-                                         (L::kStageBytes > L::kPartBytes ? L::kStageBytes
-                                                                         : L::kPartBytes));
+  // Merge the four key quarters of each row block through LDS: each of the
+  // four tiles holds the partials of two waves.
+  auto part_of = [&](int src) {
+    half_t* t = src < 2 ? kt0 : src < 4 ? vt0 : src < 6 ? kt1 : vt1;
+    return reinterpret_cast<float*>(t) + (src & 1) * (D / 8) * 64 * 4;
+  };
 #pragma unroll
   for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       floatx4 v = {w.oacc[cb][4 * g], w.oacc[cb][4 * g + 1], w.oacc[cb][4 * g + 2],
                    w.oacc[cb][4 * g + 3]};
-      *reinterpret_cast<floatx4*>(part + ((wave * (D / 8) + cb * 4 + g) * 64 + lane) * 4) = v;
+      *reinterpret_cast<floatx4*>(part_of(wave) + ((cb * 4 + g) * 64 + lane) * 4) = v;
     }
   ml[wave * 64 + lane] = make_float2(w.m_raw, w.l);
   __syncthreads();
@@ -253,7 +271,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
         for (int k = 0; k < 4; ++k) {
           const int src = k * 2 + rb;
           const floatx4 v =
-              *reinterpret_cast<const floatx4*>(part + ((src * (D / 8) + cb * 4 + g) * 64 + lane) * 4);
+              *reinterpret_cast<const floatx4*>(part_of(src) + ((cb * 4 + g) * 64 + lane) * 4);
           acc += v * wk[k];
         }
         half4 o4;
@@ -272,7 +290,13 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2) {
-  extern __shared__ __align__(16) half_t smem[];
+  // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
+  // (m, l).
+  __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
+  __shared__ __align__(16) half_t vt0[FwdLds<D>::kTileHalves];
+  __shared__ __align__(16) half_t kt1[FwdLds<D>::kTileHalves];
+  __shared__ __align__(16) half_t vt1[FwdLds<D>::kTileHalves];
+  __shared__ float2 ml[FwdLds<D>::kMLFloat2];
   const int w = xcd_work_index(gx * BH);
   if (w < 0) return;
   const int bh = w / gx;       // over B*Hq
@@ -284,12 +308,12 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const size_t kv_off = ((size_t)b * Hkv + hkv) * N * D;
   const float thr_raw = kRescaleLog2 / scale_log2;
   fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off, Lse + (size_t)bh * N,
-                              N, first, scale_log2, thr_raw, smem);
+                              N, first, scale_log2, thr_raw, kt0, vt0, kt1, vt1, ml);
   if (CAUSAL) {
     const int second = n_qtiles - 1 - first;
     if (second > first)
       fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                  Lse + (size_t)bh * N, N, second, scale_log2, thr_raw, smem);
+                                  Lse + (size_t)bh * N, N, second, scale_log2, thr_raw, kt0, vt0, kt1, vt1, ml);
   }
 }
 
@@ -299,12 +323,8 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
   const int BH = a.B * a.Hq;
   dim3 grid(xcd_grid(gx * BH));
-  const size_t smem = FwdLds<D>::kBytes;
   const float scale_log2 = kLog2e / sqrtf((float)D);
-  // One-time, idempotent: lift the dynamic-LDS cap above the 64 KB default.
-  static const hipError_t attr = allow_lds(fwd_kernel<D, CAUSAL, BOUNDS>, smem);
-  if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), smem,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2);
