@@ -23,7 +23,6 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -52,26 +51,6 @@ __device__ __forceinline__ half8 as_half8(u32x4 v) {
   return __builtin_bit_cast(half8, v);
 }
 
-// Low halves of x and y packed as (x.lo, y.lo); likewise for high halves.
-__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
-  return __builtin_amdgcn_perm(y, x, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
-  return __builtin_amdgcn_perm(y, x, 0x07060302u);
-}
-
-// Transposes a 4-row x 8-column block of halves held as four 16-byte rows
-// into eight 4-element columns: col[c] = (r0[c], r1[c], r2[c], r3[c]).
-__device__ __forceinline__ void transpose_4x8(const u32x4 (&rows)[4], u32x2 (&cols)[8]) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    cols[2 * w][0] = pack_lo(rows[0][w], rows[1][w]);
-    cols[2 * w][1] = pack_lo(rows[2][w], rows[3][w]);
-    cols[2 * w + 1][0] = pack_hi(rows[0][w], rows[1][w]);
-    cols[2 * w + 1][1] = pack_hi(rows[2][w], rows[3][w]);
-  }
-}
-
 // Swap with the lane 32 positions away (the other half of the wave).
 __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
 
@@ -85,22 +64,6 @@ typedef __attribute__((address_space(3))) short4v lds_short4;
 __device__ __forceinline__ half4 lds_read_tr(const half_t* p) {
   const short4v v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(p));
   return __builtin_bit_cast(half4, v);
-}
-
-// MFMA A operand of a product whose K index runs over the ROWS of a row-major
-// LDS tile (row stride `stride` halves): lane (l32, h) receives column
-// c0 + l32 at the 8 rows rbase + 8*(e/4) + 4h + e%4, e = 0..7. That row order
-// is the one in which a 32x32 accumulator's registers r = 8q..8q+7 enumerate
-// their rows (rbase = 16q), so such an accumulator, converted to fp16, is the
-// matching B operand without any data movement.
-__device__ __forceinline__ half8 tr_operand(const half_t* tile, int stride, int rbase, int c0,
-                                            int lane) {
-  const int n = lane & 15, grp = lane >> 4;
-  const int row = rbase + 4 * (grp >> 1) + (n >> 2);
-  const int col = c0 + 16 * (grp & 1) + 4 * (n & 3);
-  const half4 lo = lds_read_tr(tile + row * stride + col);
-  const half4 hi = lds_read_tr(tile + (row + 8) * stride + col);
-  return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
 // ---------------------------------------------------------------------------
@@ -182,125 +145,6 @@ __device__ __forceinline__ half8 tile_tr_operand(const half_t* tile, int rbase, 
   return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// One wave copies 1 KB (64 lanes x 16 B) from global memory straight into LDS
-// at `lds` (wave-uniform), lane l landing at lds + 16*l bytes.
-__device__ __forceinline__ void lds_direct16(half_t* lds, const half_t* src) {
-  __builtin_amdgcn_global_load_lds(
-      (const void*)src, (__attribute__((address_space(3))) void*)lds, 16, 0, 0);
-}
-
-// ---------------------------------------------------------------------------
-// Unpadded LDS tiles with an XOR chunk swizzle.
-//
-// Row r of a tile occupies 2*D contiguous bytes and keeps its 16-byte chunk c
-// at position c ^ g(r), where g permutes the low row bits:
-//   D = 128 (a row spans all 16 bank groups): g(r) = perm16(r & 15);
-//   D = 64 (two rows per 256 bytes): g(r) = ((r >> 1) & 1) << 2 | (r >> 2) & 3.
-// Then the 16-byte operand reads (16 consecutive rows at one chunk) and the
-// transpose reads (per half-wave: 4 consecutive rows at 4 consecutive chunks)
-// both hit 16 distinct bank groups, and a direct load covers whole rows
-// (1 KB = 1024 / (2D) rows per instruction, every lane fetching one chunk of
-// its row), which the memory pipeline serves about a quarter faster than the
-// padded pattern. The price is that the swizzle is not additive in the chunk
-// index, so each lane keeps one precomputed LDS offset per operand position.
-template <int D>
-struct Swz {
-  static constexpr int kChunks = D / 8;
-  static constexpr int kRowBytes = 2 * D;
-  static constexpr int kRowsPerInst = 1024 / kRowBytes;
-  __host__ __device__ static constexpr int g(int r) {
-    return D == 128 ? perm16(r & 15) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
-  }
-  template <int ROWS>
-  static constexpr int bytes() { return ROWS * kRowBytes; }
-
-  // Byte offset, within a tile whose rows start at a multiple of 16, of the
-  // 16-byte MFMA operand read of row (lane % 32), halves 16*kk + 8*(lane/32).
-  __device__ __forceinline__ static int rd_off(int lane, int kk) {
-    return (lane & 31) * kRowBytes + (((2 * kk) | (lane >> 5)) ^ g(lane & 15)) * 16;
-  }
-  // Byte offset of this lane's transpose read for the A operand of
-  // tr_operand(): d-block cb (columns 32cb ..), lo (hi = 0) or hi (hi = 1)
-  // row quad.
-  __device__ __forceinline__ static int tr_off(int lane, int cb, int hi) {
-    const int n = lane & 15, grp = lane >> 4, t = n >> 2, a = n & 3;
-    const int r = 4 * (grp >> 1) + t + 8 * hi;
-    const int x = 2 * (grp & 1) + (a >> 1);
-    return r * kRowBytes + ((4 * cb + x) ^ g(r)) * 16 + 8 * (a & 1);
-  }
-};
-
-// Direct-load plan for a swizzled tile of ROWS rows filled by NW waves: every
-// wave issues kParts 1 KB instructions (u = 0 .. kParts-1); the per-lane
-// global offset of part u is base + u * kStride, so one VGPR serves them all.
-template <int D, int ROWS, int NW>
-struct SwzPlan {
-  using S = Swz<D>;
-  static constexpr int kInsts = S::template bytes<ROWS>() / 1024;
-  static_assert(kInsts % NW == 0, "tile must split evenly over the waves");
-  static_assert((S::kRowsPerInst * NW) % 16 == 0, "swizzle must repeat across parts");
-  static constexpr int kParts = kInsts / NW;
-  static constexpr uint32_t kStride = (uint32_t)S::kRowsPerInst * NW * S::kRowBytes;
-  uint32_t base;
-
-  __device__ __forceinline__ void init(int wave, int lane) {
-    const int r = S::kRowsPerInst * wave + lane / S::kChunks;  // row within part 0
-    base = (uint32_t)(r * S::kRowBytes + ((lane % S::kChunks) ^ S::g(r)) * 16);
-  }
-  // Largest valid offset for a tile starting at row r0 (r0 <= N - 1).
-  __device__ __forceinline__ static uint32_t limit(int r0, int N) {
-    return (uint32_t)((N - 1 - r0) * S::kRowBytes + S::kRowBytes - 16);
-  }
-  // Part u of the load of rows r0 .. r0+ROWS-1 of g into `tile`. With CLAMP,
-  // rows >= N receive a copy of row N-1's last chunk (finite data the kernels
-  // mask).
-  template <bool CLAMP>
-  __device__ __forceinline__ void part(char* tile, const half_t* g, int r0, uint32_t lim,
-                                       int wave, int u) const {
-    uint32_t o = base + (uint32_t)u * kStride;
-    if (CLAMP) o = min(o, lim);
-    lds_direct16(reinterpret_cast<half_t*>(tile + (u * NW + wave) * 1024),
-                 reinterpret_cast<const half_t*>(
-                     reinterpret_cast<const char*>(g + (size_t)r0 * D) + o));
-  }
-};
-
-// Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
-__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
-// Loads logical rows [r0, r0 + ROWS) of a row-major (N, D) fp16 matrix into a
-// tile, using the NW waves of the workgroup. Rows >= N are clamped to row N-1
-// (finite data; the kernels mask them before they can contribute); padding
-// slots receive a copy of their row's first chunk.
-//
-// With EVEN, the tile is padded to a whole number of instructions per wave
-// (kHalves), so every wave issues exactly kParts instructions and the issue
-// needs no wave-dependent branch; the extra slots receive rows past the tile
-// (clamped to N - 1), which no reader addresses.
-template <int D, int ROWS, int NW, bool EVEN = false>
-struct TileLoad {
-  static constexpr int kInsts = Tile<D>::template insts<ROWS>();
-  static constexpr int kParts = (kInsts + NW - 1) / NW;  // instructions per wave (at most)
-  static constexpr int kHalves = (EVEN ? kParts * NW : kInsts) * 512;
-
-  // Issues this wave's instruction number u (0 <= u < kParts) of the load.
-  // Splitting the load lets a kernel spread the issue over its products: a
-  // wave that issues all of them at once stalls until the memory pipeline has
-  // accepted them.
-  __device__ __forceinline__ static void part(half_t* tile, const half_t* g, int r0, int N,
-                                              int wave, int lane, int u) {
-    using T = Tile<D>;
-    const int inst = u * NW + wave;
-    if (EVEN || kInsts % NW == 0 || inst < kInsts) {
-      const int p = inst * 64 + lane;
-      const int rho = p / T::kStride;
-      const int c = p - rho * T::kStride;
-      const int gr = min(r0 + perm16(rho), N - 1);
-      lds_direct16(tile + inst * 512, g + (size_t)gr * D + (c < T::kChunks ? c * 8 : 0));
-    }
-  }
-};
-
 // ---------------------------------------------------------------------------
 // Direct global -> LDS loads through a buffer resource (buffer_load ... lds).
 // The resource (base, size in bytes) lives in scalar registers; a load is one
@@ -328,10 +172,22 @@ __device__ __forceinline__ void lds_direct_buf(void* lds, rsrc_t r, uint32_t vof
                                              voff, soff, 0, 0);
 }
 
-// Per-lane byte offsets of a wave's TileLoad instructions relative to the
-// tile's first row. They do not depend on the stage, so a kernel computes
-// them once and each load is then a scalar offset plus one VGPR offset.
-// Padding instructions (EVEN) read the tile's first row.
+// Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Direct loads of logical rows [r0, r0 + ROWS) of a row-major (N, D) fp16
+// matrix into a tile by the NW waves of a workgroup: kInsts 1 KB instructions
+// (64 lanes x one 16-byte chunk, the padding slot of each row included), wave
+// w issuing instructions w, w + NW, ... (kParts at most). With EVEN the tile
+// is padded to a whole number of instructions per wave (kHalves), so every
+// wave issues exactly kParts and the issue needs no wave-dependent branch.
+template <int D, int ROWS, int NW, bool EVEN = false>
+struct TileLoad {
+  static constexpr int kInsts = Tile<D>::template insts<ROWS>();
+  static constexpr int kParts = (kInsts + NW - 1) / NW;  // instructions per wave (at most)
+  static constexpr int kHalves = (EVEN ? kParts * NW : kInsts) * 512;
+};
+
 template <int D, int ROWS, int NW, bool EVEN>
 struct TilePlan {
   using TL = TileLoad<D, ROWS, NW, EVEN>;
@@ -354,43 +210,6 @@ struct TilePlan {
     const int inst = u * NW + wave;
     if (EVEN || TL::kInsts % NW == 0 || inst < TL::kInsts)
       lds_direct_buf<16>(tile + inst * 512, r, off[u], (uint32_t)r0 * (uint32_t)(2 * D));
-  }
-};
-
-template <int D, int ROWS, int NW, bool EVEN = false>
-__device__ __forceinline__ void tile_load(half_t* tile, const half_t* g, int r0, int N,
-                                          int wave, int lane) {
-  using TL = TileLoad<D, ROWS, NW, EVEN>;
-#pragma unroll
-  for (int u = 0; u < TL::kParts; ++u) TL::part(tile, g, r0, N, wave, lane, u);
-}
-
-// Global -> register -> LDS staging of a block of ROWS rows x D halves by a
-// 256-thread workgroup, 16 bytes per chunk; rows >= N load as zeros. The LDS
-// copy is row-major with `kRow` = D + 8 halves per row.
-template <int D, int ROWS, int THREADS = 256>
-struct RowStage {
-  static constexpr int kRow = D + 8;
-  static constexpr int kPer = ROWS * D / 8 / THREADS;
-  static_assert(kPer * THREADS * 8 == ROWS * D, "tile must split evenly over the threads");
-  u32x4 v[kPer];
-
-  __device__ __forceinline__ void load(const half_t* src, int r0, int N, int tid, bool bounds) {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int c = tid + u * THREADS;
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-      const int r = r0 + row;
-      v[u] = load16(src + (size_t)r * D + col, !bounds || r < N);
-    }
-  }
-  __device__ __forceinline__ void store(half_t* dst, int tid) const {
-#pragma unroll
-    for (int u = 0; u < kPer; ++u) {
-      const int c = tid + u * THREADS;
-      const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(dst + row * kRow + col) = v[u];
-    }
   }
 };
 

@@ -37,11 +37,4 @@ hipError_t launch_fwd(const FwdArgs& a);
 hipError_t launch_bwd_preprocess(const BwdArgs& a);
 hipError_t launch_bwd_main(const BwdArgs& a);
 
-// Raises the kernel's dynamic-LDS limit to `bytes` once per process.
-template <typename Kernel>
-inline hipError_t allow_lds(Kernel k, size_t bytes) {
-  return hipFuncSetAttribute(reinterpret_cast<const void*>(k),
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-}
-
 }  // namespace fa
