@@ -40,7 +40,8 @@
 // row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the forward
 // kernel: S^T = K Q^T and dP^T = V dO^T with Q, dO held as B operands, then
 // dQ^T += K^T dS^T. Streamed tiles go from global memory straight into
-// double-buffered, padded, row-permuted LDS tiles (global_load_lds_dwordx4).
+// double-buffered LDS tiles of whole, chunk-swizzled rows (buffer_load ...
+// lds, 1 KB per instruction); the resident K/V use padded, row-permuted rows.
 // Steps are straight-line code (masking is index arithmetic, compiled in only
 // for causal / ragged instantiations): a branch around the MFMAs makes the
 // compiler copy the loop-carried accumulators between register files on
@@ -65,7 +66,7 @@ constexpr int kSub = 64;    // rows per streamed tile (queries in 1, keys in 2)
 // next step's direct loads are filling and does not wait for those loads.
 template <int D>
 struct BwdLds {
-  static constexpr int kTileHalves = Tile<D>::template halves<kSub>();     // staged tile
+  static constexpr int kTileHalves = Swz<D>::template bytes<kSub>() / 2;  // staged tile
   static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();  // resident K or V
   // Partial-sum exchange regions (they reuse the tiles once a phase's loop is
   // done): D/32 accumulators x 16 floats per lane for one wave.
@@ -149,13 +150,14 @@ struct KVWave {
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Kt, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int N, int lane,
-                                       int roff, int troff, float c) {
+                                       int roff, const typename Swz<D>::Offsets& so, float c) {
+    using S = Swz<D>;
     const int h = lane >> 5;
     floatx16 sacc = zero16(), pacc = zero16();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      sacc = mfma32(tile_read16<D>(Qs, m * 32, kk, roff), tile_read16<D>(Kt, kr0, kk, roff), sacc);
-      pacc = mfma32(tile_read16<D>(Os, m * 32, kk, roff), tile_read16<D>(Vt, kr0, kk, roff), pacc);
+      sacc = mfma32(S::read16(Qs, so, kk), tile_read16<D>(Kt, kr0, kk, roff), sacc);
+      pacc = mfma32(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
     // i = i0 + 32m + 8*g4 + 4h + e. Dead key columns j >= N need no mask:
@@ -183,9 +185,8 @@ struct KVWave {
     for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        acc[cb] = mfma32(tile_tr_operand<D>(Os, 32 * m + 16 * q, 32 * cb, troff), pb[q], acc[cb]);
-        acc[D / 32 + cb] =
-            mfma32(tile_tr_operand<D>(Qs, 32 * m + 16 * q, 32 * cb, troff), sb[q], acc[D / 32 + cb]);
+        acc[cb] = mfma32(S::tr_operand(Os, q, so, cb), pb[q], acc[cb]);
+        acc[D / 32 + cb] = mfma32(S::tr_operand(Qs, q, so, cb), sb[q], acc[D / 32 + cb]);
       }
   }
 };
@@ -199,13 +200,15 @@ struct QWave {
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
-                                       int i_row, int N, int lane, int roff, int troff, float c) {
+                                       int i_row, int N, int lane,
+                                       const typename Swz<D>::Offsets& so, float c) {
+    using S = Swz<D>;
     const int h = lane >> 5;
     floatx16 st = zero16(), pt = zero16();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      st = mfma32(tile_read16<D>(Ks, s * 32, kk, roff), qb[kk], st);
-      pt = mfma32(tile_read16<D>(Vs, s * 32, kk, roff), ob[kk], pt);
+      st = mfma32(S::read16(Ks, so, kk), qb[kk], st);
+      pt = mfma32(S::read16(Vs, so, kk), ob[kk], pt);
     }
     // dS^T. A lane holds query row i_row and the 16 keys
     // j = j0 + 32s + 8*g4 + 4h + e. Rows i_row >= N are never stored.
@@ -226,7 +229,7 @@ struct QWave {
     for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
       for (int q = 0; q < 2; ++q)
-        acc[cb] = mfma32(tile_tr_operand<D>(Ks, 32 * s + 16 * q, 32 * cb, troff), sb[q], acc[cb]);
+        acc[cb] = mfma32(S::tr_operand(Ks, q, so, cb), sb[q], acc[cb]);
   }
 };
 
@@ -240,8 +243,11 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2) {
   using L = BwdLds<D>;
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
-  __shared__ __align__(16) half_t ta0[L::kTileHalves], tb0[L::kTileHalves];
-  __shared__ __align__(16) half_t ta1[L::kTileHalves], tb1[L::kTileHalves];
+  // The larger alignment makes the compiler place the four staged tiles first,
+  // in the low 64 KB of LDS, where the tile base fits the 16-bit immediate of
+  // ds_read; each read is then one per-lane offset register plus a constant.
+  __shared__ __align__(1024) half_t ta0[L::kTileHalves], tb0[L::kTileHalves];
+  __shared__ __align__(1024) half_t ta1[L::kTileHalves], tb1[L::kTileHalves];
   __shared__ __align__(16) float vec0[2 * kSub], vec1[2 * kSub];
   __shared__ __align__(16) half_t kres[L::kKVTileHalves], vres[L::kKVTileHalves];
 
@@ -263,9 +269,11 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const size_t kv_off = (size_t)bkv * N * D;
   const uint32_t head_bytes = (uint32_t)N * D * 2;
   const rsrc_t rk = make_rsrc(K + kv_off, head_bytes), rv = make_rsrc(V + kv_off, head_bytes);
-  const int roff = row_lane_off<D>(lane), troff = tr_lane_off<D>(lane);
+  const int roff = row_lane_off<D>(lane);  // resident tiles (padded rows)
+  typename Swz<D>::Offsets so;             // staged tiles (swizzled rows), rows 32*half ..
+  so.init(lane, 32 * half);
 
-  TilePlan<D, kSub, kWaves, false> plan;  // staged 64-row tiles
+  SwzPlan<D, kSub, kWaves> plan;  // staged 64-row tiles
   plan.init(wave, lane);
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
@@ -309,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const rsrc_t rq = make_rsrc(Q + bhq * N * D, head_bytes);
       const rsrc_t ro = make_rsrc(dO + bhq * N * D, head_bytes);
 #pragma unroll
-      for (int u = 0; u < decltype(plan)::TL::kParts; ++u) {
+      for (int u = 0; u < decltype(plan)::kParts; ++u) {
         plan.part(tq, rq, i0, wave, u);
         plan.part(to, ro, i0, wave, u);
       }
@@ -328,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
       w.step(Qs, Os, lse2s, lse2s + kSub, kres, vres, half, w4 * 32, i0, j_col, N, lane, roff,
-             troff, scale_log2);
+             so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -402,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto fetch = [&](int t, half_t* tk, half_t* tv) {
         const int jn = min(t, n_kt - 1) * kSub;
 #pragma unroll
-        for (int u = 0; u < decltype(plan)::TL::kParts; ++u) {
+        for (int u = 0; u < decltype(plan)::kParts; ++u) {
           plan.part(tk, rk, jn, wave, u);
           plan.part(tv, rv, jn, wave, u);
         }
@@ -410,8 +418,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
         fetch(t + 1, P ? ta0 : ta1, P ? tb0 : tb1);
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, N, lane, roff, troff,
-               scale_log2);
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, N, lane, so, scale_log2);
         wait_vmem();
         __syncthreads();
       };

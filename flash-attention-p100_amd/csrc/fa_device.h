@@ -172,6 +172,97 @@ __device__ __forceinline__ void lds_direct_buf(void* lds, rsrc_t r, uint32_t vof
                                              voff, soff, 0, 0);
 }
 
+// ---------------------------------------------------------------------------
+// Unpadded LDS tiles with an XOR chunk swizzle, for tiles streamed every step.
+//
+// Row r occupies 2*D contiguous bytes and keeps its 16-byte chunk c at position
+// c ^ g(r), where g permutes the low row bits:
+//   D = 128 (a row spans all 16 bank groups): g(r) = perm16(r & 15);
+//   D = 64 (two rows per 256 bytes): g(r) = ((r >> 1) & 1) << 2 | (r >> 2) & 3.
+// The 16-byte operand reads (16 consecutive rows at one chunk) and the
+// transpose reads (per half-wave: 4 consecutive rows x 4 consecutive chunks)
+// then hit 16 distinct bank groups, and a direct load covers whole rows
+// (1024 / (2D) per instruction, every lane fetching one chunk of its row),
+// which the memory pipeline serves ~28% faster than the padded-row pattern
+// (17 vs 21.75 cycles per instruction per CU). The swizzle is not additive in
+// the chunk index, so each lane keeps one byte offset per operand position.
+template <int D>
+struct Swz {
+  static constexpr int kChunks = D / 8;
+  static constexpr int kRowBytes = 2 * D;
+  static constexpr int kRowsPerInst = 1024 / kRowBytes;
+  __host__ __device__ static constexpr int g(int r) {
+    return D == 128 ? perm16(r & 15) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+  }
+  template <int ROWS>
+  static constexpr int bytes() { return ROWS * kRowBytes; }
+
+  // Per-lane byte offsets for a wave that reads rows row0 .. row0+31 of a tile
+  // (row0 a multiple of 16): rd[kk] for the 16-byte operand read of row
+  // row0 + lane % 32 at halves 16kk + 8(lane / 32); tr[cb][hi] for the
+  // transpose read of rows row0 + 4(lane / 32) + 8hi .. +3 at columns
+  // 32cb + 16((lane / 16) % 2) + 4(lane % 4) .. +3.
+  struct Offsets {
+    int rd[D / 16];
+    int tr[D / 32][2];
+    __device__ __forceinline__ void init(int lane, int row0) {
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        rd[kk] = (row0 + (lane & 31)) * kRowBytes +
+                 (((2 * kk) | (lane >> 5)) ^ g(lane & 15)) * 16;
+      const int n = lane & 15, grp = lane >> 4, t = n >> 2, a = n & 3;
+#pragma unroll
+      for (int cb = 0; cb < D / 32; ++cb)
+#pragma unroll
+        for (int hi = 0; hi < 2; ++hi) {
+          const int r = 4 * (grp >> 1) + t + 8 * hi;
+          const int x = 2 * (grp & 1) + (a >> 1);
+          tr[cb][hi] = (row0 + r) * kRowBytes + ((4 * cb + x) ^ g(r)) * 16 + 8 * (a & 1);
+        }
+    }
+  };
+
+  // 16-byte MFMA operand: row row0 + lane % 32, halves 16kk + 8(lane / 32) .. +7.
+  __device__ __forceinline__ static half8 read16(const void* tile, const Offsets& o, int kk) {
+    return *reinterpret_cast<const half8*>(reinterpret_cast<const char*>(tile) + o.rd[kk]);
+  }
+  // Transpose-read A operand (as tile_tr_operand): column 32cb + lane % 32 at
+  // rows row0 + 16q + 8(e / 4) + 4(lane / 32) + e % 4. Adding 16 rows keeps
+  // the swizzle, so q only moves the address by a constant.
+  __device__ __forceinline__ static half8 tr_operand(const void* tile, int q, const Offsets& o,
+                                                     int cb) {
+    const char* p = reinterpret_cast<const char*>(tile) + 16 * q * kRowBytes;
+    const half4 lo = lds_read_tr(reinterpret_cast<const half_t*>(p + o.tr[cb][0]));
+    const half4 hi = lds_read_tr(reinterpret_cast<const half_t*>(p + o.tr[cb][1]));
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+};
+
+// Direct-load plan for a swizzled tile of ROWS rows filled by NW waves: every
+// wave issues kParts 1 KB instructions; the per-lane offset of part u is
+// base + u * kStride, so one VGPR (base) and a scalar offset serve them all.
+template <int D, int ROWS, int NW>
+struct SwzPlan {
+  using S = Swz<D>;
+  static constexpr int kInsts = S::template bytes<ROWS>() / 1024;
+  static_assert(kInsts % NW == 0, "tile must split evenly over the waves");
+  static_assert((S::kRowsPerInst * NW) % 16 == 0, "swizzle must repeat across parts");
+  static constexpr int kParts = kInsts / NW;
+  static constexpr uint32_t kStride = (uint32_t)S::kRowsPerInst * NW * S::kRowBytes;
+  uint32_t base;
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+    const int r = S::kRowsPerInst * wave + lane / S::kChunks;  // row within part 0
+    base = (uint32_t)(r * S::kRowBytes + ((lane % S::kChunks) ^ S::g(r)) * 16);
+  }
+  // Part u of the load of rows r0 .. r0+ROWS-1 of the (row-major) buffer `r`
+  // into `tile`; rows past the buffer's end read as zeros.
+  __device__ __forceinline__ void part(void* tile, rsrc_t r, int r0, int wave, int u) const {
+    lds_direct_buf<16>(reinterpret_cast<char*>(tile) + (u * NW + wave) * 1024, r, base,
+                       (uint32_t)r0 * (uint32_t)S::kRowBytes + (uint32_t)u * kStride);
+  }
+};
+
 // Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
