@@ -17,16 +17,21 @@
 // Per wave and 32-key step, on v_mfma_f32_32x32x16_f16 (fp32 accumulate):
 //   * S^T = K Q^T with this wave's Q^T held in registers as the B operand, so
 //     in the accumulator lane l owns query row l % 32 and the softmax row
-//     max is a per-lane max plus one exchange with the other half-wave;
+//     max is a per-lane max plus one lane swap with the other half-wave
+//     (v_permlane32_swap, no LDS round trip);
 //   * the scale is applied to the fp32 logit (never to Q in fp16,
 //     flash_fwd.cuh:94-101), folded with log2(e) into one FMA before exp2;
 //   * the running max is refreshed lazily: O and the row sum are rescaled
 //     only when some row's max grows by more than 2^8, so P stays <= 256 and
 //     the rescale (a pass over all O accumulators) is rare;
 //   * P^T leaves the accumulator as fp16 and feeds O^T += V^T P^T directly,
-//     with V^T read from the row-major V tile by the LDS transpose read.
+//     with V^T read from the row-major V tile by the LDS transpose read;
+//   * software pipeline: step j computes the softmax of S_j (made in step
+//     j-1) while the products of S_{j+1} run, so each wave has matrix work
+//     in flight during its own exponentials. K therefore runs one step ahead
+//     of V in the double buffers.
 // K and V tiles move from global memory straight into double-buffered,
-// padded, row-permuted LDS tiles (global_load_lds_dwordx4), so staging costs
+// padded, row-permuted LDS tiles (buffer_load ... lds), so staging costs
 // no registers and no LDS store instructions, and every LDS read address is a
 // per-lane base plus an immediate. The next stage's load instructions leave
 // a few at a time between the current stage's products: issued all at once,
@@ -67,26 +72,48 @@ struct FwdLds {
   static_assert(2 * kEvenParts <= kIssueSlots, "more loads than issue points");
 };
 
+// Row max over the two half-waves: lanes l and l ^ 32 hold the same query row.
+__device__ __forceinline__ float max_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <int D, bool CAUSAL, bool BOUNDS>
 struct FwdWave {
   // Per-wave state for one 32-row query block.
   half8 qb[D / 16];
   floatx16 oacc[D / 32];
+  floatx16 sc;  // raw logits S^T of the current step (this wave's 32 keys x 32 rows)
   float m_raw;  // running max of the raw (unscaled) logits; -inf before any key
   float l;      // this lane's partial row sum of p (its 16 of every 32 keys)
 
-  // `issue(s)` is called at issue points s = 0 .. D/16 + D/32 - 1.
-  template <bool MASK, class Issue>
-  __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int kq, int j0,
+  // S^T = K Q^T for this wave's 32 keys of a staged K tile.
+  __device__ __forceinline__ void s_product(const half_t* Ks, int kq, int roff) {
+    sc = zero16();
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) sc = mfma32(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], sc);
+  }
+
+  // One software-pipelined step: softmax of sc (the keys j0 .. j0+31 of this
+  // step) and O^T += V^T P^T from the V tile Vs, while (NEXT) the next step's
+  // S^T is computed from its K tile Kn. `issue(s)` is called at issue points
+  // s = 0 .. D/8 - 1 (after each product).
+  template <bool MASK, bool NEXT, class Issue>
+  __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
                                        int i_row, int N, int lane, int roff, int troff, float c,
                                        float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
-    floatx16 s = zero16();
+    floatx16 s = sc;
+    floatx16 sn = zero16();
+    constexpr int kS = D / 16;  // products of the next S^T
+    constexpr int kFront = 2;  // issued before the row max (covers its latency)
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) {
-      s = mfma32(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], s);
-      issue(kk);
-    }
+    for (int kk = 0; kk < kFront; ++kk)
+      if constexpr (NEXT) {
+        sn = mfma32(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
+        issue(kk);
+      }
     if constexpr (MASK) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -97,7 +124,7 @@ struct FwdWave {
     float mloc = s[0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) mloc = fmaxf(mloc, s[r]);
-    mloc = fmaxf(mloc, xor32(mloc));
+    mloc = max_halves(mloc);
     // Lazy rescale: only when some row's max grew by more than 2^8.
     if (__builtin_expect(__any(mloc > m_raw + thr_raw), 0)) {
       const float m_new = fmaxf(m_raw, mloc);
@@ -112,19 +139,32 @@ struct FwdWave {
     const float neg = (m_raw == -INFINITY) ? 0.f : -m_raw * c;
     half8 pb[2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float p = fast_exp2(fmaf(s[r], c, neg));
-      l += p;
-      pb[r >> 3][r & 7] = (half_t)p;
+    for (int kk = kFront; kk < kS; ++kk) {
+      if constexpr (NEXT) {
+        sn = mfma32(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
+        issue(kk);
+      }
+      // 16 exponentials spread over the remaining products.
+      constexpr int kPer = (16 + kS - kFront - 1) / (kS - kFront);
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        const int r = (kk - kFront) * kPer + e;
+        if (r < 16) {
+          const float p = fast_exp2(fmaf(s[r], c, neg));
+          l += p;
+          pb[r >> 3][r & 7] = (half_t)p;
+        }
+      }
     }
     // O^T += V^T P^T; k-step q covers keys 16q .. 16q+15 of this quarter.
 #pragma unroll
-    for (int cb = 0; cb < D / 32; ++cb)
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
+      for (int cb = 0; cb < D / 32; ++cb) {
         oacc[cb] = mfma32(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, troff), pb[q], oacc[cb]);
-        if (2 * cb + q < D / 32) issue(D / 16 + 2 * cb + q);
+        if constexpr (NEXT) issue(kS + q * (D / 32) + cb);
       }
+    if constexpr (NEXT) sc = sn;
   }
 };
 
@@ -165,64 +205,88 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
   if (BOUNDS) n_full = min(n_full, N - 32 - kq * 32 >= 0 ? (N - 32 - kq * 32) / kKV + 1 : 0);
 
+  // Software pipeline over steps j = 0 .. n_it-1. Step j reads K_{j+1} (for
+  // the next S^T) from K buffer (j+1)%2 and V_j from V buffer j%2, while it
+  // loads K_{j+2} into K buffer j%2 and V_{j+1} into V buffer (j+1)%2 (tile
+  // indices clamped to n_it-1, so every step issues the same loads; a
+  // redundant copy lands only in a buffer nobody reads in that step).
   using TL = typename L::TL;
   TilePlan<D, kKV, kWaves, false> plan;
   plan.init(wave, lane);
   const rsrc_t rk = make_rsrc(K, (uint32_t)N * D * 2), rv = make_rsrc(V, (uint32_t)N * D * 2);
+  const int k1 = min(1, n_it - 1) * kKV;
 #pragma unroll
   for (int u = 0; u < TL::kParts; ++u) {
     plan.part(kt0, rk, 0, wave, u);
     plan.part(vt0, rv, 0, wave, u);
+    plan.part(kt1, rk, k1, wave, u);
   }
   wait_vmem();
   __syncthreads();
+  w.s_product(kt0, kq, roff);
+  __syncthreads();  // K buffer 0 is refilled by step 0
 
-  // One step over stage `it` (its buffer parity P is a compile-time constant:
-  // the K and V tiles of both stages are distinct LDS objects, so the
-  // compiler can tell that this step's reads never touch the tiles the next
-  // stage's direct loads are filling, and does not wait for those loads
-  // before them). The last step re-fetches its own stage into the idle
-  // buffers, so every step issues the same loads.
-  auto run = [&](int it, auto par_tag, auto mask_tag) {
+  // Step j with buffer parity P = j % 2 (a compile-time constant, so the
+  // compiler sees that the step's reads never touch the buffers its direct
+  // loads fill and does not wait for those loads before them).
+  auto run = [&](int j, auto par_tag, auto mask_tag, auto next_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
+    constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
-    half_t* nk = P ? kt0 : kt1;
-    half_t* nv = P ? vt0 : vt1;
-    const int jn = min(it + 1, n_it - 1) * kKV;
-    if (L::kEvenParts < TL::kParts && wave < TL::kInsts % kWaves) {
-      plan.part(nk, rk, jn, wave, L::kEvenParts);
-      plan.part(nv, rv, jn, wave, L::kEvenParts);
+    half_t* lk = P ? kt1 : kt0;  // receives K_{j+2}
+    half_t* lv = P ? vt0 : vt1;  // receives V_{j+1}
+    const int jk = min(j + 2, n_it - 1) * kKV;
+    const int jv = min(j + 1, n_it - 1) * kKV;
+    if (NEXT && L::kEvenParts < TL::kParts && wave < TL::kInsts % kWaves) {
+      plan.part(lk, rk, jk, wave, L::kEvenParts);
+      plan.part(lv, rv, jv, wave, L::kEvenParts);
     }
     auto issue = [&](int s) {
       if (s < 2 * L::kEvenParts) {
-        if (s & 1) plan.part(nv, rv, jn, wave, s >> 1);
-        else plan.part(nk, rk, jn, wave, s >> 1);
+        if (s & 1) plan.part(lv, rv, jv, wave, s >> 1);
+        else plan.part(lk, rk, jk, wave, s >> 1);
       }
     };
-    const half_t* Ks = P ? kt1 : kt0;
-    const half_t* Vs = P ? vt1 : vt0;
-    w.template step<MASK>(Ks, Vs, kq, it * kKV + kq * 32, i_row, N, lane, roff, troff, c,
-                          thr_raw, issue);
-    wait_vmem();
-    __syncthreads();
+    const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
+    const half_t* Vs = P ? vt1 : vt0;  // V_j
+    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, i_row, N, lane, roff, troff, c,
+                                thr_raw, issue);
+    if (NEXT) {
+      wait_vmem();
+      __syncthreads();
+    }
   };
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-  int it = 0;
-  for (; it + 2 <= n_full; it += 2) {
-    run(it, P0{}, std::false_type{});
-    run(it + 1, P1{}, std::false_type{});
+  using T = std::true_type;
+  using F = std::false_type;
+  const int n_plain = min(n_full, n_it - 1);  // unmasked steps with a next step
+  int j = 0;
+  for (; j + 2 <= n_plain; j += 2) {
+    run(j, P0{}, F{}, T{});
+    run(j + 1, P1{}, F{}, T{});
   }
-  for (; it < n_it; ++it) {
-    const bool masked = it >= n_full;
-    if (it & 1) {
-      if (masked) run(it, P1{}, std::true_type{});
-      else run(it, P1{}, std::false_type{});
+  for (; j < n_it - 1; ++j) {
+    const bool masked = j >= n_full;
+    if (j & 1) {
+      if (masked) run(j, P1{}, T{}, T{});
+      else run(j, P1{}, F{}, T{});
     } else {
-      if (masked) run(it, P0{}, std::true_type{});
-      else run(it, P0{}, std::false_type{});
+      if (masked) run(j, P0{}, T{}, T{});
+      else run(j, P0{}, F{}, T{});
     }
   }
+  {  // last step: no next S^T, no loads
+    const bool masked = j >= n_full;
+    if (j & 1) {
+      if (masked) run(j, P1{}, T{}, F{});
+      else run(j, P1{}, F{}, F{});
+    } else {
+      if (masked) run(j, P0{}, T{}, F{});
+      else run(j, P0{}, F{}, F{});
+    }
+  }
+  __syncthreads();  // every wave is done reading the tiles (they hold the merge area)
 
   // Merge the four key quarters of each row block through LDS: each of the
   // four tiles holds the partials of two waves.
@@ -307,14 +371,13 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const size_t q_off = (size_t)bh * N * D;
   const size_t kv_off = ((size_t)b * Hkv + hkv) * N * D;
   const float thr_raw = kRescaleLog2 / scale_log2;
-  fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off, Lse + (size_t)bh * N,
-                              N, first, scale_log2, thr_raw, kt0, vt0, kt1, vt1, ml);
-  if (CAUSAL) {
-    const int second = n_qtiles - 1 - first;
-    if (second > first)
-      fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                  Lse + (size_t)bh * N, N, second, scale_log2, thr_raw, kt0, vt0, kt1, vt1, ml);
-  }
+  // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
+  const int second = n_qtiles - 1 - first;
+  const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
+  for (int t = 0; t < n_tiles; ++t)
+    fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
+                                Lse + (size_t)bh * N, N, t ? second : first, scale_log2, thr_raw,
+                                kt0, vt0, kt1, vt1, ml);
 }
 
 template <int D, bool CAUSAL, bool BOUNDS>
