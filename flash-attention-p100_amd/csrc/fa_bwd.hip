@@ -34,7 +34,9 @@
 // softmax arithmetic overlaps the other's matrix products.
 //
 // Both phases run on v_mfma_f32_32x32x16_f16. Phase 1 keeps the workgroup's
-// K and V rows resident in LDS and each wave's dK^T/dV^T in accumulators;
+// K and V rows resident (each wave's 32 K rows as MFMA operands in registers,
+// V in LDS: both in registers would exceed the 256 registers a wave has at
+// two waves per SIMD) and each wave's dK^T/dV^T in accumulators;
 // P and dS come out of the S/dP accumulators and feed dV^T += dO^T P and
 // dK^T += Q^T dS directly, with the dO^T/Q^T operands read from the
 // row-major LDS tiles by the LDS transpose read. Phase 2 mirrors the forward
@@ -144,11 +146,12 @@ __device__ __forceinline__ void partial_add(const float* region, floatx16 (&acc)
 template <int D, bool CAUSAL, bool BOUNDS>
 struct KVWave {
   floatx16 acc[2 * (D / 32)];
+  half8 kb[D / 16];  // this wave's 32 key rows of K as B operands (loop-invariant)
 
   // Query rows i0 + 32m .. +31 (m = this wave's half of the staged tile)
-  // against key rows kr0 .. kr0+31 of the resident tiles (Kt, Vt).
+  // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
-                                       const float* dvs, const half_t* Kt, const half_t* Vt,
+                                       const float* dvs, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int N, int lane,
                                        int roff, const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
@@ -156,7 +159,7 @@ struct KVWave {
     floatx16 sacc = zero16(), pacc = zero16();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      sacc = mfma32(S::read16(Qs, so, kk), tile_read16<D>(Kt, kr0, kk, roff), sacc);
+      sacc = mfma32(S::read16(Qs, so, kk), kb[kk], sacc);
       pacc = mfma32(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
@@ -335,7 +338,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const int i0 = i_start + (it % n_qt) * kSub;
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
-      w.step(Qs, Os, lse2s, lse2s + kSub, kres, vres, half, w4 * 32, i0, j_col, N, lane, roff,
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, N, lane, roff,
              so, scale_log2);
       wait_vmem();
       __syncthreads();
@@ -344,6 +347,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     fetch(0, ta0, tb0, vec0);
     wait_vmem();
     __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < D / 16; ++kk) w.kb[kk] = tile_read16<D>(kres, w4 * 32, kk, roff);
     int it = 0;
     for (; it + 2 <= n_it; it += 2) {
       step(it, P0{});
