@@ -125,14 +125,21 @@ def gpu_bench(c, steps, warmup, copy_mib=0):
 
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    # The timed steps run back to back with nothing else on the stream; a
+    # second pass with events between the kernels gives the per-kernel split
+    # (event records between kernels add gaps, so that pass is not the one
+    # the step time comes from).
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    torch.cuda.synchronize()
     for i in range(steps):
         step(evs[i])
     torch.cuda.synchronize()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
     pre_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
     main_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / steps
