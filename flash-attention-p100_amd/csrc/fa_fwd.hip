@@ -99,10 +99,11 @@ struct FwdWave {
   // step) and O^T += V^T P^T from the V tile Vs, while (NEXT) the next step's
   // S^T is computed from its K tile Kn. `issue(s)` is called at issue points
   // s = 0 .. D/8 - 1 (after each product).
+  // MASK: the step may need the causal / ragged mask, applied when `masked`.
   template <bool MASK, bool NEXT, class Issue>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
-                                       int i_row, int N, int lane, int roff, int troff, float c,
-                                       float thr_raw, const Issue& issue) {
+                                       bool masked, int i_row, int N, int lane, int roff,
+                                       int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
     floatx16 sn = zero16();
@@ -114,7 +115,7 @@ struct FwdWave {
         sn = mfma32(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
         issue(kk);
       }
-    if constexpr (MASK) {
+    if (MASK && masked) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int j = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
@@ -249,8 +250,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     };
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
-    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, i_row, N, lane, roff, troff, c,
-                                thr_raw, issue);
+    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j >= n_full, i_row, N, lane,
+                                roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
       __syncthreads();
@@ -266,26 +267,16 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     run(j, P0{}, F{}, T{});
     run(j + 1, P1{}, F{}, T{});
   }
+  // The remaining steps (the masked ones, usually one or two) take the mask
+  // at run time: fewer inlined copies of the step keep the accumulators in
+  // one set of registers.
   for (; j < n_it - 1; ++j) {
-    const bool masked = j >= n_full;
-    if (j & 1) {
-      if (masked) run(j, P1{}, T{}, T{});
-      else run(j, P1{}, F{}, T{});
-    } else {
-      if (masked) run(j, P0{}, T{}, T{});
-      else run(j, P0{}, F{}, T{});
-    }
+    if (j & 1) run(j, P1{}, T{}, T{});
+    else run(j, P0{}, T{}, T{});
   }
-  {  // last step: no next S^T, no loads
-    const bool masked = j >= n_full;
-    if (j & 1) {
-      if (masked) run(j, P1{}, T{}, F{});
-      else run(j, P1{}, F{}, F{});
-    } else {
-      if (masked) run(j, P0{}, T{}, F{});
-      else run(j, P0{}, F{}, F{});
-    }
-  }
+  // last step: no next S^T, no loads
+  if (j & 1) run(j, P1{}, T{}, F{});
+  else run(j, P0{}, T{}, F{});
   __syncthreads();  // every wave is done reading the tiles (they hold the merge area)
 
   // Merge the four key quarters of each row block through LDS: each of the
