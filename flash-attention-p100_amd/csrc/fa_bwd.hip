@@ -242,7 +242,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
     const float* __restrict__ Lse2, const float* __restrict__ Dvec,
-    float* __restrict__ dQ, half_t* __restrict__ dK, half_t* __restrict__ dV,
+    float* __restrict__ dQ, half_t* __restrict__ dQh, half_t* __restrict__ dK,
+    half_t* __restrict__ dV,
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2) {
   using L = BwdLds<D>;
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -441,16 +442,27 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       __syncthreads();
       if (!half && row_ok) {
         partial_add<D / 32>(region(4 + w4), w.acc, 0, lane);
-        float* qrow = dQ + bhq * N * D + (size_t)i_row * D;
+        const size_t row_off = bhq * N * D + (size_t)i_row * D;
+        if (dQh) {  // fp16 dQ: the fp32 result rounded to nearest even, as .to(fp16)
 #pragma unroll
-        for (int cb = 0; cb < D / 32; ++cb) {
+          for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            floatx4 v4;
+            for (int g4 = 0; g4 < 4; ++g4) {
+              half4 v4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v4[e] = w.acc[cb][4 * g4 + e] * scale;
-            *reinterpret_cast<floatx4*>(qrow + cb * 32 + 8 * g4 + 4 * h) = v4;
-          }
+              for (int e = 0; e < 4; ++e) v4[e] = (half_t)(w.acc[cb][4 * g4 + e] * scale);
+              *reinterpret_cast<half4*>(dQh + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
+            }
+        } else {
+#pragma unroll
+          for (int cb = 0; cb < D / 32; ++cb)
+#pragma unroll
+            for (int g4 = 0; g4 < 4; ++g4) {
+              floatx4 v4;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v4[e] = w.acc[cb][4 * g4 + e] * scale;
+              *reinterpret_cast<floatx4*>(dQ + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
+            }
         }
       }
       __syncthreads();  // the exchange regions are the next head's staging memory
@@ -476,7 +488,7 @@ hipError_t launch_main_t(const BwdArgs& a) {
   hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
-                     (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
+                     (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e);
   return hipGetLastError();
 }

@@ -86,12 +86,14 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* wor
   return to_code(fa::launch_bwd_preprocess(a));
 }
 
-int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
-                size_t workspace_bytes, float* dq, void* dk, void* dv, int B, int Hq, int Hkv,
-                int N, int D, int causal, void* stream) {
+// Shared by fa_bwd_main (fp32 dq) and fa_bwd_half_dq (fp16 dq16).
+static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
+                    const void* workspace, size_t workspace_bytes, float* dq, void* dq16,
+                    void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
+                    void* stream) {
   const int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
-  if (!q || !k || !v || !dO || !workspace || !dq || !dk || !dv) return FA_ERR_NULL;
+  if (!q || !k || !v || !dO || !workspace || !(dq || dq16) || !dk || !dv) return FA_ERR_NULL;
   if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
   fa::BwdArgs a{};
   a.q = q;
@@ -102,6 +104,7 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, con
   a.lse2 = reinterpret_cast<float*>(const_cast<char*>(static_cast<const char*>(workspace)) +
                                     vec_bytes(B, Hq, N));
   a.dq = dq;
+  a.dq16 = dq16;
   a.dk = dk;
   a.dv = dv;
   a.B = B;
@@ -112,6 +115,28 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, con
   a.causal = causal != 0;
   a.stream = stream;
   return to_code(fa::launch_bwd_main(a));
+}
+
+int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+                size_t workspace_bytes, float* dq, void* dk, void* dv, int B, int Hq, int Hkv,
+                int N, int D, int causal, void* stream) {
+  if (!dq) return FA_ERR_NULL;
+  return bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, nullptr, dk, dv, B, Hq, Hkv, N, D,
+                  causal, stream);
+}
+
+int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
+                   const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                   size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+                   void* stream) {
+  const int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc != FA_OK) return rc;
+  if (!workspace || !dq) return FA_ERR_NULL;
+  if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
+  int e = fa_bwd_preprocess(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, stream);
+  if (e != FA_OK) return e;
+  return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
+                  causal, stream);
 }
 
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,

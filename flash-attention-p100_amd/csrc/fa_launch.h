@@ -25,7 +25,8 @@ struct BwdArgs {
   const float* lse;
   float* dvec;   // workspace: rowsum(dO * O), (B, Hq, N)
   float* lse2;   // workspace: LSE * log2(e), (B, Hq, N)
-  float* dq;
+  float* dq;     // fp32 dQ (the reference's dtype), or
+  void* dq16;    // when non-null, fp16 dQ here instead (dq is then unused)
   void* dk;
   void* dv;
   int B, Hq, Hkv, N, D;

@@ -68,8 +68,12 @@ std::vector<at::Tensor> fa_forward(at::Tensor q, at::Tensor k, at::Tensor v, boo
   return {o, lse};
 }
 
-std::vector<at::Tensor> fa_backward(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
-                                    at::Tensor o, at::Tensor lse, bool causal) {
+// half_dq: dq comes back as fp16 (the fp32 result rounded to nearest even,
+// bit-identical to casting the fp32 dq) for the autograd backward, which
+// returns dq in q's dtype (fa_p100.py:45); otherwise fp32 as the reference.
+static std::vector<at::Tensor> backward_impl(at::Tensor q, at::Tensor k, at::Tensor v,
+                                             at::Tensor dO, at::Tensor o, at::Tensor lse,
+                                             bool causal, bool half_dq) {
   check_in(q, "q");
   check_in(dO, "dO");
   q = q.contiguous();
@@ -99,20 +103,40 @@ std::vector<at::Tensor> fa_backward(at::Tensor q, at::Tensor k, at::Tensor v, at
   c10::DeviceGuard guard(q.device());
   auto f32 = q.options().dtype(at::kFloat);
   // Same dtypes as the reference: dq fp32, dk/dv fp16 (fa_p100_ext.cu:118-123).
-  auto dq = at::empty({B, H, N, D}, f32);
+  auto dq = at::empty({B, H, N, D}, half_dq ? q.options() : f32);
   auto dk = at::empty_like(k);
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto dvec = at::empty({(int64_t)(ws_bytes / sizeof(float))}, f32);  // rowsum(dO * O)
-  check_rc(fa_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                  lse.data_ptr<float>(), dq.data_ptr<float>(), dk.data_ptr(), dv.data_ptr(),
-                  dvec.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
-                  current_stream(q)),
-           "fa_bwd");
+  if (half_dq)
+    check_rc(fa_bwd_half_dq(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(),
+                            o.data_ptr(), lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(),
+                            dv.data_ptr(), dvec.data_ptr(), ws_bytes, B, H, Hkv, N, D,
+                            causal ? 1 : 0, current_stream(q)),
+             "fa_bwd_half_dq");
+  else
+    check_rc(fa_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                    lse.data_ptr<float>(), dq.data_ptr<float>(), dk.data_ptr(), dv.data_ptr(),
+                    dvec.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
+                    current_stream(q)),
+             "fa_bwd");
   return {dq, dk, dv};
+}
+
+std::vector<at::Tensor> fa_backward(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
+                                    at::Tensor o, at::Tensor lse, bool causal) {
+  return backward_impl(q, k, v, dO, o, lse, causal, false);
+}
+
+std::vector<at::Tensor> fa_backward_half_dq(at::Tensor q, at::Tensor k, at::Tensor v,
+                                            at::Tensor dO, at::Tensor o, at::Tensor lse,
+                                            bool causal) {
+  return backward_impl(q, k, v, dO, o, lse, causal, true);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &fa_forward, "FlashAttention forward (gfx950)");
   m.def("backward", &fa_backward, "FlashAttention backward (gfx950)");
+  m.def("backward_half_dq", &fa_backward_half_dq,
+        "FlashAttention backward (gfx950), dq as fp16 (used by the autograd Function)");
 }

@@ -61,8 +61,10 @@ class _FlashAttnP100(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_o):
         q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = _ext.backward(q, k, v, grad_o.contiguous(), o, lse, ctx.causal)
-        # dq is accumulated in fp32; hand every gradient back in its input's dtype.
+        # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
+        # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
+        # `_ext.backward(...)[0].to(torch.float16)`) instead of a separate cast.
+        dq, dk, dv = _ext.backward_half_dq(q, k, v, grad_o.contiguous(), o, lse, ctx.causal)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
 
 

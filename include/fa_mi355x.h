@@ -83,6 +83,18 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO,
            int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
 
 /*
+ * fa_bwd with dq written as fp16 (B,Hq,N,D) instead of fp32: each element is
+ * the fp32 result rounded to nearest even, bit-identical to fa_bwd followed by
+ * a cast. No counterpart in the reference: it serves the autograd backward,
+ * which hands dq back in q's dtype (fa_p100.py:45), and saves that cast's pass
+ * over dq.
+ */
+int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO,
+                   const void* o, const float* lse, void* dq, void* dk, void* dv,
+                   void* workspace, size_t workspace_bytes,
+                   int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
+
+/*
  * First phase of fa_bwd, the counterpart of bwd_preprocess
  * (flash_bwd.cuh:65-78): fills `workspace` with dvec = rowsum(dO * o) and
  * lse * log2(e), both fp32 (B,Hq,N). Exposed so a host can time or schedule

@@ -54,6 +54,8 @@ def load_capi():
     lib.fa_bwd_preprocess.restype = i
     lib.fa_bwd_main.argtypes = [vp] * 5 + [sz] + [vp] * 3 + [i] * 6 + [vp]
     lib.fa_bwd_main.restype = i
+    lib.fa_bwd_half_dq.argtypes = [vp] * 10 + [sz] + [i] * 6 + [vp]
+    lib.fa_bwd_half_dq.restype = i
     return lib
 
 

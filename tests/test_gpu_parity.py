@@ -217,3 +217,32 @@ def test_backward_is_deterministic():
     b = run_flash(q, k, v, do, True)
     for x, y in zip(a, b):
         assert np.array_equal(x, y)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv,N", [(4, 4, 200), (8, 2, 333), (2, 1, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_half_dq_is_the_rounded_fp32_dq(D, Hq, Hkv, N, causal):
+    """backward_half_dq (and fa_bwd_half_dq) write dq as fp16 in the kernel:
+    bit-identical to the fp32 dq cast with .to(fp16), dk/dv unchanged."""
+    fa = _fa()
+    q, k, v, do = (t.to(DEV) for t in make_inputs(1, Hq, Hkv, N, D, seed=D + N))
+    o, lse = fa._ext.forward(q, k, v, causal, False)
+    dq32, dk32, dv32 = fa._ext.backward(q, k, v, do, o, lse, causal)
+    dq16, dk16, dv16 = fa._ext.backward_half_dq(q, k, v, do, o, lse, causal)
+    assert dq32.dtype == torch.float32 and dq16.dtype == torch.float16
+    assert torch.equal(dq16, dq32.to(torch.float16))
+    assert torch.equal(dk16, dk32) and torch.equal(dv16, dv32)
+    # Same through the C ABI, into caller-owned buffers.
+    lib = load_capi()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    ws_bytes = lib.fa_bwd_workspace_bytes(1, Hq, Hkv, N, D)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq = torch.full_like(q, 7.0)
+    dk, dv = torch.empty_like(k), torch.empty_like(v)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.fa_bwd_half_dq(p(q), p(k), p(v), p(do), p(o), p(lse), p(dq), p(dk), p(dv), p(ws),
+                            ws_bytes, 1, Hq, Hkv, N, D, int(causal), stream)
+    assert rc == 0, lib.fa_error_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, dq16) and torch.equal(dk, dk16) and torch.equal(dv, dv16)
