@@ -86,7 +86,8 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
                                                       const half_t* __restrict__ dO,
                                                       const float* __restrict__ Lse,
                                                       float* __restrict__ dvec,
-                                                      float* __restrict__ lse2, long rows) {
+                                                      float* __restrict__ lse2, long rows,
+                                                      int Hq, int N, Strides st) {
   constexpr int kLanesPerRow = D / 8;
   constexpr int kRowsPerBlock = 256 / kLanesPerRow;
   const int tid = threadIdx.x;
@@ -94,8 +95,11 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
   const int c8 = (tid % kLanesPerRow) * 8;
   float acc = 0.f;
   if (row < rows) {
-    const half8 o = as_half8(*reinterpret_cast<const u32x4*>(O + row * D + c8));
-    const half8 g = as_half8(*reinterpret_cast<const u32x4*>(dO + row * D + c8));
+    // row = (b * Hq + hq) * N + n over the dense (B, Hq, N) vectors.
+    const long bh = row / N, n = row - bh * N;
+    const size_t off = (size_t)((bh / Hq) * st.b + (bh % Hq) * st.h + n * st.n) + c8;
+    const half8 o = as_half8(*reinterpret_cast<const u32x4*>(O + off));
+    const half8 g = as_half8(*reinterpret_cast<const u32x4*>(dO + off));
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc += (float)o[e] * (float)g[e];
   }
@@ -244,7 +248,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const float* __restrict__ Lse2, const float* __restrict__ Dvec,
     float* __restrict__ dQ, half_t* __restrict__ dQh, half_t* __restrict__ dK,
     half_t* __restrict__ dV,
-    int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2) {
+    int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2,
+    Strides stq, Strides stk) {
   using L = BwdLds<D>;
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
   // The larger alignment makes the compiler place the four staged tiles first,
@@ -270,15 +275,17 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int t0 = (wi % n_tiles) * kTile;   // first row this workgroup owns
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
-  const size_t kv_off = (size_t)bkv * N * D;
-  const uint32_t head_bytes = (uint32_t)N * D * 2;
-  const rsrc_t rk = make_rsrc(K + kv_off, head_bytes), rv = make_rsrc(V + kv_off, head_bytes);
+  const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
+  const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
+  // Offset of query head hq's row 0 in Q, dO, dQ.
+  auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
   const int roff = row_lane_off<D>(lane);  // resident tiles (padded rows)
   typename Swz<D>::Offsets so;             // staged tiles (swizzled rows), rows 32*half ..
   so.init(lane, 32 * half);
 
-  SwzPlan<D, kSub, kWaves> plan;  // staged 64-row tiles
-  plan.init(wave, lane);
+  SwzPlan<D, kSub, kWaves> plan_q, plan_k;  // staged 64-row tiles of Q/dO (phase 1), K/V (2)
+  plan_q.init(wave, lane, stq.n);
+  plan_k.init(wave, lane, stk.n);
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
   // 16 KB-class exchange regions: the four staged tiles, then the halves of
@@ -297,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     KVWave<D, CAUSAL, BOUNDS> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows t0 .. t0+kTile-1
-      plan_kv.init(wave, lane);
+      plan_kv.init(wave, lane, stk.n);
 #pragma unroll
       for (int u = 0; u < decltype(plan_kv)::TL::kParts; ++u) {
         plan_kv.part(kres, rk, t0, wave, u);
@@ -317,13 +324,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       it = min(it, n_it - 1);
       const int g = it / n_qt;
       const int i0 = i_start + (it % n_qt) * kSub;
-      const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
-      const rsrc_t rq = make_rsrc(Q + bhq * N * D, head_bytes);
-      const rsrc_t ro = make_rsrc(dO + bhq * N * D, head_bytes);
+      const int hq = hkv * group + g;
+      const size_t bhq = (size_t)b * Hq + hq;
+      const rsrc_t rq = rows_rsrc<D>(Q + q_off(hq), N, stq.n);
+      const rsrc_t ro = rows_rsrc<D>(dO + q_off(hq), N, stq.n);
 #pragma unroll
-      for (int u = 0; u < decltype(plan)::kParts; ++u) {
-        plan.part(tq, rq, i0, wave, u);
-        plan.part(to, ro, i0, wave, u);
+      for (int u = 0; u < decltype(plan_q)::kParts; ++u) {
+        plan_q.part(tq, rq, i0, wave, u);
+        plan_q.part(to, ro, i0, wave, u);
       }
       if (wave == 0) vec_load64(tv, make_rsrc(Lse2 + bhq * N, (uint32_t)N * 4), i0, lane);
       if (wave == 1) vec_load64(tv + kSub, make_rsrc(Dvec + bhq * N, (uint32_t)N * 4), i0, lane);
@@ -368,8 +376,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       partial_add<D / 32>(region(2 * w4), w.acc, 0, lane);
       partial_add<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
       if (!BOUNDS || j_col < N) {
-        half_t* dkrow = dK + kv_off + (size_t)j_col * D;
-        half_t* dvrow = dV + kv_off + (size_t)j_col * D;
+        half_t* dkrow = dK + kv_off + (size_t)j_col * stk.n;
+        half_t* dvrow = dV + kv_off + (size_t)j_col * stk.n;
 #pragma unroll
         for (int cb = 0; cb < D / 32; ++cb) {
 #pragma unroll
@@ -398,14 +406,15 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int n_kt = (kv_end + kSub - 1) / kSub;
 
     for (int g = 0; g < group; ++g) {
-      const size_t bhq = (size_t)b * Hq + (size_t)hkv * group + g;
-      const half_t* Qg = Q + bhq * N * D;
-      const half_t* dOg = dO + bhq * N * D;
+      const int hq = hkv * group + g;
+      const size_t bhq = (size_t)b * Hq + hq;
+      const half_t* Qg = Q + q_off(hq);
+      const half_t* dOg = dO + q_off(hq);
       QWave<D, CAUSAL, BOUNDS> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        w.qb[kk] = as_half8(load16(Qg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
-        w.ob[kk] = as_half8(load16(dOg + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+        w.qb[kk] = as_half8(load16(Qg + (size_t)i_row * stq.n + kk * 16 + h * 8, row_ok));
+        w.ob[kk] = as_half8(load16(dOg + (size_t)i_row * stq.n + kk * 16 + h * 8, row_ok));
       }
       w.lse2 = row_ok ? Lse2[bhq * N + i_row] : 0.f;
       w.dvv = row_ok ? Dvec[bhq * N + i_row] : 0.f;
@@ -416,9 +425,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto fetch = [&](int t, half_t* tk, half_t* tv) {
         const int jn = min(t, n_kt - 1) * kSub;
 #pragma unroll
-        for (int u = 0; u < decltype(plan)::kParts; ++u) {
-          plan.part(tk, rk, jn, wave, u);
-          plan.part(tv, rv, jn, wave, u);
+        for (int u = 0; u < decltype(plan_k)::kParts; ++u) {
+          plan_k.part(tk, rk, jn, wave, u);
+          plan_k.part(tv, rv, jn, wave, u);
         }
       };
       auto step = [&](int t, auto par) {
@@ -442,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       __syncthreads();
       if (!half && row_ok) {
         partial_add<D / 32>(region(4 + w4), w.acc, 0, lane);
-        const size_t row_off = bhq * N * D + (size_t)i_row * D;
+        const size_t row_off = q_off(hq) + (size_t)i_row * stq.n;
         if (dQh) {  // fp16 dQ: the fp32 result rounded to nearest even, as .to(fp16)
 #pragma unroll
           for (int cb = 0; cb < D / 32; ++cb)
@@ -476,7 +485,8 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   const long rows = (long)a.B * a.Hq * a.N;
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   hipLaunchKernelGGL((bwd_pre_kernel<D>), grid, dim3(256), 0, (hipStream_t)a.stream,
-                     (const half_t*)a.o, (const half_t*)a.dO, a.lse, a.dvec, a.lse2, rows);
+                     (const half_t*)a.o, (const half_t*)a.dO, a.lse, a.dvec, a.lse2, rows, a.Hq,
+                     a.N, make_strides(a.layout, a.Hq, a.N, D));
   return hipGetLastError();
 }
 
@@ -489,7 +499,8 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
-                     a.B * a.Hkv, scale, scale * kLog2e);
+                     a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
+                     make_strides(a.layout, a.Hkv, a.N, D));
   return hipGetLastError();
 }
 

@@ -23,6 +23,12 @@ int check_shape(int B, int Hq, int Hkv, int N, int D) {
   return FA_OK;
 }
 
+// The (B, N, H, D) layout addresses one head's rows through a 32-bit buffer
+// range that spans all H heads: (N - 1) * H * D + D halves must fit.
+int check_bnhd(int Hq, int N, int D) {
+  return (long long)N * Hq * D > INT_MAX ? FA_ERR_TOO_LARGE : FA_OK;
+}
+
 int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }
 
 // One (B, Hq, N) float32 vector, rounded up to 256 bytes.
@@ -50,14 +56,25 @@ const char* fa_error_string(int err) {
 
 const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
+static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
+               int Hkv, int N, int D, int causal, int layout, void* stream) {
+  int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
+  if (rc != FA_OK) return rc;
+  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
+  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout};
+  return to_code(fa::launch_fwd(a));
+}
+
 int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
            int Hkv, int N, int D, int causal, int full_precision, void* stream) {
   (void)full_precision;  // fp16 products are exact in the fp32 accumulator
-  const int rc = check_shape(B, Hq, Hkv, N, D);
-  if (rc != FA_OK) return rc;
-  if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream};
-  return to_code(fa::launch_fwd(a));
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBHND, stream);
+}
+
+int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
+                int Hkv, int N, int D, int causal, void* stream) {
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBNHD, stream);
 }
 
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
@@ -65,9 +82,11 @@ size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
   return 2 * vec_bytes(B, Hq, N);
 }
 
-int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* workspace,
-                      size_t workspace_bytes, int B, int Hq, int N, int D, void* stream) {
-  const int rc = check_shape(B, Hq, Hq, N, D);
+static int bwd_pre(const void* dO, const void* o, const float* lse, void* workspace,
+                   size_t workspace_bytes, int B, int Hq, int N, int D, int layout,
+                   void* stream) {
+  int rc = check_shape(B, Hq, Hq, N, D);
+  if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!dO || !o || !lse || !workspace) return FA_ERR_NULL;
   if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
@@ -83,15 +102,22 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* wor
   a.N = N;
   a.D = D;
   a.stream = stream;
+  a.layout = layout;
   return to_code(fa::launch_bwd_preprocess(a));
 }
 
-// Shared by fa_bwd_main (fp32 dq) and fa_bwd_half_dq (fp16 dq16).
+int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* workspace,
+                      size_t workspace_bytes, int B, int Hq, int N, int D, void* stream) {
+  return bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, fa::kBHND, stream);
+}
+
+// Shared by the main-kernel entry points: fp32 dq or fp16 dq16, either layout.
 static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     const void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
-                    void* stream) {
-  const int rc = check_shape(B, Hq, Hkv, N, D);
+                    int layout, void* stream) {
+  int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !dO || !workspace || !(dq || dq16) || !dk || !dv) return FA_ERR_NULL;
   if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
@@ -114,7 +140,23 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.D = D;
   a.causal = causal != 0;
   a.stream = stream;
+  a.layout = layout;
   return to_code(fa::launch_bwd_main(a));
+}
+
+// Preprocess + main with fp16 dq (both layouts).
+static int bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
+                       const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                       size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+                       int layout, void* stream) {
+  const int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc != FA_OK) return rc;
+  if (!workspace || !dq) return FA_ERR_NULL;
+  if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
+  int e = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, layout, stream);
+  if (e != FA_OK) return e;
+  return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
+                  causal, layout, stream);
 }
 
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
@@ -122,21 +164,23 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, con
                 int N, int D, int causal, void* stream) {
   if (!dq) return FA_ERR_NULL;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, nullptr, dk, dv, B, Hq, Hkv, N, D,
-                  causal, stream);
+                  causal, fa::kBHND, stream);
 }
 
 int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
                    const float* lse, void* dq, void* dk, void* dv, void* workspace,
                    size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                    void* stream) {
-  const int rc = check_shape(B, Hq, Hkv, N, D);
-  if (rc != FA_OK) return rc;
-  if (!workspace || !dq) return FA_ERR_NULL;
-  if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
-  int e = fa_bwd_preprocess(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, stream);
-  if (e != FA_OK) return e;
-  return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
-                  causal, stream);
+  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
+                     D, causal, fa::kBHND, stream);
+}
+
+int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO, const void* o,
+                const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+                void* stream) {
+  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
+                     D, causal, fa::kBNHD, stream);
 }
 
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,

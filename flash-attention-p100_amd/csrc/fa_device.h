@@ -239,8 +239,8 @@ struct Swz {
 };
 
 // Direct-load plan for a swizzled tile of ROWS rows filled by NW waves: every
-// wave issues kParts 1 KB instructions; the per-lane offset of part u is
-// base + u * kStride, so one VGPR (base) and a scalar offset serve them all.
+// wave issues kParts 1 KB instructions; part u covers rows u * kPartRows
+// further on, so one VGPR (base) and a scalar offset serve them all.
 template <int D, int ROWS, int NW>
 struct SwzPlan {
   using S = Swz<D>;
@@ -248,18 +248,21 @@ struct SwzPlan {
   static_assert(kInsts % NW == 0, "tile must split evenly over the waves");
   static_assert((S::kRowsPerInst * NW) % 16 == 0, "swizzle must repeat across parts");
   static constexpr int kParts = kInsts / NW;
-  static constexpr uint32_t kStride = (uint32_t)S::kRowsPerInst * NW * S::kRowBytes;
+  static constexpr int kPartRows = S::kRowsPerInst * NW;  // rows per part
   uint32_t base;
+  uint32_t row_bytes;  // bytes between consecutive rows in global memory (2*D when dense)
 
-  __device__ __forceinline__ void init(int wave, int lane) {
+  __device__ __forceinline__ void init(int wave, int lane, int row_stride) {
+    row_bytes = 2u * (uint32_t)row_stride;
     const int r = S::kRowsPerInst * wave + lane / S::kChunks;  // row within part 0
-    base = (uint32_t)(r * S::kRowBytes + ((lane % S::kChunks) ^ S::g(r)) * 16);
+    base = (uint32_t)r * row_bytes + (uint32_t)(((lane % S::kChunks) ^ S::g(r)) * 16);
   }
-  // Part u of the load of rows r0 .. r0+ROWS-1 of the (row-major) buffer `r`
-  // into `tile`; rows past the buffer's end read as zeros.
+  // Part u of the load of rows r0 .. r0+ROWS-1 of the buffer `r` (rows of D
+  // halves, row_bytes apart) into `tile`; rows past the buffer's end read as
+  // zeros.
   __device__ __forceinline__ void part(void* tile, rsrc_t r, int r0, int wave, int u) const {
     lds_direct_buf<16>(reinterpret_cast<char*>(tile) + (u * NW + wave) * 1024, r, base,
-                       (uint32_t)r0 * (uint32_t)S::kRowBytes + (uint32_t)u * kStride);
+                       ((uint32_t)r0 + (uint32_t)(u * kPartRows)) * row_bytes);
   }
 };
 
@@ -283,25 +286,35 @@ template <int D, int ROWS, int NW, bool EVEN>
 struct TilePlan {
   using TL = TileLoad<D, ROWS, NW, EVEN>;
   uint32_t off[TL::kParts];
+  uint32_t row_bytes;  // bytes between consecutive rows in global memory (2*D when dense)
 
-  __device__ __forceinline__ void init(int wave, int lane) {
+  __device__ __forceinline__ void init(int wave, int lane, int row_stride) {
     using T = Tile<D>;
+    row_bytes = 2u * (uint32_t)row_stride;
 #pragma unroll
     for (int u = 0; u < TL::kParts; ++u) {
       const int p = (u * NW + wave) * 64 + lane;
       const int rho = p / T::kStride;
       const int c = p - rho * T::kStride;
       const int row = rho < ROWS ? perm16(rho) : 0;
-      off[u] = (uint32_t)(row * D + (c < T::kChunks ? c * 8 : 0)) * 2u;
+      off[u] = (uint32_t)row * row_bytes + (uint32_t)(c < T::kChunks ? c * 16 : 0);
     }
   }
-  // Loads part u of the tile whose first row is r0 from the (row-major, D
-  // halves per row) buffer `r`; rows past the buffer's end read as zeros.
+  // Loads part u of the tile whose first row is r0 from the buffer `r` (rows
+  // of D halves, row_bytes apart); rows past the buffer's end read as zeros.
   __device__ __forceinline__ void part(half_t* tile, rsrc_t r, int r0, int wave, int u) const {
     const int inst = u * NW + wave;
     if (EVEN || TL::kInsts % NW == 0 || inst < TL::kInsts)
-      lds_direct_buf<16>(tile + inst * 512, r, off[u], (uint32_t)r0 * (uint32_t)(2 * D));
+      lds_direct_buf<16>(tile + inst * 512, r, off[u], (uint32_t)r0 * row_bytes);
   }
 };
+
+// Buffer resource over the n_rows rows of one head: rows of D halves
+// row_stride halves apart. Its size ends right after row n_rows-1, so any row
+// index >= n_rows reads as zeros.
+template <int D>
+__device__ __forceinline__ rsrc_t rows_rsrc(const half_t* base, int n_rows, int row_stride) {
+  return make_rsrc(base, ((uint32_t)n_rows - 1u) * 2u * (uint32_t)row_stride + 2u * D);
+}
 
 }  // namespace fa

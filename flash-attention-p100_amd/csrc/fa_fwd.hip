@@ -172,8 +172,9 @@ struct FwdWave {
 template <int D, bool CAUSAL, bool BOUNDS>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
-                                         float* __restrict__ Lse, int N, int qtile,
-                                         float c, float thr_raw, half_t* kt0, half_t* vt0,
+                                         float* __restrict__ Lse, int N, int sq, int sk,
+                                         int qtile, float c, float thr_raw, half_t* kt0,
+                                         half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
   using L = FwdLds<D>;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -190,7 +191,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const bool row_ok = !BOUNDS || i_row < N;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
-    w.qb[kk] = as_half8(load16(Q + (size_t)i_row * D + kk * 16 + h * 8, row_ok));
+    w.qb[kk] = as_half8(load16(Q + (size_t)i_row * sq + kk * 16 + h * 8, row_ok));
 #pragma unroll
   for (int cb = 0; cb < D / 32; ++cb) w.oacc[cb] = zero16();
   w.m_raw = -INFINITY;
@@ -213,8 +214,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // redundant copy lands only in a buffer nobody reads in that step).
   using TL = typename L::TL;
   TilePlan<D, kKV, kWaves, false> plan;
-  plan.init(wave, lane);
-  const rsrc_t rk = make_rsrc(K, (uint32_t)N * D * 2), rv = make_rsrc(V, (uint32_t)N * D * 2);
+  plan.init(wave, lane, sk);
+  const rsrc_t rk = rows_rsrc<D>(K, N, sk), rv = rows_rsrc<D>(V, N, sk);
   const int k1 = min(1, n_it - 1) * kKV;
 #pragma unroll
   for (int u = 0; u < TL::kParts; ++u) {
@@ -318,7 +319,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     }
     const float inv_l = 1.f / l_star;
     if (row_ok) {
-      half_t* orow = O + (size_t)i_row * D + cb * 32;
+      half_t* orow = O + (size_t)i_row * sq + cb * 32;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -344,7 +345,8 @@ template <int D, bool CAUSAL, bool BOUNDS>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
-    int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2) {
+    int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
+    Strides stk) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -359,15 +361,16 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const int b = bh / Hq, hq = bh % Hq;
   const int Hkv = Hq / group;
   const int hkv = hq / group;  // repeat_interleave head map (flash_fwd.cuh:90)
-  const size_t q_off = (size_t)bh * N * D;
-  const size_t kv_off = ((size_t)b * Hkv + hkv) * N * D;
+  const size_t q_off = (size_t)(b * stq.b + hq * stq.h);
+  const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const float thr_raw = kRescaleLog2 / scale_log2;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                Lse + (size_t)bh * N, N, t ? second : first, scale_log2, thr_raw,
+                                Lse + (size_t)bh * N, N, stq.n, stk.n, t ? second : first,
+                                scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
 
@@ -381,7 +384,8 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
-                     n_qtiles, gx, BH, scale_log2);
+                     n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
+                     make_strides(a.layout, a.Hkv, a.N, D));
   return hipGetLastError();
 }
 

@@ -5,6 +5,22 @@
 
 namespace fa {
 
+// Memory layouts of the (B, H, N, D) fp16 tensors: kBHND is dense (B, H, N, D)
+// (the reference's layout); kBNHD stores the same logical tensor as dense
+// (B, N, H, D), the layout of the projections in a transformer block.
+enum Layout : int { kBHND = 0, kBNHD = 1 };
+
+// Element strides of one (B, H, N, D) tensor with `heads` heads.
+struct Strides {
+  long long b;  // between batches
+  long long h;  // between heads
+  int n;        // between rows (sequence positions)
+};
+inline Strides make_strides(int layout, int heads, int N, int D) {
+  if (layout == kBNHD) return {(long long)N * heads * D, (long long)D, heads * D};
+  return {(long long)heads * N * D, (long long)N * D, D};
+}
+
 struct FwdArgs {
   const void* q;
   const void* k;
@@ -14,6 +30,7 @@ struct FwdArgs {
   int B, Hq, Hkv, N, D;
   bool causal;
   void* stream;
+  int layout = kBHND;  // of q, k, v, o (lse is always dense (B, Hq, N))
 };
 
 struct BwdArgs {
@@ -32,6 +49,7 @@ struct BwdArgs {
   int B, Hq, Hkv, N, D;
   bool causal;
   void* stream;
+  int layout = kBHND;  // of q, k, v, dO, o, dq, dk, dv (lse, workspace dense)
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

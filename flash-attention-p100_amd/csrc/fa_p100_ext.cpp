@@ -134,9 +134,81 @@ std::vector<at::Tensor> fa_backward_half_dq(at::Tensor q, at::Tensor k, at::Tens
   return backward_impl(q, k, v, dO, o, lse, causal, true);
 }
 
+// The (B, N, H, D)-layout pair used by the autograd Function when q, k, v
+// arrive as (B, H, N, D) views of (B, N, H, D) storage (what the HF hook
+// passes, fa_p100_hf.py:131-140): no copy in, o and the gradients come back
+// in the same layout (dq as fp16). Arguments here are the (B, N, H, D)
+// tensors themselves; the checks and messages are the reference's, on the
+// logical (B, H, N, D) shapes.
+static void check_bnhd(const at::Tensor& t, const char* name) {
+  check_in(t, name);
+  TORCH_CHECK(t.is_contiguous(), name, " must be dense (B, N, H, D)");
+}
+
+std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  check_bnhd(q, "q");
+  check_bnhd(k, "k");
+  check_bnhd(v, "v");
+  const int B = q.size(0), N = q.size(1), H = q.size(2), D = q.size(3);
+  const int Hkv = k.size(2);
+  TORCH_CHECK(D == 64 || D == 128, "head dim must be 64 or 128, got ", D);
+  TORCH_CHECK(N > 0, "N must be positive");
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
+              ") must be a multiple of key/value heads (", Hkv, ")");
+  TORCH_CHECK(k.sizes() == v.sizes(), "k and v must match");
+  TORCH_CHECK(k.size(0) == B && k.size(1) == N && k.size(3) == D,
+              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
+              "q, k and v must be on the same device");
+  c10::DeviceGuard guard(q.device());
+  auto o = at::empty_like(q);
+  auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
+  check_rc(fa_fwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                       lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0,
+                       current_stream(q)),
+           "fa_fwd_bnhd");
+  return {o, lse};
+}
+
+std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v,
+                                         at::Tensor dO, at::Tensor o, at::Tensor lse,
+                                         bool causal) {
+  for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
+                   std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
+    check_bnhd(*tn.first, tn.second);
+  lse = lse.contiguous();
+  const int B = q.size(0), N = q.size(1), H = q.size(2), D = q.size(3);
+  const int Hkv = k.size(2);
+  TORCH_CHECK(D == 64 || D == 128, "head dim must be 64 or 128, got ", D);
+  TORCH_CHECK(N > 0, "N must be positive");
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
+  TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == B && k.size(1) == N && k.size(3) == D,
+              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(dO.sizes() == q.sizes() && o.sizes() == q.sizes(), "dO and o must match q");
+  TORCH_CHECK(lse.scalar_type() == at::kFloat && lse.dim() == 3 && lse.size(0) == B &&
+                  lse.size(1) == H && lse.size(2) == N,
+              "lse must be (B, H, N)");
+  c10::DeviceGuard guard(q.device());
+  auto dq = at::empty_like(q);  // fp16, (B, N, Hq, D)
+  auto dk = at::empty_like(k);
+  auto dv = at::empty_like(k);
+  const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
+  auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
+  check_rc(fa_bwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                       lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                       ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
+                       current_stream(q)),
+           "fa_bwd_bnhd");
+  return {dq, dk, dv};
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward", &fa_forward, "FlashAttention forward (gfx950)");
   m.def("backward", &fa_backward, "FlashAttention backward (gfx950)");
   m.def("backward_half_dq", &fa_backward_half_dq,
         "FlashAttention backward (gfx950), dq as fp16 (used by the autograd Function)");
+  m.def("forward_bnhd", &fa_forward_bnhd,
+        "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors");
+  m.def("backward_bnhd", &fa_backward_bnhd,
+        "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq as fp16");
 }

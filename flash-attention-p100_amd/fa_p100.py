@@ -48,18 +48,47 @@ def _load_ext():
 _ext = _load_ext()
 
 
+def _bnhd_storage(t):
+    """The dense (B, N, H, D) tensor a (B, H, N, D) view `t` is a transpose of,
+    or None."""
+    tt = t.transpose(1, 2)
+    return tt if tt.is_contiguous() else None
+
+
 class _FlashAttnP100(torch.autograd.Function):
-    """Autograd wrapper; same saved state and return types as fa_p100.py:31-45."""
+    """Autograd wrapper; same saved state and return types as fa_p100.py:31-45.
+
+    When q, k and v are all (B, H, N, D) views of dense (B, N, H, D) storage
+    (the projections' layout, which the HF hook passes), the kernels read and
+    write that layout directly: no copies in, and o and the gradients come
+    back as (B, H, N, D) views of (B, N, H, D) tensors. Results are
+    bit-identical to the dense path.
+    """
 
     @staticmethod
     def forward(ctx, q, k, v, causal, full_precision):
+        # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
+        # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
+        # they are dense in both layouts).
+        qb = None if q.is_contiguous() else _bnhd_storage(q)
+        kb, vb = _bnhd_storage(k), _bnhd_storage(v)
+        ctx.causal = causal
+        ctx.bnhd = qb is not None and kb is not None and vb is not None
+        if ctx.bnhd:
+            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal)
+            ctx.save_for_backward(qb, kb, vb, ob, lse)
+            return ob.transpose(1, 2)
         o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
-        ctx.causal = causal
         return o
 
     @staticmethod
     def backward(ctx, grad_o):
+        if ctx.bnhd:
+            qb, kb, vb, ob, lse = ctx.saved_tensors
+            gb = grad_o.transpose(1, 2)
+            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb.contiguous(), ob, lse, ctx.causal)
+            return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to

@@ -63,6 +63,19 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
            int full_precision, void* stream);
 
 /*
+ * fa_fwd on tensors stored as dense (B, N, H, D) instead of (B, H, N, D): q and
+ * o with Hq heads, k and v with Hkv heads (lse stays (B, Hq, N)). This is the
+ * layout of a transformer block's projections, so a caller holding
+ * (B, H, N, D) views of them (fa_p100_hf.py:131-142 transposes them) needs no
+ * copy in or out. No counterpart in the reference (the caller made the
+ * tensors contiguous, fa_p100_ext.cu:67-69, and copied o back,
+ * fa_p100_hf.py:142). Same results, bit for bit, as fa_fwd on the same
+ * logical tensors.
+ */
+int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse,
+                int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
+
+/*
  * Bytes of device workspace fa_bwd needs: two (B, Hq, N) float32 vectors, the
  * reference's `dvec` (fa_p100_ext.cu:124) and the saved LSE pre-multiplied by
  * log2(e), each rounded up to 256 bytes. 0 for an invalid shape.
@@ -93,6 +106,17 @@ int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO,
                    const void* o, const float* lse, void* dq, void* dk, void* dv,
                    void* workspace, size_t workspace_bytes,
                    int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
+
+/*
+ * fa_bwd_half_dq on (B, N, H, D)-stored q, k, v, dO, o, dq, dk, dv (see
+ * fa_fwd_bnhd). No counterpart in the reference (see fa_fwd_bnhd and
+ * fa_bwd_half_dq); bit-identical to fa_bwd_half_dq on the same logical
+ * tensors.
+ */
+int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO,
+                const void* o, const float* lse, void* dq, void* dk, void* dv,
+                void* workspace, size_t workspace_bytes,
+                int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
 
 /*
  * First phase of fa_bwd, the counterpart of bwd_preprocess

@@ -56,6 +56,10 @@ def load_capi():
     lib.fa_bwd_main.restype = i
     lib.fa_bwd_half_dq.argtypes = [vp] * 10 + [sz] + [i] * 6 + [vp]
     lib.fa_bwd_half_dq.restype = i
+    lib.fa_fwd_bnhd.argtypes = [vp] * 5 + [i] * 6 + [vp]
+    lib.fa_fwd_bnhd.restype = i
+    lib.fa_bwd_bnhd.argtypes = [vp] * 10 + [sz] + [i] * 6 + [vp]
+    lib.fa_bwd_bnhd.restype = i
     return lib
 
 

@@ -246,3 +246,56 @@ def test_half_dq_is_the_rounded_fp32_dq(D, Hq, Hkv, N, causal):
     assert rc == 0, lib.fa_error_string(rc)
     torch.cuda.synchronize()
     assert torch.equal(dq, dq16) and torch.equal(dk, dk16) and torch.equal(dv, dv16)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,Hq,Hkv,N", [(1, 4, 4, 200), (2, 8, 2, 333), (1, 2, 1, 64)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bnhd_views_match_dense_bit_for_bit(D, B, Hq, Hkv, N, causal):
+    """(B, H, N, D) views of dense (B, N, H, D) storage (what the HF hook
+    passes) go through the (B, N, H, D) kernels with no copies; o and the
+    gradients are bit-identical to the dense path and come back as views of
+    (B, N, H, D) storage."""
+    fa = _fa()
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=3 * N + D))
+    as_bnhd = lambda t: t.transpose(1, 2).contiguous().transpose(1, 2)
+    dense = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    views = [as_bnhd(t).detach().requires_grad_(True) for t in (q, k, v)]
+    assert not views[0].is_contiguous() and views[0].transpose(1, 2).is_contiguous()
+    o1 = fa.flash_attn(*dense, causal)
+    o2 = fa.flash_attn(*views, causal)
+    assert o2.transpose(1, 2).is_contiguous()
+    o1.backward(do)
+    o2.backward(as_bnhd(do))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    for a, b in zip(dense, views):
+        assert torch.equal(a.grad, b.grad)
+
+
+def test_bnhd_capi_matches_dense_capi():
+    """fa_fwd_bnhd / fa_bwd_bnhd on (B, N, H, D) buffers against fa_fwd /
+    fa_bwd_half_dq on the same logical tensors, bit for bit."""
+    lib = load_capi()
+    B, Hq, Hkv, N, D, causal = 2, 6, 3, 97, 128, 1
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=11))
+    tb = lambda t: t.transpose(1, 2).contiguous()  # (B, N, H, D)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    o, ob = torch.empty_like(q), torch.empty_like(tb(q))
+    lse, lseb = (torch.empty(B, Hq, N, device=DEV) for _ in range(2))
+    assert lib.fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, Hq, Hkv, N, D, causal, 0, s) == 0
+    qb, kb, vb, dob = tb(q), tb(k), tb(v), tb(do)
+    assert lib.fa_fwd_bnhd(p(qb), p(kb), p(vb), p(ob), p(lseb), B, Hq, Hkv, N, D, causal, s) == 0
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dqb, dkb, dvb = torch.empty_like(qb), torch.empty_like(kb), torch.empty_like(vb)
+    assert lib.fa_bwd_half_dq(p(q), p(k), p(v), p(do), p(o), p(lse), p(dq), p(dk), p(dv), p(ws),
+                              ws_bytes, B, Hq, Hkv, N, D, causal, s) == 0
+    assert lib.fa_bwd_bnhd(p(qb), p(kb), p(vb), p(dob), p(ob), p(lseb), p(dqb), p(dkb), p(dvb),
+                           p(ws), ws_bytes, B, Hq, Hkv, N, D, causal, s) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(tb(o), ob) and torch.equal(lse, lseb)
+    for a, b in ((dq, dqb), (dk, dkb), (dv, dvb)):
+        assert torch.equal(tb(a), b)
