@@ -11,8 +11,10 @@ fa_fwd, then fa_bwd_preprocess (Dv), then fa_bwd_main (dK, dV, dQ), into
 preallocated buffers. K steps are timed between two device synchronisations;
 HIP events recorded on the same stream between the launches give each
 kernel's average duration. The same step through the public autograd op
-(`flash_attn(...).backward(g)`, which adds output allocation and the dQ
-fp32->fp16 cast) is timed as `api_ms_per_step`.
+(`flash_attn(...).backward(g)`, which adds output and workspace allocation;
+its backward writes dQ as fp16) is timed as `api_ms_per_step`, and torch's own GPU
+scaled_dot_product_attention (flash and memory-efficient backends, fp16,
+same inputs) as `torch_sdpa_gpu`, for comparison.
 
 FLOPs follow the reference's convention (attention.cu:219, bwd.cu:246):
 fwd = 4*B*Hq*N^2*D, halved for causal; bwd = 2.5x fwd.
@@ -162,7 +164,40 @@ def gpu_bench(c, steps, warmup, copy_mib=0):
     torch.cuda.synchronize()
     api_ms = (time.perf_counter() - t0) * 1e3 / steps
     return dict(wall_ms=wall_ms, fwd_ms=fwd_ms, pre_ms=pre_ms, main_ms=main_ms, api_ms=api_ms,
-                device=torch.cuda.get_device_name(0))
+                device=torch.cuda.get_device_name(0), sdpa=gpu_sdpa(c, q, k, v, do, steps, warmup))
+
+
+def gpu_sdpa(c, q, k, v, do, steps, warmup):
+    """torch's own GPU scaled_dot_product_attention fwd+bwd on the same inputs
+    (fp16), each fused backend that accepts them, for comparison only."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
+    out = {}
+    for name, be in (("flash", SDPBackend.FLASH_ATTENTION),
+                     ("efficient", SDPBackend.EFFICIENT_ATTENTION)):
+        def sd():
+            for t in (qa, ka, va):
+                t.grad = None
+            with sdpa_kernel([be]):
+                torch.nn.functional.scaled_dot_product_attention(
+                    qa, ka, va, is_causal=c["causal"],
+                    enable_gqa=c["Hq"] != c["Hkv"]).backward(do)
+        try:
+            for _ in range(max(warmup, 1)):
+                sd()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                sd()
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) * 1e3 / steps
+            f_fwd, f_bwd = flops(c)
+            out[name] = {"ms_per_step": round(ms, 4),
+                         "tflops": round((f_fwd + f_bwd) / (ms * 1e-3) / 1e12, 2)}
+        except RuntimeError as ex:
+            out[name] = {"unavailable": str(ex).splitlines()[0][:160]}
+    return out
 
 
 def cpu_baseline(c, budget_s=20.0):
@@ -233,8 +268,8 @@ def read_traffic(workload):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -274,6 +309,7 @@ def main():
         "kernel_ms": {"fwd": round(r["fwd_ms"], 4), "bwd_preprocess": round(r["pre_ms"], 4),
                       "bwd_main": round(r["main_ms"], 4)},
         "api_ms_per_step": round(r["api_ms"], 4),
+        "torch_sdpa_gpu": r["sdpa"],
         "device": r["device"],
         "roofline": {"kernel": "bwd_main (fa_bwd_main)", "bound": "mfma",
                      "achieved": round(main_tf, 2), "peak": PEAK_FP16_TFLOPS,

@@ -29,7 +29,9 @@
 //              64-key tile, the 32-key half w/4; partials summed through LDS.
 //
 // Under causal masking phase 1 shrinks with t while phase 2 grows with t, so
-// the workgroups' total work is nearly equal without giving up parallelism;
+// the workgroups' total work is nearly equal without giving up parallelism
+// (phase-1 steps cost more than phase-2 steps, so the first key tiles also
+// hand part of their phase 1 to the workgroup of tile n_tiles-1-t);
 // 8 waves keep two waves on every SIMD at the headline shape, so one wave's
 // softmax arithmetic overlaps the other's matrix products.
 //
@@ -62,6 +64,15 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 128;  // rows a workgroup owns (keys in phase 1, queries in phase 2)
 constexpr int kSub = 64;    // rows per streamed tile (queries in 1, keys in 2)
+static_assert(kTile == kBwdTile, "workspace layout assumes this key tile");
+// Causal split of key tile u (see bwd_kernel): floor((group * (n_tiles-1-2u) *
+// kSplitNum - kSplitBias) / 256) of its phase-1 iterations move to workgroup
+// n_tiles-1-u. Phase-1 steps cost ~1.26x phase-2 steps, which would balance
+// at ~0.21 iterations per unit; with the slot traffic, a sweep of kSplitNum
+// over 30..100 at the headline shape was fastest at 46..53 (-3.4% against no
+// split; 80 gave no gain, 100 lost).
+constexpr int kSplitNum = 50;
+constexpr int kSplitBias = 5;
 
 // LDS: every tile is its own __shared__ object (declared in bwd_kernel), so
 // the compiler can tell that a step's reads never touch the tiles that the
@@ -87,10 +98,15 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
                                                       const float* __restrict__ Lse,
                                                       float* __restrict__ dvec,
                                                       float* __restrict__ lse2, long rows,
-                                                      int Hq, int N, Strides st) {
+                                                      int Hq, int N, Strides st,
+                                                      unsigned* __restrict__ counters,
+                                                      int n_counters) {
   constexpr int kLanesPerRow = D / 8;
   constexpr int kRowsPerBlock = 256 / kLanesPerRow;
   const int tid = threadIdx.x;
+  // The main kernel's split-tile counters start at zero (it leaves them zero,
+  // but a fresh workspace holds anything). n_counters < rows <= threads.
+  if (const long c = (long)blockIdx.x * 256 + tid; c < n_counters) counters[c] = 0u;
   const long row = (long)blockIdx.x * kRowsPerBlock + tid / kLanesPerRow;
   const int c8 = (tid % kLanesPerRow) * 8;
   float acc = 0.f;
@@ -142,6 +158,40 @@ __device__ __forceinline__ void partial_add(const float* region, floatx16 (&acc)
       const floatx4 v = *reinterpret_cast<const floatx4*>(region + ((k * 4 + g4) * 64 + lane) * 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[k0 + k][4 * g4 + e] += v[e];
+    }
+}
+
+// A split key tile's partial dK^T/dV^T pass between two workgroups through a
+// workspace slot. They may run on different XCDs, whose L2 caches are not
+// coherent with each other, so the slot is written and read with
+// device-coherent accesses (cache policy sc1: stores write through to the
+// device-coherent level before they count as complete, loads bypass
+// non-coherent copies). Slot layout [w4][k][g4][lane] x 4 floats: every
+// instruction moves 1 KB of consecutive bytes.
+constexpr int kDeviceCoherent = 16;  // sc1 bit of the buffer intrinsics' cache-policy operand
+template <int n>
+__device__ __forceinline__ void slot_store(rsrc_t r, const floatx16 (&acc)[n], int w4, int lane) {
+#pragma unroll
+  for (int k = 0; k < n; ++k)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const floatx4 v = {acc[k][4 * g4], acc[k][4 * g4 + 1], acc[k][4 * g4 + 2], acc[k][4 * g4 + 3]};
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, lane * 16,
+                                             ((w4 * n + k) * 4 + g4) * 1024, kDeviceCoherent);
+    }
+}
+template <int n>
+__device__ __forceinline__ void slot_add(rsrc_t r, floatx16 (&acc)[n], int w4, int lane) {
+#pragma unroll
+  for (int k = 0; k < n; ++k)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const floatx4 v = __builtin_bit_cast(
+          floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, lane * 16,
+                                                         ((w4 * n + k) * 4 + g4) * 1024,
+                                                         kDeviceCoherent));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[k][4 * g4 + e] += v[e];
     }
 }
 
@@ -249,8 +299,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     float* __restrict__ dQ, half_t* __restrict__ dQh, half_t* __restrict__ dK,
     half_t* __restrict__ dV,
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2,
-    Strides stq, Strides stk) {
+    Strides stq, Strides stk, unsigned* __restrict__ counters, float* __restrict__ slots,
+    int split_num, int split_bias) {
   using L = BwdLds<D>;
+  constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
   // The larger alignment makes the compiler place the four staged tiles first,
   // in the low 64 KB of LDS, where the tile base fits the 16-bit immediate of
@@ -259,6 +311,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   __shared__ __align__(1024) half_t ta1[L::kTileHalves], tb1[L::kTileHalves];
   __shared__ __align__(16) float vec0[2 * kSub], vec1[2 * kSub];
   __shared__ __align__(16) half_t kres[L::kKVTileHalves], vres[L::kKVTileHalves];
+  __shared__ unsigned xflag;  // a split tile's counter, as one thread read it
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -271,8 +324,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
 
   const int wi = xcd_work_index(n_tiles * BHkv);
   if (wi < 0) return;
-  const int bkv = wi / n_tiles;            // over B*Hkv
-  const int t0 = (wi % n_tiles) * kTile;   // first row this workgroup owns
+  const int bkv = wi / n_tiles;  // over B*Hkv
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
@@ -298,30 +350,58 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   };
 
   // =========================== phase 1: dK, dV ===========================
-  {
-    const int jw = t0 + w4 * 32;  // this wave's key rows
+  // Causal balance: phase 1 of key tile u costs more than phase 2 of query
+  // tile u saves, so the workgroups of the first tiles would finish last. Key
+  // tile u < n_tiles-1-u hands the last split(u) of its (query head, query
+  // tile) iterations to the workgroup of tile n_tiles-1-u, which runs them
+  // before its own tile. The two partial dK/dV sums meet in a workspace slot:
+  // whichever workgroup finishes second adds the other's partial to its own
+  // and stores the result (fp32 a + b == b + a, so the outcome does not depend
+  // on which one that is).
+  auto n_iters = [&](int u) {
+    return group * ((N - (CAUSAL ? u * kTile : 0) + kSub - 1) / kSub);
+  };
+  auto split = [&](int u) {
+    const int m = n_tiles - 1 - 2 * u;
+    if (!CAUSAL || m <= 0) return 0;
+    return max(0, min((group * m * split_num - split_bias) >> 8, n_iters(u) - 1));
+  };
+  const int tw = wi % n_tiles;
+  const int partner = n_tiles - 1 - tw;
+  const int x_help = partner < tw ? split(partner) : 0;  // run first, for tile `partner`
+  const int x_own = tw < partner ? split(tw) : 0;        // given to workgroup `partner`
+  const int pairs = n_tiles / 2;
+  // One inlined copy per item: a loop over the two items made the compiler
+  // keep fewer LDS operands in flight in the step (8% slower).
+  auto run_item = [&](const bool helping) {
+    const int tile = helping ? partner : tw;
+    const int tp0 = tile * kTile;  // first key row of this item
+    const int jw = tp0 + w4 * 32;  // this wave's key rows
     const int j_col = jw + l32;
+    const int n_it = n_iters(tile);
+    const int it_begin = helping ? n_it - x_help : 0;
+    const int it_end = helping ? n_it : n_it - x_own;
+    const bool shared = helping || x_own > 0;
     KVWave<D, CAUSAL, BOUNDS> w;
     {
-      TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows t0 .. t0+kTile-1
+      TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
       plan_kv.init(wave, lane, stk.n);
 #pragma unroll
       for (int u = 0; u < decltype(plan_kv)::TL::kParts; ++u) {
-        plan_kv.part(kres, rk, t0, wave, u);
-        plan_kv.part(vres, rv, t0, wave, u);
+        plan_kv.part(kres, rk, tp0, wave, u);
+        plan_kv.part(vres, rv, tp0, wave, u);
       }
     }
 #pragma unroll
     for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
 
-    const int i_start = CAUSAL ? t0 : 0;  // t0 is a multiple of kSub
+    const int i_start = CAUSAL ? tp0 : 0;  // tp0 is a multiple of kSub
     const int n_qt = (N - i_start + kSub - 1) / kSub;
-    const int n_it = group * n_qt;  // (query head, query tile) pairs, flattened
 
     // Q, dO tiles and lse2, dvec of flattened step `it` (clamped to the last
     // one, so that every step issues the same loads) into one stage.
     auto fetch = [&](int it, half_t* tq, half_t* to, float* tv) {
-      it = min(it, n_it - 1);
+      it = min(it, it_end - 1);
       const int g = it / n_qt;
       const int i0 = i_start + (it % n_qt) * kSub;
       const int hq = hkv * group + g;
@@ -353,20 +433,20 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       __syncthreads();
     };
 
-    fetch(0, ta0, tb0, vec0);
+    fetch(it_begin, ta0, tb0, vec0);
     wait_vmem();
     __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) w.kb[kk] = tile_read16<D>(kres, w4 * 32, kk, roff);
-    int it = 0;
-    for (; it + 2 <= n_it; it += 2) {
+    int it = it_begin;
+    for (; it + 2 <= it_end; it += 2) {
       step(it, P0{});
       step(it + 1, P1{});
     }
-    if (it < n_it) step(it, P0{});
+    if (it < it_end) step(it, P0{});
 
-    // Sum the two halves' partials (dV^T in region 2*w4, dK^T in 2*w4 + 1),
-    // then dK (scaled) and dV leave as fp16.
+    // Sum the two halves' partials (dV^T in region 2*w4, dK^T in region
+    // 2*w4 + 1) into the waves of the lower half.
     if (half) {
       partial_store<D / 32>(region(2 * w4), w.acc, 0, lane);
       partial_store<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
@@ -375,27 +455,61 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     if (!half) {
       partial_add<D / 32>(region(2 * w4), w.acc, 0, lane);
       partial_add<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
-      if (!BOUNDS || j_col < N) {
-        half_t* dkrow = dK + kv_off + (size_t)j_col * stk.n;
-        half_t* dvrow = dV + kv_off + (size_t)j_col * stk.n;
+    }
+    bool finish = true;
+    if (shared) {
+      const int u = helping ? partner : tw;
+      unsigned* cnt = counters + (size_t)bkv * pairs + u;
+      float* const pair_slots = slots + (size_t)(bkv * pairs + u) * 2 * kSlotFloats;
+      const rsrc_t mine = make_rsrc(pair_slots + (helping ? kSlotFloats : 0), kSlotFloats * 4);
+      const rsrc_t other = make_rsrc(pair_slots + (helping ? 0 : kSlotFloats), kSlotFloats * 4);
+      // The owner usually finishes second: if the helper is done, it adds the
+      // helper's partial without publishing its own.
+      finish = false;
+      if (!helping) {
+        if (tid == 0) xflag = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        finish = xflag == 1u;
+        __syncthreads();
+      }
+      if (!finish) {
+        if (!half) slot_store<2 * (D / 32)>(mine, w.acc, w4, lane);
+        wait_vmem();  // the partial has reached the device-coherent level
+        __syncthreads();
+        if (tid == 0)
+          xflag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        finish = xflag == 1u;
+      }
+      if (finish) {
+        if (!half) slot_add<2 * (D / 32)>(other, w.acc, w4, lane);
+        if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // dK (scaled) and dV leave as fp16.
+    if (finish && !half && (!BOUNDS || j_col < N)) {
+      half_t* dkrow = dK + kv_off + (size_t)j_col * stk.n;
+      half_t* dvrow = dV + kv_off + (size_t)j_col * stk.n;
 #pragma unroll
-        for (int cb = 0; cb < D / 32; ++cb) {
+      for (int cb = 0; cb < D / 32; ++cb) {
 #pragma unroll
-          for (int g4 = 0; g4 < 4; ++g4) {
-            half4 k4, v4;
+        for (int g4 = 0; g4 < 4; ++g4) {
+          half4 k4, v4;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              k4[e] = (half_t)(w.acc[D / 32 + cb][4 * g4 + e] * scale);
-              v4[e] = (half_t)w.acc[cb][4 * g4 + e];
-            }
-            *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
-            *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
+          for (int e = 0; e < 4; ++e) {
+            k4[e] = (half_t)(w.acc[D / 32 + cb][4 * g4 + e] * scale);
+            v4[e] = (half_t)w.acc[cb][4 * g4 + e];
           }
+          *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
+          *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
         }
       }
     }
-    __syncthreads();  // the exchange regions are the next phase's staging memory
-  }
+    __syncthreads();  // the exchange regions are the next item's or phase's staging memory
+  };
+  if (x_help > 0) run_item(true);
+  run_item(false);
+  const int t0 = tw * kTile;  // query rows of phase 2
 
   // ============================== phase 2: dQ ==============================
   {
@@ -486,7 +600,7 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   hipLaunchKernelGGL((bwd_pre_kernel<D>), grid, dim3(256), 0, (hipStream_t)a.stream,
                      (const half_t*)a.o, (const half_t*)a.dO, a.lse, a.dvec, a.lse2, rows, a.Hq,
-                     a.N, make_strides(a.layout, a.Hq, a.N, D));
+                     a.N, make_strides(a.layout, a.Hq, a.N, D), a.counters, a.n_counters);
   return hipGetLastError();
 }
 
@@ -500,7 +614,8 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D));
+                     make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots, kSplitNum,
+                     kSplitBias);
   return hipGetLastError();
 }
 

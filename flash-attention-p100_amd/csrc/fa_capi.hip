@@ -31,11 +31,6 @@ int check_bnhd(int Hq, int N, int D) {
 
 int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }
 
-// One (B, Hq, N) float32 vector, rounded up to 256 bytes.
-size_t vec_bytes(int B, int Hq, int N) {
-  return ((size_t)B * Hq * N * sizeof(float) + 255) & ~(size_t)255;
-}
-
 }  // namespace
 
 extern "C" {
@@ -79,7 +74,7 @@ int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse
 
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
   if (check_shape(B, Hq, Hkv, N, D) != FA_OK) return 0;
-  return 2 * vec_bytes(B, Hq, N);
+  return fa::bwd_workspace(B, Hq, Hkv, N, D).total;
 }
 
 static int bwd_pre(const void* dO, const void* o, const float* lse, void* workspace,
@@ -89,13 +84,19 @@ static int bwd_pre(const void* dO, const void* o, const float* lse, void* worksp
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!dO || !o || !lse || !workspace) return FA_ERR_NULL;
-  if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
+  // The vectors and counters this writes lie before the slots, whose offset
+  // depends on neither Hkv nor D.
+  const fa::BwdWorkspace w = fa::bwd_workspace(B, Hq, Hq, N, D);
+  if (workspace_bytes < w.slots) return FA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
   fa::BwdArgs a{};
   a.dO = dO;
   a.o = o;
   a.lse = lse;
-  a.dvec = static_cast<float*>(workspace);
-  a.lse2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + vec_bytes(B, Hq, N));
+  a.dvec = reinterpret_cast<float*>(ws + w.dvec);
+  a.lse2 = reinterpret_cast<float*>(ws + w.lse2);
+  a.counters = reinterpret_cast<unsigned*>(ws + w.counters);
+  a.n_counters = w.n_counters;
   a.B = B;
   a.Hq = Hq;
   a.Hkv = Hq;
@@ -113,22 +114,26 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* wor
 
 // Shared by the main-kernel entry points: fp32 dq or fp16 dq16, either layout.
 static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
-                    const void* workspace, size_t workspace_bytes, float* dq, void* dq16,
+                    void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
                     int layout, void* stream) {
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !dO || !workspace || !(dq || dq16) || !dk || !dv) return FA_ERR_NULL;
-  if (workspace_bytes < 2 * vec_bytes(B, Hq, N)) return FA_ERR_WORKSPACE;
+  const fa::BwdWorkspace w = fa::bwd_workspace(B, Hq, Hkv, N, D);
+  if (workspace_bytes < w.total) return FA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
   fa::BwdArgs a{};
   a.q = q;
   a.k = k;
   a.v = v;
   a.dO = dO;
-  a.dvec = const_cast<float*>(static_cast<const float*>(workspace));
-  a.lse2 = reinterpret_cast<float*>(const_cast<char*>(static_cast<const char*>(workspace)) +
-                                    vec_bytes(B, Hq, N));
+  a.dvec = reinterpret_cast<float*>(ws + w.dvec);
+  a.lse2 = reinterpret_cast<float*>(ws + w.lse2);
+  a.counters = reinterpret_cast<unsigned*>(ws + w.counters);
+  a.n_counters = w.n_counters;
+  a.slots = reinterpret_cast<float*>(ws + w.slots);
   a.dq = dq;
   a.dq16 = dq16;
   a.dk = dk;
@@ -159,7 +164,7 @@ static int bwd_half_dq(const void* q, const void* k, const void* v, const void* 
                   causal, layout, stream);
 }
 
-int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, const void* workspace,
+int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, void* workspace,
                 size_t workspace_bytes, float* dq, void* dk, void* dv, int B, int Hq, int Hkv,
                 int N, int D, int causal, void* stream) {
   if (!dq) return FA_ERR_NULL;

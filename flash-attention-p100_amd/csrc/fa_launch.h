@@ -33,6 +33,32 @@ struct FwdArgs {
   int layout = kBHND;  // of q, k, v, o (lse is always dense (B, Hq, N))
 };
 
+// Backward workspace, in this order (each part 256-byte aligned):
+//   dvec = rowsum(dO * O) and lse2 = LSE * log2(e), (B, Hq, N) fp32 each;
+//   one counter per pair of key tiles (u, n_tiles-1-u) per (b, head), which
+//   the preprocess kernel zeroes (sized by Hq, which bounds Hkv, so that the
+//   preprocess needs no Hkv);
+//   two fp32 partial dK/dV slots per such pair and (b, kv head).
+constexpr int kBwdTile = 128;  // key rows of one backward workgroup
+struct BwdWorkspace {
+  size_t dvec, lse2, counters, slots, total;
+  int n_counters;
+};
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+inline size_t bwd_slot_floats(int D) { return (size_t)kBwdTile * D * 2; }  // dK^T, dV^T
+inline BwdWorkspace bwd_workspace(int B, int Hq, int Hkv, int N, int D) {
+  BwdWorkspace w;
+  const size_t vec = align256((size_t)B * Hq * N * sizeof(float));
+  const int pairs_per_head = ((N + kBwdTile - 1) / kBwdTile) / 2;
+  w.dvec = 0;
+  w.lse2 = vec;
+  w.counters = 2 * vec;
+  w.n_counters = B * Hq * pairs_per_head;
+  w.slots = w.counters + align256((size_t)w.n_counters * sizeof(unsigned));
+  w.total = w.slots + (size_t)B * Hkv * pairs_per_head * 2 * bwd_slot_floats(D) * sizeof(float);
+  return w;
+}
+
 struct BwdArgs {
   const void* q;
   const void* k;
@@ -50,6 +76,9 @@ struct BwdArgs {
   bool causal;
   void* stream;
   int layout = kBHND;  // of q, k, v, dO, o, dq, dk, dv (lse, workspace dense)
+  unsigned* counters = nullptr;  // workspace: per key-tile pair (zeroed by the preprocess)
+  int n_counters = 0;
+  float* slots = nullptr;        // workspace: partial dK/dV of split key tiles
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

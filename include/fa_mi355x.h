@@ -78,7 +78,11 @@ int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse
 /*
  * Bytes of device workspace fa_bwd needs: two (B, Hq, N) float32 vectors, the
  * reference's `dvec` (fa_p100_ext.cu:124) and the saved LSE pre-multiplied by
- * log2(e), each rounded up to 256 bytes. 0 for an invalid shape.
+ * log2(e); then B*Hq*floor(ceil(N/128)/2) uint32 counters; then, for each
+ * (b, kv head) and each of those floor(ceil(N/128)/2) pairs of 128-row key
+ * tiles, two fp32 partial-sum slots of 128*D*2 floats (the backward's causal
+ * load balancing splits a short key tile's work between two workgroups).
+ * Each part is rounded up to 256 bytes. 0 for an invalid shape.
  */
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D);
 
@@ -88,7 +92,9 @@ size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D);
  * inputs/outputs. Writes dq (fp32, B,Hq,N,D), dk and dv (fp16, B,Hkv,N,D);
  * every element of the three outputs is overwritten. `workspace` must hold
  * fa_bwd_workspace_bytes() bytes. Equivalent to fa_bwd_preprocess() followed
- * by fa_bwd_main(). Deterministic: no atomics are used.
+ * by fa_bwd_main(). Deterministic: no atomic adds touch the results (an
+ * atomic counter only decides which of two workgroups adds their two partial
+ * sums, and fp32 addition is commutative), so repeated calls are bit-identical.
  */
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO,
            const void* o, const float* lse, float* dq, void* dk, void* dv,
@@ -121,8 +127,9 @@ int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO,
 /*
  * First phase of fa_bwd, the counterpart of bwd_preprocess
  * (flash_bwd.cuh:65-78): fills `workspace` with dvec = rowsum(dO * o) and
- * lse * log2(e), both fp32 (B,Hq,N). Exposed so a host can time or schedule
- * the phases separately.
+ * lse * log2(e), both fp32 (B,Hq,N), and zeroes its counters. Exposed so a
+ * host can time or schedule the phases separately. `workspace_bytes` must
+ * cover at least the vectors and counters (fa_bwd_workspace_bytes() does).
  */
 int fa_bwd_preprocess(const void* dO, const void* o, const float* lse,
                       void* workspace, size_t workspace_bytes,
@@ -133,10 +140,11 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse,
  * (flash_bwd.cuh:95-464, launched at 479-483): dK, dV (key/value-stationary)
  * and dQ (query-stationary, recomputing S and dP instead of the reference's
  * fp32 atomicAdd) in one launch, from the workspace fa_bwd_preprocess filled.
- * Overwrites dq, dk and dv.
+ * Overwrites dq, dk and dv, and uses the workspace's counters and slots
+ * (leaving the counters zero). Two calls must not share a workspace at once.
  */
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
-                const void* workspace, size_t workspace_bytes, float* dq,
+                void* workspace, size_t workspace_bytes, float* dq,
                 void* dk, void* dv, int B, int Hq, int Hkv, int N, int D,
                 int causal, void* stream);
 

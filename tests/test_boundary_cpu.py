@@ -27,8 +27,13 @@ def test_host_only_helpers():
     assert b"64 or 128" in lib.fa_error_string(10001)
     assert b"multiple" in lib.fa_error_string(10003)
     # two (B, Hq, N) float32 vectors, each rounded up to 256 bytes; 0 if invalid.
-    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 128) == 2 * 8 * 4096 * 4
-    assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 512
+    # dvec + lse2 (256-aligned), counters per key-tile pair (by Hq), then two
+    # fp32 dK/dV slots of 128 x D x 2 per pair and (b, kv head).
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 128) == (
+        2 * 8 * 4096 * 4 + 8 * 16 * 4 + 8 * 16 * 2 * 128 * 128 * 2 * 4)
+    assert lib.fa_bwd_workspace_bytes(2, 32, 8, 3001, 128) == (
+        2 * 768256 + 2 * 32 * 12 * 4 + 2 * 8 * 12 * 2 * 128 * 128 * 2 * 4)
+    assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 512  # one key tile: no pairs
     assert lib.fa_bwd_workspace_bytes(1, 8, 3, 4096, 128) == 0
     assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 80) == 0
 

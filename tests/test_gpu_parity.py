@@ -211,7 +211,9 @@ def test_noncontiguous_inputs_and_current_stream():
 
 
 def test_backward_is_deterministic():
-    """No atomics anywhere: repeated runs give bit-identical gradients."""
+    """No atomic adds on results (split key tiles' partials are added by
+    whichever workgroup finishes second, and fp32 a + b == b + a): repeated
+    runs give bit-identical gradients."""
     q, k, v, do = make_inputs(1, 8, 2, 300, 128, seed=17)
     a = run_flash(q, k, v, do, True)
     b = run_flash(q, k, v, do, True)
@@ -299,3 +301,46 @@ def test_bnhd_capi_matches_dense_capi():
     assert torch.equal(tb(o), ob) and torch.equal(lse, lseb)
     for a, b in ((dq, dqb), (dk, dkb), (dv, dvb)):
         assert torch.equal(tb(a), b)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B,Hq,Hkv,N", [(1, 4, 4, 1536), (2, 8, 2, 1000)])
+def test_split_key_tiles_share_a_workspace_across_calls(D, B, Hq, Hkv, N):
+    """Causal backward: the first key tiles' phase-1 work is split between two
+    workgroups whose partial dK/dV meet in workspace slots. One workspace
+    serves inputs A, then B, then A again, with dk/dv pre-filled with NaN
+    each time: A's gradients repeat bit for bit, B's match the oracle (a
+    stale, lost or doubly added partial fails one of the two), and the
+    split counters are back at zero after each call."""
+    lib = load_capi()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    align = lambda n: (n + 255) // 256 * 256
+    c0 = 2 * align(B * Hq * N * 4)
+    n_counters = B * Hq * (((N + 127) // 128) // 2)
+
+    def run(seed):
+        q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=seed))
+        o, lse = torch.empty_like(q), torch.empty(B, Hq, N, device=DEV)
+        assert lib.fa_fwd(p(q), p(k), p(v), p(o), p(lse), B, Hq, Hkv, N, D, 1, 0, s) == 0
+        dq = torch.empty(B, Hq, N, D, device=DEV)
+        dk = torch.full_like(k, float("nan"))
+        dv = torch.full_like(v, float("nan"))
+        rc = lib.fa_bwd(p(q), p(k), p(v), p(do), p(o), p(lse), p(dq), p(dk), p(dv), p(ws),
+                        ws_bytes, B, Hq, Hkv, N, D, 1, s)
+        assert rc == 0, lib.fa_error_string(rc)
+        torch.cuda.synchronize()
+        counters = ws[c0:c0 + 4 * n_counters].view(torch.int32)
+        assert int(counters.abs().sum()) == 0, "split counters not reset"
+        return (q, k, v, do), (dq.clone(), dk.clone(), dv.clone())
+
+    _, first = run(1)
+    inputs_b, got_b = run(2)
+    _, again = run(1)
+    for x, y in zip(first, again):
+        assert torch.equal(x, y)
+    q, k, v, do = (t.cpu().numpy() for t in inputs_b)
+    ref = ora.attention_bwd(q, k, v, do, True)
+    check_grads(tuple(np64(t) for t in got_b), ref, f"split D{D} {B},{Hq}/{Hkv},N{N}")
