@@ -1,0 +1,407 @@
+// Torch-free driver over the C ABI (test infrastructure): the counterpart of
+// the reference's standalone drivers, attention.cu (forward against a CPU
+// reference, 4 input regimes), bwd.cu (backward against a float64 analytic
+// reference, finite-difference check) and its peak sweep, for this library.
+//
+//   fa_driver check         GPU forward + backward vs the float64 C oracle
+//                           (oracle/attention_ref.c): the reference's 4 input
+//                           regimes x D x causal (attention.cu:120-160,
+//                           test_fa_p100.py:107-139), plus GQA, ragged N and
+//                           split-key-tile shapes. Exit status 1 on any miss.
+//   fa_driver fd            central finite differences of the oracle's loss
+//                           against its analytic backward (bwd.cu:136-160,
+//                           h = 1e-4, bar 1e-4). CPU only.
+//   fa_driver bench [quick] fwd / bwd / fwd+bwd TFLOPS over shapes, FLOPs by
+//                           the reference's convention (attention.cu:219,
+//                           bwd.cu:246), HIP events around back-to-back calls.
+//   fa_driver peak          fp16 MFMA throughput probe: independent
+//                           v_mfma_f32_32x32x16_f16 chains on every SIMD, the
+//                           measured ceiling for the roofline (the reference's
+//                           half2 peak sweep measured its SIMT ceiling).
+//
+// Inputs come from a fixed-seed splitmix64 + Box-Muller generator, rounded to
+// fp16; the oracle sees exactly those fp16 values.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/fa_mi355x.h"
+#include "../../oracle/attention_ref.h"
+
+namespace {
+
+#define HIP_OK(x)                                                                  \
+  do {                                                                             \
+    hipError_t e_ = (x);                                                           \
+    if (e_ != hipSuccess) {                                                        \
+      std::fprintf(stderr, "%s:%d %s: %s\n", __FILE__, __LINE__, #x,               \
+                   hipGetErrorString(e_));                                         \
+      std::exit(2);                                                                \
+    }                                                                              \
+  } while (0)
+#define FA_OK_(x)                                                                  \
+  do {                                                                             \
+    int rc_ = (x);                                                                 \
+    if (rc_ != 0) {                                                                \
+      std::fprintf(stderr, "%s:%d %s: %s\n", __FILE__, __LINE__, #x,               \
+                   fa_error_string(rc_));                                          \
+      std::exit(2);                                                                \
+    }                                                                              \
+  } while (0)
+
+// Bars (BASELINE): forward max-abs <= 4e-3, LSE max-abs <= 1e-3, gradients
+// relative L2 <= 1e-2; the reference's max|err|/RMS(ref) < 6e-2 on all
+// (test_fa_p100.py:24, 35-37).
+constexpr double kFwdMaxAbs = 4e-3, kLseMaxAbs = 1e-3, kGradRelL2 = 1e-2, kRefRel = 6e-2;
+
+struct Rng {
+  uint64_t s;
+  uint64_t next() {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  double uniform() { return ((next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+  double normal() {
+    const double u = uniform(), v = uniform();
+    return std::sqrt(-2.0 * std::log(u)) * std::cos(6.283185307179586 * v);
+  }
+};
+
+struct Shape {
+  int B, Hq, Hkv, N, D, causal;
+  size_t nq() const { return (size_t)B * Hq * N * D; }
+  size_t nk() const { return (size_t)B * Hkv * N * D; }
+  size_t nl() const { return (size_t)B * Hq * N; }
+  double fwd_flops() const { return 4.0 * B * Hq * (double)N * N * D / (causal ? 2.0 : 1.0); }
+};
+
+// fp16 values and the same values as float64.
+struct Host16 {
+  std::vector<_Float16> h;
+  std::vector<double> d;
+  void fill(size_t n, Rng& r, double scale) {
+    h.resize(n);
+    d.resize(n);
+    for (size_t i = 0; i < n; ++i) {
+      h[i] = (_Float16)(r.normal() * scale);
+      d[i] = (double)h[i];
+    }
+  }
+};
+
+template <class T>
+T* dalloc(size_t n) {
+  void* p = nullptr;
+  HIP_OK(hipMalloc(&p, n * sizeof(T) + 256));
+  return static_cast<T*>(p);
+}
+
+double max_abs(const std::vector<double>& a, const std::vector<double>& b) {
+  double m = 0;
+  for (size_t i = 0; i < a.size(); ++i) m = std::fmax(m, std::fabs(a[i] - b[i]));
+  return m;
+}
+double rel_l2(const std::vector<double>& a, const std::vector<double>& ref) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < a.size(); ++i) {
+    num += (a[i] - ref[i]) * (a[i] - ref[i]);
+    den += ref[i] * ref[i];
+  }
+  return std::sqrt(num / (den > 0 ? den : 1e-300));
+}
+double rel_max_rms(const std::vector<double>& a, const std::vector<double>& ref) {
+  double ss = 0;
+  for (double x : ref) ss += x * x;
+  const double rms = std::sqrt(ss / (double)ref.size());
+  return max_abs(a, ref) / (rms > 0 ? rms : 1e-300);
+}
+
+// One forward + backward on the GPU through the C ABI; outputs as float64.
+struct GpuResult {
+  std::vector<double> o, lse, dq, dk, dv;
+};
+GpuResult run_gpu(const Shape& s, const Host16& q, const Host16& k, const Host16& v,
+                  const Host16& g) {
+  _Float16 *dq_in = dalloc<_Float16>(s.nq()), *dk_in = dalloc<_Float16>(s.nk()),
+           *dv_in = dalloc<_Float16>(s.nk()), *dgo = dalloc<_Float16>(s.nq()),
+           *dout = dalloc<_Float16>(s.nq()), *ddk = dalloc<_Float16>(s.nk()),
+           *ddv = dalloc<_Float16>(s.nk());
+  float *dlse = dalloc<float>(s.nl()), *ddq = dalloc<float>(s.nq());
+  HIP_OK(hipMemcpy(dq_in, q.h.data(), s.nq() * 2, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dk_in, k.h.data(), s.nk() * 2, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dv_in, v.h.data(), s.nk() * 2, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(dgo, g.h.data(), s.nq() * 2, hipMemcpyHostToDevice));
+  const size_t ws_bytes = fa_bwd_workspace_bytes(s.B, s.Hq, s.Hkv, s.N, s.D);
+  char* ws = dalloc<char>(ws_bytes);
+  FA_OK_(fa_fwd(dq_in, dk_in, dv_in, dout, dlse, s.B, s.Hq, s.Hkv, s.N, s.D, s.causal, 0,
+                nullptr));
+  FA_OK_(fa_bwd(dq_in, dk_in, dv_in, dgo, dout, dlse, ddq, ddk, ddv, ws, ws_bytes, s.B, s.Hq,
+                s.Hkv, s.N, s.D, s.causal, nullptr));
+  HIP_OK(hipDeviceSynchronize());
+  std::vector<_Float16> h16(s.nq());
+  std::vector<float> h32(s.nq());
+  GpuResult r;
+  auto to_d = [](const auto& src, size_t n) {
+    std::vector<double> out(n);
+    for (size_t i = 0; i < n; ++i) out[i] = (double)src[i];
+    return out;
+  };
+  HIP_OK(hipMemcpy(h16.data(), dout, s.nq() * 2, hipMemcpyDeviceToHost));
+  r.o = to_d(h16, s.nq());
+  HIP_OK(hipMemcpy(h32.data(), dlse, s.nl() * 4, hipMemcpyDeviceToHost));
+  r.lse = to_d(h32, s.nl());
+  HIP_OK(hipMemcpy(h32.data(), ddq, s.nq() * 4, hipMemcpyDeviceToHost));
+  r.dq = to_d(h32, s.nq());
+  HIP_OK(hipMemcpy(h16.data(), ddk, s.nk() * 2, hipMemcpyDeviceToHost));
+  r.dk = to_d(h16, s.nk());
+  HIP_OK(hipMemcpy(h16.data(), ddv, s.nk() * 2, hipMemcpyDeviceToHost));
+  r.dv = to_d(h16, s.nk());
+  for (void* p : {(void*)dq_in, (void*)dk_in, (void*)dv_in, (void*)dgo, (void*)dout,
+                  (void*)ddk, (void*)ddv, (void*)dlse, (void*)ddq, (void*)ws})
+    HIP_OK(hipFree(p));
+  return r;
+}
+
+bool check_case(const char* name, const Shape& s, double scale_qk, uint64_t seed) {
+  Rng r{seed};
+  Host16 q, k, v, g;
+  q.fill(s.nq(), r, scale_qk);
+  k.fill(s.nk(), r, scale_qk);
+  v.fill(s.nk(), r, 1.0);
+  g.fill(s.nq(), r, 1.0);
+  const GpuResult got = run_gpu(s, q, k, v, g);
+  std::vector<double> o(s.nq()), lse(s.nl()), dq(s.nq()), dk(s.nk()), dv(s.nk());
+  ora_fwd(q.d.data(), k.d.data(), v.d.data(), o.data(), lse.data(), s.B, s.Hq, s.Hkv, s.N, s.D,
+          s.causal);
+  ora_bwd(q.d.data(), k.d.data(), v.d.data(), g.d.data(), dq.data(), dk.data(), dv.data(), s.B,
+          s.Hq, s.Hkv, s.N, s.D, s.causal);
+  const double fo = max_abs(got.o, o), fr = rel_max_rms(got.o, o), fl = max_abs(got.lse, lse);
+  // A gradient that is exactly zero in float64 (N = 1: softmax over one key
+  // is constant, so dQ = dK = 0) has no relative error: it must be ~0.
+  auto grad_ok = [](const std::vector<double>& got, const std::vector<double>& ref, double& l2) {
+    bool zero = true;
+    for (double x : ref) zero &= x == 0.0;
+    if (zero) {
+      l2 = max_abs(got, ref);
+      return l2 <= 1e-6;
+    }
+    l2 = rel_l2(got, ref);
+    return l2 <= kGradRelL2 && rel_max_rms(got, ref) < kRefRel;
+  };
+  double q2, k2, v2;
+  const bool gq = grad_ok(got.dq, dq, q2), gk = grad_ok(got.dk, dk, k2), gv = grad_ok(got.dv, dv, v2);
+  const bool ok = fo <= kFwdMaxAbs && fr < kRefRel && fl <= kLseMaxAbs && gq && gk && gv;
+  std::printf("%-22s B%d Hq%-2d Hkv%-2d N%-5d D%-3d %s | o %.1e (%.1e) lse %.1e | dQ %.1e dK %.1e"
+              " dV %.1e | %s\n",
+              name, s.B, s.Hq, s.Hkv, s.N, s.D, s.causal ? "causal" : "dense ", fo, fr, fl, q2,
+              k2, v2, ok ? "ok" : "FAIL");
+  std::fflush(stdout);
+  return ok;
+}
+
+int cmd_check() {
+  bool ok = true;
+  struct Regime {
+    const char* name;
+    double scale;
+  } regimes[] = {{"1 N(0,1)", 1.0}, {"2 large x10", 10.0}, {"3 near-uniform", 0.05},
+                 {"4 near-one-hot", 3.0}};
+  uint64_t seed = 1;
+  for (const Regime& g : regimes)
+    for (int D : {64, 128})
+      for (int causal : {0, 1}) ok &= check_case(g.name, {1, 4, 4, 256, D, causal}, g.scale, seed++);
+  ok &= check_case("GQA ragged", {2, 8, 2, 333, 128, 1}, 1.0, seed++);
+  ok &= check_case("GQA ragged", {2, 8, 2, 333, 128, 0}, 1.0, seed++);
+  ok &= check_case("MQA split tiles", {1, 4, 1, 1000, 64, 1}, 1.0, seed++);
+  ok &= check_case("MHA split tiles", {1, 2, 2, 1536, 128, 1}, 1.0, seed++);
+  ok &= check_case("N=1", {1, 2, 1, 1, 64, 1}, 1.0, seed++);
+  std::printf("check: %s\n", ok ? "all ok" : "FAILED");
+  return ok ? 0 : 1;
+}
+
+int cmd_fd() {
+  // The reference's method (bwd.cu:136-160): central differences of the loss
+  // sum(dO * O) in float64 with h = 1e-4 against the analytic gradient.
+  const double h = 1e-4, bar = 1e-4;
+  bool ok = true;
+  const Shape shapes[] = {{1, 2, 1, 17, 64, 1}, {1, 2, 2, 9, 128, 0}, {2, 4, 2, 13, 64, 1}};
+  uint64_t seed = 100;
+  for (const Shape& s : shapes) {
+    Rng r{seed++};
+    std::vector<double> q(s.nq()), k(s.nk()), v(s.nk()), g(s.nq());
+    for (auto* t : {&q, &k, &v, &g})
+      for (double& x : *t) x = r.normal();
+    std::vector<double> dq(s.nq()), dk(s.nk()), dv(s.nk());
+    ora_bwd(q.data(), k.data(), v.data(), g.data(), dq.data(), dk.data(), dv.data(), s.B, s.Hq,
+            s.Hkv, s.N, s.D, s.causal);
+    double worst = 0;
+    std::vector<double>* ins[] = {&q, &k, &v};
+    const std::vector<double>* grads[] = {&dq, &dk, &dv};
+    for (int t = 0; t < 3; ++t)
+      for (int n = 0; n < 24; ++n) {
+        std::vector<double>& x = *ins[t];
+        const size_t i = r.next() % x.size();
+        const double x0 = x[i];
+        x[i] = x0 + h;
+        const double lp = ora_loss(q.data(), k.data(), v.data(), g.data(), s.B, s.Hq, s.Hkv, s.N,
+                                   s.D, s.causal);
+        x[i] = x0 - h;
+        const double lm = ora_loss(q.data(), k.data(), v.data(), g.data(), s.B, s.Hq, s.Hkv, s.N,
+                                   s.D, s.causal);
+        x[i] = x0;
+        worst = std::fmax(worst, std::fabs((lp - lm) / (2 * h) - (*grads[t])[i]));
+      }
+    const bool pass = worst < bar;
+    ok &= pass;
+    std::printf("fd B%d Hq%d Hkv%d N%d D%d %s: max |fd - analytic| %.2e %s\n", s.B, s.Hq, s.Hkv,
+                s.N, s.D, s.causal ? "causal" : "dense", worst, pass ? "ok" : "FAIL");
+  }
+  return ok ? 0 : 1;
+}
+
+int cmd_bench(bool quick) {
+  std::vector<std::pair<const char*, Shape>> shapes = {
+      {"C3 headline", {1, 8, 8, 4096, 128, 1}}};
+  if (!quick) {
+    shapes.insert(shapes.end(), {{"C2", {1, 16, 16, 2048, 64, 1}},
+                                 {"C4 GQA ragged", {2, 32, 8, 3001, 128, 0}},
+                                 {"C5 layer", {1, 16, 8, 8192, 128, 1}},
+                                 {"N=1024", {4, 16, 16, 1024, 128, 1}},
+                                 {"N=16384", {1, 8, 8, 16384, 128, 1}},
+                                 {"N=4096 D=64", {1, 16, 16, 4096, 64, 1}},
+                                 {"N=4096 dense", {1, 8, 8, 4096, 128, 0}}});
+  }
+  std::printf("%-14s %-28s %9s %9s %9s %8s %8s %8s\n", "shape", "(B,Hq,Hkv,N,D,causal)",
+              "fwd ms", "bwd ms", "step ms", "fwd TF", "bwd TF", "step TF");
+  for (const auto& entry : shapes) {
+    const char* name = entry.first;
+    const Shape s = entry.second;
+    Rng r{7};
+    Host16 q, k, v, g;
+    q.fill(s.nq(), r, 1.0);
+    k.fill(s.nk(), r, 1.0);
+    v.fill(s.nk(), r, 1.0);
+    g.fill(s.nq(), r, 1.0);
+    _Float16 *dq_in = dalloc<_Float16>(s.nq()), *dk_in = dalloc<_Float16>(s.nk()),
+             *dv_in = dalloc<_Float16>(s.nk()), *dgo = dalloc<_Float16>(s.nq()),
+             *dout = dalloc<_Float16>(s.nq()), *ddk = dalloc<_Float16>(s.nk()),
+             *ddv = dalloc<_Float16>(s.nk());
+    float *dlse = dalloc<float>(s.nl()), *ddq = dalloc<float>(s.nq());
+    HIP_OK(hipMemcpy(dq_in, q.h.data(), s.nq() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dk_in, k.h.data(), s.nk() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dv_in, v.h.data(), s.nk() * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dgo, g.h.data(), s.nq() * 2, hipMemcpyHostToDevice));
+    const size_t ws_bytes = fa_bwd_workspace_bytes(s.B, s.Hq, s.Hkv, s.N, s.D);
+    char* ws = dalloc<char>(ws_bytes);
+    auto fwd = [&] {
+      FA_OK_(fa_fwd(dq_in, dk_in, dv_in, dout, dlse, s.B, s.Hq, s.Hkv, s.N, s.D, s.causal, 0,
+                    nullptr));
+    };
+    auto bwd = [&] {
+      FA_OK_(fa_bwd(dq_in, dk_in, dv_in, dgo, dout, dlse, ddq, ddk, ddv, ws, ws_bytes, s.B, s.Hq,
+                    s.Hkv, s.N, s.D, s.causal, nullptr));
+    };
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0));
+    HIP_OK(hipEventCreate(&e1));
+    const int reps = s.fwd_flops() > 2e11 ? 10 : 50;
+    auto timed = [&](auto&& fn) {
+      for (int i = 0; i < 5; ++i) fn();
+      HIP_OK(hipEventRecord(e0, nullptr));
+      for (int i = 0; i < reps; ++i) fn();
+      HIP_OK(hipEventRecord(e1, nullptr));
+      HIP_OK(hipEventSynchronize(e1));
+      float ms = 0;
+      HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+      return (double)ms / reps;
+    };
+    const double tf = timed(fwd), tb = timed(bwd), ts = timed([&] { fwd(); bwd(); });
+    const double ff = s.fwd_flops(), fb = 2.5 * ff;
+    char dims[64];
+    std::snprintf(dims, sizeof dims, "(%d,%d,%d,%d,%d,%d)", s.B, s.Hq, s.Hkv, s.N, s.D, s.causal);
+    std::printf("%-14s %-28s %9.4f %9.4f %9.4f %8.1f %8.1f %8.1f\n", name, dims, tf, tb, ts,
+                ff / tf / 1e9, fb / tb / 1e9, (ff + fb) / ts / 1e9);
+    std::fflush(stdout);
+    HIP_OK(hipEventDestroy(e0));
+    HIP_OK(hipEventDestroy(e1));
+    for (void* p : {(void*)dq_in, (void*)dk_in, (void*)dv_in, (void*)dgo, (void*)dout,
+                    (void*)ddk, (void*)ddv, (void*)dlse, (void*)ddq, (void*)ws})
+      HIP_OK(hipFree(p));
+  }
+  return 0;
+}
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+// Four independent accumulator chains per wave; every iteration issues four
+// 32x32x16 fp16 MFMAs (4 x 32768 flops).
+__global__ __launch_bounds__(256) void mfma_peak_kernel(float* out, int iters) {
+  const int t = threadIdx.x;
+  half8_t a, b;
+  for (int e = 0; e < 8; ++e) {
+    a[e] = (_Float16)(((t + e) & 7) * 0.001f);
+    b[e] = (_Float16)(((t * 3 + e) & 7) * 0.001f);
+  }
+  floatx16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+  for (int i = 0; i < iters; ++i) {
+    c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c1, 0, 0, 0);
+    c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c2, 0, 0, 0);
+    c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c3, 0, 0, 0);
+  }
+  float s = 0;
+  for (int e = 0; e < 16; ++e) s += c0[e] + c1[e] + c2[e] + c3[e];
+  out[blockIdx.x * blockDim.x + t] = s;
+}
+
+int cmd_peak() {
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, 0));
+  const int cus = prop.multiProcessorCount;
+  const int blocks = cus * 4;  // 4 blocks x 4 waves = 4 waves per SIMD
+  const int iters = 20000;
+  float* out = dalloc<float>((size_t)blocks * 256);
+  hipEvent_t e0, e1;
+  HIP_OK(hipEventCreate(&e0));
+  HIP_OK(hipEventCreate(&e1));
+  hipLaunchKernelGGL(mfma_peak_kernel, dim3(blocks), dim3(256), 0, nullptr, out, 100);
+  HIP_OK(hipGetLastError());
+  HIP_OK(hipDeviceSynchronize());
+  double best = 0;
+  for (int rep = 0; rep < 3; ++rep) {
+    HIP_OK(hipEventRecord(e0, nullptr));
+    hipLaunchKernelGGL(mfma_peak_kernel, dim3(blocks), dim3(256), 0, nullptr, out, iters);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipEventRecord(e1, nullptr));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    const double flops = (double)blocks * 4 /*waves*/ * iters * 4 * 32768.0;
+    best = std::fmax(best, flops / (ms * 1e-3) / 1e12);
+  }
+  std::printf("peak: %d CUs, v_mfma_f32_32x32x16_f16 sustained %.1f TFLOP/s (published dense "
+              "fp16 peak 2500)\n", cus, best);
+  HIP_OK(hipFree(out));
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const std::string cmd = argc > 1 ? argv[1] : "";
+  if (cmd == "check") return cmd_check();
+  if (cmd == "fd") return cmd_fd();
+  if (cmd == "bench") return cmd_bench(argc > 2 && std::string(argv[2]) == "quick");
+  if (cmd == "peak") return cmd_peak();
+  std::fprintf(stderr, "usage: %s check | fd | bench [quick] | peak\n", argv[0]);
+  return 2;
+}

@@ -1,0 +1,45 @@
+"""The torch-free driver (tests/driver/fa_driver) on the GPU: the C ABI with
+caller-owned hipMalloc buffers and no torch in the process, checked against
+the float64 C oracle over the reference's 4 input regimes and the GQA,
+ragged and split-tile shapes; a benchmark line; the MFMA throughput probe."""
+import os
+import re
+import subprocess
+
+import pytest
+
+from helpers import ROOT
+
+pytestmark = pytest.mark.gpu
+
+DRIVER = os.path.join(ROOT, "tests", "driver", "fa_driver")
+
+
+def _run(*args, timeout=100):
+    assert os.path.exists(DRIVER), "driver not built: python tests/driver/build.py"
+    print("fa_driver", *args, flush=True)
+    p = subprocess.run([DRIVER, *args], capture_output=True, text=True, timeout=timeout)
+    print(p.stdout[-4000:], p.stderr[-2000:], flush=True)
+    return p
+
+
+def test_driver_check_against_c_oracle():
+    p = _run("check")
+    assert p.returncode == 0, p.stdout + p.stderr
+    assert "check: all ok" in p.stdout
+    assert p.stdout.count("| ok") == 21
+
+
+def test_driver_bench_quick():
+    p = _run("bench", "quick")
+    assert p.returncode == 0, p.stdout + p.stderr
+    line = [l for l in p.stdout.splitlines() if l.startswith("C3 headline")][0]
+    step_tf = float(line.split()[-1])
+    assert step_tf > 100.0, line
+
+
+def test_driver_mfma_peak_probe():
+    p = _run("peak")
+    assert p.returncode == 0, p.stdout + p.stderr
+    tf = float(re.search(r"sustained ([0-9.]+) TFLOP/s", p.stdout).group(1))
+    assert 500.0 < tf <= 2600.0, tf
