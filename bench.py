@@ -1,6 +1,7 @@
 """Benchmark: fwd+bwd attention TFLOPS and % of MI355X fp16 dense MFMA peak.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu]
+    python bench.py --config C5 --steps 5 --warmup 2   (Qwen3-shaped training step)
 
 Workload (BASELINE.json metric, quoted on the headline shape): config C3,
 causal MHA, B=1, Hq=Hkv=8, N=4096, D=128, fp16 inputs from one seeded CPU
@@ -48,6 +49,58 @@ CONFIGS = {
     "C4": dict(B=2, Hq=32, Hkv=8, N=3001, D=128, causal=False, s=0.5,
                desc="non-causal GQA fwd+bwd fp16 B=2 Hq=32 Hkv=8 N=3001 D=128"),
 }
+
+
+QWEN3_C5 = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072,
+                vocab=151936, seq=8192)
+
+
+def qwen3_bench(steps, warmup):
+    """a random-init Qwen3-0.6B-shaped decoder, B=1, seq
+    8192, token ids uniform over the vocabulary, one forward + backward
+    (fp16 autocast) per step, attention through the HF hook ("fa_p100"), and
+    the same step with transformers' "sdpa" attention on the same weights."""
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    import fa_p100_hf
+
+    q = QWEN3_C5
+    cfg = Qwen3Config(vocab_size=q["vocab"], hidden_size=q["hidden"],
+                      intermediate_size=q["inter"], num_hidden_layers=q["layers"],
+                      num_attention_heads=q["heads"], num_key_value_heads=q["kv_heads"],
+                      head_dim=q["head_dim"], max_position_embeddings=q["seq"], use_cache=False)
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = Qwen3ForCausalLM(cfg)
+    model.train()
+    g = torch.Generator("cuda").manual_seed(0)
+    ids = torch.randint(0, q["vocab"], (1, q["seq"]), device="cuda", generator=g)
+
+    def step():
+        model.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", torch.float16):
+            loss = model(ids, labels=ids).loss
+        loss.backward()
+        return loss
+
+    out = {}
+    for impl in ("fa_p100", "sdpa"):
+        if impl == "fa_p100":
+            fa_p100_hf.enable_fa_p100(model)
+        else:
+            model.config._attn_implementation = "sdpa"
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        out[impl] = {"ms_per_step": round(ms, 2),
+                     "tokens_per_s": round(q["seq"] / (ms * 1e-3), 1),
+                     "loss": round(loss.item(), 4)}
+    return out
 
 
 def flops(c):
@@ -270,7 +323,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="C3", choices=sorted(CONFIGS) + ["C5"],
+                    help="C5: the Qwen3-0.6B-shaped training step (hook vs sdpa) instead")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run one device copy of MIB MiB (counter calibration)")
@@ -280,6 +334,23 @@ def main():
               "(the attention kernel at its single-GPU shape); run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.config == "C5":
+        import torch
+        r = qwen3_bench(args.steps, args.warmup)
+        fa, sd = r["fa_p100"], r["sdpa"]
+        print(json.dumps({
+            "metric": "Qwen3-0.6B-shaped training step (fwd+bwd), attention through the HF hook",
+            "value": fa["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": fa["ms_per_step"], "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+            "config": {"workload": "C5: random-init Qwen3-0.6B shape (28 layers, hidden 1024, "
+                       "16/8 heads, D=128, SwiGLU 3072, vocab 151936), B=1, seq 8192, "
+                       "fp16 autocast", **QWEN3_C5},
+            "loss": fa["loss"], "sdpa": sd,
+            "speedup_vs_sdpa": round(sd["ms_per_step"] / fa["ms_per_step"], 3),
+            "device": torch.cuda.get_device_name(0)}), flush=True)
+        return
 
     c = CONFIGS[args.config]
     f_fwd, f_bwd = flops(c)
