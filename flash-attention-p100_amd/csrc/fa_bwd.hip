@@ -92,7 +92,7 @@ struct BwdLds {
 // Preprocess: dvec[row] = sum_d float(O[row,d]) * float(dO[row,d]) from the
 // fp16-rounded O (flash_bwd.cuh:65-78), and lse2[row] = LSE[row] * log2(e),
 // the form in which the main kernel consumes the saved LSE.
-template <int D>
+template <int D, bool BF>
 __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__ O,
                                                       const half_t* __restrict__ dO,
                                                       const float* __restrict__ Lse,
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
     const half8 o = as_half8(*reinterpret_cast<const u32x4*>(O + off));
     const half8 g = as_half8(*reinterpret_cast<const u32x4*>(dO + off));
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc += (float)o[e] * (float)g[e];
+    for (int e = 0; e < 8; ++e) acc += from16<BF>(o[e]) * from16<BF>(g[e]);
   }
 #pragma unroll
   for (int off = kLanesPerRow / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
@@ -197,7 +197,7 @@ __device__ __forceinline__ void slot_add(rsrc_t r, floatx16 (&acc)[n], int w4, i
 
 // ------------------------------- phase 1 -----------------------------------
 // acc[0 .. D/32) = dV^T blocks, acc[D/32 .. 2D/32) = dK^T blocks.
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 struct KVWave {
   floatx16 acc[2 * (D / 32)];
   half8 kb[D / 16];  // this wave's 32 key rows of K as B operands (loop-invariant)
@@ -213,8 +213,8 @@ struct KVWave {
     floatx16 sacc = zero16(), pacc = zero16();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      sacc = mfma32(S::read16(Qs, so, kk), kb[kk], sacc);
-      pacc = mfma32(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
+      sacc = mfma16<BF>(S::read16(Qs, so, kk), kb[kk], sacc);
+      pacc = mfma16<BF>(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
     // i = i0 + 32m + 8*g4 + 4h + e. Dead key columns j >= N need no mask:
@@ -233,8 +233,8 @@ struct KVWave {
         float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
         if (CAUSAL) p = (idx >= lo) ? p : 0.f;
         if (BOUNDS) p = (idx < hi) ? p : 0.f;
-        pb[r >> 3][r & 7] = (half_t)p;
-        sb[r >> 3][r & 7] = (half_t)(p * (pacc[r] - d4[e]));
+        pb[r >> 3][r & 7] = to16<BF>(p);
+        sb[r >> 3][r & 7] = to16<BF>(p * (pacc[r] - d4[e]));
       }
     }
     // dV^T += dO^T P, dK^T += Q^T dS; k-step q = query rows 32m+16q .. +15.
@@ -242,14 +242,14 @@ struct KVWave {
     for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
-        acc[cb] = mfma32(S::tr_operand(Os, q, so, cb), pb[q], acc[cb]);
-        acc[D / 32 + cb] = mfma32(S::tr_operand(Qs, q, so, cb), sb[q], acc[D / 32 + cb]);
+        acc[cb] = mfma16<BF>(S::tr_operand(Os, q, so, cb), pb[q], acc[cb]);
+        acc[D / 32 + cb] = mfma16<BF>(S::tr_operand(Qs, q, so, cb), sb[q], acc[D / 32 + cb]);
       }
   }
 };
 
 // ------------------------------- phase 2 -----------------------------------
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 struct QWave {
   half8 qb[D / 16], ob[D / 16];  // this wave's Q, dO rows as B operands
   floatx16 acc[D / 32];          // dQ^T blocks
@@ -264,8 +264,8 @@ struct QWave {
     floatx16 st = zero16(), pt = zero16();
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      st = mfma32(S::read16(Ks, so, kk), qb[kk], st);
-      pt = mfma32(S::read16(Vs, so, kk), ob[kk], pt);
+      st = mfma16<BF>(S::read16(Ks, so, kk), qb[kk], st);
+      pt = mfma16<BF>(S::read16(Vs, so, kk), ob[kk], pt);
     }
     // dS^T. A lane holds query row i_row and the 16 keys
     // j = j0 + 32s + 8*g4 + 4h + e. Rows i_row >= N are never stored.
@@ -279,19 +279,19 @@ struct QWave {
       float p = fast_exp2(fmaf(st[r], c, -lse2));
       if (CAUSAL) p = (idx <= lo) ? p : 0.f;
       if (BOUNDS) p = (idx < hi) ? p : 0.f;
-      sb[r >> 3][r & 7] = (half_t)(p * (pt[r] - dvv));
+      sb[r >> 3][r & 7] = to16<BF>(p * (pt[r] - dvv));
     }
     // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15.
 #pragma unroll
     for (int cb = 0; cb < D / 32; ++cb)
 #pragma unroll
       for (int q = 0; q < 2; ++q)
-        acc[cb] = mfma32(S::tr_operand(Ks, q, so, cb), sb[q], acc[cb]);
+        acc[cb] = mfma16<BF>(S::tr_operand(Ks, q, so, cb), sb[q], acc[cb]);
   }
 };
 
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int it_begin = helping ? n_it - x_help : 0;
     const int it_end = helping ? n_it : n_it - x_own;
     const bool shared = helping || x_own > 0;
-    KVWave<D, CAUSAL, BOUNDS> w;
+    KVWave<D, CAUSAL, BOUNDS, BF> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
       plan_kv.init(wave, lane, stk.n);
@@ -497,8 +497,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           half4 k4, v4;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            k4[e] = (half_t)(w.acc[D / 32 + cb][4 * g4 + e] * scale);
-            v4[e] = (half_t)w.acc[cb][4 * g4 + e];
+            k4[e] = to16<BF>(w.acc[D / 32 + cb][4 * g4 + e] * scale);
+            v4[e] = to16<BF>(w.acc[cb][4 * g4 + e]);
           }
           *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
           *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
@@ -524,7 +524,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const size_t bhq = (size_t)b * Hq + hq;
       const half_t* Qg = Q + q_off(hq);
       const half_t* dOg = dO + q_off(hq);
-      QWave<D, CAUSAL, BOUNDS> w;
+      QWave<D, CAUSAL, BOUNDS, BF> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
         w.qb[kk] = as_half8(load16(Qg + (size_t)i_row * stq.n + kk * 16 + h * 8, row_ok));
@@ -573,7 +573,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             for (int g4 = 0; g4 < 4; ++g4) {
               half4 v4;
 #pragma unroll
-              for (int e = 0; e < 4; ++e) v4[e] = (half_t)(w.acc[cb][4 * g4 + e] * scale);
+              for (int e = 0; e < 4; ++e) v4[e] = to16<BF>(w.acc[cb][4 * g4 + e] * scale);
               *reinterpret_cast<half4*>(dQh + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
             }
         } else {
@@ -593,23 +593,23 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   }
 }
 
-template <int D>
+template <int D, bool BF>
 hipError_t launch_pre_d(const BwdArgs& a) {
   constexpr int kRowsPerBlock = 256 / (D / 8);
   const long rows = (long)a.B * a.Hq * a.N;
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
-  hipLaunchKernelGGL((bwd_pre_kernel<D>), grid, dim3(256), 0, (hipStream_t)a.stream,
+  hipLaunchKernelGGL((bwd_pre_kernel<D, BF>), grid, dim3(256), 0, (hipStream_t)a.stream,
                      (const half_t*)a.o, (const half_t*)a.dO, a.lse, a.dvec, a.lse2, rows, a.Hq,
                      a.N, make_strides(a.layout, a.Hq, a.N, D), a.counters, a.n_counters);
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
   const float scale = 1.f / sqrtf((float)D);
-  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
@@ -619,21 +619,24 @@ hipError_t launch_main_t(const BwdArgs& a) {
   return hipGetLastError();
 }
 
-template <int D>
+template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
   const bool bounds = (a.N % kTile) != 0;  // kTile is a multiple of kSub
-  if (a.causal) return bounds ? launch_main_t<D, true, true>(a) : launch_main_t<D, true, false>(a);
-  return bounds ? launch_main_t<D, false, true>(a) : launch_main_t<D, false, false>(a);
+  if (a.causal)
+    return bounds ? launch_main_t<D, true, true, BF>(a) : launch_main_t<D, true, false, BF>(a);
+  return bounds ? launch_main_t<D, false, true, BF>(a) : launch_main_t<D, false, false, BF>(a);
 }
 
 }  // namespace
 
 hipError_t launch_bwd_preprocess(const BwdArgs& a) {
-  return a.D == 64 ? launch_pre_d<64>(a) : launch_pre_d<128>(a);
+  if (a.dtype == kBF16) return a.D == 64 ? launch_pre_d<64, true>(a) : launch_pre_d<128, true>(a);
+  return a.D == 64 ? launch_pre_d<64, false>(a) : launch_pre_d<128, false>(a);
 }
 
 hipError_t launch_bwd_main(const BwdArgs& a) {
-  return a.D == 64 ? launch_main_d<64>(a) : launch_main_d<128>(a);
+  if (a.dtype == kBF16) return a.D == 64 ? launch_main_d<64, true>(a) : launch_main_d<128, true>(a);
+  return a.D == 64 ? launch_main_d<64, false>(a) : launch_main_d<128, false>(a);
 }
 
 }  // namespace fa

@@ -45,6 +45,8 @@ const char* fa_error_string(int err) {
     case FA_ERR_NULL: return "a required pointer is NULL";
     case FA_ERR_WORKSPACE: return "workspace is smaller than fa_bwd_workspace_bytes()";
     case FA_ERR_TOO_LARGE: return "shape exceeds the kernels' index range";
+    case FA_ERR_LAYOUT: return "layout must be FA_LAYOUT_BHND or FA_LAYOUT_BNHD";
+    case FA_ERR_DTYPE: return "unsupported element format";
     default: return hipGetErrorString((hipError_t)err);
   }
 }
@@ -52,24 +54,31 @@ const char* fa_error_string(int err) {
 const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
-               int Hkv, int N, int D, int causal, int layout, void* stream) {
+               int Hkv, int N, int D, int causal, int layout, int dtype, void* stream) {
+  if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
+  if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout};
+  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout, dtype};
   return to_code(fa::launch_fwd(a));
 }
 
 int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
            int Hkv, int N, int D, int causal, int full_precision, void* stream) {
   (void)full_precision;  // fp16 products are exact in the fp32 accumulator
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBHND, stream);
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBHND, fa::kFP16, stream);
 }
 
 int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
                 int Hkv, int N, int D, int causal, void* stream) {
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBNHD, stream);
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBNHD, fa::kFP16, stream);
+}
+
+int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
+                int Hkv, int N, int D, int causal, int layout, void* stream) {
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, layout, fa::kBF16, stream);
 }
 
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
@@ -78,7 +87,7 @@ size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
 }
 
 static int bwd_pre(const void* dO, const void* o, const float* lse, void* workspace,
-                   size_t workspace_bytes, int B, int Hq, int N, int D, int layout,
+                   size_t workspace_bytes, int B, int Hq, int N, int D, int layout, int dtype,
                    void* stream) {
   int rc = check_shape(B, Hq, Hq, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
@@ -104,19 +113,21 @@ static int bwd_pre(const void* dO, const void* o, const float* lse, void* worksp
   a.D = D;
   a.stream = stream;
   a.layout = layout;
+  a.dtype = dtype;
   return to_code(fa::launch_bwd_preprocess(a));
 }
 
 int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* workspace,
                       size_t workspace_bytes, int B, int Hq, int N, int D, void* stream) {
-  return bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, fa::kBHND, stream);
+  return bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, fa::kBHND, fa::kFP16,
+                 stream);
 }
 
 // Shared by the main-kernel entry points: fp32 dq or fp16 dq16, either layout.
 static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
-                    int layout, void* stream) {
+                    int layout, int dtype, void* stream) {
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -146,6 +157,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.causal = causal != 0;
   a.stream = stream;
   a.layout = layout;
+  a.dtype = dtype;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -153,15 +165,17 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
 static int bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
                        const float* lse, void* dq, void* dk, void* dv, void* workspace,
                        size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
-                       int layout, void* stream) {
+                       int layout, int dtype, void* stream) {
+  if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
+  if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
   const int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!workspace || !dq) return FA_ERR_NULL;
   if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
-  int e = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, layout, stream);
+  int e = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, layout, dtype, stream);
   if (e != FA_OK) return e;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
-                  causal, layout, stream);
+                  causal, layout, dtype, stream);
 }
 
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, void* workspace,
@@ -169,7 +183,7 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, voi
                 int N, int D, int causal, void* stream) {
   if (!dq) return FA_ERR_NULL;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, nullptr, dk, dv, B, Hq, Hkv, N, D,
-                  causal, fa::kBHND, stream);
+                  causal, fa::kBHND, fa::kFP16, stream);
 }
 
 int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
@@ -177,7 +191,7 @@ int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, 
                    size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                    void* stream) {
   return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, fa::kBHND, stream);
+                     D, causal, fa::kBHND, fa::kFP16, stream);
 }
 
 int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO, const void* o,
@@ -185,7 +199,15 @@ int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO, con
                 size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                 void* stream) {
   return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, fa::kBNHD, stream);
+                     D, causal, fa::kBNHD, fa::kFP16, stream);
+}
+
+int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* dO, const void* o,
+                const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+                int layout, void* stream) {
+  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
+                     D, causal, layout, fa::kBF16, stream);
 }
 
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,

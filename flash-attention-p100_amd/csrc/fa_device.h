@@ -31,6 +31,34 @@ __device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// 16-bit element formats. Tensors hold fp16 (the reference's format) or bf16
+// (BF); loads, LDS tiles and stores move either as opaque 16-bit values in
+// half_t containers, and only the matrix products and the conversions from
+// and to fp32 depend on the format. Conversions round to nearest even.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+template <bool BF>
+__device__ __forceinline__ floatx16 mfma16(half8 a, half8 b, floatx16 c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+template <bool BF>
+__device__ __forceinline__ half_t to16(float x) {
+  if constexpr (BF)
+    return __builtin_bit_cast(half_t, (__bf16)x);
+  else
+    return (half_t)x;
+}
+template <bool BF>
+__device__ __forceinline__ float from16(half_t x) {
+  if constexpr (BF)
+    return (float)__builtin_bit_cast(__bf16, x);
+  else
+    return (float)x;
+}
+
 __device__ __forceinline__ floatx16 zero16() {
   floatx16 z;
 #pragma unroll

@@ -79,7 +79,7 @@ __device__ __forceinline__ float max_halves(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 struct FwdWave {
   // Per-wave state for one 32-row query block.
   half8 qb[D / 16];
@@ -92,7 +92,7 @@ struct FwdWave {
   __device__ __forceinline__ void s_product(const half_t* Ks, int kq, int roff) {
     sc = zero16();
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) sc = mfma32(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], sc);
+    for (int kk = 0; kk < D / 16; ++kk) sc = mfma16<BF>(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], sc);
   }
 
   // One software-pipelined step: softmax of sc (the keys j0 .. j0+31 of this
@@ -112,7 +112,7 @@ struct FwdWave {
 #pragma unroll
     for (int kk = 0; kk < kFront; ++kk)
       if constexpr (NEXT) {
-        sn = mfma32(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
+        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
         issue(kk);
       }
     if (MASK && masked) {
@@ -142,7 +142,7 @@ struct FwdWave {
 #pragma unroll
     for (int kk = kFront; kk < kS; ++kk) {
       if constexpr (NEXT) {
-        sn = mfma32(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
+        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
         issue(kk);
       }
       // 16 exponentials spread over the remaining products.
@@ -153,7 +153,7 @@ struct FwdWave {
         if (r < 16) {
           const float p = fast_exp2(fmaf(s[r], c, neg));
           l += p;
-          pb[r >> 3][r & 7] = (half_t)p;
+          pb[r >> 3][r & 7] = to16<BF>(p);
         }
       }
     }
@@ -162,14 +162,14 @@ struct FwdWave {
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int cb = 0; cb < D / 32; ++cb) {
-        oacc[cb] = mfma32(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, troff), pb[q], oacc[cb]);
+        oacc[cb] = mfma16<BF>(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, troff), pb[q], oacc[cb]);
         if constexpr (NEXT) issue(kS + q * (D / 32) + cb);
       }
     if constexpr (NEXT) sc = sn;
   }
 };
 
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int sq, int sk,
@@ -186,7 +186,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int i_base = q0 + rb * 32;
   const int i_row = i_base + l32;
 
-  FwdWave<D, CAUSAL, BOUNDS> w;
+  FwdWave<D, CAUSAL, BOUNDS, BF> w;
   const int roff = row_lane_off<D>(lane), troff = tr_lane_off<D>(lane);
   const bool row_ok = !BOUNDS || i_row < N;
 #pragma unroll
@@ -332,7 +332,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
         }
         half4 o4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o4[e] = (half_t)(acc[e] * inv_l);
+        for (int e = 0; e < 4; ++e) o4[e] = to16<BF>(acc[e] * inv_l);
         *reinterpret_cast<half4*>(orow + 8 * g + 4 * h) = o4;
       }
       if (cb == 0 && h == 0) Lse[i_row] = (m_star * c + __log2f(l_star)) * kLn2;
@@ -341,7 +341,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   __syncthreads();  // the LDS is reused by the next tile
 }
 
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
@@ -368,20 +368,20 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
-    fwd_tile<D, CAUSAL, BOUNDS>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
+    fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
                                 Lse + (size_t)bh * N, N, stq.n, stk.n, t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
 
-template <int D, bool CAUSAL, bool BOUNDS>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 hipError_t launch_fwd_t(const FwdArgs& a) {
   const int n_qtiles = (a.N + kBR - 1) / kBR;
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
   const int BH = a.B * a.Hq;
   dim3 grid(xcd_grid(gx * BH));
   const float scale_log2 = kLog2e / sqrtf((float)D);
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
@@ -389,17 +389,19 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   return hipGetLastError();
 }
 
-template <int D>
+template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
   const bool bounds = (a.N % kKV) != 0;  // kKV is a multiple of kBR
-  if (a.causal) return bounds ? launch_fwd_t<D, true, true>(a) : launch_fwd_t<D, true, false>(a);
-  return bounds ? launch_fwd_t<D, false, true>(a) : launch_fwd_t<D, false, false>(a);
+  if (a.causal)
+    return bounds ? launch_fwd_t<D, true, true, BF>(a) : launch_fwd_t<D, true, false, BF>(a);
+  return bounds ? launch_fwd_t<D, false, true, BF>(a) : launch_fwd_t<D, false, false, BF>(a);
 }
 
 }  // namespace
 
 hipError_t launch_fwd(const FwdArgs& a) {
-  return a.D == 64 ? launch_fwd_d<64>(a) : launch_fwd_d<128>(a);
+  if (a.dtype == kBF16) return a.D == 64 ? launch_fwd_d<64, true>(a) : launch_fwd_d<128, true>(a);
+  return a.D == 64 ? launch_fwd_d<64, false>(a) : launch_fwd_d<128, false>(a);
 }
 
 }  // namespace fa

@@ -9,6 +9,8 @@ namespace fa {
 // (the reference's layout); kBNHD stores the same logical tensor as dense
 // (B, N, H, D), the layout of the projections in a transformer block.
 enum Layout : int { kBHND = 0, kBNHD = 1 };
+// Element format of the 16-bit tensors (lse and the workspace are fp32).
+enum Dtype : int { kFP16 = 0, kBF16 = 1 };
 
 // Element strides of one (B, H, N, D) tensor with `heads` heads.
 struct Strides {
@@ -31,6 +33,7 @@ struct FwdArgs {
   bool causal;
   void* stream;
   int layout = kBHND;  // of q, k, v, o (lse is always dense (B, Hq, N))
+  int dtype = kFP16;   // of q, k, v, o
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -79,6 +82,7 @@ struct BwdArgs {
   unsigned* counters = nullptr;  // workspace: per key-tile pair (zeroed by the preprocess)
   int n_counters = 0;
   float* slots = nullptr;        // workspace: partial dK/dV of split key tiles
+  int dtype = kFP16;             // of q, k, v, dO, o, dk, dv and dq16
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

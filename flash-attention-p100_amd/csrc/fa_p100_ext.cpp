@@ -7,6 +7,11 @@
 //   backward(q, k, v, dO, o, lse, causal)    -> [dq fp32 (B,Hq,N,D), dk fp16, dv fp16]
 //       fa_p100_ext.cu:103-142
 //
+// and, with no counterpart in the reference, entries used by the autograd
+// Function: backward_half_dq (dq as fp16), forward_bnhd / backward_bnhd
+// (dense (B, N, H, D) tensors) and forward_dt / backward_dt (fp16 or bf16);
+// the last four take bf16 as well as fp16.
+//
 // Plain C++ (no device code): every launch goes through the C ABI of
 // libfa_mi355x.so (include/fa_mi355x.h). Unlike the reference, which uses the
 // legacy default stream without a device guard (flash_fwd.cuh:351,
@@ -26,6 +31,16 @@ namespace {
 void check_in(const at::Tensor& t, const char* name) {
   TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
   TORCH_CHECK(t.scalar_type() == at::kHalf, name, " must be fp16");
+  TORCH_CHECK(t.dim() == 4, name, " must be (B, H, N, D)");
+}
+
+// The entry points added here beside the reference's (forward_dt,
+// backward_dt, forward_bnhd, backward_bnhd) also take bf16: q, k, v (and dO,
+// o) in one 16-bit format, results in that format.
+void check_in16(const at::Tensor& t, const char* name) {
+  TORCH_CHECK(t.is_cuda(), name, " must be a CUDA tensor");
+  TORCH_CHECK(t.scalar_type() == at::kHalf || t.scalar_type() == at::kBFloat16, name,
+              " must be fp16 or bf16");
   TORCH_CHECK(t.dim() == 4, name, " must be (B, H, N, D)");
 }
 
@@ -141,7 +156,7 @@ std::vector<at::Tensor> fa_backward_half_dq(at::Tensor q, at::Tensor k, at::Tens
 // tensors themselves; the checks and messages are the reference's, on the
 // logical (B, H, N, D) shapes.
 static void check_bnhd(const at::Tensor& t, const char* name) {
-  check_in(t, name);
+  check_in16(t, name);
   TORCH_CHECK(t.is_contiguous(), name, " must be dense (B, N, H, D)");
 }
 
@@ -160,13 +175,21 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
               "k/v must be (B, Hkv, N, D) matching q's B, N, D");
   TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
               "q, k and v must be on the same device");
+  TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
+              "q, k and v must have one dtype");
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  check_rc(fa_fwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                       lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0,
-                       current_stream(q)),
-           "fa_fwd_bnhd");
+  if (q.scalar_type() == at::kBFloat16)
+    check_rc(fa_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                         lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, FA_LAYOUT_BNHD,
+                         current_stream(q)),
+             "fa_fwd_bf16");
+  else
+    check_rc(fa_fwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                         lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0,
+                         current_stream(q)),
+             "fa_fwd_bnhd");
   return {o, lse};
 }
 
@@ -188,17 +211,101 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   TORCH_CHECK(lse.scalar_type() == at::kFloat && lse.dim() == 3 && lse.size(0) == B &&
                   lse.size(1) == H && lse.size(2) == N,
               "lse must be (B, H, N)");
+  for (const at::Tensor* t : {&k, &v, &dO, &o})
+    TORCH_CHECK(t->scalar_type() == q.scalar_type(), "q, k, v, dO and o must have one dtype");
   c10::DeviceGuard guard(q.device());
-  auto dq = at::empty_like(q);  // fp16, (B, N, Hq, D)
+  auto dq = at::empty_like(q);  // q's dtype, (B, N, Hq, D)
   auto dk = at::empty_like(k);
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  check_rc(fa_bwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                       lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                       ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
+  if (q.scalar_type() == at::kBFloat16)
+    check_rc(fa_bwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                         lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                         ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
+                         FA_LAYOUT_BNHD, current_stream(q)),
+             "fa_bwd_bf16");
+  else
+    check_rc(fa_bwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                         lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                         ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
+                         current_stream(q)),
+             "fa_bwd_bnhd");
+  return {dq, dk, dv};
+}
+
+// Dense (B, H, N, D) tensors in fp16 or bf16 (one format for all), results in
+// that format, dq included. For fp16 the same kernels as forward and
+// backward_half_dq.
+std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+  check_in16(q, "q");
+  check_in16(k, "k");
+  check_in16(v, "v");
+  if (q.scalar_type() == at::kHalf && k.scalar_type() == at::kHalf &&
+      v.scalar_type() == at::kHalf)
+    return fa_forward(q, k, v, causal, false);
+  TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
+              "q, k and v must have one dtype");
+  q = q.contiguous();
+  k = k.contiguous();
+  v = v.contiguous();
+  const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  const int Hkv = k.size(1);
+  TORCH_CHECK(D == 64 || D == 128, "head dim must be 64 or 128, got ", D);
+  TORCH_CHECK(N > 0, "N must be positive");
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
+              ") must be a multiple of key/value heads (", Hkv, ")");
+  TORCH_CHECK(k.sizes() == v.sizes(), "k and v must match");
+  TORCH_CHECK(k.size(0) == B && k.size(2) == N && k.size(3) == D,
+              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
+              "q, k and v must be on the same device");
+  c10::DeviceGuard guard(q.device());
+  auto o = at::empty_like(q);
+  auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
+  check_rc(fa_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                       lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, FA_LAYOUT_BHND,
                        current_stream(q)),
-           "fa_bwd_bnhd");
+           "fa_fwd_bf16");
+  return {o, lse};
+}
+
+std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
+                                       at::Tensor o, at::Tensor lse, bool causal) {
+  check_in16(q, "q");
+  check_in16(dO, "dO");
+  if (q.scalar_type() == at::kHalf) return backward_impl(q, k, v, dO, o, lse, causal, true);
+  q = q.contiguous();
+  k = k.contiguous();
+  v = v.contiguous();
+  dO = dO.contiguous();
+  o = o.contiguous();
+  lse = lse.contiguous();
+  const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
+  const int Hkv = k.size(1);
+  TORCH_CHECK(D == 64 || D == 128, "head dim must be 64 or 128, got ", D);
+  TORCH_CHECK(N > 0, "N must be positive");
+  TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
+  for (const at::Tensor* t : {&k, &v, &dO, &o})
+    TORCH_CHECK(t->scalar_type() == q.scalar_type(), "q, k, v, dO and o must have one dtype");
+  TORCH_CHECK(lse.scalar_type() == at::kFloat, "lse must be fp32");
+  TORCH_CHECK(k.sizes() == v.sizes() && k.dim() == 4 && k.size(0) == B && k.size(2) == N &&
+                  k.size(3) == D,
+              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(dO.sizes() == q.sizes() && o.sizes() == q.sizes(), "dO and o must match q");
+  TORCH_CHECK(lse.dim() == 3 && lse.size(0) == B && lse.size(1) == H && lse.size(2) == N,
+              "lse must be (B, H, N)");
+  c10::DeviceGuard guard(q.device());
+  auto dq = at::empty_like(q);
+  auto dk = at::empty_like(k);
+  auto dv = at::empty_like(k);
+  const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
+  auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
+  check_rc(fa_bwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                       lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                       ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, FA_LAYOUT_BHND,
+                       current_stream(q)),
+           "fa_bwd_bf16");
   return {dq, dk, dv};
 }
 
@@ -210,5 +317,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_bnhd", &fa_forward_bnhd,
         "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors");
   m.def("backward_bnhd", &fa_backward_bnhd,
-        "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq as fp16");
+        "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype");
+  m.def("forward_dt", &fa_forward_dt,
+        "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors");
+  m.def("backward_dt", &fa_backward_dt,
+        "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype");
 }

@@ -78,7 +78,10 @@ class _FlashAttnP100(torch.autograd.Function):
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
-        o, lse = _ext.forward(q, k, v, causal, full_precision)
+        if q.dtype == torch.bfloat16:
+            o, lse = _ext.forward_dt(q, k, v, causal)
+        else:
+            o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
         return o
 
@@ -86,14 +89,19 @@ class _FlashAttnP100(torch.autograd.Function):
     def backward(ctx, grad_o):
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
-            gb = grad_o.transpose(1, 2)
-            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb.contiguous(), ob, lse, ctx.causal)
+            gb = grad_o.transpose(1, 2).contiguous()
+            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal)
             return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
-        # `_ext.backward(...)[0].to(torch.float16)`) instead of a separate cast.
-        dq, dk, dv = _ext.backward_half_dq(q, k, v, grad_o.contiguous(), o, lse, ctx.causal)
+        # `_ext.backward(...)[0].to(torch.float16)`) instead of a separate cast,
+        # and backward_dt to bf16 for bf16 inputs.
+        g = grad_o.contiguous()
+        if q.dtype == torch.bfloat16:
+            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal)
+        else:
+            dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
 
 
@@ -103,6 +111,10 @@ def flash_attn(q, k, v, causal=False, full_precision=False):
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
     and D in {64, 128}. scale = 1/sqrt(D). Causal masking is top-left aligned
     (key j is hidden from query i when j > i).
+
+    Beyond the reference (which raises on anything but fp16, README.md:72-75),
+    q, k and v may also all be bf16: the products then run on the bf16 MFMA
+    with fp32 accumulation and o and the gradients come back in bf16.
     """
     return _FlashAttnP100.apply(q, k, v, causal, full_precision)
 

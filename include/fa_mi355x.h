@@ -41,8 +41,15 @@ enum {
   FA_ERR_BATCH = 10004,      /* B <= 0 */
   FA_ERR_NULL = 10005,       /* a required pointer is NULL */
   FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
-  FA_ERR_TOO_LARGE = 10007   /* an index would overflow the kernels' 32-bit row counters */
+  FA_ERR_TOO_LARGE = 10007,  /* an index would overflow the kernels' 32-bit row counters */
+  FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
+  FA_ERR_DTYPE = 10009       /* element format not supported */
 };
+
+/* Memory layouts of the 16-bit tensors, for the entry points that take one:
+ * dense (B, H, N, D) as everywhere else, or dense (B, N, H, D) (see
+ * fa_fwd_bnhd). */
+enum { FA_LAYOUT_BHND = 0, FA_LAYOUT_BNHD = 1 };
 
 /* Human-readable text for any value returned by this library. */
 const char* fa_error_string(int err);
@@ -74,6 +81,17 @@ int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
  */
 int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse,
                 int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
+
+/*
+ * fa_fwd (layout FA_LAYOUT_BHND) or fa_fwd_bnhd (FA_LAYOUT_BNHD) on bfloat16
+ * q, k, v, o (lse stays fp32): the products run on the bf16 MFMA with fp32
+ * accumulation, P is rounded to bf16 as an MFMA operand, o to bf16 (nearest
+ * even). No counterpart in the reference, which accepts fp16 only
+ * (fa_p100_ext.cu:33; README.md:72-75 lists bf16 among the unsupported
+ * inputs); for callers whose models run in bf16 and would otherwise cast.
+ */
+int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
+                int B, int Hq, int Hkv, int N, int D, int causal, int layout, void* stream);
 
 /*
  * Bytes of device workspace fa_bwd needs: two (B, Hq, N) float32 vectors, the
@@ -123,6 +141,18 @@ int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO,
                 const void* o, const float* lse, void* dq, void* dk, void* dv,
                 void* workspace, size_t workspace_bytes,
                 int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
+
+/*
+ * Backward on bfloat16 tensors (see fa_fwd_bf16): q, k, v, dO, o and the
+ * outputs dq, dk, dv are bf16 in `layout`; lse and the workspace as in
+ * fa_bwd. P and dS are rounded to bf16 as MFMA operands; dq, dk, dv are the
+ * fp32 results rounded to bf16. No counterpart in the reference (see
+ * fa_fwd_bf16).
+ */
+int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* dO,
+                const void* o, const float* lse, void* dq, void* dk, void* dv,
+                void* workspace, size_t workspace_bytes,
+                int B, int Hq, int Hkv, int N, int D, int causal, int layout, void* stream);
 
 /*
  * First phase of fa_bwd, the counterpart of bwd_preprocess

@@ -60,6 +60,10 @@ def load_capi():
     lib.fa_fwd_bnhd.restype = i
     lib.fa_bwd_bnhd.argtypes = [vp] * 10 + [sz] + [i] * 6 + [vp]
     lib.fa_bwd_bnhd.restype = i
+    lib.fa_fwd_bf16.argtypes = [vp] * 5 + [i] * 7 + [vp]
+    lib.fa_fwd_bf16.restype = i
+    lib.fa_bwd_bf16.argtypes = [vp] * 10 + [sz] + [i] * 7 + [vp]
+    lib.fa_bwd_bf16.restype = i
     return lib
 
 

@@ -52,6 +52,14 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_bwd_preprocess(z, z, z, z, 0, 1, 2, 8, 128, s) == 10005
     one = ctypes.c_void_p(1)
     assert lib.fa_bwd(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, s) == 10006
+    # bf16 entry points: layout codes, then the same shape checks.
+    assert lib.fa_fwd_bf16(*([one] * 5), 1, 2, 2, 8, 64, 0, 2, s) == 10008
+    assert lib.fa_fwd_bf16(*([one] * 5), 1, 2, 2, 8, 80, 0, 0, s) == 10001
+    assert lib.fa_fwd_bf16(z, z, z, z, z, 1, 2, 2, 8, 64, 0, 1, s) == 10005
+    assert lib.fa_bwd_bf16(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, 0, s) == 10006
+    assert lib.fa_bwd_bf16(*([one] * 10), 1 << 30, 1, 2, 2, 8, 64, 0, -1, s) == 10008
+    assert b"layout" in lib.fa_error_string(10008)
+    assert b"format" in lib.fa_error_string(10009)
 
 
 def test_binding_rejects_host_tensors_with_reference_messages():
