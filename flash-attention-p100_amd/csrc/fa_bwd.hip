@@ -206,7 +206,7 @@ struct KVWave {
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
-                                       int m, int kr0, int i0, int j_col, int N, int lane,
+                                       int m, int kr0, int i0, int j_col, int N, int Nk, int lane,
                                        int roff, const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
@@ -217,11 +217,12 @@ struct KVWave {
       pacc = mfma16<BF>(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
-    // i = i0 + 32m + 8*g4 + 4h + e. Dead key columns j >= N need no mask:
-    // they feed only dK/dV rows that are never stored.
+    // i = i0 + 32m + 8*g4 + 4h + e. Key columns past the entry's key length
+    // Nk are masked (their dK/dV rows are stored, as zeros); past N they feed
+    // only rows that are never stored.
     const int base = i0 + 32 * m + 4 * h;
     const int lo = j_col - base;  // alive when 8*g4 + e >= lo (causal)
-    const int hi = N - base;      // alive when 8*g4 + e <  hi (ragged)
+    const int hi = j_col < Nk ? N - base : 0;  // alive when 8*g4 + e < hi (ragged, key length)
     half8 pb[2], sb[2];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
@@ -257,7 +258,7 @@ struct QWave {
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
-                                       int i_row, int N, int lane,
+                                       int i_row, int Nk, int lane,
                                        const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
@@ -271,7 +272,7 @@ struct QWave {
     // j = j0 + 32s + 8*g4 + 4h + e. Rows i_row >= N are never stored.
     const int base = j0 + 32 * s + 4 * h;
     const int lo = i_row - base;  // alive when 8*g4 + e <= lo (causal)
-    const int hi = N - base;      // alive when 8*g4 + e <  hi (ragged)
+    const int hi = Nk - base;     // alive when 8*g4 + e <  hi (ragged N, key length)
     half8 sb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -300,7 +301,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     half_t* __restrict__ dV,
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2,
     Strides stq, Strides stk, unsigned* __restrict__ counters, float* __restrict__ slots,
-    int split_num, int split_bias) {
+    int split_num, int split_bias, const int* __restrict__ kv_len) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -327,6 +328,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int bkv = wi / n_tiles;  // over B*Hkv
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
+  // Per-entry key length (key padding), clamped to [1, N].
+  const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
   // Offset of query head hq's row 0 in Q, dO, dQ.
@@ -427,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const int i0 = i_start + (it % n_qt) * kSub;
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, N, lane, roff,
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, N, Nk, lane, roff,
              so, scale_log2);
       wait_vmem();
       __syncthreads();
@@ -516,7 +519,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int iw = t0 + w4 * 32;  // this wave's query rows
     const int i_row = iw + l32;
     const bool row_ok = !BOUNDS || i_row < N;
-    const int kv_end = CAUSAL ? min(N, t0 + kTile) : N;
+    const int kv_end = CAUSAL ? min(Nk, t0 + kTile) : Nk;
     const int n_kt = (kv_end + kSub - 1) / kSub;
 
     for (int g = 0; g < group; ++g) {
@@ -547,7 +550,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
         fetch(t + 1, P ? ta0 : ta1, P ? tb0 : tb1);
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, N, lane, so, scale_log2);
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, lane, so, scale_log2);
         wait_vmem();
         __syncthreads();
       };
@@ -615,13 +618,14 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots, kSplitNum,
-                     kSplitBias);
+                     kSplitBias, a.kv_len);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
-  const bool bounds = (a.N % kTile) != 0;  // kTile is a multiple of kSub
+  // Key lengths need the masked instantiation (kTile is a multiple of kSub).
+  const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr;
   if (a.causal)
     return bounds ? launch_main_t<D, true, true, BF>(a) : launch_main_t<D, true, false, BF>(a);
   return bounds ? launch_main_t<D, false, true, BF>(a) : launch_main_t<D, false, false, BF>(a);

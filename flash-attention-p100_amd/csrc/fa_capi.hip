@@ -54,14 +54,15 @@ const char* fa_error_string(int err) {
 const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
-               int Hkv, int N, int D, int causal, int layout, int dtype, void* stream) {
+               int Hkv, int N, int D, int causal, int layout, int dtype, void* stream,
+               const int* kv_len = nullptr) {
   if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout, dtype};
+  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout, dtype, kv_len};
   return to_code(fa::launch_fwd(a));
 }
 
@@ -127,7 +128,7 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* wor
 static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
-                    int layout, int dtype, void* stream) {
+                    int layout, int dtype, void* stream, const int* kv_len = nullptr) {
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -158,6 +159,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.stream = stream;
   a.layout = layout;
   a.dtype = dtype;
+  a.kv_len = kv_len;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -165,7 +167,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
 static int bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
                        const float* lse, void* dq, void* dk, void* dv, void* workspace,
                        size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
-                       int layout, int dtype, void* stream) {
+                       int layout, int dtype, void* stream, const int* kv_len = nullptr) {
   if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
   const int rc = check_shape(B, Hq, Hkv, N, D);
@@ -175,7 +177,7 @@ static int bwd_half_dq(const void* q, const void* k, const void* v, const void* 
   int e = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, layout, dtype, stream);
   if (e != FA_OK) return e;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
-                  causal, layout, dtype, stream);
+                  causal, layout, dtype, stream, kv_len);
 }
 
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, void* workspace,
@@ -208,6 +210,20 @@ int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* dO, con
                 int layout, void* stream) {
   return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
                      D, causal, layout, fa::kBF16, stream);
+}
+
+int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
+              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int dtype,
+              int layout, void* stream) {
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, layout, dtype, stream, kv_len);
+}
+
+int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const void* o,
+              const float* lse, const int* kv_len, void* dq, void* dk, void* dv,
+              void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D,
+              int causal, int dtype, int layout, void* stream) {
+  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
+                     D, causal, layout, dtype, stream, kv_len);
 }
 
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,

@@ -172,7 +172,7 @@ struct FwdWave {
 template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
-                                         float* __restrict__ Lse, int N, int sq, int sk,
+                                         float* __restrict__ Lse, int N, int Nk, int sq, int sk,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -197,7 +197,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   w.m_raw = -INFINITY;
   w.l = 0.f;
 
-  const int kv_end = CAUSAL ? min(N, q0 + kBR) : N;
+  // Keys [0, Nk) exist for this batch entry (Nk = N unless key lengths are
+  // given); later keys are masked like keys past a ragged N.
+  const int kv_end = CAUSAL ? min(Nk, q0 + kBR) : Nk;
   const int n_it = (kv_end + kKV - 1) / kKV;
   // Leading steps in which this wave's 32x32 block needs no mask. The later
   // ones run masked; blocks wholly past the diagonal or past N give exact
@@ -205,7 +207,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // share of the loads inside the same code).
   int n_full = n_it;
   if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
-  if (BOUNDS) n_full = min(n_full, N - 32 - kq * 32 >= 0 ? (N - 32 - kq * 32) / kKV + 1 : 0);
+  if (BOUNDS) n_full = min(n_full, Nk - 32 - kq * 32 >= 0 ? (Nk - 32 - kq * 32) / kKV + 1 : 0);
 
   // Software pipeline over steps j = 0 .. n_it-1. Step j reads K_{j+1} (for
   // the next S^T) from K buffer (j+1)%2 and V_j from V buffer j%2, while it
@@ -215,7 +217,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   using TL = typename L::TL;
   TilePlan<D, kKV, kWaves, false> plan;
   plan.init(wave, lane, sk);
-  const rsrc_t rk = rows_rsrc<D>(K, N, sk), rv = rows_rsrc<D>(V, N, sk);
+  const rsrc_t rk = rows_rsrc<D>(K, Nk, sk), rv = rows_rsrc<D>(V, Nk, sk);
   const int k1 = min(1, n_it - 1) * kKV;
 #pragma unroll
   for (int u = 0; u < TL::kParts; ++u) {
@@ -251,7 +253,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     };
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
-    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j >= n_full, i_row, N, lane,
+    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j >= n_full, i_row, Nk, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
-    Strides stk) {
+    Strides stk, const int* __restrict__ kv_len) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -364,12 +366,14 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const size_t q_off = (size_t)(b * stq.b + hq * stq.h);
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const float thr_raw = kRescaleLog2 / scale_log2;
+  // Per-entry key length (key padding), clamped to [1, N].
+  const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                Lse + (size_t)bh * N, N, stq.n, stk.n, t ? second : first,
+                                Lse + (size_t)bh * N, N, Nk, stq.n, stk.n, t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
@@ -385,13 +389,14 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D));
+                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  const bool bounds = (a.N % kKV) != 0;  // kKV is a multiple of kBR
+  // Key lengths need the masked instantiation (kKV is a multiple of kBR).
+  const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr;
   if (a.causal)
     return bounds ? launch_fwd_t<D, true, true, BF>(a) : launch_fwd_t<D, true, false, BF>(a);
   return bounds ? launch_fwd_t<D, false, true, BF>(a) : launch_fwd_t<D, false, false, BF>(a);

@@ -34,6 +34,7 @@ struct FwdArgs {
   void* stream;
   int layout = kBHND;  // of q, k, v, o (lse is always dense (B, Hq, N))
   int dtype = kFP16;   // of q, k, v, o
+  const int* kv_len = nullptr;  // device, B entries: keys [0, kv_len[b]) exist (else N)
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -83,6 +84,7 @@ struct BwdArgs {
   int n_counters = 0;
   float* slots = nullptr;        // workspace: partial dK/dV of split key tiles
   int dtype = kFP16;             // of q, k, v, dO, o, dk, dv and dq16
+  const int* kv_len = nullptr;   // as FwdArgs::kv_len
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

@@ -44,6 +44,21 @@ void check_in16(const at::Tensor& t, const char* name) {
   TORCH_CHECK(t.dim() == 4, name, " must be (B, H, N, D)");
 }
 
+// Optional key lengths (right padding): int32 (B,) on q's device; nullptr
+// when absent.
+const int* kv_len_ptr(const c10::optional<at::Tensor>& kv_len, const at::Tensor& q, int B) {
+  if (!kv_len.has_value()) return nullptr;
+  const at::Tensor& t = *kv_len;
+  TORCH_CHECK(t.is_cuda() && t.device() == q.device(), "kv_len must be on q's device");
+  TORCH_CHECK(t.scalar_type() == at::kInt, "kv_len must be int32");
+  TORCH_CHECK(t.dim() == 1 && t.size(0) == B && t.is_contiguous(), "kv_len must be (B,)");
+  return t.data_ptr<int>();
+}
+
+int dtype_code(const at::Tensor& q) {
+  return q.scalar_type() == at::kBFloat16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16;
+}
+
 void check_rc(int rc, const char* what) {
   TORCH_CHECK(rc == FA_OK, what, " failed: ", fa_error_string(rc));
 }
@@ -160,7 +175,8 @@ static void check_bnhd(const at::Tensor& t, const char* name) {
   TORCH_CHECK(t.is_contiguous(), name, " must be dense (B, N, H, D)");
 }
 
-std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
+                                        c10::optional<at::Tensor> kv_len) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -180,22 +196,16 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  if (q.scalar_type() == at::kBFloat16)
-    check_rc(fa_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                         lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, FA_LAYOUT_BNHD,
-                         current_stream(q)),
-             "fa_fwd_bf16");
-  else
-    check_rc(fa_fwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                         lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0,
-                         current_stream(q)),
-             "fa_fwd_bnhd");
+  check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), B, H, Hkv, N, D,
+                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BNHD, current_stream(q)),
+           "fa_fwd_ex");
   return {o, lse};
 }
 
 std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v,
                                          at::Tensor dO, at::Tensor o, at::Tensor lse,
-                                         bool causal) {
+                                         bool causal, c10::optional<at::Tensor> kv_len) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -219,31 +229,23 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  if (q.scalar_type() == at::kBFloat16)
-    check_rc(fa_bwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                         lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                         ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
-                         FA_LAYOUT_BNHD, current_stream(q)),
-             "fa_bwd_bf16");
-  else
-    check_rc(fa_bwd_bnhd(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                         lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                         ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0,
-                         current_stream(q)),
-             "fa_bwd_bnhd");
+  check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), dq.data_ptr(),
+                     dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, H, Hkv, N, D,
+                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BNHD, current_stream(q)),
+           "fa_bwd_ex");
   return {dq, dk, dv};
 }
 
 // Dense (B, H, N, D) tensors in fp16 or bf16 (one format for all), results in
-// that format, dq included. For fp16 the same kernels as forward and
-// backward_half_dq.
-std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal) {
+// that format, dq included, and optional key lengths kv_len (int32 (B,), right
+// padding: entry b has keys [0, kv_len[b])). For fp16 without kv_len the same
+// kernels as forward and backward_half_dq.
+std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
+                                      c10::optional<at::Tensor> kv_len) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
-  if (q.scalar_type() == at::kHalf && k.scalar_type() == at::kHalf &&
-      v.scalar_type() == at::kHalf)
-    return fa_forward(q, k, v, causal, false);
   TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
               "q, k and v must have one dtype");
   q = q.contiguous();
@@ -263,18 +265,18 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  check_rc(fa_fwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                       lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, FA_LAYOUT_BHND,
-                       current_stream(q)),
-           "fa_fwd_bf16");
+  check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), B, H, Hkv, N, D,
+                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BHND, current_stream(q)),
+           "fa_fwd_ex");
   return {o, lse};
 }
 
 std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
-                                       at::Tensor o, at::Tensor lse, bool causal) {
+                                       at::Tensor o, at::Tensor lse, bool causal,
+                                       c10::optional<at::Tensor> kv_len) {
   check_in16(q, "q");
   check_in16(dO, "dO");
-  if (q.scalar_type() == at::kHalf) return backward_impl(q, k, v, dO, o, lse, causal, true);
   q = q.contiguous();
   k = k.contiguous();
   v = v.contiguous();
@@ -301,11 +303,11 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  check_rc(fa_bwd_bf16(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                       lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                       ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, FA_LAYOUT_BHND,
-                       current_stream(q)),
-           "fa_bwd_bf16");
+  check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
+                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), dq.data_ptr(),
+                     dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, H, Hkv, N, D,
+                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BHND, current_stream(q)),
+           "fa_bwd_ex");
   return {dq, dk, dv};
 }
 
@@ -315,11 +317,17 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("backward_half_dq", &fa_backward_half_dq,
         "FlashAttention backward (gfx950), dq as fp16 (used by the autograd Function)");
   m.def("forward_bnhd", &fa_forward_bnhd,
-        "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors");
+        "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none());
   m.def("backward_bnhd", &fa_backward_bnhd,
-        "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype");
+        "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
+        py::arg("causal"), py::arg("kv_len") = py::none());
   m.def("forward_dt", &fa_forward_dt,
-        "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors");
+        "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
+        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none());
   m.def("backward_dt", &fa_backward_dt,
-        "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype");
+        "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
+        py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
+        py::arg("causal"), py::arg("kv_len") = py::none());
 }

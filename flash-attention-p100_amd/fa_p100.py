@@ -66,20 +66,21 @@ class _FlashAttnP100(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, full_precision):
+    def forward(ctx, q, k, v, causal, full_precision, kv_len=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
         qb = None if q.is_contiguous() else _bnhd_storage(q)
         kb, vb = _bnhd_storage(k), _bnhd_storage(v)
         ctx.causal = causal
+        ctx.kv_len = kv_len
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
-            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal)
+            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
-        if q.dtype == torch.bfloat16:
-            o, lse = _ext.forward_dt(q, k, v, causal)
+        if q.dtype == torch.bfloat16 or kv_len is not None:
+            o, lse = _ext.forward_dt(q, k, v, causal, kv_len)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -90,33 +91,38 @@ class _FlashAttnP100(torch.autograd.Function):
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
-            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal)
-            return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None
+            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len)
+            return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
         # `_ext.backward(...)[0].to(torch.float16)`) instead of a separate cast,
         # and backward_dt to bf16 for bf16 inputs.
         g = grad_o.contiguous()
-        if q.dtype == torch.bfloat16:
-            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal)
+        if q.dtype == torch.bfloat16 or ctx.kv_len is not None:
+            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None
 
 
-def flash_attn(q, k, v, causal=False, full_precision=False):
+def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
     and D in {64, 128}. scale = 1/sqrt(D). Causal masking is top-left aligned
     (key j is hidden from query i when j > i).
 
-    Beyond the reference (which raises on anything but fp16, README.md:72-75),
-    q, k and v may also all be bf16: the products then run on the bf16 MFMA
-    with fp32 accumulation and o and the gradients come back in bf16.
+    Beyond the reference (which raises on anything but fp16 and on padding
+    masks, README.md:72-75):
+      * q, k and v may also all be bf16: the products then run on the bf16
+        MFMA with fp32 accumulation, and o and the gradients come back in bf16;
+      * kv_len, an int32 tensor (B,) on q's device, gives each batch entry's
+        key length (right padding): entry b has keys [0, kv_len[b]) (values
+        clamped to [1, N]); every query row, pad rows included, attends to
+        those keys only, and the gradients of k, v past kv_len[b] are zero.
     """
-    return _FlashAttnP100.apply(q, k, v, causal, full_precision)
+    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len)
 
 
 def _expand_kv(k, n_head):

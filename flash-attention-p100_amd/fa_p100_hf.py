@@ -15,13 +15,18 @@ implementation that is not in the mask registry (masking_utils.py:819-820).
 That last point is relied on: the kernel applies causality itself, so no
 (B, H, N, N) mask is ever built. The price is that a padding mask would be
 dropped without a word, which is why `enable_fa_p100` wraps `model.forward`
-to reject one (fa_p100_hf.py:13-22, 183-211).
+to look at it first (fa_p100_hf.py:13-22, 183-211). Beyond the reference,
+which rejects every padding mask, a right-padded 2-D mask (each row ones, then
+zeros) is served exactly: its row sums go to the kernels as per-entry key
+lengths, so every position attends to the real keys only, as with eager
+attention and the same mask.
 
-Every unsupported request raises NotImplementedError instead of degrading
-(fa_p100_hf.py:24-32): attention / padding masks, output_attentions,
-head_mask, sliding windows, dropout, head_dim other than 64/128, a scale other
-than 1/sqrt(D), q_len != kv_len (KV-cache decoding).
+Every other unsupported request raises NotImplementedError instead of
+degrading (fa_p100_hf.py:24-32): other attention / padding masks,
+output_attentions, head_mask, sliding windows, dropout, head_dim other than
+64/128, a scale other than 1/sqrt(D), q_len != kv_len (KV-cache decoding).
 """
+import contextvars
 import warnings
 
 import torch
@@ -30,6 +35,22 @@ from fa_p100 import flash_attn
 
 _IMPL_NAME = "fa_p100"
 _warned_cast = False
+# Key lengths (int32 (B,) on the model's device) of the right-padded batch of
+# the model call in progress, set by enable_fa_p100's forward wrapper.
+_kv_len = contextvars.ContextVar("fa_p100_kv_len", default=None)
+
+
+def right_padding_lengths(mask):
+    """Row sums of a right-padded 2-D mask (each row: ones, then zeros, at
+    least one one) as int32, or None for any other mask."""
+    if mask.dim() != 2:
+        return None
+    m = mask != 0
+    lens = m.sum(dim=1)
+    ref = torch.arange(m.size(1), device=m.device)[None, :] < lens[:, None]
+    if not bool(torch.equal(m, ref)) or not bool((lens > 0).all()):
+        return None
+    return lens.to(torch.int32)
 
 
 def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout=0.0,
@@ -93,7 +114,14 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
 
     # GQA/MQA go to the kernel as they are: no repeat_kv copies.
     full_precision = getattr(module, "_fa_p100_full_precision", False)
-    out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision)
+    kv_len = _kv_len.get()
+    if kv_len is not None:
+        if kv_len.numel() != query.size(0) or kv_len.device != query.device:
+            raise NotImplementedError(
+                "fa_p100: the padding mask given to the model does not match this "
+                "attention call's batch.")
+    out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
+                     kv_len=kv_len)
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
 
@@ -118,8 +146,9 @@ def enable_fa_p100(model, full_precision=False):
 
     Mirrors fa_p100_hf.py:161-213: registers the implementation, points every
     config at it, records `full_precision` on every module, turns the KV cache
-    off, and wraps `model.forward` once so a padding mask or use_cache=True
-    raises instead of being silently ignored.
+    off, and wraps `model.forward` once so that use_cache=True and any
+    padding mask other than right padding raise instead of being silently
+    ignored; a right-padded mask is served through per-entry key lengths.
     """
     register()
     _set_impl(model.config, _IMPL_NAME)
@@ -139,10 +168,14 @@ def enable_fa_p100(model, full_precision=False):
         def guarded(*args, attention_mask=None, use_cache=None, **kwargs):
             # transformers drops the mask before the attention interface sees it
             # for unregistered implementations: this is the last place to catch it.
+            kv_len = None
             if attention_mask is not None and not bool(attention_mask.all()):
-                raise NotImplementedError(
-                    "fa_p100 cannot apply a padding mask, and transformers would "
-                    "discard it silently. Pack the batch so every position is real.")
+                kv_len = right_padding_lengths(attention_mask)
+                if kv_len is None:
+                    raise NotImplementedError(
+                        "fa_p100 serves only right padding (each mask row: ones, then "
+                        "zeros); this padding mask would be discarded silently. Pad on "
+                        "the right or pack the batch so every position is real.")
             # Rejected up front rather than at the first decode step, after a
             # prefill that would have succeeded.
             if use_cache:
@@ -150,7 +183,11 @@ def enable_fa_p100(model, full_precision=False):
                     "fa_p100 needs q_len == kv_len, so it cannot serve a KV cache; it "
                     "is a training kernel. Set generation_config.use_cache = False for "
                     "cache-free generation.")
-            return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
+            token = _kv_len.set(kv_len)
+            try:
+                return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
+            finally:
+                _kv_len.reset(token)
 
         model.forward = guarded
         model._fa_p100_guarded = True

@@ -51,6 +51,9 @@ enum {
  * fa_fwd_bnhd). */
 enum { FA_LAYOUT_BHND = 0, FA_LAYOUT_BNHD = 1 };
 
+/* Element formats of the 16-bit tensors, for the entry points that take one. */
+enum { FA_DTYPE_FP16 = 0, FA_DTYPE_BF16 = 1 };
+
 /* Human-readable text for any value returned by this library. */
 const char* fa_error_string(int err);
 
@@ -177,6 +180,26 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
                 void* workspace, size_t workspace_bytes, float* dq,
                 void* dk, void* dv, int B, int Hq, int Hkv, int N, int D,
                 int causal, void* stream);
+
+/*
+ * The general pair, covering every variant above plus key padding: element
+ * format `dtype` (FA_DTYPE_FP16 / FA_DTYPE_BF16), `layout`
+ * (FA_LAYOUT_BHND / FA_LAYOUT_BNHD) and, when `kv_len` is not NULL, a device
+ * array of B int32 key lengths: for batch entry b only keys
+ * [0, kv_len[b]) exist (right padding; values are clamped to [1, N]), every
+ * query row (pad rows included) attends to those keys only, and dk/dv rows
+ * past kv_len[b] come out zero. fa_bwd_ex writes dq in `dtype`. No
+ * counterpart in the reference, which raises on padding masks and on bf16
+ * (README.md:72-75, fa_p100_hf.py:64-70); kv_len serves the HF hook's
+ * right-padded batches.
+ */
+int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
+              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int dtype,
+              int layout, void* stream);
+int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const void* o,
+              const float* lse, const int* kv_len, void* dq, void* dk, void* dv,
+              void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D,
+              int causal, int dtype, int layout, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -60,35 +60,42 @@ def _group_sum(g, hkv):
     return g.reshape(b, hkv, hq // hkv, n, d).sum(axis=2)
 
 
-def _scores(q, k, causal, dtype):
+def _scores(q, k, causal, dtype, kv_len=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
     (flash_fwd.cuh:94-101, 220-224). Causal is top-left aligned with
     q_len == kv_len: key col is masked for query row when col > row
-    (flash_fwd.cuh:239).
+    (flash_fwd.cuh:239). With `kv_len` (B ints, an extension: the reference
+    has no padding masks) key col is also masked for batch entry b when
+    col >= kv_len[b], clamped to [1, N] as the kernels do.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d)
     s = np.matmul(q.astype(dtype), np.swapaxes(k.astype(dtype), -1, -2)) * dtype(scale)
+    n = q.shape[-2]
     if causal:
-        n = q.shape[-2]
         mask = np.triu(np.ones((n, n), dtype=bool), 1)
         s = np.where(mask, -np.inf, s).astype(dtype)
+    if kv_len is not None:
+        lens = np.clip(np.asarray(kv_len).reshape(-1), 1, n)
+        cols = np.arange(n)[None, :] >= lens[:, None]  # (B, N) masked key columns
+        s = np.where(cols[:, None, None, :], -np.inf, s).astype(dtype)
     return s
 
 
-def attention_fwd(q, k, v, causal=False, dtype=np.float64):
+def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
-    (flash_fwd.cuh:324-329).
+    (flash_fwd.cuh:324-329). `kv_len`: optional per-entry key lengths (see
+    _scores).
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len)
     m = s.max(axis=-1, keepdims=True)
     p = np.exp(s - m)
     l = p.sum(axis=-1, keepdims=True)
@@ -102,7 +109,7 @@ def bwd_preprocess(o, do, dtype=np.float64):
     return (np.asarray(o).astype(dtype) * np.asarray(do).astype(dtype)).sum(axis=-1)
 
 
-def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64):
+def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -118,8 +125,8 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64)
     qd = q.astype(dtype)
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
-        o, lse = attention_fwd(q, k, v, causal, dtype)
-    s = _scores(q, ke, causal, dtype)
+        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len)
+    s = _scores(q, ke, causal, dtype, kv_len)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     dv = np.matmul(np.swapaxes(p, -1, -2), dod)
     dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
@@ -130,9 +137,9 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64)
     return dq, _group_sum(dk, hkv), _group_sum(dv, hkv)
 
 
-def attention_loss(q, k, v, do, causal=False, dtype=np.float64):
+def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

@@ -79,9 +79,13 @@ def test_public_api_surface_matches_reference():
     import fa_p100
     import fa_p100_hf
     sig = inspect.signature(fa_p100.flash_attn)
-    assert list(sig.parameters) == ["q", "k", "v", "causal", "full_precision"]
+    # The reference's parameters, in order, with its defaults; kv_len (key
+    # lengths, an extension) comes last and defaults to None, so every
+    # reference call binds the same way.
+    assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False
+    assert list(sig.parameters)[5:] == ["kv_len"] and sig.parameters["kv_len"].default is None
     for name in ("_FlashAttnP100", "reference", "_expand_kv", "_ext"):
         assert hasattr(fa_p100, name)
     for name in ("fa_p100_attention_forward", "register", "enable_fa_p100", "_set_impl"):

@@ -84,7 +84,14 @@ def test_register_and_enable():
     assert model.forward is inner
 
     ids = torch.zeros(1, 6, dtype=torch.long)
-    with pytest.raises(NotImplementedError, match="padding mask"):
+    # Left padding, holes and all-zero rows still raise; right padding is
+    # served (tests/test_gpu_hf.py runs it against eager with the mask).
+    for mask in ([[0, 0, 1, 1, 1, 1]], [[1, 1, 0, 1, 1, 1]], [[0, 0, 0, 0, 0, 0]]):
+        with pytest.raises(NotImplementedError, match="right padding"):
+            model(ids, attention_mask=torch.tensor(mask))
+    assert hf.right_padding_lengths(torch.tensor([[1, 1, 1, 1, 0, 0], [1] * 6])).tolist() == [4, 6]
+    assert hf.right_padding_lengths(torch.tensor([[1, 0, 1, 0, 0, 0]])) is None
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         model(ids, attention_mask=torch.tensor([[1, 1, 1, 1, 0, 0]]))
     with pytest.raises(NotImplementedError, match="KV cache"):
         model(ids, use_cache=True)

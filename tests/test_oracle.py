@@ -176,3 +176,48 @@ def test_planted_mistakes_are_caught():
     # Planted: mask orientation flipped (future visible, past hidden).
     bad, _ = ora.attention_fwd(q[:, :, ::-1], k[:, :, ::-1], v[:, :, ::-1], True)
     assert not np.allclose(bad[:, :, ::-1], good)
+
+
+# ---------------------------------------------------------------------------
+# Key lengths (right padding; an extension beyond the reference, which raises
+# on padding masks).
+@pytest.mark.parametrize("causal", [False, True])
+def test_kv_len_pins(causal):
+    rng = np.random.default_rng(31)
+    b, hq, hkv, n, d = 3, 4, 2, 23, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    lens = np.array([n, 9, 1])
+    o, lse = ora.attention_fwd(q, k, v, causal, kv_len=lens)
+    dq, dk, dv = ora.attention_bwd(q, k, v, do, causal, kv_len=lens)
+    # Full length: identical to no key lengths; out-of-range lengths clamp.
+    o_full, _ = ora.attention_fwd(q, k, v, causal)
+    assert np.array_equal(o[0], o_full[0])
+    o_clamp, _ = ora.attention_fwd(q, k, v, causal, kv_len=np.array([n + 5, 9, 0]))
+    assert np.array_equal(o_clamp, o)
+    for i, L in enumerate(lens):
+        # Against attention over the truncated keys, as an independent
+        # float64 library routine with explicit masks.
+        qb, kb, vb = (torch.tensor(x[i:i + 1]) for x in (q, k, v))
+        ke = kb.repeat_interleave(hq // hkv, dim=1)[:, :, :L]
+        ve = vb.repeat_interleave(hq // hkv, dim=1)[:, :, :L]
+        mask = torch.ones(n, L, dtype=torch.bool)
+        if causal:  # key j < L visible to row i when j <= i
+            mask = torch.tril(torch.ones(n, n, dtype=torch.bool))[:, :L]
+        ref = F.scaled_dot_product_attention(qb, ke, ve, attn_mask=mask)
+        assert np.allclose(o[i:i + 1], ref.numpy(), atol=1e-12)
+        # Keys past the length get exactly zero gradient.
+        assert not np.any(dk[i, :, L:]) and not np.any(dv[i, :, L:])
+    # The backward is the gradient of the loss with the same lengths.
+    h = 1e-4
+    for which, g in ((0, dq), (1, dk), (2, dv)):
+        for _ in range(4):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, causal, kv_len=lens)
+                  - ora.attention_loss(*minus, do, causal, kv_len=lens)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
