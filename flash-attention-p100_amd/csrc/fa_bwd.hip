@@ -206,7 +206,7 @@ struct KVWave {
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
-                                       int m, int kr0, int i0, int j_col, int N, int Nk, int lane,
+                                       int m, int kr0, int i0, int j_col, int row_end, int lane,
                                        int roff, const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
@@ -217,12 +217,12 @@ struct KVWave {
       pacc = mfma16<BF>(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
-    // i = i0 + 32m + 8*g4 + 4h + e. Key columns past the entry's key length
-    // Nk are masked (their dK/dV rows are stored, as zeros); past N they feed
-    // only rows that are never stored.
+    // i = i0 + 32m + 8*g4 + 4h + e; rows from row_end on are masked: past N,
+    // past the key's sliding window, or all of them for a key past the
+    // entry's key length (its dK/dV rows are stored, as zeros).
     const int base = i0 + 32 * m + 4 * h;
-    const int lo = j_col - base;  // alive when 8*g4 + e >= lo (causal)
-    const int hi = j_col < Nk ? N - base : 0;  // alive when 8*g4 + e < hi (ragged, key length)
+    const int lo = j_col - base;     // alive when 8*g4 + e >= lo (causal)
+    const int hi = row_end - base;   // alive when 8*g4 + e <  hi
     half8 pb[2], sb[2];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
@@ -258,7 +258,7 @@ struct QWave {
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
-                                       int i_row, int Nk, int lane,
+                                       int i_row, int Nk, int key_lo, int lane,
                                        const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
@@ -271,15 +271,16 @@ struct QWave {
     // dS^T. A lane holds query row i_row and the 16 keys
     // j = j0 + 32s + 8*g4 + 4h + e. Rows i_row >= N are never stored.
     const int base = j0 + 32 * s + 4 * h;
-    const int lo = i_row - base;  // alive when 8*g4 + e <= lo (causal)
-    const int hi = Nk - base;     // alive when 8*g4 + e <  hi (ragged N, key length)
+    const int lo = i_row - base;   // alive when 8*g4 + e <= lo (causal)
+    const int hi = Nk - base;      // alive when 8*g4 + e <  hi (ragged N, key length)
+    const int lw = key_lo - base;  // alive when 8*g4 + e >= lw (sliding window)
     half8 sb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int idx = 8 * (r >> 2) + (r & 3);
       float p = fast_exp2(fmaf(st[r], c, -lse2));
       if (CAUSAL) p = (idx <= lo) ? p : 0.f;
-      if (BOUNDS) p = (idx < hi) ? p : 0.f;
+      if (BOUNDS) p = (idx < hi && idx >= lw) ? p : 0.f;
       sb[r >> 3][r & 7] = to16<BF>(p * (pt[r] - dvv));
     }
     // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15.
@@ -301,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     half_t* __restrict__ dV,
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2,
     Strides stq, Strides stk, unsigned* __restrict__ counters, float* __restrict__ slots,
-    int split_num, int split_bias, const int* __restrict__ kv_len) {
+    int split_num, int split_bias, const int* __restrict__ kv_len, int window) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -330,6 +331,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int b = bkv / Hkv, hkv = bkv % Hkv;
   // Per-entry key length (key padding), clamped to [1, N].
   const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
+  // Causal sliding window (only in the masked instantiation): row i sees keys
+  // (i - Wb, i]; 0 = none.
+  const int Wb = BOUNDS ? window : 0;
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
   // Offset of query head hq's row 0 in Q, dO, dQ.
@@ -361,12 +365,15 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // whichever workgroup finishes second adds the other's partial to its own
   // and stores the result (fp32 a + b == b + a, so the outcome does not depend
   // on which one that is).
+  // Query rows of key tile u's phase 1: from its diagonal (causal) to the end,
+  // or to the last row whose window reaches the tile.
+  auto q_end = [&](int u) { return Wb > 0 ? min(N, u * kTile + kTile + Wb - 1) : N; };
   auto n_iters = [&](int u) {
-    return group * ((N - (CAUSAL ? u * kTile : 0) + kSub - 1) / kSub);
+    return group * ((q_end(u) - (CAUSAL ? u * kTile : 0) + kSub - 1) / kSub);
   };
   auto split = [&](int u) {
     const int m = n_tiles - 1 - 2 * u;
-    if (!CAUSAL || m <= 0) return 0;
+    if (!CAUSAL || m <= 0 || Wb > 0) return 0;  // windows leave the tiles' work equal
     return max(0, min((group * m * split_num - split_bias) >> 8, n_iters(u) - 1));
   };
   const int tw = wi % n_tiles;
@@ -399,7 +406,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
 
     const int i_start = CAUSAL ? tp0 : 0;  // tp0 is a multiple of kSub
-    const int n_qt = (N - i_start + kSub - 1) / kSub;
+    const int n_qt = (q_end(tile) - i_start + kSub - 1) / kSub;
+    // Rows this wave's key column reaches (see KVWave::step).
+    const int row_end = j_col < Nk ? (Wb > 0 ? min(N, j_col + Wb) : N) : 0;
 
     // Q, dO tiles and lse2, dvec of flattened step `it` (clamped to the last
     // one, so that every step issues the same loads) into one stage.
@@ -430,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const int i0 = i_start + (it % n_qt) * kSub;
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, N, Nk, lane, roff,
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_end, lane, roff,
              so, scale_log2);
       wait_vmem();
       __syncthreads();
@@ -521,6 +530,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const bool row_ok = !BOUNDS || i_row < N;
     const int kv_end = CAUSAL ? min(Nk, t0 + kTile) : Nk;
     const int n_kt = (kv_end + kSub - 1) / kSub;
+    // With a window, key tiles left of every row's window are skipped, and
+    // each row masks the keys left of its own.
+    const int t_lo = Wb > 0 ? max(0, t0 - Wb + 1) / kSub : 0;
+    const int key_lo = Wb > 0 ? i_row - Wb + 1 : -(1 << 30);
 
     for (int g = 0; g < group; ++g) {
       const int hq = hkv * group + g;
@@ -550,14 +563,15 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
         fetch(t + 1, P ? ta0 : ta1, P ? tb0 : tb1);
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, lane, so, scale_log2);
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, key_lo, lane, so,
+               scale_log2);
         wait_vmem();
         __syncthreads();
       };
-      fetch(0, ta0, tb0);
+      fetch(t_lo, ta0, tb0);
       wait_vmem();
       __syncthreads();
-      int t = 0;
+      int t = t_lo;  // buffer parity counts from t_lo
       for (; t + 2 <= n_kt; t += 2) {
         step(t, P0{});
         step(t + 1, P1{});
@@ -618,14 +632,15 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots, kSplitNum,
-                     kSplitBias, a.kv_len);
+                     kSplitBias, a.kv_len, a.window);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
-  // Key lengths need the masked instantiation (kTile is a multiple of kSub).
-  const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr;
+  // Key lengths and windows need the masked instantiation (kTile is a
+  // multiple of kSub).
+  const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0;
   if (a.causal)
     return bounds ? launch_main_t<D, true, true, BF>(a) : launch_main_t<D, true, false, BF>(a);
   return bounds ? launch_main_t<D, false, true, BF>(a) : launch_main_t<D, false, false, BF>(a);

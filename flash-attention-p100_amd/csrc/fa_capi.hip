@@ -4,7 +4,7 @@
 // torch (fa_p100_ext.cu:59-65, 111-113): head dim, positive N, the head
 // grouping. Tensor-type checks ("must be a CUDA tensor", "must be fp16") live
 // in the torch extension, where tensors exist. Nothing here allocates or keeps
-// state beyond each kernel's one-time LDS-limit attribute.
+// state: every kernel's LDS is static, so launches need no attributes set.
 #include <limits.h>
 
 #include "../../include/fa_mi355x.h"
@@ -47,6 +47,7 @@ const char* fa_error_string(int err) {
     case FA_ERR_TOO_LARGE: return "shape exceeds the kernels' index range";
     case FA_ERR_LAYOUT: return "layout must be FA_LAYOUT_BHND or FA_LAYOUT_BNHD";
     case FA_ERR_DTYPE: return "unsupported element format";
+    case FA_ERR_WINDOW: return "sliding window must be >= 0 and needs causal masking";
     default: return hipGetErrorString((hipError_t)err);
   }
 }
@@ -55,14 +56,16 @@ const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
                int Hkv, int N, int D, int causal, int layout, int dtype, void* stream,
-               const int* kv_len = nullptr) {
+               const int* kv_len = nullptr, int window = 0) {
+  if (window < 0 || (window > 0 && !causal)) return FA_ERR_WINDOW;
   if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout, dtype, kv_len};
+  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout, dtype, kv_len,
+                window};
   return to_code(fa::launch_fwd(a));
 }
 
@@ -128,7 +131,8 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* wor
 static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
-                    int layout, int dtype, void* stream, const int* kv_len = nullptr) {
+                    int layout, int dtype, void* stream, const int* kv_len = nullptr,
+                    int window = 0) {
   int rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -160,6 +164,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.layout = layout;
   a.dtype = dtype;
   a.kv_len = kv_len;
+  a.window = window;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -167,7 +172,9 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
 static int bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
                        const float* lse, void* dq, void* dk, void* dv, void* workspace,
                        size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
-                       int layout, int dtype, void* stream, const int* kv_len = nullptr) {
+                       int layout, int dtype, void* stream, const int* kv_len = nullptr,
+                       int window = 0) {
+  if (window < 0 || (window > 0 && !causal)) return FA_ERR_WINDOW;
   if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
   const int rc = check_shape(B, Hq, Hkv, N, D);
@@ -177,7 +184,7 @@ static int bwd_half_dq(const void* q, const void* k, const void* v, const void* 
   int e = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, layout, dtype, stream);
   if (e != FA_OK) return e;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
-                  causal, layout, dtype, stream, kv_len);
+                  causal, layout, dtype, stream, kv_len, window);
 }
 
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, void* workspace,
@@ -213,17 +220,17 @@ int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* dO, con
 }
 
 int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
-              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int dtype,
-              int layout, void* stream) {
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, layout, dtype, stream, kv_len);
+              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int window,
+              int dtype, int layout, void* stream) {
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, layout, dtype, stream, kv_len, window);
 }
 
 int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const void* o,
               const float* lse, const int* kv_len, void* dq, void* dk, void* dv,
               void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D,
-              int causal, int dtype, int layout, void* stream) {
+              int causal, int window, int dtype, int layout, void* stream) {
   return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, layout, dtype, stream, kv_len);
+                     D, causal, layout, dtype, stream, kv_len, window);
 }
 
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,

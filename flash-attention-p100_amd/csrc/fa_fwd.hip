@@ -102,7 +102,7 @@ struct FwdWave {
   // MASK: the step may need the causal / ragged mask, applied when `masked`.
   template <bool MASK, bool NEXT, class Issue>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
-                                       bool masked, int i_row, int N, int lane, int roff,
+                                       bool masked, int i_row, int N, int w_lo, int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
@@ -119,7 +119,8 @@ struct FwdWave {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int j = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        if ((CAUSAL && j > i_row) || (BOUNDS && j >= N)) s[r] = -INFINITY;
+        // w_lo: the last key left of this row's sliding window (INT_MIN if none)
+        if ((CAUSAL && j > i_row) || (BOUNDS && (j >= N || j <= w_lo))) s[r] = -INFINITY;
       }
     }
     float mloc = s[0];
@@ -172,7 +173,7 @@ struct FwdWave {
 template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
-                                         float* __restrict__ Lse, int N, int Nk, int sq, int sk,
+                                         float* __restrict__ Lse, int N, int Nk, int W, int sq, int sk,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -205,6 +206,17 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // ones run masked; blocks wholly past the diagonal or past N give exact
   // zeros there (their few products are not skipped, so every wave issues its
   // share of the loads inside the same code).
+  // Sliding window W (causal only; 0 = none): row i sees keys (i - W, i], so
+  // this tile's first visible key is q0 - W + 1 and the steps before j_lo are
+  // skipped; a wave's steps before n_head (blocks reaching left of its rows'
+  // windows) are masked, like the diagonal ones.
+  // Only the masked instantiation (BOUNDS) takes a window, so the others keep
+  // their loop structure.
+  const int Wb = BOUNDS ? W : 0;
+  const int j_lo = Wb > 0 ? max(0, q0 - Wb + 1) / kKV : 0;
+  const int win_last = i_base + 31 - Wb - kq * 32;  // last masked block start (Wb > 0)
+  const int n_head = Wb > 0 && win_last >= 0 ? max(j_lo, win_last / kKV + 1) : j_lo;
+  const int w_lo = Wb > 0 ? i_row - Wb : INT_MIN;
   int n_full = n_it;
   if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
   if (BOUNDS) n_full = min(n_full, Nk - 32 - kq * 32 >= 0 ? (Nk - 32 - kq * 32) / kKV + 1 : 0);
@@ -218,11 +230,11 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   TilePlan<D, kKV, kWaves, false> plan;
   plan.init(wave, lane, sk);
   const rsrc_t rk = rows_rsrc<D>(K, Nk, sk), rv = rows_rsrc<D>(V, Nk, sk);
-  const int k1 = min(1, n_it - 1) * kKV;
+  const int k1 = min(j_lo + 1, n_it - 1) * kKV;
 #pragma unroll
   for (int u = 0; u < TL::kParts; ++u) {
-    plan.part(kt0, rk, 0, wave, u);
-    plan.part(vt0, rv, 0, wave, u);
+    plan.part(kt0, rk, j_lo * kKV, wave, u);
+    plan.part(vt0, rv, j_lo * kKV, wave, u);
     plan.part(kt1, rk, k1, wave, u);
   }
   wait_vmem();
@@ -253,7 +265,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     };
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
-    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j >= n_full, i_row, Nk, lane,
+    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
+                                Nk, w_lo, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -265,7 +278,16 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   using T = std::true_type;
   using F = std::false_type;
   const int n_plain = min(n_full, n_it - 1);  // unmasked steps with a next step
-  int j = 0;
+  // Buffer parity counts from j_lo. Every wave runs steps j_lo .. n_it-1, one
+  // barrier each; only which of them are masked differs between waves.
+  int j = j_lo;
+  if (Wb > 0) {  // masked steps at the window's left edge
+    for (; j < min(n_head, n_it - 1); ++j) {
+      if ((j - j_lo) & 1) run(j, P1{}, T{}, T{});
+      else run(j, P0{}, T{}, T{});
+    }
+    if (((j - j_lo) & 1) && j < n_plain) run(j++, P1{}, T{}, T{});  // even parity for the loop
+  }
   for (; j + 2 <= n_plain; j += 2) {
     run(j, P0{}, F{}, T{});
     run(j + 1, P1{}, F{}, T{});
@@ -274,11 +296,11 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // at run time: fewer inlined copies of the step keep the accumulators in
   // one set of registers.
   for (; j < n_it - 1; ++j) {
-    if (j & 1) run(j, P1{}, T{}, T{});
+    if ((j - j_lo) & 1) run(j, P1{}, T{}, T{});
     else run(j, P0{}, T{}, T{});
   }
   // last step: no next S^T, no loads
-  if (j & 1) run(j, P1{}, T{}, F{});
+  if ((j - j_lo) & 1) run(j, P1{}, T{}, F{});
   else run(j, P0{}, T{}, F{});
   __syncthreads();  // every wave is done reading the tiles (they hold the merge area)
 
@@ -319,7 +341,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
       wk[k] = (mk[k] == -INFINITY) ? 0.f : fast_exp2((mk[k] - m_star) * c);
       l_star += wk[k] * lk[k];
     }
-    const float inv_l = 1.f / l_star;
+    // A row that saw no key (key lengths with a window: pad rows past the
+    // window) gets O = 0 and LSE = +inf, so its backward P is 0 as well.
+    const float inv_l = l_star > 0.f ? 1.f / l_star : 0.f;
     if (row_ok) {
       half_t* orow = O + (size_t)i_row * sq + cb * 32;
 #pragma unroll
@@ -337,7 +361,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
         for (int e = 0; e < 4; ++e) o4[e] = to16<BF>(acc[e] * inv_l);
         *reinterpret_cast<half4*>(orow + 8 * g + 4 * h) = o4;
       }
-      if (cb == 0 && h == 0) Lse[i_row] = (m_star * c + __log2f(l_star)) * kLn2;
+      if (cb == 0 && h == 0)
+        Lse[i_row] = l_star > 0.f ? (m_star * c + __log2f(l_star)) * kLn2 : INFINITY;
     }
   }
   __syncthreads();  // the LDS is reused by the next tile
@@ -348,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
-    Strides stk, const int* __restrict__ kv_len) {
+    Strides stk, const int* __restrict__ kv_len, int window) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -373,7 +398,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                Lse + (size_t)bh * N, N, Nk, stq.n, stk.n, t ? second : first,
+                                Lse + (size_t)bh * N, N, Nk, window, stq.n, stk.n,
+                                t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
@@ -389,14 +415,15 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len);
+                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  // Key lengths need the masked instantiation (kKV is a multiple of kBR).
-  const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr;
+  // Key lengths and windows need the masked instantiation (kKV is a multiple
+  // of kBR).
+  const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0;
   if (a.causal)
     return bounds ? launch_fwd_t<D, true, true, BF>(a) : launch_fwd_t<D, true, false, BF>(a);
   return bounds ? launch_fwd_t<D, false, true, BF>(a) : launch_fwd_t<D, false, false, BF>(a);

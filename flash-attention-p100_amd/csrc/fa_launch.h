@@ -35,6 +35,7 @@ struct FwdArgs {
   int layout = kBHND;  // of q, k, v, o (lse is always dense (B, Hq, N))
   int dtype = kFP16;   // of q, k, v, o
   const int* kv_len = nullptr;  // device, B entries: keys [0, kv_len[b]) exist (else N)
+  int window = 0;               // causal sliding window W: row i sees keys (i - W, i]; 0 = none
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -85,6 +86,7 @@ struct BwdArgs {
   float* slots = nullptr;        // workspace: partial dK/dV of split key tiles
   int dtype = kFP16;             // of q, k, v, dO, o, dk, dv and dq16
   const int* kv_len = nullptr;   // as FwdArgs::kv_len
+  int window = 0;                // as FwdArgs::window
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

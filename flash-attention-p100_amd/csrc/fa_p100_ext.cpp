@@ -176,7 +176,7 @@ static void check_bnhd(const at::Tensor& t, const char* name) {
 }
 
 std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
-                                        c10::optional<at::Tensor> kv_len) {
+                                        c10::optional<at::Tensor> kv_len, int64_t window) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -198,14 +198,16 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), B, H, Hkv, N, D,
-                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BNHD, current_stream(q)),
+                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BNHD,
+                     current_stream(q)),
            "fa_fwd_ex");
   return {o, lse};
 }
 
 std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v,
                                          at::Tensor dO, at::Tensor o, at::Tensor lse,
-                                         bool causal, c10::optional<at::Tensor> kv_len) {
+                                         bool causal, c10::optional<at::Tensor> kv_len,
+                                         int64_t window) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -232,17 +234,19 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), dq.data_ptr(),
                      dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, H, Hkv, N, D,
-                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BNHD, current_stream(q)),
+                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BNHD,
+                     current_stream(q)),
            "fa_bwd_ex");
   return {dq, dk, dv};
 }
 
 // Dense (B, H, N, D) tensors in fp16 or bf16 (one format for all), results in
 // that format, dq included, and optional key lengths kv_len (int32 (B,), right
-// padding: entry b has keys [0, kv_len[b])). For fp16 without kv_len the same
+// padding: entry b has keys [0, kv_len[b])) and sliding window (causal: row i
+// sees keys (i - window, i]; 0 = none). For fp16 without either, the same
 // kernels as forward and backward_half_dq.
 std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
-                                      c10::optional<at::Tensor> kv_len) {
+                                      c10::optional<at::Tensor> kv_len, int64_t window) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -267,14 +271,15 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), B, H, Hkv, N, D,
-                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BHND, current_stream(q)),
+                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BHND,
+                     current_stream(q)),
            "fa_fwd_ex");
   return {o, lse};
 }
 
 std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
                                        at::Tensor o, at::Tensor lse, bool causal,
-                                       c10::optional<at::Tensor> kv_len) {
+                                       c10::optional<at::Tensor> kv_len, int64_t window) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -306,7 +311,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), dq.data_ptr(),
                      dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, H, Hkv, N, D,
-                     causal ? 1 : 0, dtype_code(q), FA_LAYOUT_BHND, current_stream(q)),
+                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BHND,
+                     current_stream(q)),
            "fa_bwd_ex");
   return {dq, dk, dv};
 }
@@ -318,16 +324,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "FlashAttention backward (gfx950), dq as fp16 (used by the autograd Function)");
   m.def("forward_bnhd", &fa_forward_bnhd,
         "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors", py::arg("q"),
-        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none());
+        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
-        py::arg("causal"), py::arg("kv_len") = py::none());
+        py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
-        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none());
+        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
-        py::arg("causal"), py::arg("kv_len") = py::none());
+        py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
 }

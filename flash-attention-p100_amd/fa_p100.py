@@ -66,7 +66,7 @@ class _FlashAttnP100(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, full_precision, kv_len=None):
+    def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -74,13 +74,14 @@ class _FlashAttnP100(torch.autograd.Function):
         kb, vb = _bnhd_storage(k), _bnhd_storage(v)
         ctx.causal = causal
         ctx.kv_len = kv_len
+        ctx.window = window
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
-            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len)
+            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
-        if q.dtype == torch.bfloat16 or kv_len is not None:
-            o, lse = _ext.forward_dt(q, k, v, causal, kv_len)
+        if q.dtype == torch.bfloat16 or kv_len is not None or window:
+            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -91,22 +92,24 @@ class _FlashAttnP100(torch.autograd.Function):
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
-            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len)
-            return dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2), None, None, None
+            dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
+                                            ctx.window)
+            return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
+                    None, None, None, None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
         # `_ext.backward(...)[0].to(torch.float16)`) instead of a separate cast,
         # and backward_dt to bf16 for bf16 inputs.
         g = grad_o.contiguous()
-        if q.dtype == torch.bfloat16 or ctx.kv_len is not None:
-            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len)
+        if q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window:
+            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None
 
 
-def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None):
+def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -120,9 +123,18 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None):
       * kv_len, an int32 tensor (B,) on q's device, gives each batch entry's
         key length (right padding): entry b has keys [0, kv_len[b]) (values
         clamped to [1, N]); every query row, pad rows included, attends to
-        those keys only, and the gradients of k, v past kv_len[b] are zero.
+        those keys only, and the gradients of k, v past kv_len[b] are zero;
+      * sliding_window W (causal only): query row i attends to keys
+        (i - W, i]. A row that then sees no key at all (only possible with
+        kv_len: a pad row more than W past its entry's length) gets o = 0 and
+        zero gradients.
     """
-    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len)
+    window = 0
+    if sliding_window is not None:
+        window = int(sliding_window)
+        if window <= 0 or not causal:
+            raise ValueError("sliding_window must be positive and needs causal=True")
+    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window)
 
 
 def _expand_kv(k, n_head):

@@ -21,10 +21,15 @@ zeros) is served exactly: its row sums go to the kernels as per-entry key
 lengths, so every position attends to the real keys only, as with eager
 attention and the same mask.
 
+Also beyond the reference, a causal layer's sliding window (Qwen3's and
+Mistral-style `sliding_window`) runs in the kernels: row i sees keys
+(i - W, i], as transformers' own sliding-window mask.
+
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): other attention / padding masks,
-output_attentions, head_mask, sliding windows, dropout, head_dim other than
-64/128, a scale other than 1/sqrt(D), q_len != kv_len (KV-cache decoding).
+output_attentions, head_mask, a window on non-causal attention, dropout,
+head_dim other than 64/128, a scale other than 1/sqrt(D), q_len != kv_len
+(KV-cache decoding).
 """
 import contextvars
 import warnings
@@ -73,10 +78,6 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             "output_attentions=True is not available; use attn_implementation='eager'.")
     if kwargs.get("head_mask") is not None:
         raise NotImplementedError("fa_p100 does not support head_mask.")
-    if kwargs.get("sliding_window") is not None:
-        raise NotImplementedError(
-            f"fa_p100 is dense or causal only; this layer asks for a sliding window "
-            f"of {kwargs['sliding_window']}.")
     if dropout:
         raise NotImplementedError(f"fa_p100 has no attention dropout (got {dropout}).")
 
@@ -95,6 +96,11 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
 
     if is_causal is None:
         is_causal = getattr(module, "is_causal", True) and query.size(2) > 1
+    sliding_window = kwargs.get("sliding_window")
+    if sliding_window is not None and (not is_causal or sliding_window <= 0):
+        raise NotImplementedError(
+            f"fa_p100 serves sliding windows on causal attention only; this layer asks for "
+            f"a window of {sliding_window} with is_causal={is_causal}.")
 
     # The kernels take fp16. Under fp16 autocast, Qwen3's fp32 q_norm/k_norm
     # weights and rotary tables hand q and k over in fp32 while v is fp16, so
@@ -121,7 +127,7 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
                 "fa_p100: the padding mask given to the model does not match this "
                 "attention call's batch.")
     out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
-                     kv_len=kv_len)
+                     kv_len=kv_len, sliding_window=sliding_window)
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
 

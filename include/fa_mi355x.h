@@ -43,7 +43,8 @@ enum {
   FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
   FA_ERR_TOO_LARGE = 10007,  /* an index would overflow the kernels' 32-bit row counters */
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
-  FA_ERR_DTYPE = 10009       /* element format not supported */
+  FA_ERR_DTYPE = 10009,      /* element format not supported */
+  FA_ERR_WINDOW = 10010      /* sliding window < 0, or > 0 without causal masking */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -182,24 +183,27 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
                 int causal, void* stream);
 
 /*
- * The general pair, covering every variant above plus key padding: element
- * format `dtype` (FA_DTYPE_FP16 / FA_DTYPE_BF16), `layout`
- * (FA_LAYOUT_BHND / FA_LAYOUT_BNHD) and, when `kv_len` is not NULL, a device
- * array of B int32 key lengths: for batch entry b only keys
- * [0, kv_len[b]) exist (right padding; values are clamped to [1, N]), every
- * query row (pad rows included) attends to those keys only, and dk/dv rows
- * past kv_len[b] come out zero. fa_bwd_ex writes dq in `dtype`. No
- * counterpart in the reference, which raises on padding masks and on bf16
- * (README.md:72-75, fa_p100_hf.py:64-70); kv_len serves the HF hook's
- * right-padded batches.
+ * The general pair, covering every variant above plus key padding and
+ * sliding windows: element format `dtype` (FA_DTYPE_FP16 / FA_DTYPE_BF16),
+ * `layout` (FA_LAYOUT_BHND / FA_LAYOUT_BNHD);
+ *   - `kv_len`, when not NULL, a device array of B int32 key lengths: for
+ *     batch entry b only keys [0, kv_len[b]) exist (right padding; values are
+ *     clamped to [1, N]), every query row (pad rows included) attends to those
+ *     keys only, and dk/dv rows past kv_len[b] come out zero;
+ *   - `window` W > 0 (causal only): query row i attends to keys (i - W, i].
+ *     With key lengths too, a pad row more than W past its entry's length sees
+ *     no key: its o is 0, its lse +inf and its gradients 0.
+ * fa_bwd_ex writes dq in `dtype`. No counterpart in the reference, which
+ * raises on padding masks, sliding windows and bf16 (README.md:72-75,
+ * fa_p100_hf.py:64-82); kv_len and window serve the HF hook.
  */
 int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
-              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int dtype,
-              int layout, void* stream);
+              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int window,
+              int dtype, int layout, void* stream);
 int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const void* o,
               const float* lse, const int* kv_len, void* dq, void* dk, void* dv,
               void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D,
-              int causal, int dtype, int layout, void* stream);
+              int causal, int window, int dtype, int layout, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

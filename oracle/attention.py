@@ -60,7 +60,7 @@ def _group_sum(g, hkv):
     return g.reshape(b, hkv, hq // hkv, n, d).sum(axis=2)
 
 
-def _scores(q, k, causal, dtype, kv_len=None):
+def _scores(q, k, causal, dtype, kv_len=None, window=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
@@ -68,7 +68,9 @@ def _scores(q, k, causal, dtype, kv_len=None):
     q_len == kv_len: key col is masked for query row when col > row
     (flash_fwd.cuh:239). With `kv_len` (B ints, an extension: the reference
     has no padding masks) key col is also masked for batch entry b when
-    col >= kv_len[b], clamped to [1, N] as the kernels do.
+    col >= kv_len[b], clamped to [1, N] as the kernels do. With `window` W
+    (causal only, another extension) key col is also masked for row when
+    col <= row - W: each row sees its last W keys.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d)
@@ -77,6 +79,11 @@ def _scores(q, k, causal, dtype, kv_len=None):
     if causal:
         mask = np.triu(np.ones((n, n), dtype=bool), 1)
         s = np.where(mask, -np.inf, s).astype(dtype)
+    if window is not None:
+        if not causal:
+            raise ValueError("a sliding window needs causal masking")
+        mask = np.tril(np.ones((n, n), dtype=bool), -int(window))
+        s = np.where(mask, -np.inf, s).astype(dtype)
     if kv_len is not None:
         lens = np.clip(np.asarray(kv_len).reshape(-1), 1, n)
         cols = np.arange(n)[None, :] >= lens[:, None]  # (B, N) masked key columns
@@ -84,23 +91,28 @@ def _scores(q, k, causal, dtype, kv_len=None):
     return s
 
 
-def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None):
+def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
-    (flash_fwd.cuh:324-329). `kv_len`: optional per-entry key lengths (see
-    _scores).
+    (flash_fwd.cuh:324-329). `kv_len`, `window`: optional per-entry key
+    lengths and sliding window (see _scores).
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype, kv_len)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window)
     m = s.max(axis=-1, keepdims=True)
+    # A row that sees no key at all (only with both key lengths and a window:
+    # pad rows more than W past their entry's length) gets O = 0 and
+    # LSE = +inf, so that the backward's P = exp(S - LSE) is 0 there too.
+    empty = m == -np.inf
+    m = np.where(empty, 0, m)
     p = np.exp(s - m)
     l = p.sum(axis=-1, keepdims=True)
-    o = np.matmul(p / l, v.astype(dtype))
-    lse = (m + np.log(l))[..., 0]
+    o = np.matmul(p / np.where(empty, 1, l), v.astype(dtype))
+    lse = np.where(empty, np.inf, m + np.log(np.where(empty, 1, l)))[..., 0]
     return o, lse
 
 
@@ -109,7 +121,8 @@ def bwd_preprocess(o, do, dtype=np.float64):
     return (np.asarray(o).astype(dtype) * np.asarray(do).astype(dtype)).sum(axis=-1)
 
 
-def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None):
+def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
+                  window=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -125,8 +138,8 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     qd = q.astype(dtype)
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
-        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len)
-    s = _scores(q, ke, causal, dtype, kv_len)
+        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window)
+    s = _scores(q, ke, causal, dtype, kv_len, window)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     dv = np.matmul(np.swapaxes(p, -1, -2), dod)
     dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
@@ -137,9 +150,9 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     return dq, _group_sum(dk, hkv), _group_sum(dv, hkv)
 
 
-def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None):
+def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

@@ -64,6 +64,10 @@ def load_capi():
     lib.fa_fwd_bf16.restype = i
     lib.fa_bwd_bf16.argtypes = [vp] * 10 + [sz] + [i] * 7 + [vp]
     lib.fa_bwd_bf16.restype = i
+    lib.fa_fwd_ex.argtypes = [vp] * 6 + [i] * 9 + [vp]
+    lib.fa_fwd_ex.restype = i
+    lib.fa_bwd_ex.argtypes = [vp] * 11 + [sz] + [i] * 9 + [vp]
+    lib.fa_bwd_ex.restype = i
     return lib
 
 

@@ -58,6 +58,9 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd_bf16(z, z, z, z, z, 1, 2, 2, 8, 64, 0, 1, s) == 10005
     assert lib.fa_bwd_bf16(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, 0, s) == 10006
     assert lib.fa_bwd_bf16(*([one] * 10), 1 << 30, 1, 2, 2, 8, 64, 0, -1, s) == 10008
+    assert lib.fa_fwd_ex(*([one] * 6), 1, 2, 2, 8, 64, 0, 16, 0, 0, s) == 10010  # window, no causal
+    assert lib.fa_fwd_ex(*([one] * 6), 1, 2, 2, 8, 64, 1, -1, 0, 0, s) == 10010
+    assert lib.fa_bwd_ex(*([one] * 11), 0, 1, 2, 2, 8, 64, 0, 4, 0, 0, s) == 10010
     assert b"layout" in lib.fa_error_string(10008)
     assert b"format" in lib.fa_error_string(10009)
 
@@ -79,13 +82,14 @@ def test_public_api_surface_matches_reference():
     import fa_p100
     import fa_p100_hf
     sig = inspect.signature(fa_p100.flash_attn)
-    # The reference's parameters, in order, with its defaults; kv_len (key
-    # lengths, an extension) comes last and defaults to None, so every
-    # reference call binds the same way.
+    # The reference's parameters, in order, with its defaults; the extensions
+    # (key lengths, sliding window) come after them and default to None, so
+    # every reference call binds the same way.
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False
-    assert list(sig.parameters)[5:] == ["kv_len"] and sig.parameters["kv_len"].default is None
+    assert list(sig.parameters)[5:] == ["kv_len", "sliding_window"]
+    assert all(sig.parameters[n].default is None for n in ("kv_len", "sliding_window"))
     for name in ("_FlashAttnP100", "reference", "_expand_kv", "_ext"):
         assert hasattr(fa_p100, name)
     for name in ("fa_p100_attention_forward", "register", "enable_fa_p100", "_set_impl"):

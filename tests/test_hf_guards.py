@@ -26,7 +26,8 @@ MOD = types.SimpleNamespace(is_causal=True)
     (dict(attention_mask=torch.ones(1, 1, 4, 4)), "attention mask"),
     (dict(attention_mask=None, output_attentions=True), "output_attentions"),
     (dict(attention_mask=None, head_mask=torch.ones(4)), "head_mask"),
-    (dict(attention_mask=None, sliding_window=128), "sliding window of 128"),
+    (dict(attention_mask=None, sliding_window=128, is_causal=False), "a window of 128"),
+    (dict(attention_mask=None, sliding_window=0), "a window of 0"),
     (dict(attention_mask=None, dropout=0.1), "dropout"),
 ])
 def test_unsupported_requests_raise(kwargs, match):

@@ -221,3 +221,45 @@ def test_kv_len_pins(causal):
             fd = (ora.attention_loss(*plus, do, causal, kv_len=lens)
                   - ora.attention_loss(*minus, do, causal, kv_len=lens)) / (2 * h)
             assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
+
+
+@pytest.mark.parametrize("window", [1, 5, 23, 40])
+def test_sliding_window_pins(window):
+    """Sliding window W (causal; an extension): row i sees keys (i - W, i].
+    Pinned against torch SDPA with an explicit band mask, W >= N equal to
+    plain causal, W = 1 giving O = V row by row, and finite differences."""
+    rng = np.random.default_rng(window)
+    b, hq, hkv, n, d = 2, 4, 2, 23, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    lens = np.array([n, 11])
+    o, _ = ora.attention_fwd(q, k, v, True, kv_len=lens, window=window)
+    grads = ora.attention_bwd(q, k, v, do, True, kv_len=lens, window=window)
+    i, j = np.arange(n)[:, None], np.arange(n)[None, :]
+    for e, L in enumerate(lens):
+        band = (j <= i) & (j > i - window) & (j < L)
+        ke = torch.tensor(np.repeat(k[e:e + 1], hq // hkv, axis=1))
+        ve = torch.tensor(np.repeat(v[e:e + 1], hq // hkv, axis=1))
+        ref = F.scaled_dot_product_attention(torch.tensor(q[e:e + 1]), ke, ve,
+                                             attn_mask=torch.tensor(band)).numpy()
+        seen = band.any(axis=1)  # rows with no key at all: O = 0, zero gradients
+        assert np.allclose(o[e][:, seen], ref[0][:, seen], atol=1e-12)
+        assert not np.any(o[e][:, ~seen]) and not np.any(grads[0][e][:, ~seen])
+    if window >= n:
+        assert np.array_equal(o, ora.attention_fwd(q, k, v, True, kv_len=lens)[0])
+    if window == 1:  # each row sees only itself (entry 0 has every key)
+        assert np.allclose(o[0], np.repeat(v, hq // hkv, axis=1)[0], atol=1e-12)
+    h = 1e-4
+    for which, g in enumerate(grads):
+        for _ in range(4):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, True, kv_len=lens, window=window)
+                  - ora.attention_loss(*minus, do, True, kv_len=lens, window=window)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
+    with pytest.raises(ValueError):
+        ora.attention_fwd(q, k, v, False, window=window)
