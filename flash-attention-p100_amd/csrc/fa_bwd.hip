@@ -206,8 +206,9 @@ struct KVWave {
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
-                                       int m, int kr0, int i0, int j_col, int row_end, int lane,
-                                       int roff, const typename Swz<D>::Offsets& so, float c) {
+                                       int m, int kr0, int i0, int j_col, int row_end,
+                                       float alibi_raw, int lane, int roff,
+                                       const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
     floatx16 sacc = zero16(), pacc = zero16();
@@ -223,6 +224,11 @@ struct KVWave {
     const int base = i0 + 32 * m + 4 * h;
     const int lo = j_col - base;     // alive when 8*g4 + e >= lo (causal)
     const int hi = row_end - base;   // alive when 8*g4 + e <  hi
+    if (BOUNDS && alibi_raw != 0.f) {  // ALiBi: -slope |i - j| in raw-score units
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        sacc[r] -= alibi_raw * fabsf((float)(base + 8 * (r >> 2) + (r & 3) - j_col));
+    }
     half8 pb[2], sb[2];
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
@@ -258,7 +264,7 @@ struct QWave {
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
-                                       int i_row, int Nk, int key_lo, int lane,
+                                       int i_row, int Nk, int key_lo, float alibi_raw, int lane,
                                        const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
@@ -274,6 +280,11 @@ struct QWave {
     const int lo = i_row - base;   // alive when 8*g4 + e <= lo (causal)
     const int hi = Nk - base;      // alive when 8*g4 + e <  hi (ragged N, key length)
     const int lw = key_lo - base;  // alive when 8*g4 + e >= lw (sliding window)
+    if (BOUNDS && alibi_raw != 0.f) {  // ALiBi: -slope |i - j| in raw-score units
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        st[r] -= alibi_raw * fabsf((float)(i_row - base - 8 * (r >> 2) - (r & 3)));
+    }
     half8 sb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -302,7 +313,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     half_t* __restrict__ dV,
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2,
     Strides stq, Strides stk, unsigned* __restrict__ counters, float* __restrict__ slots,
-    int split_num, int split_bias, const int* __restrict__ kv_len, int window) {
+    int split_num, int split_bias, const int* __restrict__ kv_len, int window,
+    const float* __restrict__ alibi) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -439,8 +451,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const int i0 = i_start + (it % n_qt) * kSub;
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_end, lane, roff,
-             so, scale_log2);
+      const float alibi_raw =
+          BOUNDS && alibi ? alibi[hkv * group + (it / n_qt)] / scale : 0.f;  // step's query head
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_end, alibi_raw, lane,
+             roff, so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -538,6 +552,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     for (int g = 0; g < group; ++g) {
       const int hq = hkv * group + g;
       const size_t bhq = (size_t)b * Hq + hq;
+      const float alibi_raw = BOUNDS && alibi ? alibi[hq] / scale : 0.f;
       const half_t* Qg = Q + q_off(hq);
       const half_t* dOg = dO + q_off(hq);
       QWave<D, CAUSAL, BOUNDS, BF> w;
@@ -563,8 +578,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
         fetch(t + 1, P ? ta0 : ta1, P ? tb0 : tb1);
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, key_lo, lane, so,
-               scale_log2);
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, key_lo, alibi_raw, lane,
+               so, scale_log2);
         wait_vmem();
         __syncthreads();
       };
@@ -632,15 +647,16 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots, kSplitNum,
-                     kSplitBias, a.kv_len, a.window);
+                     kSplitBias, a.kv_len, a.window, a.alibi);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
-  // Key lengths and windows need the masked instantiation (kTile is a
+  // Key lengths, windows and ALiBi need the masked instantiation (kTile is a
   // multiple of kSub).
-  const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0;
+  const bool bounds =
+      (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 || a.alibi != nullptr;
   if (a.causal)
     return bounds ? launch_main_t<D, true, true, BF>(a) : launch_main_t<D, true, false, BF>(a);
   return bounds ? launch_main_t<D, false, true, BF>(a) : launch_main_t<D, false, false, BF>(a);

@@ -54,35 +54,61 @@ const char* fa_error_string(int err) {
 
 const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
+// Options: every field checked; the defaults are fp16, (B, H, N, D), no key
+// lengths, no window, no ALiBi.
+constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0, nullptr};
+
+static int check_opts(const fa_options& op, int causal) {
+  if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
+  if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
+  if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
+  return FA_OK;
+}
+
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
-               int Hkv, int N, int D, int causal, int layout, int dtype, void* stream,
-               const int* kv_len = nullptr, int window = 0) {
-  if (window < 0 || (window > 0 && !causal)) return FA_ERR_WINDOW;
-  if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
-  if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
-  int rc = check_shape(B, Hq, Hkv, N, D);
-  if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
+               int Hkv, int N, int D, int causal, const fa_options& op, void* stream) {
+  int rc = check_opts(op, causal);
+  if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
-  fa::FwdArgs a{q, k, v, o, lse, B, Hq, Hkv, N, D, causal != 0, stream, layout, dtype, kv_len,
-                window};
+  fa::FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.N = N;
+  a.D = D;
+  a.causal = causal != 0;
+  a.stream = stream;
+  a.layout = op.layout;
+  a.dtype = op.dtype;
+  a.kv_len = op.kv_len;
+  a.window = op.window;
+  a.alibi = op.alibi_slopes;
   return to_code(fa::launch_fwd(a));
 }
 
 int fa_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
            int Hkv, int N, int D, int causal, int full_precision, void* stream) {
   (void)full_precision;  // fp16 products are exact in the fp32 accumulator
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBHND, fa::kFP16, stream);
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, kDefaultOpts, stream);
 }
 
 int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
                 int Hkv, int N, int D, int causal, void* stream) {
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, fa::kBNHD, fa::kFP16, stream);
+  fa_options op = kDefaultOpts;
+  op.layout = fa::kBNHD;
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, op, stream);
 }
 
-int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
-                int Hkv, int N, int D, int causal, int layout, void* stream) {
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, layout, fa::kBF16, stream);
+int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
+              int Hkv, int N, int D, int causal, const fa_options* opts, void* stream) {
+  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, opts ? *opts : kDefaultOpts, stream);
 }
 
 size_t fa_bwd_workspace_bytes(int B, int Hq, int Hkv, int N, int D) {
@@ -127,14 +153,14 @@ int fa_bwd_preprocess(const void* dO, const void* o, const float* lse, void* wor
                  stream);
 }
 
-// Shared by the main-kernel entry points: fp32 dq or fp16 dq16, either layout.
+// Shared by the main-kernel entry points: fp32 dq or 16-bit dq16.
 static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
-                    int layout, int dtype, void* stream, const int* kv_len = nullptr,
-                    int window = 0) {
-  int rc = check_shape(B, Hq, Hkv, N, D);
-  if (rc == FA_OK && layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
+                    const fa_options& op, void* stream) {
+  int rc = check_opts(op, causal);
+  if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !dO || !workspace || !(dq || dq16) || !dk || !dv) return FA_ERR_NULL;
   const fa::BwdWorkspace w = fa::bwd_workspace(B, Hq, Hkv, N, D);
@@ -161,30 +187,28 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.D = D;
   a.causal = causal != 0;
   a.stream = stream;
-  a.layout = layout;
-  a.dtype = dtype;
-  a.kv_len = kv_len;
-  a.window = window;
+  a.layout = op.layout;
+  a.dtype = op.dtype;
+  a.kv_len = op.kv_len;
+  a.window = op.window;
+  a.alibi = op.alibi_slopes;
   return to_code(fa::launch_bwd_main(a));
 }
 
-// Preprocess + main with fp16 dq (both layouts).
-static int bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
-                       const float* lse, void* dq, void* dk, void* dv, void* workspace,
-                       size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
-                       int layout, int dtype, void* stream, const int* kv_len = nullptr,
-                       int window = 0) {
-  if (window < 0 || (window > 0 && !causal)) return FA_ERR_WINDOW;
-  if (layout != fa::kBHND && layout != fa::kBNHD) return FA_ERR_LAYOUT;
-  if (dtype != fa::kFP16 && dtype != fa::kBF16) return FA_ERR_DTYPE;
-  const int rc = check_shape(B, Hq, Hkv, N, D);
+// Preprocess + main with dq in the element format.
+static int bwd_16(const void* q, const void* k, const void* v, const void* dO, const void* o,
+                  const float* lse, void* dq, void* dk, void* dv, void* workspace,
+                  size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+                  const fa_options& op, void* stream) {
+  int rc = check_opts(op, causal);
+  if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!workspace || !dq) return FA_ERR_NULL;
   if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;
-  int e = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, layout, dtype, stream);
-  if (e != FA_OK) return e;
+  rc = bwd_pre(dO, o, lse, workspace, workspace_bytes, B, Hq, N, D, op.layout, op.dtype, stream);
+  if (rc != FA_OK) return rc;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, nullptr, dq, dk, dv, B, Hq, Hkv, N, D,
-                  causal, layout, dtype, stream, kv_len, window);
+                  causal, op, stream);
 }
 
 int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, void* workspace,
@@ -192,45 +216,33 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO, voi
                 int N, int D, int causal, void* stream) {
   if (!dq) return FA_ERR_NULL;
   return bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, nullptr, dk, dv, B, Hq, Hkv, N, D,
-                  causal, fa::kBHND, fa::kFP16, stream);
+                  causal, kDefaultOpts, stream);
 }
 
 int fa_bwd_half_dq(const void* q, const void* k, const void* v, const void* dO, const void* o,
                    const float* lse, void* dq, void* dk, void* dv, void* workspace,
                    size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                    void* stream) {
-  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, fa::kBHND, fa::kFP16, stream);
+  return bwd_16(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N, D,
+                causal, kDefaultOpts, stream);
 }
 
 int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO, const void* o,
                 const float* lse, void* dq, void* dk, void* dv, void* workspace,
                 size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                 void* stream) {
-  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, fa::kBNHD, fa::kFP16, stream);
-}
-
-int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* dO, const void* o,
-                const float* lse, void* dq, void* dk, void* dv, void* workspace,
-                size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
-                int layout, void* stream) {
-  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, layout, fa::kBF16, stream);
-}
-
-int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
-              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int window,
-              int dtype, int layout, void* stream) {
-  return fwd(q, k, v, o, lse, B, Hq, Hkv, N, D, causal, layout, dtype, stream, kv_len, window);
+  fa_options op = kDefaultOpts;
+  op.layout = fa::kBNHD;
+  return bwd_16(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N, D,
+                causal, op, stream);
 }
 
 int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const void* o,
-              const float* lse, const int* kv_len, void* dq, void* dk, void* dv,
-              void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D,
-              int causal, int window, int dtype, int layout, void* stream) {
-  return bwd_half_dq(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N,
-                     D, causal, layout, dtype, stream, kv_len, window);
+              const float* lse, void* dq, void* dk, void* dv, void* workspace,
+              size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+              const fa_options* opts, void* stream) {
+  return bwd_16(q, k, v, dO, o, lse, dq, dk, dv, workspace, workspace_bytes, B, Hq, Hkv, N, D,
+                causal, opts ? *opts : kDefaultOpts, stream);
 }
 
 int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const void* o,

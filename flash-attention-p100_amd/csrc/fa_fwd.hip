@@ -102,7 +102,8 @@ struct FwdWave {
   // MASK: the step may need the causal / ragged mask, applied when `masked`.
   template <bool MASK, bool NEXT, class Issue>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
-                                       bool masked, int i_row, int N, int w_lo, int lane, int roff,
+                                       bool masked, int i_row, int N, int w_lo, float alibi_raw,
+                                       int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
@@ -115,6 +116,14 @@ struct FwdWave {
         sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
         issue(kk);
       }
+    // ALiBi (masked instantiation only): -slope |i - j| in raw-score units.
+    if (BOUNDS && alibi_raw != 0.f) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int j = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
+        s[r] -= alibi_raw * fabsf((float)(i_row - j));
+      }
+    }
     if (MASK && masked) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -173,7 +182,8 @@ struct FwdWave {
 template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
-                                         float* __restrict__ Lse, int N, int Nk, int W, int sq, int sk,
+                                         float* __restrict__ Lse, int N, int Nk, int W,
+                                         float alibi_raw, int sq, int sk,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -266,7 +276,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
-                                Nk, w_lo, lane,
+                                Nk, w_lo, alibi_raw, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -373,7 +383,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
-    Strides stk, const int* __restrict__ kv_len, int window) {
+    Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -393,12 +403,14 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const float thr_raw = kRescaleLog2 / scale_log2;
   // Per-entry key length (key padding), clamped to [1, N].
   const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
+  // ALiBi slope of this query head in raw-score units (slope / scale).
+  const float alibi_raw = alibi ? alibi[hq] * kLog2e / scale_log2 : 0.f;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                Lse + (size_t)bh * N, N, Nk, window, stq.n, stk.n,
+                                Lse + (size_t)bh * N, N, Nk, window, alibi_raw, stq.n, stk.n,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
@@ -415,15 +427,16 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window);
+                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window, a.alibi);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  // Key lengths and windows need the masked instantiation (kKV is a multiple
-  // of kBR).
-  const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0;
+  // Key lengths, windows and ALiBi need the masked instantiation (kKV is a
+  // multiple of kBR).
+  const bool bounds =
+      (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 || a.alibi != nullptr;
   if (a.causal)
     return bounds ? launch_fwd_t<D, true, true, BF>(a) : launch_fwd_t<D, true, false, BF>(a);
   return bounds ? launch_fwd_t<D, false, true, BF>(a) : launch_fwd_t<D, false, false, BF>(a);

@@ -36,6 +36,7 @@ struct FwdArgs {
   int dtype = kFP16;   // of q, k, v, o
   const int* kv_len = nullptr;  // device, B entries: keys [0, kv_len[b]) exist (else N)
   int window = 0;               // causal sliding window W: row i sees keys (i - W, i]; 0 = none
+  const float* alibi = nullptr; // device, Hq slopes: score(i, j) += -slope * |i - j|
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -87,6 +88,7 @@ struct BwdArgs {
   int dtype = kFP16;             // of q, k, v, dO, o, dk, dv and dq16
   const int* kv_len = nullptr;   // as FwdArgs::kv_len
   int window = 0;                // as FwdArgs::window
+  const float* alibi = nullptr;  // as FwdArgs::alibi
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

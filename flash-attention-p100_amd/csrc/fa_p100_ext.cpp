@@ -59,6 +59,27 @@ int dtype_code(const at::Tensor& q) {
   return q.scalar_type() == at::kBFloat16 ? FA_DTYPE_BF16 : FA_DTYPE_FP16;
 }
 
+// Optional ALiBi slopes: fp32 (Hq,) on q's device; nullptr when absent.
+const float* alibi_ptr(const c10::optional<at::Tensor>& slopes, const at::Tensor& q, int H) {
+  if (!slopes.has_value()) return nullptr;
+  const at::Tensor& t = *slopes;
+  TORCH_CHECK(t.is_cuda() && t.device() == q.device(), "alibi_slopes must be on q's device");
+  TORCH_CHECK(t.scalar_type() == at::kFloat, "alibi_slopes must be fp32");
+  TORCH_CHECK(t.dim() == 1 && t.size(0) == H && t.is_contiguous(), "alibi_slopes must be (Hq,)");
+  return t.data_ptr<float>();
+}
+
+fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Tensor>& kv_len,
+                     int64_t window, const c10::optional<at::Tensor>& alibi, int B, int H) {
+  fa_options op{};
+  op.dtype = dtype_code(q);
+  op.layout = layout;
+  op.kv_len = kv_len_ptr(kv_len, q, B);
+  op.window = (int)window;
+  op.alibi_slopes = alibi_ptr(alibi, q, H);
+  return op;
+}
+
 void check_rc(int rc, const char* what) {
   TORCH_CHECK(rc == FA_OK, what, " failed: ", fa_error_string(rc));
 }
@@ -176,7 +197,8 @@ static void check_bnhd(const at::Tensor& t, const char* name) {
 }
 
 std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
-                                        c10::optional<at::Tensor> kv_len, int64_t window) {
+                                        c10::optional<at::Tensor> kv_len, int64_t window,
+    c10::optional<at::Tensor> alibi_slopes) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -196,9 +218,9 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
+  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, B, H);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), B, H, Hkv, N, D,
-                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BNHD,
+                     lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
            "fa_fwd_ex");
   return {o, lse};
@@ -207,7 +229,7 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
 std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v,
                                          at::Tensor dO, at::Tensor o, at::Tensor lse,
                                          bool causal, c10::optional<at::Tensor> kv_len,
-                                         int64_t window) {
+                                         int64_t window, c10::optional<at::Tensor> alibi_slopes) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -231,10 +253,10 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
+  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, B, H);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), dq.data_ptr(),
-                     dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, H, Hkv, N, D,
-                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BNHD,
+                     lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                     ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
            "fa_bwd_ex");
   return {dq, dk, dv};
@@ -242,11 +264,13 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
 
 // Dense (B, H, N, D) tensors in fp16 or bf16 (one format for all), results in
 // that format, dq included, and optional key lengths kv_len (int32 (B,), right
-// padding: entry b has keys [0, kv_len[b])) and sliding window (causal: row i
-// sees keys (i - window, i]; 0 = none). For fp16 without either, the same
-// kernels as forward and backward_half_dq.
+// padding: entry b has keys [0, kv_len[b])), sliding window (causal: row i
+// sees keys (i - window, i]; 0 = none) and ALiBi slopes (fp32 (Hq,): score
+// -slope |i - j|). For fp16 without these, the same kernels as forward and
+// backward_half_dq.
 std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
-                                      c10::optional<at::Tensor> kv_len, int64_t window) {
+                                      c10::optional<at::Tensor> kv_len, int64_t window,
+    c10::optional<at::Tensor> alibi_slopes) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -269,9 +293,9 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
+  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, B, H);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
-                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), B, H, Hkv, N, D,
-                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BHND,
+                     lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
            "fa_fwd_ex");
   return {o, lse};
@@ -279,7 +303,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
 
 std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
                                        at::Tensor o, at::Tensor lse, bool causal,
-                                       c10::optional<at::Tensor> kv_len, int64_t window) {
+                                       c10::optional<at::Tensor> kv_len, int64_t window,
+    c10::optional<at::Tensor> alibi_slopes) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -308,10 +333,10 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
+  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, B, H);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
-                     lse.data_ptr<float>(), kv_len_ptr(kv_len, q, B), dq.data_ptr(),
-                     dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, B, H, Hkv, N, D,
-                     causal ? 1 : 0, (int)window, dtype_code(q), FA_LAYOUT_BHND,
+                     lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                     ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
            "fa_bwd_ex");
   return {dq, dk, dv};
@@ -324,16 +349,20 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "FlashAttention backward (gfx950), dq as fp16 (used by the autograd Function)");
   m.def("forward_bnhd", &fa_forward_bnhd,
         "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors", py::arg("q"),
-        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
+        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
+        py::arg("alibi_slopes") = py::none());
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
-        py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
+        py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
+        py::arg("alibi_slopes") = py::none());
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
-        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
+        py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
+        py::arg("alibi_slopes") = py::none());
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
-        py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0);
+        py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
+        py::arg("alibi_slopes") = py::none());
 }

@@ -66,7 +66,7 @@ class _FlashAttnP100(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0):
+    def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -75,13 +75,14 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.causal = causal
         ctx.kv_len = kv_len
         ctx.window = window
+        ctx.alibi = alibi
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
-            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window)
+            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
-        if q.dtype == torch.bfloat16 or kv_len is not None or window:
-            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window)
+        if q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None:
+            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -93,23 +94,26 @@ class _FlashAttnP100(torch.autograd.Function):
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
-                                            ctx.window)
+                                            ctx.window, ctx.alibi)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
-                    None, None, None, None)
+                    None, None, None, None, None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
         # `_ext.backward(...)[0].to(torch.float16)`) instead of a separate cast,
         # and backward_dt to bf16 for bf16 inputs.
         g = grad_o.contiguous()
-        if q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window:
-            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window)
+        if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
+                or ctx.alibi is not None):
+            dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
+                                          ctx.alibi)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
 
 
-def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None):
+def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
+               alibi_slopes=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -127,14 +131,24 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
       * sliding_window W (causal only): query row i attends to keys
         (i - W, i]. A row that then sees no key at all (only possible with
         kv_len: a pad row more than W past its entry's length) gets o = 0 and
-        zero gradients.
+        zero gradients;
+      * alibi_slopes, a float32 tensor (Hq,) on q's device: query head h adds
+        the bias -alibi_slopes[h] * |i - j| to its scaled score of key j
+        (ALiBi, in the symmetric form that also serves non-causal attention;
+        under causal masking j <= i, so it is -slope * (i - j)). The slopes
+        are constants: no gradient flows to them.
     """
     window = 0
     if sliding_window is not None:
         window = int(sliding_window)
         if window <= 0 or not causal:
             raise ValueError("sliding_window must be positive and needs causal=True")
-    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window)
+    if alibi_slopes is not None:
+        if alibi_slopes.dim() != 1 or alibi_slopes.numel() != q.size(1):
+            raise ValueError(f"alibi_slopes must have shape ({q.size(1)},), got "
+                             f"{tuple(alibi_slopes.shape)}")
+        alibi_slopes = alibi_slopes.detach().float().contiguous()
+    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes)
 
 
 def _expand_kv(k, n_head):

@@ -87,17 +87,6 @@ int fa_fwd_bnhd(const void* q, const void* k, const void* v, void* o, float* lse
                 int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
 
 /*
- * fa_fwd (layout FA_LAYOUT_BHND) or fa_fwd_bnhd (FA_LAYOUT_BNHD) on bfloat16
- * q, k, v, o (lse stays fp32): the products run on the bf16 MFMA with fp32
- * accumulation, P is rounded to bf16 as an MFMA operand, o to bf16 (nearest
- * even). No counterpart in the reference, which accepts fp16 only
- * (fa_p100_ext.cu:33; README.md:72-75 lists bf16 among the unsupported
- * inputs); for callers whose models run in bf16 and would otherwise cast.
- */
-int fa_fwd_bf16(const void* q, const void* k, const void* v, void* o, float* lse,
-                int B, int Hq, int Hkv, int N, int D, int causal, int layout, void* stream);
-
-/*
  * Bytes of device workspace fa_bwd needs: two (B, Hq, N) float32 vectors, the
  * reference's `dvec` (fa_p100_ext.cu:124) and the saved LSE pre-multiplied by
  * log2(e); then B*Hq*floor(ceil(N/128)/2) uint32 counters; then, for each
@@ -147,18 +136,6 @@ int fa_bwd_bnhd(const void* q, const void* k, const void* v, const void* dO,
                 int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
 
 /*
- * Backward on bfloat16 tensors (see fa_fwd_bf16): q, k, v, dO, o and the
- * outputs dq, dk, dv are bf16 in `layout`; lse and the workspace as in
- * fa_bwd. P and dS are rounded to bf16 as MFMA operands; dq, dk, dv are the
- * fp32 results rounded to bf16. No counterpart in the reference (see
- * fa_fwd_bf16).
- */
-int fa_bwd_bf16(const void* q, const void* k, const void* v, const void* dO,
-                const void* o, const float* lse, void* dq, void* dk, void* dv,
-                void* workspace, size_t workspace_bytes,
-                int B, int Hq, int Hkv, int N, int D, int causal, int layout, void* stream);
-
-/*
  * First phase of fa_bwd, the counterpart of bwd_preprocess
  * (flash_bwd.cuh:65-78): fills `workspace` with dvec = rowsum(dO * o) and
  * lse * log2(e), both fp32 (B,Hq,N), and zeroes its counters. Exposed so a
@@ -183,27 +160,46 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
                 int causal, void* stream);
 
 /*
- * The general pair, covering every variant above plus key padding and
- * sliding windows: element format `dtype` (FA_DTYPE_FP16 / FA_DTYPE_BF16),
- * `layout` (FA_LAYOUT_BHND / FA_LAYOUT_BNHD);
- *   - `kv_len`, when not NULL, a device array of B int32 key lengths: for
- *     batch entry b only keys [0, kv_len[b]) exist (right padding; values are
- *     clamped to [1, N]), every query row (pad rows included) attends to those
- *     keys only, and dk/dv rows past kv_len[b] come out zero;
- *   - `window` W > 0 (causal only): query row i attends to keys (i - W, i].
- *     With key lengths too, a pad row more than W past its entry's length sees
- *     no key: its o is 0, its lse +inf and its gradients 0.
- * fa_bwd_ex writes dq in `dtype`. No counterpart in the reference, which
- * raises on padding masks, sliding windows and bf16 (README.md:72-75,
- * fa_p100_hf.py:64-82); kv_len and window serve the HF hook.
+ * Options of the general pair below; a zeroed struct (or a NULL pointer)
+ * means fp16, dense (B, H, N, D), no key lengths, no window, no ALiBi.
+ *   - dtype: FA_DTYPE_FP16 or FA_DTYPE_BF16 for q, k, v, o, dO, dq, dk, dv
+ *     (bf16: products on the bf16 MFMA with fp32 accumulation, P and dS
+ *     rounded to bf16 as operands, outputs rounded to nearest even);
+ *   - layout: FA_LAYOUT_BHND or FA_LAYOUT_BNHD (see fa_fwd_bnhd);
+ *   - kv_len: NULL, or a device array of B int32 key lengths: for batch entry
+ *     b only keys [0, kv_len[b]) exist (right padding; values are clamped to
+ *     [1, N]), every query row (pad rows included) attends to those keys
+ *     only, and dk/dv rows past kv_len[b] come out zero;
+ *   - window: 0, or W > 0 (causal only): query row i attends to keys
+ *     (i - W, i]. With key lengths too, a pad row more than W past its
+ *     entry's length sees no key: its o is 0, its lse +inf, its gradients 0;
+ *   - alibi_slopes: NULL, or a device array of Hq fp32 slopes: the scaled
+ *     score of query row i and key j of query head h gets
+ *     -alibi_slopes[h] * |i - j| added (the usual ALiBi bias).
+ */
+typedef struct fa_options {
+  int dtype;
+  int layout;
+  const int* kv_len;
+  int window;
+  const float* alibi_slopes;
+} fa_options;
+
+/*
+ * The general pair: every entry point above is one of its cases, plus bf16,
+ * key padding, sliding windows and ALiBi (`opts`). fa_bwd_ex writes dq in
+ * the element format (fp16 or bf16); lse and the workspace as in fa_bwd. No
+ * counterpart in the reference, which raises on all four (README.md:72-75,
+ * fa_p100_ext.cu:33, fa_p100_hf.py:64-82); the HF hook uses key lengths and
+ * windows.
  */
 int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
-              const int* kv_len, int B, int Hq, int Hkv, int N, int D, int causal, int window,
-              int dtype, int layout, void* stream);
+              int B, int Hq, int Hkv, int N, int D, int causal, const fa_options* opts,
+              void* stream);
 int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const void* o,
-              const float* lse, const int* kv_len, void* dq, void* dk, void* dv,
-              void* workspace, size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D,
-              int causal, int window, int dtype, int layout, void* stream);
+              const float* lse, void* dq, void* dk, void* dv, void* workspace,
+              size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
+              const fa_options* opts, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -60,7 +60,7 @@ def _group_sum(g, hkv):
     return g.reshape(b, hkv, hq // hkv, n, d).sum(axis=2)
 
 
-def _scores(q, k, causal, dtype, kv_len=None, window=None):
+def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
@@ -70,12 +70,20 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None):
     has no padding masks) key col is also masked for batch entry b when
     col >= kv_len[b], clamped to [1, N] as the kernels do. With `window` W
     (causal only, another extension) key col is also masked for row when
-    col <= row - W: each row sees its last W keys.
+    col <= row - W: each row sees its last W keys. With `alibi` (Hq slopes,
+    another extension) query head h adds -alibi[h] * |row - col| to every
+    scaled logit before the masks.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d)
     s = np.matmul(q.astype(dtype), np.swapaxes(k.astype(dtype), -1, -2)) * dtype(scale)
     n = q.shape[-2]
+    if alibi is not None:
+        slopes = np.asarray(alibi, dtype=np.float64).reshape(-1)
+        if slopes.size != q.shape[1]:
+            raise ValueError("alibi needs one slope per query head")
+        dist = np.abs(np.arange(n)[:, None] - np.arange(n)[None, :]).astype(np.float64)
+        s = (s - (slopes[:, None, None] * dist[None]).astype(dtype)[None]).astype(dtype)
     if causal:
         mask = np.triu(np.ones((n, n), dtype=bool), 1)
         s = np.where(mask, -np.inf, s).astype(dtype)
@@ -91,18 +99,19 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None):
     return s
 
 
-def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None):
+def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None,
+                  alibi=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
-    (flash_fwd.cuh:324-329). `kv_len`, `window`: optional per-entry key
-    lengths and sliding window (see _scores).
+    (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`: optional per-entry
+    key lengths, sliding window and ALiBi slopes (see _scores).
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi)
     m = s.max(axis=-1, keepdims=True)
     # A row that sees no key at all (only with both key lengths and a window:
     # pad rows more than W past their entry's length) gets O = 0 and
@@ -122,7 +131,7 @@ def bwd_preprocess(o, do, dtype=np.float64):
 
 
 def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
-                  window=None):
+                  window=None, alibi=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -138,8 +147,8 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     qd = q.astype(dtype)
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
-        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window)
-    s = _scores(q, ke, causal, dtype, kv_len, window)
+        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi)
+    s = _scores(q, ke, causal, dtype, kv_len, window, alibi)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     dv = np.matmul(np.swapaxes(p, -1, -2), dod)
     dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
@@ -150,9 +159,10 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     return dq, _group_sum(dk, hkv), _group_sum(dv, hkv)
 
 
-def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None):
+def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None,
+                   alibi=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

@@ -60,15 +60,28 @@ def load_capi():
     lib.fa_fwd_bnhd.restype = i
     lib.fa_bwd_bnhd.argtypes = [vp] * 10 + [sz] + [i] * 6 + [vp]
     lib.fa_bwd_bnhd.restype = i
-    lib.fa_fwd_bf16.argtypes = [vp] * 5 + [i] * 7 + [vp]
-    lib.fa_fwd_bf16.restype = i
-    lib.fa_bwd_bf16.argtypes = [vp] * 10 + [sz] + [i] * 7 + [vp]
-    lib.fa_bwd_bf16.restype = i
-    lib.fa_fwd_ex.argtypes = [vp] * 6 + [i] * 9 + [vp]
+    opts = ctypes.POINTER(FaOptions)
+    lib.fa_fwd_ex.argtypes = [vp] * 5 + [i] * 6 + [opts, vp]
     lib.fa_fwd_ex.restype = i
-    lib.fa_bwd_ex.argtypes = [vp] * 11 + [sz] + [i] * 9 + [vp]
+    lib.fa_bwd_ex.argtypes = [vp] * 10 + [sz] + [i] * 6 + [opts, vp]
     lib.fa_bwd_ex.restype = i
     return lib
+
+
+class FaOptions(ctypes.Structure):
+    """struct fa_options of include/fa_mi355x.h (same field order and types)."""
+    _fields_ = [("dtype", ctypes.c_int), ("layout", ctypes.c_int),
+                ("kv_len", ctypes.c_void_p), ("window", ctypes.c_int),
+                ("alibi_slopes", ctypes.c_void_p)]
+
+
+def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None):
+    """A pointer to an FaOptions; kv_len / alibi_slopes are device addresses
+    (ints) or tensors."""
+    def addr(x):
+        return None if x is None else (x if isinstance(x, int) else x.data_ptr())
+    o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes))
+    return ctypes.pointer(o)
 
 
 def np64(t):

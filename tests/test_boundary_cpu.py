@@ -8,7 +8,7 @@ import ctypes
 import pytest
 import torch
 
-from helpers import LIB, header_functions, load_capi
+from helpers import LIB, fa_opts, header_functions, load_capi
 
 
 def test_library_exports_every_declared_symbol():
@@ -52,17 +52,25 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_bwd_preprocess(z, z, z, z, 0, 1, 2, 8, 128, s) == 10005
     one = ctypes.c_void_p(1)
     assert lib.fa_bwd(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, s) == 10006
-    # bf16 entry points: layout codes, then the same shape checks.
-    assert lib.fa_fwd_bf16(*([one] * 5), 1, 2, 2, 8, 64, 0, 2, s) == 10008
-    assert lib.fa_fwd_bf16(*([one] * 5), 1, 2, 2, 8, 80, 0, 0, s) == 10001
-    assert lib.fa_fwd_bf16(z, z, z, z, z, 1, 2, 2, 8, 64, 0, 1, s) == 10005
-    assert lib.fa_bwd_bf16(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, 0, s) == 10006
-    assert lib.fa_bwd_bf16(*([one] * 10), 1 << 30, 1, 2, 2, 8, 64, 0, -1, s) == 10008
-    assert lib.fa_fwd_ex(*([one] * 6), 1, 2, 2, 8, 64, 0, 16, 0, 0, s) == 10010  # window, no causal
-    assert lib.fa_fwd_ex(*([one] * 6), 1, 2, 2, 8, 64, 1, -1, 0, 0, s) == 10010
-    assert lib.fa_bwd_ex(*([one] * 11), 0, 1, 2, 2, 8, 64, 0, 4, 0, 0, s) == 10010
+    # fa_fwd_ex / fa_bwd_ex: the options (element format, layout, window) are
+    # checked first, then the same shape, pointer and workspace checks.
+    bf16 = 1
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(bf16, 2), s) == 10008
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(2, 0), s) == 10009
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 80, 0, fa_opts(bf16), s) == 10001
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, fa_opts(bf16, 1), s) == 10005
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, None, s) == 10005  # NULL: defaults
+    assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, fa_opts(bf16), s) == 10006
+    assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 2, 2, 8, 64, 0, fa_opts(bf16, -1), s) == 10008
+    # a window needs causal masking and must not be negative
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(window=16), s) == 10010
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(window=-1), s) == 10010
+    assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, fa_opts(window=4), s) == 10010
+    # BNHD puts every head of a row in one 32-bit buffer range
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 1 << 12, 1, 1 << 14, 128, 0, fa_opts(0, 1), s) == 10007
     assert b"layout" in lib.fa_error_string(10008)
     assert b"format" in lib.fa_error_string(10009)
+    assert b"window" in lib.fa_error_string(10010)
 
 
 def test_binding_rejects_host_tensors_with_reference_messages():
@@ -83,13 +91,14 @@ def test_public_api_surface_matches_reference():
     import fa_p100_hf
     sig = inspect.signature(fa_p100.flash_attn)
     # The reference's parameters, in order, with its defaults; the extensions
-    # (key lengths, sliding window) come after them and default to None, so
-    # every reference call binds the same way.
+    # (key lengths, sliding window, ALiBi slopes) come after them and default
+    # to None, so every reference call binds the same way.
+    extensions = ["kv_len", "sliding_window", "alibi_slopes"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False
-    assert list(sig.parameters)[5:] == ["kv_len", "sliding_window"]
-    assert all(sig.parameters[n].default is None for n in ("kv_len", "sliding_window"))
+    assert list(sig.parameters)[5:] == extensions
+    assert all(sig.parameters[n].default is None for n in extensions)
     for name in ("_FlashAttnP100", "reference", "_expand_kv", "_ext"):
         assert hasattr(fa_p100, name)
     for name in ("fa_p100_attention_forward", "register", "enable_fa_p100", "_set_impl"):

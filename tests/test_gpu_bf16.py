@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import load_capi
+from helpers import fa_opts, load_capi
 from oracle import attention as ora
 
 pytestmark = pytest.mark.gpu
@@ -96,9 +96,9 @@ def test_bf16_bnhd_views_match_dense_bit_for_bit(D):
 
 
 def test_bf16_capi_matches_op():
-    """fa_fwd_bf16 / fa_bwd_bf16 (layout FA_LAYOUT_BHND) on caller-owned
-    buffers give the op's results bit for bit, and the wrong format is
-    rejected by the binding with a message."""
+    """fa_fwd_ex / fa_bwd_ex with options {FA_DTYPE_BF16, FA_LAYOUT_BHND} on
+    caller-owned buffers give the op's results bit for bit, and the wrong
+    format is rejected by the binding with a message."""
     import fa_p100
     lib = load_capi()
     B, Hq, Hkv, N, D, causal = 1, 4, 2, 257, 128, 1
@@ -108,12 +108,13 @@ def test_bf16_capi_matches_op():
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     o, lse = torch.empty_like(q), torch.empty(B, Hq, N, device=DEV)
-    assert lib.fa_fwd_bf16(p(q), p(k), p(v), p(o), p(lse), B, Hq, Hkv, N, D, causal, 0, s) == 0
+    opts = fa_opts(dtype=1, layout=0)
+    assert lib.fa_fwd_ex(p(q), p(k), p(v), p(o), p(lse), B, Hq, Hkv, N, D, causal, opts, s) == 0
     ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)
     ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    rc = lib.fa_bwd_bf16(p(q), p(k), p(v), p(do), p(o), p(lse), p(dq), p(dk), p(dv), p(ws),
-                         ws_bytes, B, Hq, Hkv, N, D, causal, 0, s)
+    rc = lib.fa_bwd_ex(p(q), p(k), p(v), p(do), p(o), p(lse), p(dq), p(dk), p(dv), p(ws),
+                       ws_bytes, B, Hq, Hkv, N, D, causal, opts, s)
     assert rc == 0, lib.fa_error_string(rc)
     torch.cuda.synchronize()
     for a, b in ((o, o_op), (lse, lse_op), (dq, dq_op), (dk, dk_op), (dv, dv_op)):

@@ -263,3 +263,103 @@ def test_sliding_window_pins(window):
             assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
     with pytest.raises(ValueError):
         ora.attention_fwd(q, k, v, False, window=window)
+
+
+def alibi_slopes(h):
+    """The ALiBi paper's geometric slopes 2^(-8 i / h), i = 1 .. h."""
+    return np.array([2.0 ** (-8.0 * (i + 1) / h) for i in range(h)])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_alibi_pins(causal):
+    """ALiBi slopes (an extension): head h adds -slope[h] * |i - j| to every
+    scaled logit. Pinned against torch SDPA + autograd in float64 with the
+    bias as a float mask, against the causal identity -slope (i - j) ==
+    +slope j up to a per-row constant (so a per-key bias gives the same O),
+    slope 0 equal to no ALiBi, a huge slope giving O = V row by row (a sign
+    slip would pick the farthest key), and finite differences."""
+    rng = np.random.default_rng(7 + causal)
+    b, hq, hkv, n, d = 2, 4, 2, 21, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    slopes = alibi_slopes(hq) * 4  # steep enough that the bias matters at n = 21
+    lens = np.array([n, 13])
+    o, lse = ora.attention_fwd(q, k, v, causal, kv_len=lens, alibi=slopes)
+    grads = ora.attention_bwd(q, k, v, do, causal, kv_len=lens, alibi=slopes)
+
+    i, j = np.arange(n)[:, None], np.arange(n)[None, :]
+    tq = torch.tensor(q, requires_grad=True)
+    tk = torch.tensor(k, requires_grad=True)
+    tv = torch.tensor(v, requires_grad=True)
+    bias = -torch.tensor(slopes)[:, None, None] * torch.tensor(np.abs(i - j), dtype=torch.float64)
+    keep = torch.tensor(j < lens[:, None, None])[:, None]  # (B, 1, 1, N) key lengths
+    if causal:
+        keep = keep & torch.tensor(j <= i)
+    mask = torch.where(keep, bias[None], torch.tensor(-math.inf, dtype=torch.float64))
+    ref = F.scaled_dot_product_attention(tq, tk.repeat_interleave(hq // hkv, 1),
+                                         tv.repeat_interleave(hq // hkv, 1), attn_mask=mask)
+    ref.backward(torch.tensor(do))
+    assert np.allclose(o, ref.detach().numpy(), atol=1e-12)
+    for got, t in zip(grads, (tq, tk, tv)):
+        assert np.allclose(got, t.grad.numpy(), atol=1e-10)
+    ref_lse = torch.logsumexp(
+        (tq.detach() @ tk.detach().repeat_interleave(hq // hkv, 1).transpose(-1, -2))
+        / math.sqrt(d) + mask, dim=-1).numpy()
+    assert np.allclose(lse, ref_lse, atol=1e-12)
+    # Planted: a flipped sign or the slopes in reversed head order fail that check.
+    for bad_slopes in (-slopes, slopes[::-1].copy()):
+        bad, _ = ora.attention_fwd(q, k, v, causal, kv_len=lens, alibi=bad_slopes)
+        assert not np.allclose(bad, ref.detach().numpy(), atol=1e-6)
+
+    if causal:  # per-key bias +slope j: same O, LSE shifted by -slope i
+        per_key = torch.where(keep, torch.tensor(slopes)[:, None, None]
+                              * torch.tensor(j, dtype=torch.float64)[None],
+                              torch.tensor(-math.inf, dtype=torch.float64))
+        alt = F.scaled_dot_product_attention(
+            torch.tensor(q), torch.tensor(k).repeat_interleave(hq // hkv, 1),
+            torch.tensor(v).repeat_interleave(hq // hkv, 1), attn_mask=per_key)
+        assert np.allclose(o, alt.numpy(), atol=1e-12)
+    assert np.array_equal(ora.attention_fwd(q, k, v, causal, kv_len=lens, alibi=np.zeros(hq))[0],
+                          ora.attention_fwd(q, k, v, causal, kv_len=lens)[0])
+    # Huge slopes: each row keeps its own key only, so O = V (GQA-expanded)
+    # and LSE = scaled q_i . k_i.
+    o_big, lse_big = ora.attention_fwd(q, k, v, causal, alibi=np.full(hq, 1e4))
+    ve = np.repeat(v, hq // hkv, axis=1)
+    ke = np.repeat(k, hq // hkv, axis=1)
+    assert np.allclose(o_big, ve, atol=1e-12)
+    assert np.allclose(lse_big, (q * ke).sum(-1) / math.sqrt(d), atol=1e-12)
+
+    h = 1e-4
+    for which, g in enumerate(grads):
+        for _ in range(4):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, causal, kv_len=lens, alibi=slopes)
+                  - ora.attention_loss(*minus, do, causal, kv_len=lens, alibi=slopes)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
+    with pytest.raises(ValueError):
+        ora.attention_fwd(q, k, v, causal, alibi=slopes[:2])
+
+
+def test_alibi_with_window_matches_sdpa():
+    """ALiBi combined with a sliding window and key lengths, against SDPA."""
+    rng = np.random.default_rng(99)
+    b, hq, hkv, n, d, w = 2, 2, 1, 17, 8, 6
+    q, k, v = rnd(rng, b, hq, n, d), rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    slopes, lens = np.array([0.5, 0.125]), np.array([17, 9])
+    o, _ = ora.attention_fwd(q, k, v, True, kv_len=lens, window=w, alibi=slopes)
+    i, j = np.arange(n)[:, None], np.arange(n)[None, :]
+    for e, L in enumerate(lens):
+        band = (j <= i) & (j > i - w) & (j < L)
+        seen = band.any(axis=1)
+        bias = -slopes[:, None, None] * np.abs(i - j)[None]
+        mask = torch.tensor(np.where(band[None], bias, -np.inf))
+        ref = F.scaled_dot_product_attention(
+            torch.tensor(q[e:e + 1]), torch.tensor(np.repeat(k[e:e + 1], hq, 1)),
+            torch.tensor(np.repeat(v[e:e + 1], hq, 1)), attn_mask=mask[None]).numpy()
+        assert np.allclose(o[e][:, seen], ref[0][:, seen], atol=1e-12)
+        assert not np.any(o[e][:, ~seen])
