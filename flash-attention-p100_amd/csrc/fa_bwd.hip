@@ -67,11 +67,13 @@ constexpr int kSub = 64;    // rows per streamed tile (queries in 1, keys in 2)
 static_assert(kTile == kBwdTile, "workspace layout assumes this key tile");
 // Causal split of key tile u (see bwd_kernel): floor((group * (n_tiles-1-2u) *
 // kSplitNum - kSplitBias) / 256) of its phase-1 iterations move to workgroup
-// n_tiles-1-u. Phase-1 steps cost ~1.26x phase-2 steps, which would balance
-// at ~0.21 iterations per unit; with the slot traffic, a sweep of kSplitNum
-// over 30..100 at the headline shape was fastest at 46..53 (-3.4% against no
-// split; 80 gave no gain, 100 lost).
-constexpr int kSplitNum = 50;
+// n_tiles-1-u. Phase-1 steps cost more than phase-2 steps, so the iterations
+// move from the phase-1-heavy low tiles to the phase-2-heavy high ones. Swept
+// over 50..110 (same-box A/B): fastest at 76..86 for B=1 H=8 N=4096 D=128,
+// 66..76 for H=16 N=2048 D=64 and 76 for H=16 N=8192 D=128; 110 lost
+// everywhere. The best rate grew from ~50 when phase 2's operand reads moved
+// ahead of their products (phase-2 steps got cheaper).
+constexpr int kSplitNum = 76;
 constexpr int kSplitBias = 5;
 
 // LDS: every tile is its own __shared__ object (declared in bwd_kernel), so
@@ -225,9 +227,10 @@ struct KVWave {
     const int lo = j_col - base;     // alive when 8*g4 + e >= lo (causal)
     const int hi = row_end - base;   // alive when 8*g4 + e <  hi
     if (BOUNDS && alibi_raw != 0.f) {  // ALiBi: -slope |i - j| in raw-score units
+      const float d0 = (float)(base - j_col);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        sacc[r] -= alibi_raw * fabsf((float)(base + 8 * (r >> 2) + (r & 3) - j_col));
+        sacc[r] = fmaf(-alibi_raw, fabsf(d0 + (float)(8 * (r >> 2) + (r & 3))), sacc[r]);
     }
     half8 pb[2], sb[2];
 #pragma unroll
@@ -269,10 +272,21 @@ struct QWave {
     using S = Swz<D>;
     const int h = lane >> 5;
     floatx16 st = zero16(), pt = zero16();
+    // Operands are read one k-step ahead of their products, so that no
+    // product waits for its own LDS read.
+    half8 ka = S::read16(Ks, so, 0), va = S::read16(Vs, so, 0);
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      st = mfma16<BF>(S::read16(Ks, so, kk), qb[kk], st);
-      pt = mfma16<BF>(S::read16(Vs, so, kk), ob[kk], pt);
+      half8 kn = ka, vn = va;
+      if (kk + 1 < D / 16) {
+        kn = S::read16(Ks, so, kk + 1);
+        vn = S::read16(Vs, so, kk + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      st = mfma16<BF>(ka, qb[kk], st);
+      pt = mfma16<BF>(va, ob[kk], pt);
+      ka = kn;
+      va = vn;
     }
     // dS^T. A lane holds query row i_row and the 16 keys
     // j = j0 + 32s + 8*g4 + 4h + e. Rows i_row >= N are never stored.
@@ -281,9 +295,10 @@ struct QWave {
     const int hi = Nk - base;      // alive when 8*g4 + e <  hi (ragged N, key length)
     const int lw = key_lo - base;  // alive when 8*g4 + e >= lw (sliding window)
     if (BOUNDS && alibi_raw != 0.f) {  // ALiBi: -slope |i - j| in raw-score units
+      const float d0 = (float)(i_row - base);
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        st[r] -= alibi_raw * fabsf((float)(i_row - base - 8 * (r >> 2) - (r & 3)));
+        st[r] = fmaf(-alibi_raw, fabsf(d0 - (float)(8 * (r >> 2) + (r & 3))), st[r]);
     }
     half8 sb[2];
 #pragma unroll
@@ -294,12 +309,17 @@ struct QWave {
       if (BOUNDS) p = (idx < hi && idx >= lw) ? p : 0.f;
       sb[r >> 3][r & 7] = to16<BF>(p * (pt[r] - dvv));
     }
-    // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15.
+    // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15 (operands one ahead).
+    half8 kt = S::tr_operand(Ks, 0, so, 0);
 #pragma unroll
-    for (int cb = 0; cb < D / 32; ++cb)
-#pragma unroll
-      for (int q = 0; q < 2; ++q)
-        acc[cb] = mfma16<BF>(S::tr_operand(Ks, q, so, cb), sb[q], acc[cb]);
+    for (int u = 0; u < 2 * (D / 32); ++u) {
+      const int cb = u >> 1, q = u & 1;
+      half8 kt_next = kt;
+      if (u + 1 < 2 * (D / 32)) kt_next = S::tr_operand(Ks, (u + 1) & 1, so, (u + 1) >> 1);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[cb] = mfma16<BF>(kt, sb[q], acc[cb]);
+      kt = kt_next;
+    }
   }
 };
 

@@ -116,13 +116,13 @@ struct FwdWave {
         sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
         issue(kk);
       }
-    // ALiBi (masked instantiation only): -slope |i - j| in raw-score units.
+    // ALiBi (masked instantiation only): -slope |i - j| in raw-score units,
+    // from one distance per lane and constant offsets (exact in fp32).
     if (BOUNDS && alibi_raw != 0.f) {
+      const float d0 = (float)(i_row - j0 - 4 * h);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int j = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        s[r] -= alibi_raw * fabsf((float)(i_row - j));
-      }
+      for (int r = 0; r < 16; ++r)
+        s[r] = fmaf(-alibi_raw, fabsf(d0 - (float)(8 * (r >> 2) + (r & 3))), s[r]);
     }
     if (MASK && masked) {
 #pragma unroll
