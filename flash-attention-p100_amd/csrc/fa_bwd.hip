@@ -334,7 +334,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     int N, int Hq, int group, int n_tiles, int BHkv, float scale, float scale_log2,
     Strides stq, Strides stk, unsigned* __restrict__ counters, float* __restrict__ slots,
     int split_num, int split_bias, const int* __restrict__ kv_len, int window,
-    const float* __restrict__ alibi) {
+    const float* __restrict__ alibi, const int* __restrict__ seg_start,
+    const int* __restrict__ seg_end) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -366,6 +367,26 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // Causal sliding window (only in the masked instantiation): row i sees keys
   // (i - Wb, i]; 0 = none.
   const int Wb = BOUNDS ? window : 0;
+  // Packed sequences (causal, masked instantiation only): token i's sequence
+  // is [sst[i], sen[i]). With a window they bound the rows and keys each
+  // token reaches: key j reaches rows [j, upper(j)) and row i keys
+  // [lower(i), i]; both bounds never decrease, and are clamped so that every
+  // token reaches itself and no index leaves [0, N].
+  const int* const sst = BOUNDS && seg_start ? seg_start + (size_t)b * N : nullptr;
+  const int* const sen = BOUNDS && seg_end ? seg_end + (size_t)b * N : nullptr;
+  const bool narrowed = BOUNDS && (Wb > 0 || sst != nullptr);
+  auto upper = [&](int j) {
+    j = min(j, N - 1);
+    int hi = Wb > 0 ? min(N, j + Wb) : N;
+    if (sen) hi = min(hi, max(sen[j], j + 1));
+    return hi;
+  };
+  auto lower = [&](int i) {
+    i = min(i, N - 1);
+    int lo = Wb > 0 ? i - Wb + 1 : 0;
+    if (sst) lo = max(lo, min(sst[i], i));
+    return max(lo, 0);
+  };
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
   // Offset of query head hq's row 0 in Q, dO, dQ.
@@ -398,14 +419,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // and stores the result (fp32 a + b == b + a, so the outcome does not depend
   // on which one that is).
   // Query rows of key tile u's phase 1: from its diagonal (causal) to the end,
-  // or to the last row whose window reaches the tile.
-  auto q_end = [&](int u) { return Wb > 0 ? min(N, u * kTile + kTile + Wb - 1) : N; };
+  // or to the last row whose window or sequence reaches the tile.
+  auto q_end = [&](int u) { return narrowed ? upper(u * kTile + kTile - 1) : N; };
   auto n_iters = [&](int u) {
     return group * ((q_end(u) - (CAUSAL ? u * kTile : 0) + kSub - 1) / kSub);
   };
   auto split = [&](int u) {
     const int m = n_tiles - 1 - 2 * u;
-    if (!CAUSAL || m <= 0 || Wb > 0) return 0;  // windows leave the tiles' work equal
+    if (!CAUSAL || m <= 0 || narrowed) return 0;  // windows leave the tiles' work equal
     return max(0, min((group * m * split_num - split_bias) >> 8, n_iters(u) - 1));
   };
   const int tw = wi % n_tiles;
@@ -440,7 +461,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int i_start = CAUSAL ? tp0 : 0;  // tp0 is a multiple of kSub
     const int n_qt = (q_end(tile) - i_start + kSub - 1) / kSub;
     // Rows this wave's key column reaches (see KVWave::step).
-    const int row_end = j_col < Nk ? (Wb > 0 ? min(N, j_col + Wb) : N) : 0;
+    const int row_end = j_col < Nk ? (narrowed ? upper(j_col) : N) : 0;
 
     // Q, dO tiles and lse2, dvec of flattened step `it` (clamped to the last
     // one, so that every step issues the same loads) into one stage.
@@ -566,8 +587,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int n_kt = (kv_end + kSub - 1) / kSub;
     // With a window, key tiles left of every row's window are skipped, and
     // each row masks the keys left of its own.
-    const int t_lo = Wb > 0 ? max(0, t0 - Wb + 1) / kSub : 0;
-    const int key_lo = Wb > 0 ? i_row - Wb + 1 : -(1 << 30);
+    const int t_lo = narrowed ? lower(t0) / kSub : 0;
+    const int key_lo = narrowed ? lower(i_row) : -(1 << 30);
 
     for (int g = 0; g < group; ++g) {
       const int hq = hkv * group + g;
@@ -667,16 +688,16 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots, kSplitNum,
-                     kSplitBias, a.kv_len, a.window, a.alibi);
+                     kSplitBias, a.kv_len, a.window, a.alibi, a.seg_start, a.seg_end);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
-  // Key lengths, windows and ALiBi need the masked instantiation (kTile is a
-  // multiple of kSub).
-  const bool bounds =
-      (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 || a.alibi != nullptr;
+  // Key lengths, windows, packed sequences and ALiBi need the masked
+  // instantiation (kTile is a multiple of kSub).
+  const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
+                      a.alibi != nullptr || a.seg_start != nullptr;
   if (a.causal)
     return bounds ? launch_main_t<D, true, true, BF>(a) : launch_main_t<D, true, false, BF>(a);
   return bounds ? launch_main_t<D, false, true, BF>(a) : launch_main_t<D, false, false, BF>(a);

@@ -48,6 +48,8 @@ const char* fa_error_string(int err) {
     case FA_ERR_LAYOUT: return "layout must be FA_LAYOUT_BHND or FA_LAYOUT_BNHD";
     case FA_ERR_DTYPE: return "unsupported element format";
     case FA_ERR_WINDOW: return "sliding window must be >= 0 and needs causal masking";
+    case FA_ERR_SEGMENTS:
+      return "packed sequences need causal masking and both seg_start and seg_end";
     default: return hipGetErrorString((hipError_t)err);
   }
 }
@@ -56,12 +58,14 @@ const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
 // Options: every field checked; the defaults are fp16, (B, H, N, D), no key
 // lengths, no window, no ALiBi.
-constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0, nullptr};
+constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0, nullptr, nullptr, nullptr};
 
 static int check_opts(const fa_options& op, int causal) {
   if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
   if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
+  if ((op.seg_start != nullptr) != (op.seg_end != nullptr) || (op.seg_start && !causal))
+    return FA_ERR_SEGMENTS;
   return FA_OK;
 }
 
@@ -90,6 +94,8 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.kv_len = op.kv_len;
   a.window = op.window;
   a.alibi = op.alibi_slopes;
+  a.seg_start = op.seg_start;
+  a.seg_end = op.seg_end;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -192,6 +198,8 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.kv_len = op.kv_len;
   a.window = op.window;
   a.alibi = op.alibi_slopes;
+  a.seg_start = op.seg_start;
+  a.seg_end = op.seg_end;
   return to_code(fa::launch_bwd_main(a));
 }
 

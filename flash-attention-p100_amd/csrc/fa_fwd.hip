@@ -183,7 +183,8 @@ template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int Nk, int W,
-                                         float alibi_raw, int sq, int sk,
+                                         const int* __restrict__ sst, float alibi_raw, int sq,
+                                         int sk,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -216,17 +217,26 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // ones run masked; blocks wholly past the diagonal or past N give exact
   // zeros there (their few products are not skipped, so every wave issues its
   // share of the loads inside the same code).
-  // Sliding window W (causal only; 0 = none): row i sees keys (i - W, i], so
-  // this tile's first visible key is q0 - W + 1 and the steps before j_lo are
-  // skipped; a wave's steps before n_head (blocks reaching left of its rows'
-  // windows) are masked, like the diagonal ones.
-  // Only the masked instantiation (BOUNDS) takes a window, so the others keep
-  // their loop structure.
+  // Causal left bounds: row i sees keys from lower(i) on, the larger of its
+  // sliding window's first key i - W + 1 (W = 0: none) and the first token of
+  // its packed sequence sst[i] (sst = nullptr: none), clamped to [0, i].
+  // lower() does not decrease with i, so this tile's first visible key is
+  // lower(q0) and the steps before j_lo are skipped; a wave's steps before
+  // n_head (blocks reaching left of its last row's bound) are masked, like the
+  // diagonal ones. Only the masked instantiation (BOUNDS) takes left bounds,
+  // so the others keep their loop structure.
   const int Wb = BOUNDS ? W : 0;
-  const int j_lo = Wb > 0 ? max(0, q0 - Wb + 1) / kKV : 0;
-  const int win_last = i_base + 31 - Wb - kq * 32;  // last masked block start (Wb > 0)
-  const int n_head = Wb > 0 && win_last >= 0 ? max(j_lo, win_last / kKV + 1) : j_lo;
-  const int w_lo = Wb > 0 ? i_row - Wb : INT_MIN;
+  const bool narrowed = BOUNDS && (Wb > 0 || sst != nullptr);
+  auto lower = [&](int i) {
+    i = min(i, N - 1);
+    int lo = Wb > 0 ? i - Wb + 1 : 0;
+    if (sst) lo = max(lo, min(sst[i], i));
+    return max(lo, 0);
+  };
+  const int j_lo = narrowed ? lower(q0) / kKV : 0;
+  const int win_last = narrowed ? lower(i_base + 31) - 1 - kq * 32 : -1;  // last masked block start
+  const int n_head = win_last >= 0 ? max(j_lo, win_last / kKV + 1) : j_lo;
+  const int w_lo = narrowed ? lower(i_row) - 1 : INT_MIN;
   int n_full = n_it;
   if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
   if (BOUNDS) n_full = min(n_full, Nk - 32 - kq * 32 >= 0 ? (Nk - 32 - kq * 32) / kKV + 1 : 0);
@@ -291,7 +301,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // Buffer parity counts from j_lo. Every wave runs steps j_lo .. n_it-1, one
   // barrier each; only which of them are masked differs between waves.
   int j = j_lo;
-  if (Wb > 0) {  // masked steps at the window's left edge
+  if (narrowed) {  // masked steps at the rows' left bounds
     for (; j < min(n_head, n_it - 1); ++j) {
       if ((j - j_lo) & 1) run(j, P1{}, T{}, T{});
       else run(j, P0{}, T{}, T{});
@@ -383,7 +393,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
-    Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi) {
+    Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi,
+    const int* __restrict__ seg_start) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -410,7 +421,9 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
-                                Lse + (size_t)bh * N, N, Nk, window, alibi_raw, stq.n, stk.n,
+                                Lse + (size_t)bh * N, N, Nk, window,
+                                seg_start ? seg_start + (size_t)b * N : nullptr, alibi_raw, stq.n,
+                                stk.n,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
@@ -427,16 +440,17 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window, a.alibi);
+                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window, a.alibi,
+                     a.seg_start);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  // Key lengths, windows and ALiBi need the masked instantiation (kKV is a
-  // multiple of kBR).
-  const bool bounds =
-      (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 || a.alibi != nullptr;
+  // Key lengths, windows, packed sequences and ALiBi need the masked
+  // instantiation (kKV is a multiple of kBR).
+  const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
+                      a.alibi != nullptr || a.seg_start != nullptr;
   if (a.causal)
     return bounds ? launch_fwd_t<D, true, true, BF>(a) : launch_fwd_t<D, true, false, BF>(a);
   return bounds ? launch_fwd_t<D, false, true, BF>(a) : launch_fwd_t<D, false, false, BF>(a);

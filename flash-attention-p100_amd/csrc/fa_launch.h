@@ -37,6 +37,11 @@ struct FwdArgs {
   const int* kv_len = nullptr;  // device, B entries: keys [0, kv_len[b]) exist (else N)
   int window = 0;               // causal sliding window W: row i sees keys (i - W, i]; 0 = none
   const float* alibi = nullptr; // device, Hq slopes: score(i, j) += -slope * |i - j|
+  // Packed sequences (causal only), device (B, N) each: token i of entry b
+  // belongs to the sequence of tokens [seg_start[b][i], seg_end[b][i]) and
+  // sees keys of that sequence only.
+  const int* seg_start = nullptr;
+  const int* seg_end = nullptr;
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -89,6 +94,8 @@ struct BwdArgs {
   const int* kv_len = nullptr;   // as FwdArgs::kv_len
   int window = 0;                // as FwdArgs::window
   const float* alibi = nullptr;  // as FwdArgs::alibi
+  const int* seg_start = nullptr;  // as FwdArgs::seg_start
+  const int* seg_end = nullptr;    // as FwdArgs::seg_end
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

@@ -69,14 +69,30 @@ const float* alibi_ptr(const c10::optional<at::Tensor>& slopes, const at::Tensor
   return t.data_ptr<float>();
 }
 
+// Optional packed-sequence bounds: int32 (B, N) on q's device; nullptr when absent.
+const int* seg_ptr(const c10::optional<at::Tensor>& seg, const at::Tensor& q, int B, int N,
+                   const char* name) {
+  if (!seg.has_value()) return nullptr;
+  const at::Tensor& t = *seg;
+  TORCH_CHECK(t.is_cuda() && t.device() == q.device(), name, " must be on q's device");
+  TORCH_CHECK(t.scalar_type() == at::kInt, name, " must be int32");
+  TORCH_CHECK(t.dim() == 2 && t.size(0) == B && t.size(1) == N && t.is_contiguous(), name,
+              " must be (B, N)");
+  return t.data_ptr<int>();
+}
+
 fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Tensor>& kv_len,
-                     int64_t window, const c10::optional<at::Tensor>& alibi, int B, int H) {
+                     int64_t window, const c10::optional<at::Tensor>& alibi,
+                     const c10::optional<at::Tensor>& seg_start,
+                     const c10::optional<at::Tensor>& seg_end, int B, int H, int N) {
   fa_options op{};
   op.dtype = dtype_code(q);
   op.layout = layout;
   op.kv_len = kv_len_ptr(kv_len, q, B);
   op.window = (int)window;
   op.alibi_slopes = alibi_ptr(alibi, q, H);
+  op.seg_start = seg_ptr(seg_start, q, B, N, "seg_start");
+  op.seg_end = seg_ptr(seg_end, q, B, N, "seg_end");
   return op;
 }
 
@@ -198,7 +214,8 @@ static void check_bnhd(const at::Tensor& t, const char* name) {
 
 std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
                                         c10::optional<at::Tensor> kv_len, int64_t window,
-    c10::optional<at::Tensor> alibi_slopes) {
+    c10::optional<at::Tensor> alibi_slopes,
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -218,7 +235,7 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, B, H);
+  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -229,7 +246,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
 std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v,
                                          at::Tensor dO, at::Tensor o, at::Tensor lse,
                                          bool causal, c10::optional<at::Tensor> kv_len,
-                                         int64_t window, c10::optional<at::Tensor> alibi_slopes) {
+                                         int64_t window, c10::optional<at::Tensor> alibi_slopes,
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -253,7 +271,7 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, B, H);
+  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -270,7 +288,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
 // backward_half_dq.
 std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
                                       c10::optional<at::Tensor> kv_len, int64_t window,
-    c10::optional<at::Tensor> alibi_slopes) {
+    c10::optional<at::Tensor> alibi_slopes,
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -293,7 +312,7 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, B, H);
+  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -304,7 +323,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
 std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v, at::Tensor dO,
                                        at::Tensor o, at::Tensor lse, bool causal,
                                        c10::optional<at::Tensor> kv_len, int64_t window,
-    c10::optional<at::Tensor> alibi_slopes) {
+    c10::optional<at::Tensor> alibi_slopes,
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -333,7 +353,7 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, B, H);
+  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -350,19 +370,23 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("forward_bnhd", &fa_forward_bnhd,
         "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
-        py::arg("alibi_slopes") = py::none());
+        py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
+        py::arg("seg_end") = py::none());
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
-        py::arg("alibi_slopes") = py::none());
+        py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
+        py::arg("seg_end") = py::none());
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
-        py::arg("alibi_slopes") = py::none());
+        py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
+        py::arg("seg_end") = py::none());
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
-        py::arg("alibi_slopes") = py::none());
+        py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
+        py::arg("seg_end") = py::none());
 }

@@ -66,7 +66,8 @@ class _FlashAttnP100(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None):
+    def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None,
+                segs=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -76,13 +77,17 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.kv_len = kv_len
         ctx.window = window
         ctx.alibi = alibi
+        ctx.segs = segs
+        seg_start, seg_end = segs if segs is not None else (None, None)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
-            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi)
+            ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
+                                        seg_end)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
-        if q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None:
-            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi)
+        if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
+                or segs is not None):
+            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -90,13 +95,14 @@ class _FlashAttnP100(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_o):
+        seg_start, seg_end = ctx.segs if ctx.segs is not None else (None, None)
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
-                                            ctx.window, ctx.alibi)
+                                            ctx.window, ctx.alibi, seg_start, seg_end)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
-                    None, None, None, None, None)
+                    None, None, None, None, None, None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
@@ -104,16 +110,17 @@ class _FlashAttnP100(torch.autograd.Function):
         # and backward_dt to bf16 for bf16 inputs.
         g = grad_o.contiguous()
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
-                or ctx.alibi is not None):
+                or ctx.alibi is not None or ctx.segs is not None):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
-                                          ctx.alibi)
+                                          ctx.alibi, seg_start, seg_end)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None
+        return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
+                None)
 
 
 def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-               alibi_slopes=None):
+               alibi_slopes=None, segment_ids=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -136,7 +143,13 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         the bias -alibi_slopes[h] * |i - j| to its scaled score of key j
         (ALiBi, in the symmetric form that also serves non-causal attention;
         under causal masking j <= i, so it is -slope * (i - j)). The slopes
-        are constants: no gradient flows to them.
+        are constants: no gradient flows to them;
+      * segment_ids, an integer tensor (B, N) on q's device (causal only):
+        several sequences packed into each batch entry. Each maximal run of
+        equal ids is one sequence, and a token attends to the keys of its own
+        sequence only (causal within it), as if each sequence had been run
+        alone. Also accepted: the (seg_start, seg_end) pair segment_bounds()
+        makes from such ids, for callers that reuse one packing across calls.
     """
     window = 0
     if sliding_window is not None:
@@ -148,7 +161,39 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
             raise ValueError(f"alibi_slopes must have shape ({q.size(1)},), got "
                              f"{tuple(alibi_slopes.shape)}")
         alibi_slopes = alibi_slopes.detach().float().contiguous()
-    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes)
+    segs = None
+    if segment_ids is not None:
+        if not causal:
+            raise ValueError("segment_ids (packed sequences) needs causal=True")
+        pair = isinstance(segment_ids, (tuple, list))
+        shape = tuple(segment_ids[0].shape) if pair else tuple(segment_ids.shape)
+        if shape != (q.size(0), q.size(2)):
+            raise ValueError(f"segment_ids must have shape ({q.size(0)}, {q.size(2)}), got "
+                             f"{shape}")
+        segs = tuple(segment_ids) if pair else segment_bounds(segment_ids)
+    return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes,
+                                segs)
+
+
+def segment_bounds(segment_ids):
+    """(seg_start, seg_end), int32 (B, N) each, of packed sequences.
+
+    A sequence is a maximal run of equal ids along a row: token i belongs to
+    the run [seg_start[b, i], seg_end[b, i]). These are the bounds the kernels
+    take (fa_options.seg_start / seg_end in the C ABI). Computed with a few
+    device-side scans; nothing is copied to the host.
+    """
+    s = segment_ids
+    B, N = s.shape
+    idx = torch.arange(N, device=s.device, dtype=torch.int64).expand(B, N)
+    change = s[:, 1:] != s[:, :-1]  # a new run starts at i + 1
+    starts = torch.ones(B, N, dtype=torch.bool, device=s.device)
+    starts[:, 1:] = change
+    ends = torch.ones(B, N, dtype=torch.bool, device=s.device)  # a run ends after i
+    ends[:, :-1] = change
+    seg_start = torch.where(starts, idx, torch.zeros_like(idx)).cummax(dim=1).values
+    seg_end = torch.where(ends, idx + 1, torch.full_like(idx, N)).flip(1).cummin(dim=1).values.flip(1)
+    return seg_start.to(torch.int32).contiguous(), seg_end.to(torch.int32).contiguous()
 
 
 def _expand_kv(k, n_head):

@@ -23,7 +23,12 @@ attention and the same mask.
 
 Also beyond the reference, a causal layer's sliding window (Qwen3's and
 Mistral-style `sliding_window`) runs in the kernels: row i sees keys
-(i - W, i], as transformers' own sliding-window mask.
+(i - W, i], as transformers' own sliding-window mask; and packed sequences
+(several sequences in one row, marked by `position_ids` that restart, as
+transformers' DataCollatorWithFlattening produces them) attend within their
+own sequence only, as transformers' packed-sequence mask does for eager and
+sdpa (masking_utils.find_packed_sequence_indices). The reference, which
+ignores position_ids, attended across the packed sequences.
 
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): other attention / padding masks,
@@ -36,13 +41,40 @@ import warnings
 
 import torch
 
-from fa_p100 import flash_attn
+from fa_p100 import flash_attn, segment_bounds
 
 _IMPL_NAME = "fa_p100"
 _warned_cast = False
 # Key lengths (int32 (B,) on the model's device) of the right-padded batch of
 # the model call in progress, set by enable_fa_p100's forward wrapper.
 _kv_len = contextvars.ContextVar("fa_p100_kv_len", default=None)
+# Packed-sequence bounds (seg_start, seg_end) of the model call in progress, or
+# _NOT_PACKED once that call's position_ids were found to hold one sequence per
+# row; unset (None) outside enable_fa_p100's forward wrapper.
+_NOT_PACKED = ()
+_segs = contextvars.ContextVar("fa_p100_segs", default=None)
+
+
+def packed_segment_ids(position_ids, batch):
+    """Sequence ids of packed rows, as transformers derives them: a new
+    sequence starts wherever a position id is not its predecessor's plus one
+    (masking_utils.find_packed_sequence_indices). Returns (batch, N) ids, or
+    None when every row holds one sequence. Synchronises with the device."""
+    pos = position_ids
+    if pos.dim() == 1:
+        pos = pos[None]
+    first = pos[:, :1] - 1
+    ids = (torch.diff(pos, prepend=first, dim=-1) != 1).cumsum(-1)
+    if not bool((ids[:, -1] != 0).any()):
+        return None
+    if ids.size(0) != batch:
+        ids = ids.expand(batch, -1)
+    return ids
+
+
+def _packed_bounds(position_ids, batch):
+    ids = packed_segment_ids(position_ids, batch)
+    return _NOT_PACKED if ids is None else segment_bounds(ids)
 
 
 def right_padding_lengths(mask):
@@ -118,6 +150,25 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             _warned_cast = True
         query, key, value = query.half(), key.half(), value.half()
 
+    # Packed sequences: bounds from the model call's position_ids (computed
+    # once per call by enable_fa_p100's wrapper, here when it is absent).
+    segs = _segs.get()
+    position_ids = kwargs.get("position_ids")
+    if segs is None and position_ids is not None:
+        segs = _packed_bounds(position_ids, query.size(0))
+    if segs is _NOT_PACKED or segs is None:
+        segs = None
+    else:
+        if not is_causal:
+            raise NotImplementedError(
+                "fa_p100 serves packed sequences (restarting position_ids) on causal "
+                "attention only.")
+        if tuple(segs[0].shape) != (query.size(0), query.size(2)) \
+                or segs[0].device != query.device:
+            raise NotImplementedError(
+                "fa_p100: the packed position_ids given to the model do not match this "
+                "attention call's batch and length.")
+
     # GQA/MQA go to the kernel as they are: no repeat_kv copies.
     full_precision = getattr(module, "_fa_p100_full_precision", False)
     kv_len = _kv_len.get()
@@ -127,7 +178,7 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
                 "fa_p100: the padding mask given to the model does not match this "
                 "attention call's batch.")
     out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
-                     kv_len=kv_len, sliding_window=sliding_window)
+                     kv_len=kv_len, sliding_window=sliding_window, segment_ids=segs)
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
 
@@ -189,10 +240,23 @@ def enable_fa_p100(model, full_precision=False):
                     "fa_p100 needs q_len == kv_len, so it cannot serve a KV cache; it "
                     "is a training kernel. Set generation_config.use_cache = False for "
                     "cache-free generation.")
+            # Packed sequences: restarting position_ids (checked once per call).
+            segs = _NOT_PACKED
+            position_ids = kwargs.get("position_ids")
+            if position_ids is not None:
+                ref = kwargs.get("input_ids")
+                if ref is None:
+                    ref = kwargs.get("inputs_embeds")
+                if ref is None and args:
+                    ref = args[0]
+                batch = ref.size(0) if ref is not None else position_ids.size(0)
+                segs = _packed_bounds(position_ids, batch)
             token = _kv_len.set(kv_len)
+            token_s = _segs.set(segs)
             try:
                 return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
             finally:
+                _segs.reset(token_s)
                 _kv_len.reset(token)
 
         model.forward = guarded

@@ -44,7 +44,8 @@ enum {
   FA_ERR_TOO_LARGE = 10007,  /* an index would overflow the kernels' 32-bit row counters */
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
-  FA_ERR_WINDOW = 10010      /* sliding window < 0, or > 0 without causal masking */
+  FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */
+  FA_ERR_SEGMENTS = 10011    /* packed sequences without causal masking, or only one bound array */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -161,7 +162,8 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
 
 /*
  * Options of the general pair below; a zeroed struct (or a NULL pointer)
- * means fp16, dense (B, H, N, D), no key lengths, no window, no ALiBi.
+ * means fp16, dense (B, H, N, D), no key lengths, no window, no ALiBi, no
+ * packed sequences.
  *   - dtype: FA_DTYPE_FP16 or FA_DTYPE_BF16 for q, k, v, o, dO, dq, dk, dv
  *     (bf16: products on the bf16 MFMA with fp32 accumulation, P and dS
  *     rounded to bf16 as operands, outputs rounded to nearest even);
@@ -175,7 +177,16 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *     entry's length sees no key: its o is 0, its lse +inf, its gradients 0;
  *   - alibi_slopes: NULL, or a device array of Hq fp32 slopes: the scaled
  *     score of query row i and key j of query head h gets
- *     -alibi_slopes[h] * |i - j| added (the usual ALiBi bias).
+ *     -alibi_slopes[h] * |i - j| added (the usual ALiBi bias);
+ *   - seg_start, seg_end: both NULL, or two device arrays of B * N int32
+ *     (causal only): several sequences packed into each batch entry. Token i
+ *     of entry b belongs to the sequence of tokens
+ *     [seg_start[b*N+i], seg_end[b*N+i]) and attends to keys of that
+ *     sequence only (with the causal mask, keys seg_start .. i). The arrays
+ *     must describe contiguous sequences that tile [0, N) (so both never
+ *     decrease along a row); other contents give undefined attention values
+ *     but no access outside the tensors (each bound is clamped to reach at
+ *     least the token itself).
  */
 typedef struct fa_options {
   int dtype;
@@ -183,15 +194,18 @@ typedef struct fa_options {
   const int* kv_len;
   int window;
   const float* alibi_slopes;
+  const int* seg_start;
+  const int* seg_end;
 } fa_options;
 
 /*
  * The general pair: every entry point above is one of its cases, plus bf16,
- * key padding, sliding windows and ALiBi (`opts`). fa_bwd_ex writes dq in
- * the element format (fp16 or bf16); lse and the workspace as in fa_bwd. No
- * counterpart in the reference, which raises on all four (README.md:72-75,
- * fa_p100_ext.cu:33, fa_p100_hf.py:64-82); the HF hook uses key lengths and
- * windows.
+ * key padding, sliding windows, ALiBi and packed sequences (`opts`).
+ * fa_bwd_ex writes dq in the element format (fp16 or bf16); lse and the
+ * workspace as in fa_bwd. No counterpart in the reference, which raises on
+ * bf16, masks and windows (README.md:72-75, fa_p100_ext.cu:33,
+ * fa_p100_hf.py:64-82) and has no bias or packing input; the HF hook uses key
+ * lengths, windows and packed sequences.
  */
 int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
               int B, int Hq, int Hkv, int N, int D, int causal, const fa_options* opts,

@@ -60,7 +60,7 @@ def _group_sum(g, hkv):
     return g.reshape(b, hkv, hq // hkv, n, d).sum(axis=2)
 
 
-def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None):
+def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
@@ -72,7 +72,9 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None):
     (causal only, another extension) key col is also masked for row when
     col <= row - W: each row sees its last W keys. With `alibi` (Hq slopes,
     another extension) query head h adds -alibi[h] * |row - col| to every
-    scaled logit before the masks.
+    scaled logit before the masks. With `segments` (B x N ids, causal only,
+    another extension: packed sequences) each maximal run of equal ids is one
+    sequence and key col is masked for row unless both lie in the same run.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d)
@@ -92,6 +94,14 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None):
             raise ValueError("a sliding window needs causal masking")
         mask = np.tril(np.ones((n, n), dtype=bool), -int(window))
         s = np.where(mask, -np.inf, s).astype(dtype)
+    if segments is not None:
+        if not causal:
+            raise ValueError("packed sequences need causal masking")
+        seg = np.asarray(segments).reshape(q.shape[0], n)
+        run = np.concatenate([np.zeros((seg.shape[0], 1), dtype=np.int64),
+                              np.cumsum(seg[:, 1:] != seg[:, :-1], axis=1)], axis=1)
+        other = run[:, :, None] != run[:, None, :]  # (B, N, N): different sequences
+        s = np.where(other[:, None], -np.inf, s).astype(dtype)
     if kv_len is not None:
         lens = np.clip(np.asarray(kv_len).reshape(-1), 1, n)
         cols = np.arange(n)[None, :] >= lens[:, None]  # (B, N) masked key columns
@@ -100,18 +110,19 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None):
 
 
 def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None,
-                  alibi=None):
+                  alibi=None, segments=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
-    (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`: optional per-entry
-    key lengths, sliding window and ALiBi slopes (see _scores).
+    (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`, `segments`:
+    optional per-entry key lengths, sliding window, ALiBi slopes and packed
+    sequence ids (see _scores).
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments)
     m = s.max(axis=-1, keepdims=True)
     # A row that sees no key at all (only with both key lengths and a window:
     # pad rows more than W past their entry's length) gets O = 0 and
@@ -131,7 +142,7 @@ def bwd_preprocess(o, do, dtype=np.float64):
 
 
 def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
-                  window=None, alibi=None):
+                  window=None, alibi=None, segments=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -147,8 +158,8 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     qd = q.astype(dtype)
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
-        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi)
-    s = _scores(q, ke, causal, dtype, kv_len, window, alibi)
+        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments)
+    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     dv = np.matmul(np.swapaxes(p, -1, -2), dod)
     dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
@@ -160,9 +171,9 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
 
 
 def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None,
-                   alibi=None):
+                   alibi=None, segments=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

@@ -72,15 +72,18 @@ class FaOptions(ctypes.Structure):
     """struct fa_options of include/fa_mi355x.h (same field order and types)."""
     _fields_ = [("dtype", ctypes.c_int), ("layout", ctypes.c_int),
                 ("kv_len", ctypes.c_void_p), ("window", ctypes.c_int),
-                ("alibi_slopes", ctypes.c_void_p)]
+                ("alibi_slopes", ctypes.c_void_p), ("seg_start", ctypes.c_void_p),
+                ("seg_end", ctypes.c_void_p)]
 
 
-def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None):
-    """A pointer to an FaOptions; kv_len / alibi_slopes are device addresses
-    (ints) or tensors."""
+def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_start=None,
+            seg_end=None):
+    """A pointer to an FaOptions; the array fields are device addresses (ints)
+    or tensors."""
     def addr(x):
         return None if x is None else (x if isinstance(x, int) else x.data_ptr())
-    o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes))
+    o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes), addr(seg_start),
+                  addr(seg_end))
     return ctypes.pointer(o)
 
 

@@ -66,6 +66,12 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(window=16), s) == 10010
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(window=-1), s) == 10010
     assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, fa_opts(window=4), s) == 10010
+    # packed sequences: causal only, and both bound arrays or neither
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(seg_start=1, seg_end=1),
+                         s) == 10011
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(seg_start=1), s) == 10011
+    assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 1, fa_opts(seg_end=1), s) == 10011
+    assert b"packed" in lib.fa_error_string(10011)
     # BNHD puts every head of a row in one 32-bit buffer range
     assert lib.fa_fwd_ex(*([one] * 5), 1, 1 << 12, 1, 1 << 14, 128, 0, fa_opts(0, 1), s) == 10007
     assert b"layout" in lib.fa_error_string(10008)
@@ -93,7 +99,7 @@ def test_public_api_surface_matches_reference():
     # The reference's parameters, in order, with its defaults; the extensions
     # (key lengths, sliding window, ALiBi slopes) come after them and default
     # to None, so every reference call binds the same way.
-    extensions = ["kv_len", "sliding_window", "alibi_slopes"]
+    extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False

@@ -101,3 +101,26 @@ def test_register_and_enable():
     # device check stops host tensors.
     with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         model(ids, attention_mask=torch.ones(1, 6, dtype=torch.long))
+
+
+def test_packed_position_ids_become_segment_bounds():
+    """Restarting position_ids mark packed sequences exactly as transformers'
+    find_packed_sequence_indices does; one sequence per row gives None; the
+    bounds are each token's [start, end) run; a packed batch on a
+    non-causal call raises."""
+    from fa_p100 import segment_bounds
+    pos = torch.tensor([[0, 1, 2, 0, 1, 0, 1, 2, 3]])
+    ids = hf.packed_segment_ids(pos, 1)
+    assert ids.tolist() == [[0, 0, 0, 1, 1, 2, 2, 2, 2]]
+    from transformers.masking_utils import find_packed_sequence_indices
+    assert torch.equal(ids, find_packed_sequence_indices(pos))
+    assert hf.packed_segment_ids(torch.arange(9)[None], 1) is None
+    assert hf.packed_segment_ids(torch.arange(9)[None] + 5, 2) is None  # offset, one sequence
+    assert hf.packed_segment_ids(pos, 3).shape == (3, 9)  # broadcast over the batch
+    start, end = segment_bounds(ids)
+    assert start.tolist() == [[0, 0, 0, 3, 3, 5, 5, 5, 5]]
+    assert end.tolist() == [[3, 3, 3, 5, 5, 9, 9, 9, 9]]
+    q, k, v = qkv(n=9)
+    with pytest.raises(NotImplementedError, match="causal attention only"):
+        hf.fa_p100_attention_forward(types.SimpleNamespace(is_causal=False), q, k, v, None,
+                                     position_ids=pos)

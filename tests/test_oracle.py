@@ -363,3 +363,69 @@ def test_alibi_with_window_matches_sdpa():
             torch.tensor(np.repeat(v[e:e + 1], hq, 1)), attn_mask=mask[None]).numpy()
         assert np.allclose(o[e][:, seen], ref[0][:, seen], atol=1e-12)
         assert not np.any(o[e][:, ~seen])
+
+
+# ---------------------------------------------------------------------------
+# Packed sequences (an extension): several causal sequences in one row.
+def test_packed_sequence_pins():
+    """Each maximal run of equal segment ids attends within itself only.
+    Pinned by running every sequence alone through the plain causal oracle
+    (outputs, LSE and gradients must match row for row), against torch SDPA
+    with the block-diagonal causal mask, one run equal to plain causal, the
+    run definition (ids need not be sorted: a repeated id after a change is a
+    new sequence), with key lengths and a window, and finite differences."""
+    rng = np.random.default_rng(31)
+    b, hq, hkv, n, d = 2, 4, 2, 23, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    seg = np.array([[0] * 5 + [1] * 1 + [2] * 9 + [3] * 8,
+                    [7] * 10 + [3] * 6 + [7] * 7])  # entry 1: ids 7, 3, 7 = three runs
+    o, lse = ora.attention_fwd(q, k, v, True, segments=seg)
+    grads = ora.attention_bwd(q, k, v, do, True, segments=seg)
+    runs = {0: [(0, 5), (5, 6), (6, 15), (15, 23)], 1: [(0, 10), (10, 16), (16, 23)]}
+    for e, spans in runs.items():
+        for a, z in spans:
+            sl = (slice(e, e + 1), slice(None), slice(a, z))
+            o1, l1 = ora.attention_fwd(q[sl], k[sl], v[sl], True)
+            g1 = ora.attention_bwd(q[sl], k[sl], v[sl], do[sl], True)
+            assert np.allclose(o[sl], o1, atol=1e-12) and np.allclose(lse[sl], l1, atol=1e-12)
+            for got, ref in zip(grads, g1):
+                assert np.allclose(got[sl], ref, atol=1e-12)
+        i, j = np.arange(n)[:, None], np.arange(n)[None, :]
+        run = np.concatenate([[0], np.cumsum(seg[e, 1:] != seg[e, :-1])])
+        mask = (j <= i) & (run[:, None] == run[None, :])
+        ref = F.scaled_dot_product_attention(
+            torch.tensor(q[e:e + 1]), torch.tensor(np.repeat(k[e:e + 1], hq // hkv, 1)),
+            torch.tensor(np.repeat(v[e:e + 1], hq // hkv, 1)), attn_mask=torch.tensor(mask))
+        assert np.allclose(o[e], ref[0].numpy(), atol=1e-12)
+    one = np.zeros((b, n), dtype=np.int64)
+    assert np.array_equal(ora.attention_fwd(q, k, v, True, segments=one)[0],
+                          ora.attention_fwd(q, k, v, True)[0])
+    # Planted: ignoring the packing attends across sequences.
+    assert not np.allclose(ora.attention_fwd(q, k, v, True)[0], o, atol=1e-6)
+    # With key lengths and a window too: each sequence alone, keys cut at the
+    # entry's length and at the window.
+    lens = np.array([n, 12])
+    o2, _ = ora.attention_fwd(q, k, v, True, kv_len=lens, window=4, segments=seg)
+    for e, spans in runs.items():
+        for a, z in spans:
+            zz = min(z, lens[e]) if a < lens[e] else a
+            if zz <= a:
+                continue
+            sl = (slice(e, e + 1), slice(None), slice(a, zz))
+            o1, _ = ora.attention_fwd(q[sl], k[sl], v[sl], True, window=4)
+            assert np.allclose(o2[sl], o1, atol=1e-12)
+    h = 1e-4
+    for which, g in enumerate(grads):
+        for _ in range(4):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, True, segments=seg)
+                  - ora.attention_loss(*minus, do, True, segments=seg)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
+    with pytest.raises(ValueError):
+        ora.attention_fwd(q, k, v, False, segments=seg)
