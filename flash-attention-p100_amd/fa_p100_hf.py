@@ -19,7 +19,10 @@ to look at it first (fa_p100_hf.py:13-22, 183-211). Beyond the reference,
 which rejects every padding mask, a right-padded 2-D mask (each row ones, then
 zeros) is served exactly: its row sums go to the kernels as per-entry key
 lengths, so every position attends to the real keys only, as with eager
-attention and the same mask.
+attention and the same mask. Left (and both-sided) padding is served on
+causal layers too: the pads form a packed sequence of their own (below), so
+every real token attends to the real keys only, as with eager; only the pad
+rows' outputs, which nothing reads, differ.
 
 Also beyond the reference, a causal layer's sliding window (Qwen3's and
 Mistral-style `sliding_window`) runs in the kernels: row i sees keys
@@ -88,6 +91,30 @@ def right_padding_lengths(mask):
     if not bool(torch.equal(m, ref)) or not bool((lens > 0).all()):
         return None
     return lens.to(torch.int32)
+
+
+def padding_spans(mask):
+    """(first, end) int32 (B,) of a 2-D mask whose ones form one contiguous,
+    non-empty run per row (left, right or both-sided padding), or None for
+    any other mask."""
+    if mask.dim() != 2:
+        return None
+    m = mask != 0
+    lens = m.sum(dim=1)
+    first = m.int().argmax(dim=1)  # first one (0 for an all-zero row, caught below)
+    idx = torch.arange(m.size(1), device=m.device)[None, :]
+    ref = (idx >= first[:, None]) & (idx < (first + lens)[:, None])
+    if not bool(torch.equal(m, ref)) or not bool((lens > 0).all()):
+        return None
+    return first.to(torch.int32), (first + lens).to(torch.int32)
+
+
+def _left_padding_segments(first, n):
+    """Sequence ids (B, n) that put each row's left pads in a sequence of
+    their own (0) and the rest in another (1), so that causal real tokens
+    see real keys only."""
+    idx = torch.arange(n, device=first.device)[None, :]
+    return (idx >= first[:, None].long()).to(torch.int32)
 
 
 def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout=0.0,
@@ -205,7 +232,8 @@ def enable_fa_p100(model, full_precision=False):
     config at it, records `full_precision` on every module, turns the KV cache
     off, and wraps `model.forward` once so that use_cache=True and any
     padding mask other than right padding raise instead of being silently
-    ignored; a right-padded mask is served through per-entry key lengths.
+    ignored; a right-padded mask is served through per-entry key lengths and
+    a left-padded one (causal layers) through packed-sequence bounds.
     """
     register()
     _set_impl(model.config, _IMPL_NAME)
@@ -225,14 +253,19 @@ def enable_fa_p100(model, full_precision=False):
         def guarded(*args, attention_mask=None, use_cache=None, **kwargs):
             # transformers drops the mask before the attention interface sees it
             # for unregistered implementations: this is the last place to catch it.
-            kv_len = None
+            kv_len, left = None, None
             if attention_mask is not None and not bool(attention_mask.all()):
-                kv_len = right_padding_lengths(attention_mask)
-                if kv_len is None:
+                spans = padding_spans(attention_mask)
+                if spans is None:
                     raise NotImplementedError(
-                        "fa_p100 serves only right padding (each mask row: ones, then "
-                        "zeros); this padding mask would be discarded silently. Pad on "
-                        "the right or pack the batch so every position is real.")
+                        "fa_p100 serves only padding masks whose ones form one run per row "
+                        "(right, left or both-sided padding); this mask would be discarded "
+                        "silently. Pad at the ends or pack the batch so every position is "
+                        "real.")
+                first, end = spans
+                kv_len = end  # keys past the run exist for no row
+                if bool((first > 0).any()):
+                    left = first
             # Rejected up front rather than at the first decode step, after a
             # prefill that would have succeeded.
             if use_cache:
@@ -241,9 +274,25 @@ def enable_fa_p100(model, full_precision=False):
                     "is a training kernel. Set generation_config.use_cache = False for "
                     "cache-free generation.")
             # Packed sequences: restarting position_ids (checked once per call).
+            # Left padding rides on the same bounds: the pads form a sequence
+            # of their own, so real tokens (causal) see real keys only.
             segs = _NOT_PACKED
             position_ids = kwargs.get("position_ids")
-            if position_ids is not None:
+            if left is not None:
+                # Position ids of the pads are arbitrary (generate() sets them to
+                # 1); a restart between two real tokens would mean packing too.
+                # kv_len is each row's end of real tokens.
+                if position_ids is not None:
+                    pos = position_ids if position_ids.dim() == 2 else position_ids[None]
+                    idx = torch.arange(1, pos.size(-1), device=pos.device)[None, :]
+                    real_pair = (idx > left[:, None].long()) & (idx < kv_len[:, None].long())
+                    restart = (torch.diff(pos, dim=-1) != 1) & real_pair
+                    if bool(restart.any()):
+                        raise NotImplementedError(
+                            "fa_p100 does not serve left padding and packed sequences "
+                            "together.")
+                segs = segment_bounds(_left_padding_segments(left, attention_mask.size(1)))
+            elif position_ids is not None:
                 ref = kwargs.get("input_ids")
                 if ref is None:
                     ref = kwargs.get("inputs_embeds")

@@ -140,3 +140,66 @@ def test_hf_hook_right_padding_matches_eager_with_mask():
     for n, g in grads["eager"].items():
         rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
         assert rel < 5e-2, (n, rel)
+
+
+def test_hf_hook_left_and_both_sided_padding_match_eager_with_mask():
+    """Left- and both-sided-padded rows through the hook (the pads become a
+    packed sequence of their own): logits at every real position within the
+    eager-vs-sdpa envelope of eager with the same mask (pad rows, which
+    nothing reads, are not compared), with generate()-style position ids
+    too, and a training step's loss and attention gradients against eager
+    (the loss over real rows only)."""
+    import fa_p100_hf
+    from test_gpu_hf import qwen3
+    N = 320
+    spans = [(0, 320), (70, 320), (5, 200), (100, 101)]  # (first, end) of the real tokens
+    idx = torch.arange(N, device=DEV)[None, :]
+    first = torch.tensor([a for a, _ in spans], device=DEV)[:, None]
+    end = torch.tensor([z for _, z in spans], device=DEV)[:, None]
+    mask = ((idx >= first) & (idx < end)).long()
+    ids = torch.randint(0, 1000, (len(spans), N), device=DEV,
+                        generator=torch.Generator(DEV).manual_seed(9))
+    gen_pos = (mask.cumsum(-1) - 1).masked_fill(mask == 0, 1)  # what generate() passes
+
+    def logits(model, impl, **kw):
+        model.config._attn_implementation = impl
+        with torch.no_grad(), torch.autocast("cuda", torch.float16):
+            return model(ids, attention_mask=mask, **kw).logits.float()
+
+    model = qwen3(2, 512, 8, 2, 64, 1024, 1000).eval()
+    for kw in ({}, {"position_ids": gen_pos}):
+        eager, sdpa = logits(model, "eager", **kw), logits(model, "sdpa", **kw)
+        fa_p100_hf.enable_fa_p100(model)
+        fa = logits(model, "fa_p100", **kw)
+        real = mask.bool()
+        env, gap = (sdpa - eager).abs()[real], (fa - eager).abs()[real]
+        assert gap.mean() <= 2 * env.mean() + 1e-4, (kw.keys(), gap.mean().item())
+        for b, (a, z) in enumerate(spans):
+            g = (fa - eager).abs()[b, a:z].mean().item()
+            e = (sdpa - eager).abs()[b, a:z].mean().item()
+            assert g <= 2 * e + 1e-4, (b, g, e)
+
+    # With HF's label shift the last left pad would predict the first real
+    # token, putting a pad row (whose output every implementation defines
+    # differently: eager lets it see all keys) into the loss; mask that label
+    # so the loss reads real rows only.
+    labels = ids.masked_fill(mask == 0, -100)
+    labels[torch.arange(len(spans), device=DEV), first[:, 0]] = -100
+    losses, grads = {}, {}
+    for impl in ("eager", "sdpa", "fa_p100"):
+        m = qwen3(2, 256, 4, 2, 64, 512, 1000, seed=3)
+        if impl == "fa_p100":
+            fa_p100_hf.enable_fa_p100(m)
+        else:
+            m.config._attn_implementation = impl
+        with torch.autocast("cuda", torch.float16):
+            out = m(ids, attention_mask=mask, labels=labels)
+        out.loss.backward()
+        losses[impl] = out.loss.item()
+        grads[impl] = {n: p.grad.float().clone() for n, p in m.named_parameters()
+                       if "self_attn" in n and p.grad is not None}
+    assert abs(losses["fa_p100"] - losses["eager"]) <= 1e-3 * abs(losses["eager"])
+    for n, g in grads["eager"].items():
+        rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
+        env_g = ((grads["sdpa"][n] - g).norm() / g.norm()).item()
+        assert rel <= max(5e-2, 2 * env_g), (n, rel, env_g)

@@ -85,13 +85,19 @@ def test_register_and_enable():
     assert model.forward is inner
 
     ids = torch.zeros(1, 6, dtype=torch.long)
-    # Left padding, holes and all-zero rows still raise; right padding is
-    # served (tests/test_gpu_hf.py runs it against eager with the mask).
-    for mask in ([[0, 0, 1, 1, 1, 1]], [[1, 1, 0, 1, 1, 1]], [[0, 0, 0, 0, 0, 0]]):
-        with pytest.raises(NotImplementedError, match="right padding"):
+    # Holes and all-zero rows still raise; right, left and both-sided padding
+    # are served (tests/test_gpu_kvlen.py runs them against eager with the mask).
+    for mask in ([[1, 1, 0, 1, 1, 1]], [[0, 0, 0, 0, 0, 0]], [[0, 1, 0, 1, 1, 0]]):
+        with pytest.raises(NotImplementedError, match="one run per row"):
             model(ids, attention_mask=torch.tensor(mask))
     assert hf.right_padding_lengths(torch.tensor([[1, 1, 1, 1, 0, 0], [1] * 6])).tolist() == [4, 6]
     assert hf.right_padding_lengths(torch.tensor([[1, 0, 1, 0, 0, 0]])) is None
+    first, end = hf.padding_spans(torch.tensor([[0, 0, 1, 1, 1, 1], [1, 1, 1, 0, 0, 0],
+                                                [0, 1, 1, 1, 0, 0]]))
+    assert first.tolist() == [2, 0, 1] and end.tolist() == [6, 3, 4]
+    assert hf.padding_spans(torch.tensor([[1, 0, 1, 1, 1, 1]])) is None
+    assert hf._left_padding_segments(first, 6).tolist() == [
+        [0, 0, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1], [0, 1, 1, 1, 1, 1]]
     with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         model(ids, attention_mask=torch.tensor([[1, 1, 1, 1, 0, 0]]))
     with pytest.raises(NotImplementedError, match="KV cache"):
