@@ -69,11 +69,12 @@ static_assert(kTile == kBwdTile, "workspace layout assumes this key tile");
 // kSplitNum - kSplitBias) / 256) of its phase-1 iterations move to workgroup
 // n_tiles-1-u. Phase-1 steps cost more than phase-2 steps, so the iterations
 // move from the phase-1-heavy low tiles to the phase-2-heavy high ones. Swept
-// over 50..110 (same-box A/B): fastest at 76..86 for B=1 H=8 N=4096 D=128,
-// 66..76 for H=16 N=2048 D=64 and 76 for H=16 N=8192 D=128; 110 lost
-// everywhere. The best rate grew from ~50 when phase 2's operand reads moved
-// ahead of their products (phase-2 steps got cheaper).
-constexpr int kSplitNum = 76;
+// over 50..110 (same-box A/B) with phase 2's operands read ahead: fastest at
+// 76..86 for B=1 H=8 N=4096 D=128, 66..76 for H=16 N=2048 D=64 and 76 for
+// H=16 N=8192 D=128; 110 lost everywhere (the best rate had been ~50 before
+// phase-2 steps got cheaper). With phase 1's operands read ahead too, 66 beat
+// 76 and 86 on all three shapes by 0.4-1.7%.
+constexpr int kSplitNum = 66;
 constexpr int kSplitBias = 5;
 
 // LDS: every tile is its own __shared__ object (declared in bwd_kernel), so
@@ -214,10 +215,23 @@ struct KVWave {
     using S = Swz<D>;
     const int h = lane >> 5;
     floatx16 sacc = zero16(), pacc = zero16();
+    // Operands read one k-step ahead of their products.
+    half8 qa = S::read16(Qs, so, 0), oa = S::read16(Os, so, 0);
+    half8 va = tile_read16<D>(Vt, kr0, 0, roff);
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      sacc = mfma16<BF>(S::read16(Qs, so, kk), kb[kk], sacc);
-      pacc = mfma16<BF>(S::read16(Os, so, kk), tile_read16<D>(Vt, kr0, kk, roff), pacc);
+      half8 qn = qa, on = oa, vn = va;
+      if (kk + 1 < D / 16) {
+        qn = S::read16(Qs, so, kk + 1);
+        on = S::read16(Os, so, kk + 1);
+        vn = tile_read16<D>(Vt, kr0, kk + 1, roff);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      sacc = mfma16<BF>(qa, kb[kk], sacc);
+      pacc = mfma16<BF>(oa, va, pacc);
+      qa = qn;
+      oa = on;
+      va = vn;
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
     // i = i0 + 32m + 8*g4 + 4h + e; rows from row_end on are masked: past N,
