@@ -33,6 +33,9 @@ own sequence only, as transformers' packed-sequence mask does for eager and
 sdpa (masking_utils.find_packed_sequence_indices). The reference, which
 ignores position_ids, attended across the packed sequences.
 
+The kernels run in the autocast dtype (fp16 or bf16; bf16 inputs without
+autocast stay bf16); the reference cast everything to fp16.
+
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): other attention / padding masks,
 output_attentions, head_mask, a window on non-causal attention, dropout,
@@ -161,21 +164,29 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             f"fa_p100 serves sliding windows on causal attention only; this layer asks for "
             f"a window of {sliding_window} with is_causal={is_causal}.")
 
-    # The kernels take fp16. Under fp16 autocast, Qwen3's fp32 q_norm/k_norm
-    # weights and rotary tables hand q and k over in fp32 while v is fp16, so
-    # casting here is the normal path; outside autocast it is worth a warning.
+    # The kernels take fp16 or bf16. Under autocast, Qwen3's fp32 q_norm/k_norm
+    # weights and rotary tables hand q and k over in fp32 while v is in the
+    # autocast dtype, so casting to that dtype is the normal path. Without
+    # autocast, bf16 inputs stay bf16 and anything else goes to fp16 (the
+    # reference's only format), with one warning.
     orig_dtype = query.dtype
-    if query.dtype != torch.float16 or key.dtype != torch.float16 \
-            or value.dtype != torch.float16:
-        sanctioned = (torch.is_autocast_enabled("cuda")
-                      and torch.get_autocast_dtype("cuda") == torch.float16)
-        if not sanctioned and not _warned_cast:
+    autocast_dt = (torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda")
+                   else None)
+    if autocast_dt in (torch.float16, torch.bfloat16):
+        target = autocast_dt
+    elif query.dtype == key.dtype == value.dtype == torch.bfloat16:
+        target = torch.bfloat16
+    else:
+        target = torch.float16
+    if query.dtype != target or key.dtype != target or value.dtype != target:
+        if autocast_dt != target and not _warned_cast:
             warnings.warn(
-                f"fa_p100 casts q={query.dtype} k={key.dtype} v={value.dtype} to float16 "
-                "outside fp16 autocast; the kernels are fp16 only. Run the step under "
-                "torch.autocast('cuda', torch.float16).", stacklevel=2)
+                f"fa_p100 casts q={query.dtype} k={key.dtype} v={value.dtype} to {target} "
+                "outside fp16/bf16 autocast; the kernels take fp16 or bf16. Run the step "
+                "under torch.autocast('cuda', torch.float16) or torch.bfloat16.",
+                stacklevel=2)
             _warned_cast = True
-        query, key, value = query.half(), key.half(), value.half()
+        query, key, value = query.to(target), key.to(target), value.to(target)
 
     # Packed sequences: bounds from the model call's position_ids (computed
     # once per call by enable_fa_p100's wrapper, here when it is absent).

@@ -108,3 +108,49 @@ def test_qwen3_0p6b_shaped_training_step_through_hook():
     assert abs(out.loss.item() - torch.log(torch.tensor(151936.0)).item()) < 1.0
     q_grad = model.model.layers[0].self_attn.q_proj.weight.grad
     assert q_grad is not None and torch.isfinite(q_grad).all() and q_grad.abs().sum() > 0
+
+
+def test_hook_runs_bf16_under_bf16_autocast():
+    """Under bf16 autocast the hook runs the bf16 kernels (the reference cast
+    to fp16): no cast warning, logits within twice the eager-vs-sdpa envelope
+    of eager in bf16, and a training step's loss and attention gradients
+    against eager within max(5e-2, twice sdpa's distance from eager)."""
+    import warnings
+    import fa_p100_hf
+    ids = torch.randint(0, 1000, (2, 300), device="cuda",
+                        generator=torch.Generator("cuda").manual_seed(2))
+
+    def logits(m, impl):
+        m.config._attn_implementation = impl
+        with torch.no_grad(), torch.autocast("cuda", torch.bfloat16):
+            return m(ids).logits.float()
+
+    model = qwen3(2, 512, 8, 2, 128, 1024, 1000).eval()
+    eager, sdpa = logits(model, "eager"), logits(model, "sdpa")
+    fa_p100_hf.enable_fa_p100(model)
+    fa_p100_hf._warned_cast = False
+    with warnings.catch_warnings(record=True) as w:
+        warnings.simplefilter("always")
+        fa = logits(model, "fa_p100")
+    assert not [x for x in w if "casts" in str(x.message)]
+    env, gap = (sdpa - eager).abs(), (fa - eager).abs()
+    assert gap.mean() <= 2 * env.mean() + 1e-4, (gap.mean().item(), env.mean().item())
+
+    losses, grads = {}, {}
+    for impl in ("eager", "sdpa", "fa_p100"):
+        m = qwen3(2, 256, 4, 2, 64, 512, 1000, seed=3)
+        if impl == "fa_p100":
+            fa_p100_hf.enable_fa_p100(m)
+        else:
+            m.config._attn_implementation = impl
+        with torch.autocast("cuda", torch.bfloat16):
+            out = m(ids, labels=ids)
+        out.loss.backward()
+        losses[impl] = out.loss.item()
+        grads[impl] = {n: p.grad.float().clone() for n, p in m.named_parameters()
+                       if "self_attn" in n and p.grad is not None}
+    assert abs(losses["fa_p100"] - losses["eager"]) <= 2e-3 * abs(losses["eager"])
+    for n, g in grads["eager"].items():
+        rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
+        env_g = ((grads["sdpa"][n] - g).norm() / g.norm()).item()
+        assert rel <= max(5e-2, 2 * env_g), (n, rel, env_g)
