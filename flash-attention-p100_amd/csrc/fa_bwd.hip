@@ -280,9 +280,11 @@ struct QWave {
   float lse2, dvv;
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
+  template <class Issue>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
                                        int i_row, int Nk, int key_lo, float alibi_raw, int lane,
-                                       const typename Swz<D>::Offsets& so, float c) {
+                                       const typename Swz<D>::Offsets& so, float c,
+                                       const Issue& issue) {
     using S = Swz<D>;
     const int h = lane >> 5;
     floatx16 st = zero16(), pt = zero16();
@@ -299,6 +301,7 @@ struct QWave {
       __builtin_amdgcn_sched_barrier(0);
       st = mfma16<BF>(ka, qb[kk], st);
       pt = mfma16<BF>(va, ob[kk], pt);
+      issue(kk);
       ka = kn;
       va = vn;
     }
@@ -632,9 +635,18 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       };
       auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
-        fetch(t + 1, P ? ta0 : ta1, P ? tb0 : tb1);
+        // The next stage's loads go out between this step's products.
+        const int jn = min(t + 1, n_kt - 1) * kSub;
+        auto issue = [&](int q) {
+          constexpr int kParts = decltype(plan_k)::kParts;
+          static_assert(2 * kParts <= D / 16, "every load needs an issue point");
+          if (q < 2 * kParts) {
+            if (q & 1) plan_k.part(P ? tb0 : tb1, rv, jn, wave, q >> 1);
+            else plan_k.part(P ? ta0 : ta1, rk, jn, wave, q >> 1);
+          }
+        };
         w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, key_lo, alibi_raw, lane,
-               so, scale_log2);
+               so, scale_log2, issue);
         wait_vmem();
         __syncthreads();
       };
