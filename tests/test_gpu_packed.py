@@ -235,3 +235,27 @@ def test_hf_hook_packed_batch_matches_eager():
         rel = ((grads["fa_p100"][n] - gr).norm() / gr.norm()).item()
         env_g = ((grads["sdpa"][n] - gr).norm() / gr.norm()).item()
         assert rel <= max(5e-2, 2 * env_g), (n, rel, env_g)
+
+
+def test_packed_with_alibi_matches_oracle():
+    """Packed sequences and ALiBi slopes together (both ride on the masked
+    instantiation): against the oracle with the same ids and slopes."""
+    import fa_p100
+    B, Hq, Hkv, N, D = 2, 4, 2, 600, 128
+    seg = np.stack([ids_from_lengths([200, 1, 399]), ids_from_lengths([64, 536])])
+    slopes = np.array([2.0 ** (-8.0 * (i + 1) / Hq) for i in range(Hq)], dtype=np.float32)
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=21)
+    qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    al = torch.tensor(slopes, device=DEV)
+    o = fa_p100.flash_attn(qg, kg, vg, True, alibi_slopes=al,
+                           segment_ids=torch.tensor(seg, device=DEV))
+    o.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    qn, kn, vn, dn = (t.float().numpy() for t in (q, k, v, do))
+    sl = slopes.astype(np.float64)
+    ref_o, _ = ora.attention_fwd(qn, kn, vn, True, alibi=sl, segments=seg)
+    assert ora.max_abs(np64(o), ref_o) <= FWD_MAX_ABS
+    ref = ora.attention_bwd(qn, kn, vn, dn, True, alibi=sl, segments=seg)
+    for name, g, r in zip(("dQ", "dK", "dV"), (qg.grad, kg.grad, vg.grad), ref):
+        l2, rr = ora.rel_l2(np64(g), r), ora.rel_max_rms(np64(g), r)
+        assert l2 <= GRAD_REL_L2 and rr < REF_REL, (name, l2, rr)
