@@ -209,7 +209,7 @@ struct KVWave {
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
-                                       int m, int kr0, int i0, int j_col, int row_end,
+                                       int m, int kr0, int i0, int j_col, int row_lo, int row_end,
                                        float alibi_raw, int lane, int roff,
                                        const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
@@ -238,7 +238,7 @@ struct KVWave {
     // past the key's sliding window, or all of them for a key past the
     // entry's key length (its dK/dV rows are stored, as zeros).
     const int base = i0 + 32 * m + 4 * h;
-    const int lo = j_col - base;     // alive when 8*g4 + e >= lo (causal)
+    const int lo = row_lo - base;    // alive when 8*g4 + e >= lo (causal: row_lo = j_col)
     const int hi = row_end - base;   // alive when 8*g4 + e <  hi
     if (BOUNDS && alibi_raw != 0.f) {  // ALiBi: -slope |i - j| in raw-score units
       const float d0 = (float)(base - j_col);
@@ -255,7 +255,7 @@ struct KVWave {
       for (int e = 0; e < 4; ++e) {
         const int r = 4 * g4 + e, idx = 8 * g4 + e;
         float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
-        if (CAUSAL) p = (idx >= lo) ? p : 0.f;
+        if (CAUSAL || BOUNDS) p = (idx >= lo) ? p : 0.f;
         if (BOUNDS) p = (idx < hi) ? p : 0.f;
         pb[r >> 3][r & 7] = to16<BF>(p);
         sb[r >> 3][r & 7] = to16<BF>(p * (pacc[r] - d4[e]));
@@ -404,6 +404,18 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     if (sst) lo = max(lo, min(sst[i], i));
     return max(lo, 0);
   };
+  // Without causal masking, packed sequences also bound each row's keys from
+  // above (row i sees keys below row_hi(i)) and each key's rows from below
+  // (key j reaches rows from col_lo(j) on); both never decrease.
+  const bool packed_nc = BOUNDS && !CAUSAL && sst != nullptr;
+  auto row_hi = [&](int i) {
+    i = min(i, N - 1);
+    return packed_nc ? min(Nk, max(sen[i], i + 1)) : Nk;
+  };
+  auto col_lo = [&](int j) {
+    j = min(j, N - 1);
+    return packed_nc ? max(0, min(sst[j], j)) : 0;
+  };
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
   // Offset of query head hq's row 0 in Q, dO, dQ.
@@ -438,9 +450,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // Query rows of key tile u's phase 1: from its diagonal (causal) to the end,
   // or to the last row whose window or sequence reaches the tile.
   auto q_end = [&](int u) { return narrowed ? upper(u * kTile + kTile - 1) : N; };
-  auto n_iters = [&](int u) {
-    return group * ((q_end(u) - (CAUSAL ? u * kTile : 0) + kSub - 1) / kSub);
-  };
+  // ... and from its diagonal (causal) or the start of its first key's
+  // sequence, rounded down to a streamed tile (u * kTile is a multiple of kSub).
+  auto q_start = [&](int u) { return CAUSAL ? u * kTile : col_lo(u * kTile) / kSub * kSub; };
+  auto n_iters = [&](int u) { return group * ((q_end(u) - q_start(u) + kSub - 1) / kSub); };
   auto split = [&](int u) {
     const int m = n_tiles - 1 - 2 * u;
     if (!CAUSAL || m <= 0 || narrowed) return 0;  // windows leave the tiles' work equal
@@ -475,7 +488,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
 #pragma unroll
     for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
 
-    const int i_start = CAUSAL ? tp0 : 0;  // tp0 is a multiple of kSub
+    const int i_start = q_start(tile);
+    const int row_lo = CAUSAL ? j_col : packed_nc ? col_lo(j_col) : -(1 << 30);
     const int n_qt = (q_end(tile) - i_start + kSub - 1) / kSub;
     // Rows this wave's key column reaches (see KVWave::step).
     const int row_end = j_col < Nk ? (narrowed ? upper(j_col) : N) : 0;
@@ -511,8 +525,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       // mask; they occur only on the diagonal, so they are not skipped.
       const float alibi_raw =
           BOUNDS && alibi ? alibi[hkv * group + (it / n_qt)] / scale : 0.f;  // step's query head
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_end, alibi_raw, lane,
-             roff, so, scale_log2);
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
+             alibi_raw, lane, roff, so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -600,7 +614,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int iw = t0 + w4 * 32;  // this wave's query rows
     const int i_row = iw + l32;
     const bool row_ok = !BOUNDS || i_row < N;
-    const int kv_end = CAUSAL ? min(Nk, t0 + kTile) : Nk;
+    const int kv_end = CAUSAL ? min(Nk, t0 + kTile) : row_hi(t0 + kTile - 1);
+    const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
     const int n_kt = (kv_end + kSub - 1) / kSub;
     // With a window, key tiles left of every row's window are skipped, and
     // each row masks the keys left of its own.
@@ -645,7 +660,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             else plan_k.part(P ? ta0 : ta1, rk, jn, wave, q >> 1);
           }
         };
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, Nk, key_lo, alibi_raw, lane,
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, lane,
                so, scale_log2, issue);
         wait_vmem();
         __syncthreads();

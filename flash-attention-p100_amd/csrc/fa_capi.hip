@@ -49,7 +49,7 @@ const char* fa_error_string(int err) {
     case FA_ERR_DTYPE: return "unsupported element format";
     case FA_ERR_WINDOW: return "sliding window must be >= 0 and needs causal masking";
     case FA_ERR_SEGMENTS:
-      return "packed sequences need causal masking and both seg_start and seg_end";
+      return "packed sequences need both seg_start and seg_end";
     default: return hipGetErrorString((hipError_t)err);
   }
 }
@@ -64,8 +64,7 @@ static int check_opts(const fa_options& op, int causal) {
   if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
   if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
-  if ((op.seg_start != nullptr) != (op.seg_end != nullptr) || (op.seg_start && !causal))
-    return FA_ERR_SEGMENTS;
+  if ((op.seg_start != nullptr) != (op.seg_end != nullptr)) return FA_ERR_SEGMENTS;
   return FA_OK;
 }
 

@@ -183,8 +183,8 @@ template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int Nk, int W,
-                                         const int* __restrict__ sst, float alibi_raw, int sq,
-                                         int sk,
+                                         const int* __restrict__ sst, const int* __restrict__ sen,
+                                         float alibi_raw, int sq, int sk,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -210,8 +210,15 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   w.l = 0.f;
 
   // Keys [0, Nk) exist for this batch entry (Nk = N unless key lengths are
-  // given); later keys are masked like keys past a ragged N.
-  const int kv_end = CAUSAL ? min(Nk, q0 + kBR) : Nk;
+  // given); later keys are masked like keys past a ragged N. Without causal
+  // masking, packed sequences also end each row's keys at row_hi(i) =
+  // min(Nk, sen[i]) (at least i + 1), which does not decrease with i.
+  const bool packed_nc = BOUNDS && !CAUSAL && sen != nullptr;
+  auto row_hi = [&](int i) {
+    i = min(i, N - 1);
+    return packed_nc ? min(Nk, max(sen[i], i + 1)) : Nk;
+  };
+  const int kv_end = CAUSAL ? min(Nk, q0 + kBR) : row_hi(q0 + kBR - 1);
   const int n_it = (kv_end + kKV - 1) / kKV;
   // Leading steps in which this wave's 32x32 block needs no mask. The later
   // ones run masked; blocks wholly past the diagonal or past N give exact
@@ -239,7 +246,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int w_lo = narrowed ? lower(i_row) - 1 : INT_MIN;
   int n_full = n_it;
   if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
-  if (BOUNDS) n_full = min(n_full, Nk - 32 - kq * 32 >= 0 ? (Nk - 32 - kq * 32) / kKV + 1 : 0);
+  const int k_hi = row_hi(i_base);  // smallest key bound of this wave's rows
+  if (BOUNDS) n_full = min(n_full, k_hi - 32 - kq * 32 >= 0 ? (k_hi - 32 - kq * 32) / kKV + 1 : 0);
+  const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
 
   // Software pipeline over steps j = 0 .. n_it-1. Step j reads K_{j+1} (for
   // the next S^T) from K buffer (j+1)%2 and V_j from V buffer j%2, while it
@@ -286,7 +295,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
-                                Nk, w_lo, alibi_raw, lane,
+                                lane_hi, w_lo, alibi_raw, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -394,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
     Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi,
-    const int* __restrict__ seg_start) {
+    const int* __restrict__ seg_start, const int* __restrict__ seg_end) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -422,7 +431,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
                                 Lse + (size_t)bh * N, N, Nk, window,
-                                seg_start ? seg_start + (size_t)b * N : nullptr, alibi_raw, stq.n,
+                                seg_start ? seg_start + (size_t)b * N : nullptr,
+                                seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, stq.n,
                                 stk.n,
                                 t ? second : first,
                                 scale_log2, thr_raw,
@@ -441,7 +451,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window, a.alibi,
-                     a.seg_start);
+                     a.seg_start, a.seg_end);
   return hipGetLastError();
 }
 

@@ -144,11 +144,11 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         (ALiBi, in the symmetric form that also serves non-causal attention;
         under causal masking j <= i, so it is -slope * (i - j)). The slopes
         are constants: no gradient flows to them;
-      * segment_ids, an integer tensor (B, N) on q's device (causal only):
-        several sequences packed into each batch entry. Each maximal run of
-        equal ids is one sequence, and a token attends to the keys of its own
-        sequence only (causal within it), as if each sequence had been run
-        alone. Also accepted: the (seg_start, seg_end) pair segment_bounds()
+      * segment_ids, an integer tensor (B, N) on q's device: several
+        sequences packed into each batch entry. Each maximal run of equal ids
+        is one sequence, and a token attends to the keys of its own sequence
+        only (causal within it when causal=True), as if each sequence had been
+        run alone. Also accepted: the (seg_start, seg_end) pair segment_bounds()
         makes from such ids, for callers that reuse one packing across calls.
     """
     window = 0
@@ -163,8 +163,6 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         alibi_slopes = alibi_slopes.detach().float().contiguous()
     segs = None
     if segment_ids is not None:
-        if not causal:
-            raise ValueError("segment_ids (packed sequences) needs causal=True")
         pair = isinstance(segment_ids, (tuple, list))
         shape = tuple(segment_ids[0].shape) if pair else tuple(segment_ids.shape)
         if shape != (q.size(0), q.size(2)):

@@ -197,10 +197,6 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
     if segs is _NOT_PACKED or segs is None:
         segs = None
     else:
-        if not is_causal:
-            raise NotImplementedError(
-                "fa_p100 serves packed sequences (restarting position_ids) on causal "
-                "attention only.")
         if tuple(segs[0].shape) != (query.size(0), query.size(2)) \
                 or segs[0].device != query.device:
             raise NotImplementedError(

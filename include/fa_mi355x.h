@@ -45,7 +45,7 @@ enum {
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */
-  FA_ERR_SEGMENTS = 10011    /* packed sequences without causal masking, or only one bound array */
+  FA_ERR_SEGMENTS = 10011    /* packed sequences with only one of the two bound arrays */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -178,11 +178,11 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *   - alibi_slopes: NULL, or a device array of Hq fp32 slopes: the scaled
  *     score of query row i and key j of query head h gets
  *     -alibi_slopes[h] * |i - j| added (the usual ALiBi bias);
- *   - seg_start, seg_end: both NULL, or two device arrays of B * N int32
- *     (causal only): several sequences packed into each batch entry. Token i
- *     of entry b belongs to the sequence of tokens
- *     [seg_start[b*N+i], seg_end[b*N+i]) and attends to keys of that
- *     sequence only (with the causal mask, keys seg_start .. i). The arrays
+ *   - seg_start, seg_end: both NULL, or two device arrays of B * N int32:
+ *     several sequences packed into each batch entry. Token i of entry b
+ *     belongs to the sequence of tokens [seg_start[b*N+i], seg_end[b*N+i])
+ *     and attends to keys of that sequence only (with the causal mask, keys
+ *     seg_start .. i; without it, the whole sequence). The arrays
  *     must describe contiguous sequences that tile [0, N) (so both never
  *     decrease along a row); other contents give undefined attention values
  *     but no access outside the tensors (each bound is clamped to reach at

@@ -72,8 +72,8 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
     (causal only, another extension) key col is also masked for row when
     col <= row - W: each row sees its last W keys. With `alibi` (Hq slopes,
     another extension) query head h adds -alibi[h] * |row - col| to every
-    scaled logit before the masks. With `segments` (B x N ids, causal only,
-    another extension: packed sequences) each maximal run of equal ids is one
+    scaled logit before the masks. With `segments` (B x N ids, another
+    extension: packed sequences) each maximal run of equal ids is one
     sequence and key col is masked for row unless both lie in the same run.
     """
     d = q.shape[-1]
@@ -95,8 +95,6 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
         mask = np.tril(np.ones((n, n), dtype=bool), -int(window))
         s = np.where(mask, -np.inf, s).astype(dtype)
     if segments is not None:
-        if not causal:
-            raise ValueError("packed sequences need causal masking")
         seg = np.asarray(segments).reshape(q.shape[0], n)
         run = np.concatenate([np.zeros((seg.shape[0], 1), dtype=np.int64),
                               np.cumsum(seg[:, 1:] != seg[:, :-1], axis=1)], axis=1)

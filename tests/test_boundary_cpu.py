@@ -66,10 +66,11 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(window=16), s) == 10010
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(window=-1), s) == 10010
     assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, fa_opts(window=4), s) == 10010
-    # packed sequences: causal only, and both bound arrays or neither
-    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(seg_start=1, seg_end=1),
-                         s) == 10011
+    # packed sequences: both bound arrays or neither (causal or not)
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(seg_start=1), s) == 10011
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(seg_start=1), s) == 10011
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, fa_opts(seg_start=1, seg_end=1),
+                         s) == 10005  # both arrays, non-causal: accepted, then the NULL check
     assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 1, fa_opts(seg_end=1), s) == 10011
     assert b"packed" in lib.fa_error_string(10011)
     # BNHD puts every head of a row in one 32-bit buffer range

@@ -26,32 +26,32 @@ def ids_from_lengths(lengths):
     return np.concatenate([np.full(n, i) for i, n in enumerate(lengths)])
 
 
-def run(q, k, v, do, seg, lens=None, window=None):
+def run(q, k, v, do, seg, lens=None, window=None, causal=True):
     import fa_p100
     kv_len = None if lens is None else torch.tensor(lens, dtype=torch.int32, device=DEV)
     sid = torch.tensor(seg, device=DEV)
     qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
-    o = fa_p100.flash_attn(qg, kg, vg, True, kv_len=kv_len, sliding_window=window,
+    o = fa_p100.flash_attn(qg, kg, vg, causal, kv_len=kv_len, sliding_window=window,
                            segment_ids=sid)
     o.backward(do.to(DEV))
     s0, s1 = fa_p100.segment_bounds(sid)
-    _, lse = fa_p100._ext.forward_dt(qg.detach(), kg.detach(), vg.detach(), True, kv_len,
+    _, lse = fa_p100._ext.forward_dt(qg.detach(), kg.detach(), vg.detach(), causal, kv_len,
                                      window or 0, None, s0, s1)
     torch.cuda.synchronize()
     return o, lse, qg.grad, kg.grad, vg.grad
 
 
-def check(got, q, k, v, do, seg, what, lens=None, window=None):
+def check(got, q, k, v, do, seg, what, lens=None, window=None, causal=True):
     o, lse, dq, dk, dv = got
     qn, kn, vn, dn = (t.float().numpy() for t in (q, k, v, do))
-    ref_o, ref_lse = ora.attention_fwd(qn, kn, vn, True, kv_len=lens, window=window,
+    ref_o, ref_lse = ora.attention_fwd(qn, kn, vn, causal, kv_len=lens, window=window,
                                        segments=seg)
     assert ora.max_abs(np64(o), ref_o) <= FWD_MAX_ABS, what
     assert ora.rel_max_rms(np64(o), ref_o) < REF_REL, what
     seen = np.isfinite(ref_lse)
     assert np.array_equal(np.isfinite(np64(lse)), seen), what
     assert ora.max_abs(np64(lse)[seen], ref_lse[seen]) <= LSE_MAX_ABS, what
-    ref = ora.attention_bwd(qn, kn, vn, dn, True, kv_len=lens, window=window, segments=seg)
+    ref = ora.attention_bwd(qn, kn, vn, dn, causal, kv_len=lens, window=window, segments=seg)
     for name, g, r in zip(("dQ", "dK", "dV"), (dq, dk, dv), ref):
         g = np64(g)
         assert np.isfinite(g).all(), (what, name)
@@ -70,13 +70,23 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("B,Hq,Hkv,N,lengths", CASES)
-def test_packed_matches_oracle(D, B, Hq, Hkv, N, lengths):
+def test_packed_matches_oracle(D, B, Hq, Hkv, N, lengths, causal):
     q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=N + D + B)
     seg = np.stack([ids_from_lengths(l) for l in lengths])
-    got = run(q, k, v, do, seg)
-    check(got, q, k, v, do, seg, f"packed {lengths} D{D} {B},{Hq}/{Hkv},N{N}")
+    got = run(q, k, v, do, seg, causal=causal)
+    check(got, q, k, v, do, seg, f"packed {lengths} D{D} {B},{Hq}/{Hkv},N{N} causal={causal}",
+          causal=causal)
+
+
+def test_packed_non_causal_with_key_lengths():
+    B, Hq, Hkv, N, D = 2, 4, 2, 700, 128
+    seg = np.stack([ids_from_lengths([250, 50, 400]), ids_from_lengths([100, 600])])
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=77)
+    check(run(q, k, v, do, seg, lens=[700, 420], causal=False), q, k, v, do, seg,
+          "packed non-causal lens", lens=[700, 420], causal=False)
 
 
 def test_packed_equals_each_sequence_alone():
@@ -159,14 +169,12 @@ def test_packed_bf16_bnhd_and_capi():
                                                    None, s0, s1)
     for a, b in ((o, o_op), (lse, lse_op), (dq, dq_op), (dk, dk_op), (dv, dv_op)):
         assert torch.equal(a, b)
-    with pytest.raises(ValueError, match="causal"):
-        fa_p100.flash_attn(q, k, v, False, segment_ids=sid)
     with pytest.raises(ValueError, match="segment_ids must have shape"):
         fa_p100.flash_attn(q, k, v, True, segment_ids=sid[:, :10])
     with pytest.raises(RuntimeError, match="seg_start must be int32"):
         fa_p100._ext.forward_dt(q, k, v, True, None, 0, None, s0.long(), s1)
-    with pytest.raises(RuntimeError, match="packed sequences need causal"):
-        fa_p100._ext.forward_dt(q, k, v, False, None, 0, None, s0, s1)
+    with pytest.raises(RuntimeError, match="packed sequences need both"):
+        fa_p100._ext.forward_dt(q, k, v, True, None, 0, None, s0, None)
 
 
 def test_hf_hook_packed_batch_matches_eager():

@@ -127,6 +127,8 @@ def test_packed_position_ids_become_segment_bounds():
     assert start.tolist() == [[0, 0, 0, 3, 3, 5, 5, 5, 5]]
     assert end.tolist() == [[3, 3, 3, 5, 5, 9, 9, 9, 9]]
     q, k, v = qkv(n=9)
-    with pytest.raises(NotImplementedError, match="causal attention only"):
+    # A packed non-causal call passes the guards (the host tensors then stop
+    # at the binding's device check).
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         hf.fa_p100_attention_forward(types.SimpleNamespace(is_causal=False), q, k, v, None,
                                      position_ids=pos)

@@ -368,7 +368,8 @@ def test_alibi_with_window_matches_sdpa():
 # ---------------------------------------------------------------------------
 # Packed sequences (an extension): several causal sequences in one row.
 def test_packed_sequence_pins():
-    """Each maximal run of equal segment ids attends within itself only.
+    """Each maximal run of equal segment ids attends within itself only
+    (causal and not).
     Pinned by running every sequence alone through the plain causal oracle
     (outputs, LSE and gradients must match row for row), against torch SDPA
     with the block-diagonal causal mask, one run equal to plain causal, the
@@ -427,5 +428,21 @@ def test_packed_sequence_pins():
             fd = (ora.attention_loss(*plus, do, True, segments=seg)
                   - ora.attention_loss(*minus, do, True, segments=seg)) / (2 * h)
             assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
-    with pytest.raises(ValueError):
-        ora.attention_fwd(q, k, v, False, segments=seg)
+    # Without causal masking: each sequence alone, bidirectional, and SDPA
+    # with the block-diagonal mask.
+    o_nc, lse_nc = ora.attention_fwd(q, k, v, False, segments=seg)
+    g_nc = ora.attention_bwd(q, k, v, do, False, segments=seg)
+    for e, spans in runs.items():
+        for a, z in spans:
+            sl = (slice(e, e + 1), slice(None), slice(a, z))
+            o1, l1 = ora.attention_fwd(q[sl], k[sl], v[sl], False)
+            g1 = ora.attention_bwd(q[sl], k[sl], v[sl], do[sl], False)
+            assert np.allclose(o_nc[sl], o1, atol=1e-12) and np.allclose(lse_nc[sl], l1, atol=1e-12)
+            for got, ref in zip(g_nc, g1):
+                assert np.allclose(got[sl], ref, atol=1e-12)
+        run = np.concatenate([[0], np.cumsum(seg[e, 1:] != seg[e, :-1])])
+        ref = F.scaled_dot_product_attention(
+            torch.tensor(q[e:e + 1]), torch.tensor(np.repeat(k[e:e + 1], hq // hkv, 1)),
+            torch.tensor(np.repeat(v[e:e + 1], hq // hkv, 1)),
+            attn_mask=torch.tensor(run[:, None] == run[None, :]))
+        assert np.allclose(o_nc[e], ref[0].numpy(), atol=1e-12)
