@@ -722,7 +722,7 @@ template <int D, bool CAUSAL, bool BOUNDS, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
-  const float scale = 1.f / sqrtf((float)D);
+  const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)D);
   hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,

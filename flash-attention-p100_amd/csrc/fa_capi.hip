@@ -7,6 +7,8 @@
 // state: every kernel's LDS is static, so launches need no attributes set.
 #include <limits.h>
 
+#include <cmath>
+
 #include "../../include/fa_mi355x.h"
 #include "fa_launch.h"
 
@@ -50,6 +52,7 @@ const char* fa_error_string(int err) {
     case FA_ERR_WINDOW: return "sliding window must be >= 0 and needs causal masking";
     case FA_ERR_SEGMENTS:
       return "packed sequences need both seg_start and seg_end";
+    case FA_ERR_SCALE: return "softmax scale must be 0 (1/sqrt(D)) or positive and finite";
     default: return hipGetErrorString((hipError_t)err);
   }
 }
@@ -58,13 +61,14 @@ const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
 // Options: every field checked; the defaults are fp16, (B, H, N, D), no key
 // lengths, no window, no ALiBi.
-constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0, nullptr, nullptr, nullptr};
+constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0, nullptr, nullptr, nullptr, 0.f};
 
 static int check_opts(const fa_options& op, int causal) {
   if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
   if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
   if ((op.seg_start != nullptr) != (op.seg_end != nullptr)) return FA_ERR_SEGMENTS;
+  if (!(op.scale >= 0.f) || !std::isfinite(op.scale)) return FA_ERR_SCALE;
   return FA_OK;
 }
 
@@ -95,6 +99,7 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.alibi = op.alibi_slopes;
   a.seg_start = op.seg_start;
   a.seg_end = op.seg_end;
+  a.scale = op.scale;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -199,6 +204,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.alibi = op.alibi_slopes;
   a.seg_start = op.seg_start;
   a.seg_end = op.seg_end;
+  a.scale = op.scale;
   return to_code(fa::launch_bwd_main(a));
 }
 

@@ -445,7 +445,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
   const int BH = a.B * a.Hq;
   dim3 grid(xcd_grid(gx * BH));
-  const float scale_log2 = kLog2e / sqrtf((float)D);
+  const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)D));
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,

@@ -42,6 +42,7 @@ struct FwdArgs {
   // sees keys of that sequence only.
   const int* seg_start = nullptr;
   const int* seg_end = nullptr;
+  float scale = 0.f;  // softmax scale of the logits; 0 = 1/sqrt(D)
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -96,6 +97,7 @@ struct BwdArgs {
   const float* alibi = nullptr;  // as FwdArgs::alibi
   const int* seg_start = nullptr;  // as FwdArgs::seg_start
   const int* seg_end = nullptr;    // as FwdArgs::seg_end
+  float scale = 0.f;               // as FwdArgs::scale
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

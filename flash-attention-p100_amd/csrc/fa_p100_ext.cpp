@@ -84,7 +84,8 @@ const int* seg_ptr(const c10::optional<at::Tensor>& seg, const at::Tensor& q, in
 fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Tensor>& kv_len,
                      int64_t window, const c10::optional<at::Tensor>& alibi,
                      const c10::optional<at::Tensor>& seg_start,
-                     const c10::optional<at::Tensor>& seg_end, int B, int H, int N) {
+                     const c10::optional<at::Tensor>& seg_end, double scale, int B, int H,
+                     int N) {
   fa_options op{};
   op.dtype = dtype_code(q);
   op.layout = layout;
@@ -93,6 +94,7 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
   op.alibi_slopes = alibi_ptr(alibi, q, H);
   op.seg_start = seg_ptr(seg_start, q, B, N, "seg_start");
   op.seg_end = seg_ptr(seg_end, q, B, N, "seg_end");
+  op.scale = (float)scale;
   return op;
 }
 
@@ -215,7 +217,8 @@ static void check_bnhd(const at::Tensor& t, const char* name) {
 std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
                                         c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
-    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
+    double scale) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -235,7 +238,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
+  const fa_options op =
+      make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -247,7 +251,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
                                          at::Tensor dO, at::Tensor o, at::Tensor lse,
                                          bool causal, c10::optional<at::Tensor> kv_len,
                                          int64_t window, c10::optional<at::Tensor> alibi_slopes,
-    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
+    double scale) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -271,7 +276,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
+  const fa_options op =
+      make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -289,7 +295,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
 std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
                                       c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
-    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
+    double scale) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -312,7 +319,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
+  const fa_options op =
+      make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -324,7 +332,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
                                        at::Tensor o, at::Tensor lse, bool causal,
                                        c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
-    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end) {
+    c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
+    double scale) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -353,7 +362,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  const fa_options op = make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, B, H, N);
+  const fa_options op =
+      make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -371,22 +381,22 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none());
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none());
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none());
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none());
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
 }

@@ -67,7 +67,7 @@ class _FlashAttnP100(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None,
-                segs=None):
+                segs=None, scale=0.0):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -78,16 +78,18 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.window = window
         ctx.alibi = alibi
         ctx.segs = segs
+        ctx.scale = scale
         seg_start, seg_end = segs if segs is not None else (None, None)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
-                                        seg_end)
+                                        seg_end, scale)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
         if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
-                or segs is not None):
-            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end)
+                or segs is not None or scale):
+            o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end,
+                                     scale)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -100,9 +102,9 @@ class _FlashAttnP100(torch.autograd.Function):
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
-                                            ctx.window, ctx.alibi, seg_start, seg_end)
+                                            ctx.window, ctx.alibi, seg_start, seg_end, ctx.scale)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
-                    None, None, None, None, None, None)
+                    None, None, None, None, None, None, None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
@@ -110,17 +112,17 @@ class _FlashAttnP100(torch.autograd.Function):
         # and backward_dt to bf16 for bf16 inputs.
         g = grad_o.contiguous()
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
-                or ctx.alibi is not None or ctx.segs is not None):
+                or ctx.alibi is not None or ctx.segs is not None or ctx.scale):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
-                                          ctx.alibi, seg_start, seg_end)
+                                          ctx.alibi, seg_start, seg_end, ctx.scale)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
-                None)
+                None, None)
 
 
 def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-               alibi_slopes=None, segment_ids=None):
+               alibi_slopes=None, segment_ids=None, softmax_scale=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -149,7 +151,10 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         is one sequence, and a token attends to the keys of its own sequence
         only (causal within it when causal=True), as if each sequence had been
         run alone. Also accepted: the (seg_start, seg_end) pair segment_bounds()
-        makes from such ids, for callers that reuse one packing across calls.
+        makes from such ids, for callers that reuse one packing across calls;
+      * softmax_scale: a positive float used in place of 1/sqrt(D) (the
+        reference fixes 1/sqrt(D), fa_p100_ext.cu:71); the returned LSE is in
+        units of the scaled logits.
     """
     window = 0
     if sliding_window is not None:
@@ -169,8 +174,13 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
             raise ValueError(f"segment_ids must have shape ({q.size(0)}, {q.size(2)}), got "
                              f"{shape}")
         segs = tuple(segment_ids) if pair else segment_bounds(segment_ids)
+    scale = 0.0
+    if softmax_scale is not None:
+        scale = float(softmax_scale)
+        if not (scale > 0.0 and math.isfinite(scale)):
+            raise ValueError(f"softmax_scale must be positive and finite, got {softmax_scale}")
     return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes,
-                                segs)
+                                segs, scale)
 
 
 def segment_bounds(segment_ids):

@@ -39,8 +39,8 @@ autocast stay bf16); the reference cast everything to fp16.
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): other attention / padding masks,
 output_attentions, head_mask, a window on non-causal attention, dropout,
-head_dim other than 64/128, a scale other than 1/sqrt(D), q_len != kv_len
-(KV-cache decoding).
+head_dim other than 64/128, q_len != kv_len (KV-cache decoding). A scale other
+than 1/sqrt(D), which the reference rejected, goes to the kernels.
 """
 import contextvars
 import warnings
@@ -146,11 +146,11 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
     head_dim = query.size(-1)
     if head_dim not in (64, 128):
         raise NotImplementedError(f"fa_p100 supports head_dim 64 or 128, got {head_dim}.")
-    # The kernels fix scale = 1/sqrt(D); any other request would be mis-scaled.
+    # The reference fixed scale = 1/sqrt(D) and raised on anything else; the
+    # kernels take the model's scale (softmax_scale) when it differs.
+    softmax_scale = None
     if scaling is not None and abs(scaling - head_dim ** -0.5) > 1e-6:
-        raise NotImplementedError(
-            f"fa_p100 fixes the scale at 1/sqrt(D) = {head_dim ** -0.5:.6g}; "
-            f"the model asked for {scaling:.6g}.")
+        softmax_scale = float(scaling)
     if key.size(2) != query.size(2):
         raise NotImplementedError(
             f"fa_p100 needs q_len == kv_len (got q={query.size(2)}, kv={key.size(2)}); "
@@ -212,7 +212,8 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
                 "fa_p100: the padding mask given to the model does not match this "
                 "attention call's batch.")
     out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
-                     kv_len=kv_len, sliding_window=sliding_window, segment_ids=segs)
+                     kv_len=kv_len, sliding_window=sliding_window, segment_ids=segs,
+                     softmax_scale=softmax_scale)
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
 

@@ -45,7 +45,8 @@ enum {
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */
-  FA_ERR_SEGMENTS = 10011    /* packed sequences with only one of the two bound arrays */
+  FA_ERR_SEGMENTS = 10011,   /* packed sequences with only one of the two bound arrays */
+  FA_ERR_SCALE = 10012       /* softmax scale negative or not finite */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -186,7 +187,11 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *     must describe contiguous sequences that tile [0, N) (so both never
  *     decrease along a row); other contents give undefined attention values
  *     but no access outside the tensors (each bound is clamped to reach at
- *     least the token itself).
+ *     least the token itself);
+ *   - scale: 0 (the reference's fixed 1/sqrt(D), fa_p100_ext.cu:71, 117), or
+ *     a positive softmax scale applied to q . k before the masks; dq and dk
+ *     carry it as they carry 1/sqrt(D), and lse is in units of the scaled
+ *     logits.
  */
 typedef struct fa_options {
   int dtype;
@@ -196,6 +201,7 @@ typedef struct fa_options {
   const float* alibi_slopes;
   const int* seg_start;
   const int* seg_end;
+  float scale;
 } fa_options;
 
 /*

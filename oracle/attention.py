@@ -60,7 +60,8 @@ def _group_sum(g, hkv):
     return g.reshape(b, hkv, hq // hkv, n, d).sum(axis=2)
 
 
-def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=None):
+def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=None,
+            scale=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
@@ -77,7 +78,7 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
     sequence and key col is masked for row unless both lie in the same run.
     """
     d = q.shape[-1]
-    scale = 1.0 / math.sqrt(d)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
     s = np.matmul(q.astype(dtype), np.swapaxes(k.astype(dtype), -1, -2)) * dtype(scale)
     n = q.shape[-2]
     if alibi is not None:
@@ -108,7 +109,7 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
 
 
 def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None,
-                  alibi=None, segments=None):
+                  alibi=None, segments=None, scale=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
@@ -120,7 +121,7 @@ def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=N
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments, scale)
     m = s.max(axis=-1, keepdims=True)
     # A row that sees no key at all (only with both key lengths and a window:
     # pad rows more than W past their entry's length) gets O = 0 and
@@ -140,7 +141,7 @@ def bwd_preprocess(o, do, dtype=np.float64):
 
 
 def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
-                  window=None, alibi=None, segments=None):
+                  window=None, alibi=None, segments=None, scale=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -150,28 +151,28 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     q = np.asarray(q)
     hq, hkv = q.shape[1], np.asarray(k).shape[1]
     d = q.shape[-1]
-    scale = dtype(1.0 / math.sqrt(d))
+    sc = dtype(1.0 / math.sqrt(d) if scale is None else scale)
     ke = expand_kv(np.asarray(k), hq).astype(dtype)
     ve = expand_kv(np.asarray(v), hq).astype(dtype)
     qd = q.astype(dtype)
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
-        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments)
-    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments)
+        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale)
+    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments, scale)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     dv = np.matmul(np.swapaxes(p, -1, -2), dod)
     dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
     dvec = bwd_preprocess(o, dod, dtype)
     ds = p * (dp - dvec[..., None])
-    dq = np.matmul(ds, ke) * scale
-    dk = np.matmul(np.swapaxes(ds, -1, -2), qd) * scale
+    dq = np.matmul(ds, ke) * sc
+    dk = np.matmul(np.swapaxes(ds, -1, -2), qd) * sc
     return dq, _group_sum(dk, hkv), _group_sum(dv, hkv)
 
 
 def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None,
-                   alibi=None, segments=None):
+                   alibi=None, segments=None, scale=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

@@ -73,17 +73,17 @@ class FaOptions(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int), ("layout", ctypes.c_int),
                 ("kv_len", ctypes.c_void_p), ("window", ctypes.c_int),
                 ("alibi_slopes", ctypes.c_void_p), ("seg_start", ctypes.c_void_p),
-                ("seg_end", ctypes.c_void_p)]
+                ("seg_end", ctypes.c_void_p), ("scale", ctypes.c_float)]
 
 
 def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_start=None,
-            seg_end=None):
+            seg_end=None, scale=0.0):
     """A pointer to an FaOptions; the array fields are device addresses (ints)
     or tensors."""
     def addr(x):
         return None if x is None else (x if isinstance(x, int) else x.data_ptr())
     o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes), addr(seg_start),
-                  addr(seg_end))
+                  addr(seg_end), scale)
     return ctypes.pointer(o)
 
 

@@ -73,6 +73,11 @@ def test_capi_validation_returns_before_any_launch():
                          s) == 10005  # both arrays, non-causal: accepted, then the NULL check
     assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 1, fa_opts(seg_end=1), s) == 10011
     assert b"packed" in lib.fa_error_string(10011)
+    # softmax scale: 0 (1/sqrt(D)) or positive and finite
+    for bad in (-1.0, float("inf"), float("nan")):
+        assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(scale=bad), s) == 10012
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, fa_opts(scale=0.3), s) == 10005
+    assert b"scale" in lib.fa_error_string(10012)
     # BNHD puts every head of a row in one 32-bit buffer range
     assert lib.fa_fwd_ex(*([one] * 5), 1, 1 << 12, 1, 1 << 14, 128, 0, fa_opts(0, 1), s) == 10007
     assert b"layout" in lib.fa_error_string(10008)
@@ -100,7 +105,7 @@ def test_public_api_surface_matches_reference():
     # The reference's parameters, in order, with its defaults; the extensions
     # (key lengths, sliding window, ALiBi slopes) come after them and default
     # to None, so every reference call binds the same way.
-    extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids"]
+    extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids", "softmax_scale"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False

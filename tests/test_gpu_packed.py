@@ -267,3 +267,4 @@ def test_packed_with_alibi_matches_oracle():
     for name, g, r in zip(("dQ", "dK", "dV"), (qg.grad, kg.grad, vg.grad), ref):
         l2, rr = ora.rel_l2(np64(g), r), ora.rel_max_rms(np64(g), r)
         assert l2 <= GRAD_REL_L2 and rr < REF_REL, (name, l2, rr)
+

@@ -41,7 +41,9 @@ def test_head_dim_scale_and_kv_len_guards():
     with pytest.raises(NotImplementedError, match="head_dim 64 or 128, got 96"):
         hf.fa_p100_attention_forward(MOD, q, k, v, None)
     q, k, v = qkv(d=128)
-    with pytest.raises(NotImplementedError, match="scale"):
+    # Another scale passes the guards now (the host tensors then stop at the
+    # binding's device check); the reference raised here.
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         hf.fa_p100_attention_forward(MOD, q, k, v, None, scaling=0.1)
     q, k, v = qkv(n=1, kv_len=9)
     with pytest.raises(NotImplementedError, match="q_len == kv_len"):

@@ -446,3 +446,39 @@ def test_packed_sequence_pins():
             torch.tensor(np.repeat(v[e:e + 1], hq // hkv, 1)),
             attn_mask=torch.tensor(run[:, None] == run[None, :]))
         assert np.allclose(o_nc[e], ref[0].numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_softmax_scale_pins(causal):
+    """A softmax scale other than 1/sqrt(D) (an extension): against torch SDPA
+    with its own `scale` argument and autograd in float64, the default scale
+    equal to no argument, and finite differences (dq, dk carry the scale)."""
+    rng = np.random.default_rng(5 + causal)
+    b, hq, hkv, n, d, sc = 1, 4, 2, 19, 16, 0.37
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    o, lse = ora.attention_fwd(q, k, v, causal, scale=sc)
+    grads = ora.attention_bwd(q, k, v, do, causal, scale=sc)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    ref = F.scaled_dot_product_attention(tq, tk.repeat_interleave(hq // hkv, 1),
+                                         tv.repeat_interleave(hq // hkv, 1), is_causal=causal,
+                                         scale=sc)
+    ref.backward(torch.tensor(do))
+    assert np.allclose(o, ref.detach().numpy(), atol=1e-12)
+    for got, t in zip(grads, (tq, tk, tv)):
+        assert np.allclose(got, t.grad.numpy(), atol=1e-10)
+    assert np.array_equal(ora.attention_fwd(q, k, v, causal, scale=1 / math.sqrt(d))[0],
+                          ora.attention_fwd(q, k, v, causal)[0])
+    assert not np.allclose(ora.attention_fwd(q, k, v, causal)[0], o, atol=1e-6)
+    h = 1e-4
+    for which, g in enumerate(grads):
+        for _ in range(3):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, causal, scale=sc)
+                  - ora.attention_loss(*minus, do, causal, scale=sc)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
