@@ -20,10 +20,26 @@ same inputs) as `torch_sdpa_gpu`, for comparison.
 FLOPs follow the reference's convention (attention.cu:219, bwd.cu:246):
 fwd = 4*B*Hq*N^2*D, halved for causal; bwd = 2.5x fwd.
 
-cpu_baseline: the float64-pinned oracle's float32 restatement (numpy, the
-"port") timed on the host cores over a bounded sample of the same workload;
-torch's CPU scaled_dot_product_attention fwd+bwd (fp32) on the same sample is
-reported beside it.
+Beside the headline, the metric's D=64 leg (causal B=1 Hq=Hkv=16 N=4096
+D=64, the reference's BENCH.log:268 shape) is timed the same way under "d64".
+
+Before the W warmup steps the step runs untimed for about half a second, so
+that the GPU has left its idle clocks whatever W is (W=5 steps are ~1 ms of
+work); the timed region is exactly K steps either way.
+
+roofline: the dominant kernel (fa_bwd_main) at its algorithmic FLOPs (the
+bwd count above) over its average duration, measured with HIP events on the
+launch stream in a second pass of K steps; the peak is the fp16 dense MFMA
+rate, 2.4 GHz x 256 CUs x 4 SIMDs x 1024 FLOP/clk = 2516.6 TFLOP/s (AMD's
+published 2.5 PFLOP/s). profiles/ holds rocprofv3 kernel-trace summaries of
+this same command, whose bwd_main average agrees with the event time.
+
+cpu_baseline (BASELINE.md's CPU plan): torch's CPU
+scaled_dot_product_attention fwd+bwd in fp32 on the whole headline workload
+(same inputs as the GPU), 2 warmups then the median of 5 timed iterations, on
+the host threads of the GPU box's CPU share; the float64-pinned oracle's
+float32 numpy restatement (the "port") is timed beside it on one
+(batch, head) slice.
 """
 import argparse
 import ctypes
@@ -38,7 +54,9 @@ for _p in (ROOT, PKG):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
-PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA, AMD published (no sparsity)
+# MI355X dense fp16 MFMA rate: 2.4 GHz x 256 CUs x 4 SIMDs x 1024 FLOP/clk
+# (AMD publishes 2.5 PFLOP/s dense, no sparsity).
+PEAK_FP16_TFLOPS = 2.4e9 * 256 * 4 * 1024 / 1e12  # 2516.58
 P100_HEADLINE_TFLOPS = 120.259e9 / 45.485e-3 / 1e12  # 45.485 ms on P100
 
 CONFIGS = {
@@ -48,7 +66,10 @@ CONFIGS = {
                desc="causal MHA fwd+bwd fp16 B=1 Hq=Hkv=8 N=4096 D=128 (headline)"),
     "C4": dict(B=2, Hq=32, Hkv=8, N=3001, D=128, causal=False, s=0.5,
                desc="non-causal GQA fwd+bwd fp16 B=2 Hq=32 Hkv=8 N=3001 D=128"),
+    "D64": dict(B=1, Hq=16, Hkv=16, N=4096, D=64, causal=True, s=1.0,
+                desc="causal MHA fwd+bwd fp16 B=1 Hq=Hkv=16 N=4096 D=64 (the metric's D=64 leg)"),
 }
+SPIN_UP_S = 0.5  # untimed running before the warmup steps (clock ramp)
 
 
 QWEN3_C5 = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072,
@@ -132,7 +153,7 @@ def load_capi():
     return lib
 
 
-def gpu_bench(c, steps, warmup, copy_mib=0):
+def gpu_bench(c, steps, warmup, copy_mib=0, compare=True):
     import torch
     import fa_p100  # noqa: F401  (fails loudly if the binding is not built)
 
@@ -178,6 +199,11 @@ def gpu_bench(c, steps, warmup, copy_mib=0):
         if ev is not None:
             ev[3].record(stream)
 
+    t_spin = time.perf_counter()
+    while time.perf_counter() - t_spin < SPIN_UP_S:
+        for _ in range(10):
+            step()
+        torch.cuda.synchronize()
     for _ in range(warmup):
         step()
     # The timed steps run back to back with nothing else on the stream; a
@@ -199,6 +225,10 @@ def gpu_bench(c, steps, warmup, copy_mib=0):
     pre_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
     main_ms = sum(e[2].elapsed_time(e[3]) for e in evs) / steps
 
+    out = dict(wall_ms=wall_ms, fwd_ms=fwd_ms, pre_ms=pre_ms, main_ms=main_ms,
+               device=torch.cuda.get_device_name(0))
+    if not compare:
+        return out
     # Same step through the public autograd op.
     import fa_p100 as fa
     qa, ka, va = (t.clone().requires_grad_(True) for t in (q, k, v))
@@ -216,8 +246,8 @@ def gpu_bench(c, steps, warmup, copy_mib=0):
         api_step()
     torch.cuda.synchronize()
     api_ms = (time.perf_counter() - t0) * 1e3 / steps
-    return dict(wall_ms=wall_ms, fwd_ms=fwd_ms, pre_ms=pre_ms, main_ms=main_ms, api_ms=api_ms,
-                device=torch.cuda.get_device_name(0), sdpa=gpu_sdpa(c, q, k, v, do, steps, warmup))
+    out.update(api_ms=api_ms, sdpa=gpu_sdpa(c, q, k, v, do, steps, warmup))
+    return out
 
 
 def gpu_sdpa(c, q, k, v, do, steps, warmup):
@@ -253,37 +283,39 @@ def gpu_sdpa(c, q, k, v, do, steps, warmup):
     return out
 
 
-def cpu_baseline(c, budget_s=20.0):
-    """Oracle (numpy fp32) fwd+bwd on host cores over a bounded sample of the workload."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Host threads of this job's CPU share: OMP_NUM_THREADS when the box
+    sets it (16 per GPU on the MI355X pool), else every CPU."""
+    try:
+        return max(1, int(os.environ["OMP_NUM_THREADS"]))
+    except (KeyError, ValueError):
+        return os.cpu_count() or 1
+
+
+def cpu_baseline(c, port_budget_s=10.0):
+    """BASELINE.md's CPU plan: torch's CPU scaled_dot_product_attention
+    fwd+bwd, fp32, on the whole workload (the GPU's inputs, in fp32), 2
+    warmups then the median of 5 timed iterations. The oracle's numpy fp32
+    restatement (the "port") is timed beside it on one (batch, head) slice."""
     import numpy as np
     import torch
     from oracle import attention as ora
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max((x.get("num_threads", 1) for x in threadpool_info()), default=1)
-    except Exception:
-        cores = os.cpu_count() or 1
-    # Sample: one (batch, head) slice of the workload, repeated within the budget.
-    q, k, v, do = make_inputs(dict(c, B=1, Hq=1, Hkv=1), torch)
-    qn, kn, vn, don = (t.float().numpy() for t in (q, k, v, do))
-    one = dict(c, B=1, Hq=1, Hkv=1)
-    f_fwd, f_bwd = flops(one)
 
-    def run():
-        o, lse = ora.attention_fwd(qn, kn, vn, c["causal"], dtype=np.float32)
-        ora.attention_bwd(qn, kn, vn, don, c["causal"], o=o, lse=lse, dtype=np.float32)
-
-    run()
-    reps, t_tot = 0, 0.0
-    while t_tot < budget_s / 2 and reps < 500:
-        t0 = time.perf_counter()
-        run()
-        t_tot += time.perf_counter() - t0
-        reps += 1
-    port = (f_fwd + f_bwd) * reps / t_tot / 1e12
-
-    # torch CPU SDPA fp32 fwd+bwd on the same sample (BASELINE.md's CPU plan).
-    torch.set_num_threads(os.cpu_count() or 1)
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    f_fwd, f_bwd = flops(c)
+    q, k, v, do = make_inputs(c, torch)
     tq, tk, tv = (t.float().requires_grad_(True) for t in (q, k, v))
     tdo = do.float()
 
@@ -293,20 +325,45 @@ def cpu_baseline(c, budget_s=20.0):
         torch.nn.functional.scaled_dot_product_attention(
             tq, tk, tv, is_causal=c["causal"], enable_gqa=c["Hq"] != c["Hkv"]).backward(tdo)
 
-    sdpa()
-    sreps, s_tot = 0, 0.0
-    while s_tot < budget_s / 2 and sreps < 50:
+    for _ in range(2):
+        sdpa()
+    times = []
+    for _ in range(5):
         t0 = time.perf_counter()
         sdpa()
-        s_tot += time.perf_counter() - t0
-        sreps += 1
-    sdpa_tf = (f_fwd + f_bwd) * sreps / s_tot / 1e12
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    value = (f_fwd + f_bwd) / med / 1e12
+
+    # The port on one (batch, head) slice, repeated within a budget.
+    one = dict(c, B=1, Hq=1, Hkv=1)
+    qs, ks, vs, dos = make_inputs(one, torch)
+    qn, kn, vn, don = (t.float().numpy() for t in (qs, ks, vs, dos))
+    p_fwd, p_bwd = flops(one)
+
+    def run():
+        o, lse = ora.attention_fwd(qn, kn, vn, c["causal"], dtype=np.float32)
+        ora.attention_bwd(qn, kn, vn, don, c["causal"], o=o, lse=lse, dtype=np.float32)
+
+    run()
+    reps, t_tot = 0, 0.0
+    while t_tot < port_budget_s and reps < 500:
+        t0 = time.perf_counter()
+        run()
+        t_tot += time.perf_counter() - t0
+        reps += 1
     return {
-        "value": round(port, 4), "unit": "TFLOPS", "cores": int(cores), "kind": "port",
-        "sample": (f"1 of {c['B'] * c['Hq']} (batch, head) slices of {c['desc']}: numpy fp32 "
-                   f"oracle fwd+bwd x{reps} in {t_tot:.1f} s, FLOPs by the same convention"),
-        "torch_sdpa_cpu_fp32": {"value": round(sdpa_tf, 4), "unit": "TFLOPS",
-                                "threads": torch.get_num_threads(), "reps": sreps},
+        "value": round(value, 4), "unit": "TFLOPS", "cores": threads, "kind": "port",
+        "impl": "torch.nn.functional.scaled_dot_product_attention fwd+bwd, fp32, CPU",
+        "cpu_model": cpu_model(),
+        "ms_per_step": round(med * 1e3, 1),
+        "sample": (f"the whole workload ({c['desc']}) in fp32 on the same inputs; 2 warmups, "
+                   f"median of 5 ({', '.join(f'{t * 1e3:.0f}' for t in times)} ms); "
+                   "FLOPs by the same convention"),
+        "oracle_port_numpy_fp32": {
+            "value": round((p_fwd + p_bwd) * reps / t_tot / 1e12, 4),
+            "unit": "TFLOPS", "threads": "numpy's BLAS pool",
+            "sample": f"1 of {c['B'] * c['Hq']} (batch, head) slices, x{reps} in {t_tot:.1f} s"},
     }
 
 
@@ -328,6 +385,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run one device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--no-d64", action="store_true",
+                    help="skip the D=64 leg beside the headline (C3) line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -383,10 +442,27 @@ def main():
         "torch_sdpa_gpu": r["sdpa"],
         "device": r["device"],
         "roofline": {"kernel": "bwd_main (fa_bwd_main)", "bound": "mfma",
-                     "achieved": round(main_tf, 2), "peak": PEAK_FP16_TFLOPS,
+                     "achieved": round(main_tf, 2), "peak": round(PEAK_FP16_TFLOPS, 1),
                      "unit": "TFLOP/s", "frac": round(main_tf / PEAK_FP16_TFLOPS, 4),
-                     "traffic": traffic},
+                     "traffic": traffic,
+                     "time_source": "HIP events on the launch stream, second pass of K steps",
+                     "kernel_ms": round(r["main_ms"], 4),
+                     "algorithmic_gflop": round(f_bwd / 1e9, 3)},
     }
+    if args.config == "C3" and not args.no_d64:
+        d = CONFIGS["D64"]
+        d_fwd, d_bwd = flops(d)
+        rd = gpu_bench(d, args.steps, args.warmup, compare=False)
+        d_val = (d_fwd + d_bwd) / (rd["wall_ms"] * 1e-3) / 1e12
+        out["d64"] = {
+            "workload": f"D64: {d['desc']}", "value": round(d_val, 2), "unit": "TFLOPS",
+            "ms_per_step": round(rd["wall_ms"], 4),
+            "pct_peak": round(100 * d_val / PEAK_FP16_TFLOPS, 2),
+            "fwd_tflops": round(d_fwd / (rd["fwd_ms"] * 1e-3) / 1e12, 2),
+            "bwd_tflops": round(d_bwd / ((rd["pre_ms"] + rd["main_ms"]) * 1e-3) / 1e12, 2),
+            "kernel_ms": {"fwd": round(rd["fwd_ms"], 4), "bwd_preprocess": round(rd["pre_ms"], 4),
+                          "bwd_main": round(rd["main_ms"], 4)},
+            "p100_reference_ms": 29.596}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(c)
     print(json.dumps(out), flush=True)

@@ -384,8 +384,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // Causal sliding window (only in the masked instantiation): row i sees keys
   // (i - Wb, i]; 0 = none.
   const int Wb = BOUNDS ? window : 0;
-  // Packed sequences (causal, masked instantiation only): token i's sequence
-  // is [sst[i], sen[i]). With a window they bound the rows and keys each
+  // Packed sequences (masked instantiation only): token i's sequence is
+  // [sst[i], sen[i]). With a window they bound the rows and keys each
   // token reaches: key j reaches rows [j, upper(j)) and row i keys
   // [lower(i), i]; both bounds never decrease, and are clamped so that every
   // token reaches itself and no index leaves [0, N].
@@ -563,24 +563,38 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const rsrc_t other = make_rsrc(pair_slots + (helping ? 0 : kSlotFloats), kSlotFloats * 4);
       // The owner usually finishes second: if the helper is done, it adds the
       // helper's partial without publishing its own.
+      //
+      // Ordering (HIP/HSA memory model, agent scope, as the two workgroups may
+      // sit on different XCDs): a publisher's threads store their part of the
+      // slot, each issues a release fence, and after the workgroup barrier
+      // one thread bumps the counter with an acquire-release RMW; a consumer
+      // reads the counter with acquire semantics (load or the same RMW), and
+      // after the barrier that shares the value every thread issues an acquire
+      // fence before it reads the other slot. Release fence -> barrier ->
+      // counter and counter -> barrier -> acquire fence is the fence /
+      // barrier / atomic idiom that orders every thread's slot accesses
+      // across the two workgroups.
       finish = false;
       if (!helping) {
-        if (tid == 0) xflag = __hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) xflag = __hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         finish = xflag == 1u;
         __syncthreads();
       }
       if (!finish) {
         if (!half) slot_store<2 * (D / 32)>(mine, w.acc, w4, lane);
-        wait_vmem();  // the partial has reached the device-coherent level
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         __syncthreads();
         if (tid == 0)
-          xflag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          xflag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         __syncthreads();
         finish = xflag == 1u;
       }
       if (finish) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (!half) slot_add<2 * (D / 32)>(other, w.acc, w4, lane);
+        // Both partials are consumed: the counter goes back to zero for the
+        // next call (relaxed: the next call is ordered behind this launch).
         if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
@@ -728,8 +742,9 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots, kSplitNum,
-                     kSplitBias, a.kv_len, a.window, a.alibi, a.seg_start, a.seg_end);
+                     make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots,
+                     a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
+                     a.alibi, a.seg_start, a.seg_end);
   return hipGetLastError();
 }
 
@@ -745,6 +760,16 @@ hipError_t launch_main_d(const BwdArgs& a) {
 }
 
 }  // namespace
+
+unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D) {
+  const unsigned long long rows = (unsigned long long)B * Hq * N;
+  const unsigned long long rows_per_block = 256 / (D / 8);
+  const unsigned long long pre = (rows + rows_per_block - 1) / rows_per_block * 256;
+  const unsigned long long tiles = ((unsigned long long)N + kTile - 1) / kTile;
+  const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hkv;
+  const unsigned long long main = (wgs + kXcds - 1) / kXcds * kXcds * kThreads;
+  return pre > main ? pre : main;
+}
 
 hipError_t launch_bwd_preprocess(const BwdArgs& a) {
   if (a.dtype == kBF16) return a.D == 64 ? launch_pre_d<64, true>(a) : launch_pre_d<128, true>(a);

@@ -20,8 +20,13 @@ int check_shape(int B, int Hq, int Hkv, int N, int D) {
   if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return FA_ERR_HEADS;
   if (B <= 0) return FA_ERR_BATCH;
   // Kernels index rows of one (b, h) slice with 32-bit ints and whole tensors
-  // with 64-bit offsets; grid.y is B*H (limit 65535 on the launch).
-  if ((long long)B * Hq > 65535 || (long long)N * D > INT_MAX) return FA_ERR_TOO_LARGE;
+  // with 64-bit offsets; every launch is a 1-D grid whose work-item count
+  // (workgroups x threads) must fit the dispatch packet's 32-bit field.
+  if ((long long)N * D > INT_MAX) return FA_ERR_TOO_LARGE;
+  constexpr unsigned long long kMaxItems = 0xFFFFFFFFull;
+  if (fa::fwd_launch_items(B, Hq, N, D) > kMaxItems ||
+      fa::bwd_launch_items(B, Hq, Hkv, N, D) > kMaxItems)
+    return FA_ERR_TOO_LARGE;
   return FA_OK;
 }
 

@@ -468,6 +468,13 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
 
 }  // namespace
 
+unsigned long long fwd_launch_items(int B, int Hq, int N, int D) {
+  (void)D;
+  const unsigned long long tiles = ((unsigned long long)N + kBR - 1) / kBR;  // non-causal grid
+  const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hq;
+  return (wgs + kXcds - 1) / kXcds * kXcds * kThreads;
+}
+
 hipError_t launch_fwd(const FwdArgs& a) {
   if (a.dtype == kBF16) return a.D == 64 ? launch_fwd_d<64, true>(a) : launch_fwd_d<128, true>(a);
   return a.D == 64 ? launch_fwd_d<64, false>(a) : launch_fwd_d<128, false>(a);

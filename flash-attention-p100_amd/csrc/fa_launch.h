@@ -37,9 +37,9 @@ struct FwdArgs {
   const int* kv_len = nullptr;  // device, B entries: keys [0, kv_len[b]) exist (else N)
   int window = 0;               // causal sliding window W: row i sees keys (i - W, i]; 0 = none
   const float* alibi = nullptr; // device, Hq slopes: score(i, j) += -slope * |i - j|
-  // Packed sequences (causal only), device (B, N) each: token i of entry b
-  // belongs to the sequence of tokens [seg_start[b][i], seg_end[b][i]) and
-  // sees keys of that sequence only.
+  // Packed sequences, device (B, N) each: token i of entry b belongs to the
+  // sequence of tokens [seg_start[b][i], seg_end[b][i]) and sees keys of that
+  // sequence only (with causal masking, those up to itself).
   const int* seg_start = nullptr;
   const int* seg_end = nullptr;
   float scale = 0.f;  // softmax scale of the logits; 0 = 1/sqrt(D)
@@ -90,7 +90,10 @@ struct BwdArgs {
   int layout = kBHND;  // of q, k, v, dO, o, dq, dk, dv (lse, workspace dense)
   unsigned* counters = nullptr;  // workspace: per key-tile pair (zeroed by the preprocess)
   int n_counters = 0;
-  float* slots = nullptr;        // workspace: partial dK/dV of split key tiles
+  // Workspace: partial dK/dV of split key tiles. Null turns the causal split
+  // off (every key tile's phase 1 stays in its own workgroup), so neither the
+  // slots nor the counters are touched.
+  float* slots = nullptr;
   int dtype = kFP16;             // of q, k, v, dO, o, dk, dv and dq16
   const int* kv_len = nullptr;   // as FwdArgs::kv_len
   int window = 0;                // as FwdArgs::window
@@ -103,5 +106,13 @@ struct BwdArgs {
 hipError_t launch_fwd(const FwdArgs& a);
 hipError_t launch_bwd_preprocess(const BwdArgs& a);
 hipError_t launch_bwd_main(const BwdArgs& a);
+
+// Work-items (workgroups x threads) of the largest launch each pass makes for
+// a shape (either masking). An AMD dispatch packet counts its grid in
+// work-items in 32-bit fields, and the kernels number their work items with
+// int, so a shape is launchable when these fit in 32 bits (checked by the C
+// ABI before any launch).
+unsigned long long fwd_launch_items(int B, int Hq, int N, int D);
+unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D);
 
 }  // namespace fa

@@ -42,7 +42,6 @@ output_attentions, head_mask, a window on non-causal attention, dropout,
 head_dim other than 64/128, q_len != kv_len (KV-cache decoding). A scale other
 than 1/sqrt(D), which the reference rejected, goes to the kernels.
 """
-import contextvars
 import warnings
 
 import torch
@@ -51,14 +50,19 @@ from fa_p100 import flash_attn, segment_bounds
 
 _IMPL_NAME = "fa_p100"
 _warned_cast = False
-# Key lengths (int32 (B,) on the model's device) of the right-padded batch of
-# the model call in progress, set by enable_fa_p100's forward wrapper.
-_kv_len = contextvars.ContextVar("fa_p100_kv_len", default=None)
-# Packed-sequence bounds (seg_start, seg_end) of the model call in progress, or
-# _NOT_PACKED once that call's position_ids were found to hold one sequence per
-# row; unset (None) outside enable_fa_p100's forward wrapper.
+# enable_fa_p100's forward wrapper hands every attention call of a model call
+# the batch's padding and packing as one keyword argument, (kv_len, segs):
+#   kv_len: key lengths, int32 (B,) on the model's device, of a padded batch,
+#           or None;
+#   segs:   packed-sequence bounds (seg_start, seg_end), or _NOT_PACKED once
+#           the call's position_ids were found to hold one sequence per row.
+# transformers passes a model's **kwargs down to each decoder layer and from
+# there to the attention interface, and gradient checkpointing replays a
+# layer with the same kwargs, so a layer recomputed in the backward pass sees
+# the same bounds as its first forward (state kept beside the call, such as a
+# context variable, is gone by then).
+_BOUNDS_KW = "fa_p100_bounds"
 _NOT_PACKED = ()
-_segs = contextvars.ContextVar("fa_p100_segs", default=None)
 
 
 def packed_segment_ids(position_ids, batch):
@@ -188,9 +192,9 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             _warned_cast = True
         query, key, value = query.to(target), key.to(target), value.to(target)
 
-    # Packed sequences: bounds from the model call's position_ids (computed
-    # once per call by enable_fa_p100's wrapper, here when it is absent).
-    segs = _segs.get()
+    # Padding and packing of the model call (enable_fa_p100's wrapper); when
+    # the hook runs without it, packed sequences come from position_ids here.
+    kv_len, segs = kwargs.pop(_BOUNDS_KW, None) or (None, None)
     position_ids = kwargs.get("position_ids")
     if segs is None and position_ids is not None:
         segs = _packed_bounds(position_ids, query.size(0))
@@ -205,7 +209,6 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
 
     # GQA/MQA go to the kernel as they are: no repeat_kv copies.
     full_precision = getattr(module, "_fa_p100_full_precision", False)
-    kv_len = _kv_len.get()
     if kv_len is not None:
         if kv_len.numel() != query.size(0) or kv_len.device != query.device:
             raise NotImplementedError(
@@ -308,13 +311,8 @@ def enable_fa_p100(model, full_precision=False):
                     ref = args[0]
                 batch = ref.size(0) if ref is not None else position_ids.size(0)
                 segs = _packed_bounds(position_ids, batch)
-            token = _kv_len.set(kv_len)
-            token_s = _segs.set(segs)
-            try:
-                return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
-            finally:
-                _segs.reset(token_s)
-                _kv_len.reset(token)
+            kwargs[_BOUNDS_KW] = (kv_len, segs)
+            return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
 
         model.forward = guarded
         model._fa_p100_guarded = True

@@ -17,7 +17,8 @@
  *   - fp16 buffers hold IEEE binary16 (`_Float16` / `__half` / torch.half).
  *   - Query head h reads key/value head h / (Hq/Hkv), which is
  *     `repeat_interleave` over the head axis (fa_p100.py:58-62).
- *   - scale = 1/sqrt(D) is fixed (fa_p100_ext.cu:71, 117).
+ *   - The softmax scale is 1/sqrt(D) (fa_p100_ext.cu:71, 117) unless
+ *     fa_options.scale gives another (the fa_fwd_ex / fa_bwd_ex pair).
  *   - `stream` is a hipStream_t (NULL = the null stream). Every launch is
  *     asynchronous on it; the call returns after enqueueing.
  *   - Return value: FA_OK (0), an FA_ERR_* validation code (nothing was
@@ -41,7 +42,7 @@ enum {
   FA_ERR_BATCH = 10004,      /* B <= 0 */
   FA_ERR_NULL = 10005,       /* a required pointer is NULL */
   FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
-  FA_ERR_TOO_LARGE = 10007,  /* an index would overflow the kernels' 32-bit row counters */
+  FA_ERR_TOO_LARGE = 10007,  /* N*D, or a launch's work-item count, exceeds 32 bits */
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */

@@ -116,3 +116,54 @@ def test_public_api_surface_matches_reference():
     for name in ("fa_p100_attention_forward", "register", "enable_fa_p100", "_set_impl"):
         assert hasattr(fa_p100_hf, name)
     assert callable(fa_p100._ext.forward) and callable(fa_p100._ext.backward)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("B,Hq,Hkv,N,D", [(2, 4, 4, 37, 64), (1, 8, 2, 64, 128),
+                                           (2, 4, 1, 19, 64)])
+def test_reference_helper_matches_the_oracle(B, Hq, Hkv, N, D, causal, dtype):
+    """fa_p100.reference (fa_p100.py:58-75's plain-torch attention, re-shipped
+    for users' own checks) against the float64 oracle, itself pinned against
+    torch SDPA, finite differences and closed forms in test_oracle.py: MHA,
+    GQA and MQA, causal and dense, fp32 and fp16 inputs. The result is
+    rounded to the input dtype, so the bar is that dtype's rounding of
+    |O| <= max|V| plus the fp32 arithmetic; a wrong head map (tile instead of
+    repeat_interleave) or a flipped causal mask is caught too."""
+    import numpy as np
+
+    import fa_p100
+    from oracle import attention as ora
+    g = torch.Generator().manual_seed(B * 1000 + Hq * 100 + N)
+    q, k, v = (torch.randn(B, h, N, D, generator=g).to(dtype) for h in (Hq, Hkv, Hkv))
+    got = fa_p100.reference(q, k, v, causal)
+    assert got.dtype == dtype and got.shape == q.shape
+    f64 = lambda t: t.double().numpy()
+    ref, _ = ora.attention_fwd(f64(q), f64(k), f64(v), causal)
+    tol = 2e-3 if dtype == torch.float16 else 2e-5
+    assert ora.max_abs(f64(got), ref) <= tol
+    # Planted mistakes the bar must see: the wrong GQA head map, and the
+    # mask flipped to the other triangle.
+    if Hq != Hkv and Hkv > 1:
+        tiled = lambda t: t.repeat(1, Hq // Hkv, 1, 1)
+        wrong, _ = ora.attention_fwd(f64(q), f64(tiled(k)), f64(tiled(v)), causal)
+        assert ora.max_abs(f64(got), wrong) > 10 * tol
+    if causal:
+        flip = lambda t: t.flip(2)
+        wrong, _ = ora.attention_fwd(f64(flip(q)), f64(flip(k)), f64(flip(v)), True)
+        assert ora.max_abs(f64(got), np.flip(wrong, 2)) > 10 * tol
+
+
+def test_shape_limits_follow_the_one_dimensional_grids():
+    """Every launch is a 1-D grid, so B*Hq is not bounded by a 65535 grid.y
+    any more: B*Hq = 65536 (and well beyond) passes validation. What is
+    bounded is each launch's work-item count (workgroups x threads), which
+    the dispatch packet holds in 32 bits, and N*D (32-bit row offsets);
+    fa_bwd_workspace_bytes returns 0 exactly for a shape validation rejects."""
+    lib = load_capi()
+    for B, Hq, Hkv, N, D in [(1, 65536, 65536, 64, 64), (2, 32768, 8, 128, 128),
+                             (65536, 1, 1, 1, 64), (1, 1, 1, 1 << 20, 128)]:
+        assert lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D) > 0, (B, Hq, Hkv, N, D)
+    # 2^23 query heads of 4096 rows need more than 2^32 forward work-items.
+    assert lib.fa_bwd_workspace_bytes(1 << 13, 1 << 10, 1 << 10, 4096, 128) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 1, 1, (1 << 31) // 64, 128) == 0  # N*D > 2^31-1

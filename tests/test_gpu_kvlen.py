@@ -203,3 +203,47 @@ def test_hf_hook_left_and_both_sided_padding_match_eager_with_mask():
         rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
         env_g = ((grads["sdpa"][n] - g).norm() / g.norm()).item()
         assert rel <= max(5e-2, 2 * env_g), (n, rel, env_g)
+
+
+@pytest.mark.parametrize("padding", ["right", "left"])
+def test_hf_hook_padding_under_gradient_checkpointing_matches_eager(padding):
+    """Gradient checkpointing re-runs each decoder layer inside backward, after
+    the model call has returned; the hook must then see the batch's padding
+    again (key lengths for right padding, packed-sequence bounds for left
+    padding), or the recomputed layers attend to pad keys and the gradients
+    belong to another forward than the loss. Loss and attention-weight
+    gradients of a checkpointed training step through the hook against eager
+    with the same mask (also checkpointed)."""
+    import fa_p100_hf
+    from test_gpu_hf import qwen3
+    N = 256
+    spans = [(0, 256), (0, 131), (40, 256), (9, 200)] if padding == "left" else \
+        [(0, 256), (0, 131), (0, 17), (0, 200)]
+    idx = torch.arange(N, device=DEV)[None, :]
+    first = torch.tensor([a for a, _ in spans], device=DEV)[:, None]
+    end = torch.tensor([z for _, z in spans], device=DEV)[:, None]
+    mask = ((idx >= first) & (idx < end)).long()
+    ids = torch.randint(0, 1000, (len(spans), N), device=DEV,
+                        generator=torch.Generator(DEV).manual_seed(21))
+    labels = ids.masked_fill(mask == 0, -100)
+    labels[torch.arange(len(spans), device=DEV), first[:, 0]] = -100  # see the left-padding test
+    losses, grads = {}, {}
+    for impl in ("eager", "sdpa", "fa_p100"):
+        m = qwen3(2, 256, 4, 2, 64, 512, 1000, seed=5)
+        if impl == "fa_p100":
+            fa_p100_hf.enable_fa_p100(m)
+        else:
+            m.config._attn_implementation = impl
+        m.gradient_checkpointing_enable()
+        m.train()
+        with torch.autocast("cuda", torch.float16):
+            out = m(ids, attention_mask=mask, labels=labels)
+        out.loss.backward()
+        losses[impl] = out.loss.item()
+        grads[impl] = {n: p.grad.float().clone() for n, p in m.named_parameters()
+                       if "self_attn" in n and p.grad is not None}
+    assert abs(losses["fa_p100"] - losses["eager"]) <= 1e-3 * abs(losses["eager"])
+    for n, g in grads["eager"].items():
+        rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
+        env_g = ((grads["sdpa"][n] - g).norm() / g.norm()).item()
+        assert rel <= max(5e-2, 2 * env_g), (n, rel, env_g)

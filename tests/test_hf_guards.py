@@ -134,3 +134,47 @@ def test_packed_position_ids_become_segment_bounds():
     with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         hf.fa_p100_attention_forward(types.SimpleNamespace(is_causal=False), q, k, v, None,
                                      position_ids=pos)
+
+
+def test_checkpointed_layers_see_the_padding_in_their_recompute(monkeypatch):
+    """With gradient checkpointing every decoder layer runs its forward a
+    second time inside backward, after the model call has returned. The
+    padding (key lengths) and packing (sequence bounds) that enable_fa_p100's
+    wrapper derived from the mask must reach that recompute too: the bounds
+    ride on the model call's kwargs, which checkpointing replays. A spy
+    stands in for the kernel call (CPU) and records what each call got."""
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    seen = []
+
+    def spy(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
+            segment_ids=None, softmax_scale=None):
+        seen.append((torch.is_grad_enabled(),
+                     None if kv_len is None else kv_len.tolist(),
+                     None if segment_ids is None else segment_ids[0].tolist()))
+        g = q.size(1) // k.size(1)
+        return torch.nn.functional.scaled_dot_product_attention(
+            q.float(), k.float().repeat_interleave(g, 1), v.float().repeat_interleave(g, 1),
+            is_causal=causal).to(q.dtype)
+
+    monkeypatch.setattr(hf, "flash_attn", spy)
+    cfg = Qwen3Config(vocab_size=64, hidden_size=64, intermediate_size=64, num_hidden_layers=2,
+                      num_attention_heads=2, num_key_value_heads=1, head_dim=64,
+                      use_cache=False)
+    torch.manual_seed(0)
+    model = Qwen3ForCausalLM(cfg)
+    hf.enable_fa_p100(model)
+    model.gradient_checkpointing_enable()
+    model.train()
+    ids = torch.randint(0, 64, (2, 6))
+    for mask, kv_len, seg_start in (
+            (torch.tensor([[1, 1, 1, 1, 0, 0], [1, 1, 1, 1, 1, 1]]), [4, 6], None),  # right
+            (torch.tensor([[0, 0, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1]]), [6, 6],         # left
+             [[0, 0, 2, 2, 2, 2], [0, 0, 0, 0, 0, 0]])):
+        seen.clear()
+        loss = model(ids, attention_mask=mask, labels=ids).loss
+        first = list(seen)
+        loss.backward()
+        recompute = seen[len(first):]
+        assert len(first) == len(recompute) == 2  # one call per layer, each replayed
+        for _, kl, ss in first + recompute:
+            assert kl == kv_len and ss == seg_start
