@@ -8,6 +8,7 @@
 #include <limits.h>
 
 #include <cmath>
+#include <mutex>
 
 #include "../../include/fa_mi355x.h"
 #include "fa_launch.h"
@@ -38,6 +39,39 @@ int check_bnhd(int Hq, int N, int D) {
 
 int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }
 
+// ---------------------------------------------------------------------------
+// Built-in scratch for fa_bwd_noalloc: the backward's two per-row vectors
+// (dvec = rowsum(dO * o) and lse * log2(e)) live in this file-scope device
+// array instead of a caller-allocated workspace. Every GPU the library runs on
+// holds its own copy until the process ends. In host code `scratch` names a
+// host-side stand-in, not a device address, so host code never passes it to a
+// kernel: the device address comes from hipGetSymbolAddress, taken once per
+// device (with that device current) on the entry point's first call there.
+constexpr size_t kScratchBytes = (size_t)FA_BWD_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+hipError_t g_scratch_err[kMaxDevices];
+float* g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's scratch, or an error code.
+int scratch_of_current_device(float** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? static_cast<float*>(p) : nullptr;
+  });
+  if (g_scratch_err[dev] != hipSuccess) return (int)g_scratch_err[dev];
+  if (g_scratch_ptr[dev] == nullptr) return (int)hipErrorInvalidSymbol;
+  *out = g_scratch_ptr[dev];
+  return FA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -58,6 +92,9 @@ const char* fa_error_string(int err) {
     case FA_ERR_SEGMENTS:
       return "packed sequences need both seg_start and seg_end";
     case FA_ERR_SCALE: return "softmax scale must be 0 (1/sqrt(D)) or positive and finite";
+    case FA_ERR_SCRATCH:
+      return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
+             "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
     default: return hipGetErrorString((hipError_t)err);
   }
 }
@@ -275,6 +312,48 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const vo
   if (e != FA_OK) return e;
   return fa_bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, dk, dv, B, Hq, Hkv, N, D,
                      causal, stream);
+}
+
+int fa_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO, const void* o,
+                   const float* lse, float* dq, void* dk, void* dv, int B, int Hq, int Hkv, int N,
+                   int D, int causal, void* stream) {
+  int rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc != FA_OK) return rc;
+  // Two (B, Hq, N) fp32 vectors, each 256-byte aligned, must fit.
+  const size_t vec = fa::align256((size_t)B * Hq * N * sizeof(float));
+  if (2 * vec > kScratchBytes) return FA_ERR_SCRATCH;
+  if (!q || !k || !v || !dO || !o || !lse || !dq || !dk || !dv) return FA_ERR_NULL;
+  float* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc != FA_OK) return rc;
+  fa::BwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.dO = dO;
+  a.o = o;
+  a.lse = lse;
+  // Both vectors are written in full by the preprocess before the main kernel
+  // reads them, so nothing in the scratch needs clearing between calls. No
+  // counters or slots: the main kernel runs without the causal split.
+  a.dvec = ws;
+  a.lse2 = ws + vec / sizeof(float);
+  a.counters = nullptr;
+  a.n_counters = 0;
+  a.slots = nullptr;
+  a.dq = dq;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.N = N;
+  a.D = D;
+  a.causal = causal != 0;
+  a.stream = stream;
+  a.dk = dk;
+  a.dv = dv;
+  rc = to_code(fa::launch_bwd_preprocess(a));
+  if (rc != FA_OK) return rc;
+  return to_code(fa::launch_bwd_main(a));
 }
 
 }  // extern "C"

@@ -47,7 +47,8 @@ enum {
   FA_ERR_DTYPE = 10009,      /* element format not supported */
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */
   FA_ERR_SEGMENTS = 10011,   /* packed sequences with only one of the two bound arrays */
-  FA_ERR_SCALE = 10012       /* softmax scale negative or not finite */
+  FA_ERR_SCALE = 10012,      /* softmax scale negative or not finite */
+  FA_ERR_SCRATCH = 10013     /* fa_bwd_noalloc: the shape needs more than its scratch */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -221,6 +222,26 @@ int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const
               const float* lse, void* dq, void* dk, void* dv, void* workspace,
               size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
               const fa_options* opts, void* stream);
+
+/*
+ * fa_bwd without a workspace argument and without any allocation. No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory at the call (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The backward's two per-row vectors live in
+ * a built-in device array of FA_BWD_NOALLOC_SCRATCH_BYTES per GPU (held until
+ * the process ends), so the shape must satisfy 2 * align256(B*Hq*N*4) <=
+ * FA_BWD_NOALLOC_SCRATCH_BYTES (B*Hq*N <= 2^21 rows), else FA_ERR_SCRATCH and
+ * nothing is launched. The causal load balancing that needs workspace slots is
+ * off, so dk and dv may differ from fa_bwd's in the last bits (dq is the same);
+ * results are deterministic. `stream` must belong to the current device.
+ * Every call on a GPU shares that GPU's scratch: calls that overlap in time
+ * on one GPU (other streams, other host threads) race and give wrong results;
+ * calls ordered on one stream are fine.
+ */
+#define FA_BWD_NOALLOC_SCRATCH_BYTES (16u << 20)
+int fa_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO,
+                   const void* o, const float* lse, float* dq, void* dk, void* dv,
+                   int B, int Hq, int Hkv, int N, int D, int causal, void* stream);
 
 #ifdef __cplusplus
 }  /* extern "C" */

@@ -65,6 +65,9 @@ def load_capi():
     lib.fa_fwd_ex.restype = i
     lib.fa_bwd_ex.argtypes = [vp] * 10 + [sz] + [i] * 6 + [opts, vp]
     lib.fa_bwd_ex.restype = i
+    if hasattr(lib, "fa_bwd_noalloc"):
+        lib.fa_bwd_noalloc.argtypes = [vp] * 9 + [i] * 6 + [vp]
+        lib.fa_bwd_noalloc.restype = i
     return lib
 
 
