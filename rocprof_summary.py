@@ -3,12 +3,14 @@
     python rocprof_summary.py --workload C3 --trace T --fetch F --write W [--sq S ...]
 
 T is the output directory of
-    rocprofv3 --kernel-trace --stats -d T -o trace --output-format csv -- python3 bench.py --no-cpu
+    rocprofv3 --kernel-trace --stats -d T -o trace --output-format csv -- \
+        python3 bench.py --no-cpu --no-d64
 F and W are the output directories of the two counter runs
     rocprofv3 --pmc FETCH_SIZE -d F -o fetch --output-format csv -- \
-        python3 bench.py --no-cpu --steps 3 --warmup 1 --copy-calibration 256
+        python3 bench.py --no-cpu --no-d64 --steps 3 --warmup 1 --copy-calibration 256
     rocprofv3 --pmc WRITE_SIZE -d W -o write --output-format csv -- (same bench command)
-and each optional S a counter run with up to 8 SQ counters.
+and each optional S a counter run with up to 8 SQ counters (the two sets the
+summaries list). --no-d64 keeps the traces to the headline shape's kernels.
 
 FETCH_SIZE / WRITE_SIZE are reported in KiB per dispatch. The 256 MiB device
 copy that --copy-calibration runs first must read and write 256 MiB; the ratio
@@ -97,8 +99,15 @@ def main():
                 sq[k][n] = sum(vals) / len(vals)
 
     os.makedirs(a.out, exist_ok=True)
-    cmd_bench = "python3 bench.py --no-cpu"
-    cmd_cnt = "python3 bench.py --no-cpu --steps 3 --warmup 1 --copy-calibration %d" % a.copy_mib
+    cmd_bench = "python3 bench.py --no-cpu --no-d64"
+    cmd_cnt = ("python3 bench.py --no-cpu --no-d64 --steps 3 --warmup 1 --copy-calibration %d"
+               % a.copy_mib)
+    cmd_sq = "python3 bench.py --no-cpu --no-d64 --steps 3 --warmup 1"
+    sq_sets = [
+        "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS "
+        "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
+        "SQ_ACTIVE_INST_LDS SQ_ACTIVE_INST_VALU SQ_INSTS_VALU_TRANS_F32 SQ_LDS_BANK_CONFLICT "
+        "SQ_WAIT_INST_LDS"]
     for k in ("fwd", "bwd_main", "bwd_preprocess"):
         if k not in stats:
             continue
@@ -117,6 +126,8 @@ def main():
             f"    rocprofv3 --kernel-trace --stats -d OUT/trace -o trace --output-format csv -- {cmd_bench}",
             f"    rocprofv3 --pmc FETCH_SIZE -d OUT/fetch -o fetch --output-format csv -- {cmd_cnt}",
             f"    rocprofv3 --pmc WRITE_SIZE -d OUT/write -o write --output-format csv -- {cmd_cnt}",
+            *[f"    rocprofv3 --pmc {sq_sets[i]} -d OUT/sq{i} -o sq{i} --output-format csv -- {cmd_sq}"
+              for i in range(min(len(a.sq or []), len(sq_sets)))],
             f"    python rocprof_summary.py --workload {a.workload} --trace OUT/trace "
             "--fetch OUT/fetch --write OUT/write" + (" --sq " + " ".join(f"OUT/sq{i}" for i in range(len(a.sq))) if a.sq else ""),
             "",
