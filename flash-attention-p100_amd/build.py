@@ -24,7 +24,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 LIB_NAME = "libfa_mi355x.so"
 EXT_NAME = "fa_p100_ext"
-KERNEL_SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_capi.hip"]
+KERNEL_SOURCES = ["fa_fwd.hip", "fa_bwd.hip", "fa_mask.hip", "fa_capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC",

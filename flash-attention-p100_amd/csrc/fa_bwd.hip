@@ -207,10 +207,12 @@ struct KVWave {
 
   // Query rows i0 + 32m .. +31 (m = this wave's half of the staged tile)
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
+  // mtw: the mask bits of key j_col for this step's 32 query rows i0 + 32m ..
+  // (bit = row offset; all set without a mask).
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int row_lo, int row_end,
-                                       float alibi_raw, int lane, int roff,
+                                       float alibi_raw, uint32_t mtw, int lane, int roff,
                                        const typename Swz<D>::Offsets& so, float c) {
     using S = Swz<D>;
     const int h = lane >> 5;
@@ -256,7 +258,7 @@ struct KVWave {
         const int r = 4 * g4 + e, idx = 8 * g4 + e;
         float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
         if (CAUSAL || BOUNDS) p = (idx >= lo) ? p : 0.f;
-        if (BOUNDS) p = (idx < hi) ? p : 0.f;
+        if (BOUNDS) p = (idx < hi && ((mtw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
         pb[r >> 3][r & 7] = to16<BF>(p);
         sb[r >> 3][r & 7] = to16<BF>(p * (pacc[r] - d4[e]));
       }
@@ -280,9 +282,11 @@ struct QWave {
   float lse2, dvv;
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
+  // mw: row i_row's mask bits for keys j0 + 32s .. (all set without a mask).
   template <class Issue>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
-                                       int i_row, int Nk, int key_lo, float alibi_raw, int lane,
+                                       int i_row, int Nk, int key_lo, float alibi_raw,
+                                       uint32_t mw, int lane,
                                        const typename Swz<D>::Offsets& so, float c,
                                        const Issue& issue) {
     using S = Swz<D>;
@@ -323,7 +327,7 @@ struct QWave {
       const int idx = 8 * (r >> 2) + (r & 3);
       float p = fast_exp2(fmaf(st[r], c, -lse2));
       if (CAUSAL) p = (idx <= lo) ? p : 0.f;
-      if (BOUNDS) p = (idx < hi && idx >= lw) ? p : 0.f;
+      if (BOUNDS) p = (idx < hi && idx >= lw && ((mw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
       sb[r >> 3][r & 7] = to16<BF>(p * (pt[r] - dvv));
     }
     // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15 (operands one ahead).
@@ -341,7 +345,9 @@ struct QWave {
 };
 
 // ---------------------------------------------------------------------------
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+// BITMASK: the arbitrary-mask instantiation (with BOUNDS); its bit tests stay out
+// of the others, whose D = 128 copies have no registers to spare.
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
@@ -352,7 +358,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     Strides stq, Strides stk, unsigned* __restrict__ counters, float* __restrict__ slots,
     int split_num, int split_bias, const int* __restrict__ kv_len, int window,
     const float* __restrict__ alibi, const int* __restrict__ seg_start,
-    const int* __restrict__ seg_end) {
+    const int* __restrict__ seg_end, const uint32_t* __restrict__ mask,
+    const uint32_t* __restrict__ mask_t, int mask_heads) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -420,6 +427,13 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
   // Offset of query head hq's row 0 in Q, dO, dQ.
   auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
+  // Arbitrary mask (BITMASK instantiation): query head hq's bit plane,
+  // rows of W32 words, row-major (phase 2: row = query) or transposed (phase
+  // 1: row = key). Word indices are clamped (bits past N are masked anyway).
+  const int W32 = (N + 31) >> 5;
+  auto plane = [&](const uint32_t* m, int hq) {
+    return m + ((size_t)b * mask_heads + (mask_heads == 1 ? 0 : hq)) * N * W32;
+  };
   const int roff = row_lane_off<D>(lane);  // resident tiles (padded rows)
   typename Swz<D>::Offsets so;             // staged tiles (swizzled rows), rows 32*half ..
   so.init(lane, 32 * half);
@@ -525,8 +539,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       // mask; they occur only on the diagonal, so they are not skipped.
       const float alibi_raw =
           BOUNDS && alibi ? alibi[hkv * group + (it / n_qt)] / scale : 0.f;  // step's query head
+      // Key j_col's mask word for the step's query rows (clamped: rows past N
+      // are masked by row_end, keys past N have row_end = 0).
+      const uint32_t mtw =
+          BITMASK ? plane(mask_t, hkv * group + it / n_qt)[(size_t)min(j_col, N - 1) * W32 +
+                                                            min((i0 + 32 * half) >> 5, W32 - 1)]
+                   : ~0u;
       w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
-             alibi_raw, lane, roff, so, scale_log2);
+             alibi_raw, mtw, lane, roff, so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -645,6 +665,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const float alibi_raw = BOUNDS && alibi ? alibi[hq] / scale : 0.f;
       const half_t* Qg = Q + q_off(hq);
       const half_t* dOg = dO + q_off(hq);
+      // This lane's row of the mask (rows past N are never stored).
+      const uint32_t* mrow = BITMASK ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
       QWave<D, CAUSAL, BOUNDS, BF> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
@@ -677,8 +699,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             else plan_k.part(P ? ta0 : ta1, rk, jn, wave, q >> 1);
           }
         };
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, lane,
-               so, scale_log2, issue);
+        const uint32_t mw =
+            BITMASK ? mrow[min(t * (kSub / 32) + half, W32 - 1)] : ~0u;  // keys t*kSub + 32*half ..
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, mw,
+               lane, so, scale_log2, issue);
         wait_vmem();
         __syncthreads();
       };
@@ -735,31 +759,36 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
   const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)D);
-  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots,
                      a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
-                     a.alibi, a.seg_start, a.seg_end);
+                     a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
-  // Key lengths, windows, packed sequences and ALiBi need the masked
+  // Key lengths, windows, packed sequences, ALiBi and masks need the masked
   // instantiation (kTile is a multiple of kSub).
   const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
+  if (a.mask)
+    return a.causal ? launch_main_t<D, true, true, true, BF>(a)
+                    : launch_main_t<D, false, true, true, BF>(a);
   if (a.causal)
-    return bounds ? launch_main_t<D, true, true, BF>(a) : launch_main_t<D, true, false, BF>(a);
-  return bounds ? launch_main_t<D, false, true, BF>(a) : launch_main_t<D, false, false, BF>(a);
+    return bounds ? launch_main_t<D, true, true, false, BF>(a)
+                  : launch_main_t<D, true, false, false, BF>(a);
+  return bounds ? launch_main_t<D, false, true, false, BF>(a)
+                : launch_main_t<D, false, false, false, BF>(a);
 }
 
 }  // namespace

@@ -92,6 +92,8 @@ const char* fa_error_string(int err) {
     case FA_ERR_SEGMENTS:
       return "packed sequences need both seg_start and seg_end";
     case FA_ERR_SCALE: return "softmax scale must be 0 (1/sqrt(D)) or positive and finite";
+    case FA_ERR_MASK:
+      return "mask_heads must be 1 or Hq, and the backward needs mask_t with mask";
     case FA_ERR_SCRATCH:
       return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
              "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
@@ -102,21 +104,27 @@ const char* fa_error_string(int err) {
 const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 
 // Options: every field checked; the defaults are fp16, (B, H, N, D), no key
-// lengths, no window, no ALiBi.
-constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0, nullptr, nullptr, nullptr, 0.f};
+// lengths, no window, no ALiBi, no packed sequences, no mask.
+constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0,       nullptr,
+                                     nullptr,   nullptr,   0.f,     nullptr, nullptr, 0};
 
-static int check_opts(const fa_options& op, int causal) {
+// `backward`: the pass reads mask_t too.
+static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
   if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
   if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
   if ((op.seg_start != nullptr) != (op.seg_end != nullptr)) return FA_ERR_SEGMENTS;
   if (!(op.scale >= 0.f) || !std::isfinite(op.scale)) return FA_ERR_SCALE;
+  if (op.mask != nullptr) {
+    if (op.mask_heads != 1 && op.mask_heads != Hq) return FA_ERR_MASK;
+    if (backward && op.mask_t == nullptr) return FA_ERR_MASK;
+  }
   return FA_OK;
 }
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
                int Hkv, int N, int D, int causal, const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal);
+  int rc = check_opts(op, causal, Hq, false);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -142,6 +150,8 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.seg_start = op.seg_start;
   a.seg_end = op.seg_end;
   a.scale = op.scale;
+  a.mask = op.mask;
+  a.mask_heads = op.mask_heads;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -210,7 +220,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
                     const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal);
+  int rc = check_opts(op, causal, Hq, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -247,6 +257,9 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.seg_start = op.seg_start;
   a.seg_end = op.seg_end;
   a.scale = op.scale;
+  a.mask = op.mask;
+  a.mask_t = op.mask_t;
+  a.mask_heads = op.mask_heads;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -255,7 +268,7 @@ static int bwd_16(const void* q, const void* k, const void* v, const void* dO, c
                   const float* lse, void* dq, void* dk, void* dv, void* workspace,
                   size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                   const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal);
+  int rc = check_opts(op, causal, Hq, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!workspace || !dq) return FA_ERR_NULL;
@@ -312,6 +325,14 @@ int fa_bwd(const void* q, const void* k, const void* v, const void* dO, const vo
   if (e != FA_OK) return e;
   return fa_bwd_main(q, k, v, dO, workspace, workspace_bytes, dq, dk, dv, B, Hq, Hkv, N, D,
                      causal, stream);
+}
+
+int fa_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* bits_t,
+                 void* stream) {
+  if (N <= 0) return FA_ERR_SEQLEN;
+  if (P <= 0) return FA_ERR_BATCH;
+  if (!dense || !bits) return FA_ERR_NULL;
+  return to_code(fa::launch_pack_mask(dense, P, N, bits, bits_t, stream));
 }
 
 int fa_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO, const void* o,

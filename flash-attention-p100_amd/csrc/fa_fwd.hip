@@ -103,7 +103,7 @@ struct FwdWave {
   template <bool MASK, bool NEXT, class Issue>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
                                        bool masked, int i_row, int N, int w_lo, float alibi_raw,
-                                       int lane, int roff,
+                                       uint32_t mw, int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
@@ -127,9 +127,12 @@ struct FwdWave {
     if (MASK && masked) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int j = j0 + 8 * (r >> 2) + 4 * h + (r & 3);
-        // w_lo: the last key left of this row's sliding window (INT_MIN if none)
-        if ((CAUSAL && j > i_row) || (BOUNDS && (j >= N || j <= w_lo))) s[r] = -INFINITY;
+        const int jj = 8 * (r >> 2) + 4 * h + (r & 3);
+        const int j = j0 + jj;
+        // w_lo: the last key left of this row's sliding window (INT_MIN if none);
+        // mw: this row's mask bits for keys j0 .. j0+31 (all set without a mask)
+        if ((CAUSAL && j > i_row) || (BOUNDS && (j >= N || j <= w_lo || !((mw >> jj) & 1u))))
+          s[r] = -INFINITY;
       }
     }
     float mloc = s[0];
@@ -179,12 +182,15 @@ struct FwdWave {
   }
 };
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+// BITMASK: the arbitrary-mask instantiation (with BOUNDS); its bit tests stay out
+// of the others, whose D = 128 copies have no registers to spare.
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int Nk, int W,
                                          const int* __restrict__ sst, const int* __restrict__ sen,
-                                         float alibi_raw, int sq, int sk,
+                                         float alibi_raw, const uint32_t* __restrict__ mbase,
+                                         int W32, int sq, int sk,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -249,6 +255,13 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int k_hi = row_hi(i_base);  // smallest key bound of this wave's rows
   if (BOUNDS) n_full = min(n_full, k_hi - 32 - kq * 32 >= 0 ? (k_hi - 32 - kq * 32) / kKV + 1 : 0);
   const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
+  // Arbitrary mask (BITMASK instantiation): this row's bit words; every step
+  // then takes the mask. Word w covers keys 32w .. 32w+31, and a wave's 32
+  // keys of step j are word (kKV / 32) j + kq (clamped: keys past N are
+  // masked anyway).
+  const uint32_t* mrow = BITMASK ? mbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
+  if (BITMASK) n_full = 0;
+  auto mword = [&](int j) { return BITMASK ? mrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
 
   // Software pipeline over steps j = 0 .. n_it-1. Step j reads K_{j+1} (for
   // the next S^T) from K buffer (j+1)%2 and V_j from V buffer j%2, while it
@@ -274,10 +287,13 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // Step j with buffer parity P = j % 2 (a compile-time constant, so the
   // compiler sees that the step's reads never touch the buffers its direct
   // loads fill and does not wait for those loads before them).
+  uint32_t mw = mword(j_lo);  // mask bits of the next step to run
   auto run = [&](int j, auto par_tag, auto mask_tag, auto next_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
+    const uint32_t mw_now = mw;
+    if (BITMASK && NEXT) mw = mword(j + 1);
     half_t* lk = P ? kt1 : kt0;  // receives K_{j+2}
     half_t* lv = P ? vt0 : vt1;  // receives V_{j+1}
     const int jk = min(j + 2, n_it - 1) * kKV;
@@ -295,7 +311,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
-                                lane_hi, w_lo, alibi_raw, lane,
+                                lane_hi, w_lo, alibi_raw, mw_now, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -397,13 +413,14 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   __syncthreads();  // the LDS is reused by the next tile
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
     Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi,
-    const int* __restrict__ seg_start, const int* __restrict__ seg_end) {
+    const int* __restrict__ seg_start, const int* __restrict__ seg_end,
+    const uint32_t* __restrict__ mask, int mask_heads) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -425,45 +442,54 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
   // ALiBi slope of this query head in raw-score units (slope / scale).
   const float alibi_raw = alibi ? alibi[hq] * kLog2e / scale_log2 : 0.f;
+  // This (b, head)'s mask plane (a plane shared by all heads when mask_heads == 1).
+  const int W32 = (N + 31) >> 5;
+  const uint32_t* mbase =
+      BITMASK ? mask + ((size_t)b * mask_heads + (mask_heads == 1 ? 0 : hq)) * N * W32 : nullptr;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
-    fwd_tile<D, CAUSAL, BOUNDS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
+    fwd_tile<D, CAUSAL, BOUNDS, BITMASK, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
                                 Lse + (size_t)bh * N, N, Nk, window,
                                 seg_start ? seg_start + (size_t)b * N : nullptr,
-                                seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, stq.n,
-                                stk.n,
+                                seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, mbase,
+                                W32, stq.n, stk.n,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
 hipError_t launch_fwd_t(const FwdArgs& a) {
   const int n_qtiles = (a.N + kBR - 1) / kBR;
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
   const int BH = a.B * a.Hq;
   dim3 grid(xcd_grid(gx * BH));
   const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)D));
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
                      make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window, a.alibi,
-                     a.seg_start, a.seg_end);
+                     a.seg_start, a.seg_end, a.mask, a.mask_heads);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  // Key lengths, windows, packed sequences and ALiBi need the masked
+  // Key lengths, windows, packed sequences, ALiBi and masks need the masked
   // instantiation (kKV is a multiple of kBR).
   const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
+  if (a.mask)
+    return a.causal ? launch_fwd_t<D, true, true, true, BF>(a)
+                    : launch_fwd_t<D, false, true, true, BF>(a);
   if (a.causal)
-    return bounds ? launch_fwd_t<D, true, true, BF>(a) : launch_fwd_t<D, true, false, BF>(a);
-  return bounds ? launch_fwd_t<D, false, true, BF>(a) : launch_fwd_t<D, false, false, BF>(a);
+    return bounds ? launch_fwd_t<D, true, true, false, BF>(a)
+                  : launch_fwd_t<D, true, false, false, BF>(a);
+  return bounds ? launch_fwd_t<D, false, true, false, BF>(a)
+                : launch_fwd_t<D, false, false, false, BF>(a);
 }
 
 }  // namespace

@@ -2,6 +2,7 @@
 // Arguments are validated by the C ABI (fa_capi.hip) before these are called.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdint.h>
 
 namespace fa {
 
@@ -43,6 +44,12 @@ struct FwdArgs {
   const int* seg_start = nullptr;
   const int* seg_end = nullptr;
   float scale = 0.f;  // softmax scale of the logits; 0 = 1/sqrt(D)
+  // Arbitrary boolean mask, device, bit-packed in rows of W = ceil(N / 32)
+  // words: bit j % 32 of word ((b * mask_heads + h') * N + i) * W + j / 32 is
+  // set iff query i may attend key j (h' = query head h when mask_heads == Hq,
+  // 0 when mask_heads == 1). Applied on top of every other mask.
+  const uint32_t* mask = nullptr;
+  int mask_heads = 0;
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -101,11 +108,20 @@ struct BwdArgs {
   const int* seg_start = nullptr;  // as FwdArgs::seg_start
   const int* seg_end = nullptr;    // as FwdArgs::seg_end
   float scale = 0.f;               // as FwdArgs::scale
+  const uint32_t* mask = nullptr;  // as FwdArgs::mask
+  // The same bits transposed: bit i % 32 of word ((b * mask_heads + h') * N +
+  // j) * W + i / 32 (set iff query i may attend key j); required with mask.
+  const uint32_t* mask_t = nullptr;
+  int mask_heads = 0;              // as FwdArgs::mask_heads
 };
 
 hipError_t launch_fwd(const FwdArgs& a);
 hipError_t launch_bwd_preprocess(const BwdArgs& a);
 hipError_t launch_bwd_main(const BwdArgs& a);
+// Dense boolean mask (P planes of N x N bytes) to the bit layouts of
+// FwdArgs::mask (bits) and BwdArgs::mask_t (bits_t, skipped when null).
+hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* bits_t,
+                            void* stream);
 
 // Work-items (workgroups x threads) of the largest launch each pass makes for
 // a shape (either masking). An AMD dispatch packet counts its grid in

@@ -1,0 +1,100 @@
+// Bit-packing of a dense boolean attention mask into the two layouts the
+// kernels read: rows of W = ceil(N / 32) words per query (the forward and the
+// backward's dQ phase, one word per lane and 32-key step) and the transpose,
+// rows of W words per key (the backward's dK/dV phase, whose lanes own keys).
+// No counterpart in the reference, which takes no mask (fa_p100_hf.py:64-70).
+//
+// Both kernels are HBM-bound byte work: N*N bytes in, N*N/8 bytes out per
+// plane. Grid-stride loops over 64-bit word indices keep the grid small.
+#include <hip/hip_runtime.h>
+
+#include "fa_launch.h"
+
+namespace fa {
+namespace {
+
+constexpr int kPackThreads = 256;
+constexpr long long kPackMaxBlocks = 1 << 16;
+
+// One 32-key word per thread, consecutive threads on consecutive words of a
+// row (a wave reads 2 KB of contiguous mask bytes). VEC: rows start 16-byte
+// aligned (N % 16 == 0 and an aligned base), so each 16-key half is one load.
+template <bool VEC>
+__global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(const uint8_t* __restrict__ dense,
+                                                                 uint32_t* __restrict__ bits,
+                                                                 long long rows, int N, int W) {
+  const long long total = rows * W;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += stride) {
+    const long long r = g / W;
+    const int w = (int)(g - r * W);
+    const uint8_t* src = dense + r * N + 32 * w;
+    const int n = min(32, N - 32 * w);  // keys of this word that exist
+    uint32_t word = 0;
+    if (VEC) {
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        if (16 * half < n) {
+          const uint4 x = *reinterpret_cast<const uint4*>(src + 16 * half);
+          const uint32_t v[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            word |= (uint32_t)(((v[e >> 2] >> (8 * (e & 3))) & 0xffu) != 0u) << (16 * half + e);
+        }
+      }
+    } else {
+      for (int e = 0; e < n; ++e) word |= (uint32_t)(src[e] != 0) << e;
+    }
+    bits[g] = word;
+  }
+}
+
+// One 32-query word of one key per thread. Consecutive threads take
+// consecutive keys of the same 32 query rows, so each of the 32 byte loads is
+// contiguous across the wave; the word stores are W words apart.
+__global__ __launch_bounds__(kPackThreads) void pack_cols_kernel(const uint8_t* __restrict__ dense,
+                                                                 uint32_t* __restrict__ bits_t,
+                                                                 long long planes, int N, int W) {
+  const long long total = planes * W * N;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += stride) {
+    // g = (p * W + w) * N + j: key j fastest.
+    const long long pw = g / N;
+    const int j = (int)(g - pw * N);
+    const long long p = pw / W;
+    const int w = (int)(pw - p * W);
+    const int i0 = 32 * w;
+    const int n = min(32, N - i0);  // query rows of this word that exist
+    const uint8_t* src = dense + (p * N + i0) * (long long)N + j;
+    uint32_t word = 0;
+    for (int e = 0; e < n; ++e) word |= (uint32_t)(src[(long long)e * N] != 0) << e;
+    bits_t[(p * N + j) * W + w] = word;
+  }
+}
+
+unsigned blocks_for(long long items) {
+  const long long b = (items + kPackThreads - 1) / kPackThreads;
+  return (unsigned)(b < kPackMaxBlocks ? (b > 0 ? b : 1) : kPackMaxBlocks);
+}
+
+}  // namespace
+
+hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* bits_t,
+                            void* stream) {
+  const int W = (N + 31) / 32;
+  const long long rows = (long long)P * N;
+  const bool vec = N % 16 == 0 && (reinterpret_cast<uintptr_t>(dense) & 15u) == 0;
+  if (vec)
+    hipLaunchKernelGGL(pack_rows_kernel<true>, dim3(blocks_for(rows * W)), dim3(kPackThreads), 0,
+                       (hipStream_t)stream, dense, bits, rows, N, W);
+  else
+    hipLaunchKernelGGL(pack_rows_kernel<false>, dim3(blocks_for(rows * W)), dim3(kPackThreads), 0,
+                       (hipStream_t)stream, dense, bits, rows, N, W);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || bits_t == nullptr) return e;
+  hipLaunchKernelGGL(pack_cols_kernel, dim3(blocks_for(rows * W)), dim3(kPackThreads), 0,
+                     (hipStream_t)stream, dense, bits_t, (long long)P, N, W);
+  return hipGetLastError();
+}
+
+}  // namespace fa

@@ -10,7 +10,8 @@
 // and, with no counterpart in the reference, entries used by the autograd
 // Function: backward_half_dq (dq as fp16), forward_bnhd / backward_bnhd
 // (dense (B, N, H, D) tensors) and forward_dt / backward_dt (fp16 or bf16);
-// the last four take bf16 as well as fp16.
+// the last four take bf16 as well as fp16; pack_mask bit-packs a boolean
+// mask for their `mask` / `mask_t` arguments.
 //
 // Plain C++ (no device code): every launch goes through the C ABI of
 // libfa_mi355x.so (include/fa_mi355x.h). Unlike the reference, which uses the
@@ -81,11 +82,27 @@ const int* seg_ptr(const c10::optional<at::Tensor>& seg, const at::Tensor& q, in
   return t.data_ptr<int>();
 }
 
+// Optional bit-packed mask (pack_mask's output): int32 (B, 1 or Hq, N,
+// ceil(N/32)) on q's device; nullptr when absent. Sets *heads to dim 1.
+const uint32_t* mask_ptr(const c10::optional<at::Tensor>& m, const at::Tensor& q, int B, int H,
+                         int N, const char* name, int* heads) {
+  if (!m.has_value()) return nullptr;
+  const at::Tensor& t = *m;
+  TORCH_CHECK(t.is_cuda() && t.device() == q.device(), name, " must be on q's device");
+  TORCH_CHECK(t.scalar_type() == at::kInt, name, " must be int32 (packed bits)");
+  TORCH_CHECK(t.dim() == 4 && t.size(0) == B && (t.size(1) == 1 || t.size(1) == H) &&
+                  t.size(2) == N && t.size(3) == (N + 31) / 32 && t.is_contiguous(),
+              name, " must be (B, 1 or Hq, N, ceil(N/32))");
+  *heads = (int)t.size(1);
+  return reinterpret_cast<const uint32_t*>(t.data_ptr<int>());
+}
+
 fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Tensor>& kv_len,
                      int64_t window, const c10::optional<at::Tensor>& alibi,
                      const c10::optional<at::Tensor>& seg_start,
-                     const c10::optional<at::Tensor>& seg_end, double scale, int B, int H,
-                     int N) {
+                     const c10::optional<at::Tensor>& seg_end, double scale,
+                     const c10::optional<at::Tensor>& mask,
+                     const c10::optional<at::Tensor>& mask_t, int B, int H, int N) {
   fa_options op{};
   op.dtype = dtype_code(q);
   op.layout = layout;
@@ -95,6 +112,11 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
   op.seg_start = seg_ptr(seg_start, q, B, N, "seg_start");
   op.seg_end = seg_ptr(seg_end, q, B, N, "seg_end");
   op.scale = (float)scale;
+  int heads = 0, heads_t = 0;
+  op.mask = mask_ptr(mask, q, B, H, N, "mask", &heads);
+  op.mask_t = mask_ptr(mask_t, q, B, H, N, "mask_t", &heads_t);
+  TORCH_CHECK(!op.mask_t || (op.mask && heads_t == heads), "mask_t must come with a mask of its shape");
+  op.mask_heads = heads;
   return op;
 }
 
@@ -218,7 +240,7 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
                                         c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -239,7 +261,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   const fa_options op =
-      make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
+      make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
+                mask, mask_t, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -252,7 +275,7 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
                                          bool causal, c10::optional<at::Tensor> kv_len,
                                          int64_t window, c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -277,7 +300,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   const fa_options op =
-      make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
+      make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
+                mask, mask_t, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -289,14 +313,15 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
 // Dense (B, H, N, D) tensors in fp16 or bf16 (one format for all), results in
 // that format, dq included, and optional key lengths kv_len (int32 (B,), right
 // padding: entry b has keys [0, kv_len[b])), sliding window (causal: row i
-// sees keys (i - window, i]; 0 = none) and ALiBi slopes (fp32 (Hq,): score
-// -slope |i - j|). For fp16 without these, the same kernels as forward and
-// backward_half_dq.
+// sees keys (i - window, i]; 0 = none), ALiBi slopes (fp32 (Hq,): score
+// -slope |i - j|), packed-sequence bounds, a softmax scale and a bit-packed
+// mask (pack_mask's bits; the backward needs bits_t as mask_t too). For fp16
+// without these, the same kernels as forward and backward_half_dq.
 std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, bool causal,
                                       c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -320,7 +345,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   const fa_options op =
-      make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
+      make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
+                mask, mask_t, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -333,7 +359,7 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
                                        c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -363,7 +389,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   const fa_options op =
-      make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale, B, H, N);
+      make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
+                mask, mask_t, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -372,7 +399,39 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   return {dq, dk, dv};
 }
 
+// Dense boolean mask (..., N, N) (nonzero = may attend) to the packed words
+// the kernels read: bits (..., N, ceil(N/32)) and, with `transposed`, bits_t
+// of the same shape holding the transpose (see fa_pack_mask).
+std::vector<at::Tensor> fa_pack_mask_t(at::Tensor dense, bool transposed) {
+  TORCH_CHECK(dense.is_cuda(), "mask must be a CUDA tensor");
+  TORCH_CHECK(dense.scalar_type() == at::kBool || dense.scalar_type() == at::kByte,
+              "mask must be bool or uint8");
+  TORCH_CHECK(dense.dim() >= 2 && dense.size(-1) == dense.size(-2) && dense.size(-1) > 0,
+              "mask must be (..., N, N)");
+  dense = dense.contiguous();
+  const int64_t N = dense.size(-1);
+  TORCH_CHECK(N <= INT32_MAX, "mask too large");
+  const int64_t P = dense.numel() / (N * N);
+  TORCH_CHECK(P > 0 && P <= INT32_MAX, "mask must hold at least one plane");
+  std::vector<int64_t> shape(dense.sizes().begin(), dense.sizes().end());
+  shape.back() = (N + 31) / 32;
+  c10::DeviceGuard guard(dense.device());
+  auto opts = dense.options().dtype(at::kInt);
+  auto bits = at::empty(shape, opts);
+  at::Tensor bits_t = transposed ? at::empty(shape, opts) : at::Tensor();
+  check_rc(fa_pack_mask(reinterpret_cast<const uint8_t*>(dense.data_ptr()), (int)P, (int)N,
+                        reinterpret_cast<uint32_t*>(bits.data_ptr<int>()),
+                        transposed ? reinterpret_cast<uint32_t*>(bits_t.data_ptr<int>()) : nullptr,
+                        current_stream(dense)),
+           "fa_pack_mask");
+  if (!transposed) return {bits};
+  return {bits, bits_t};
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("pack_mask", &fa_pack_mask_t,
+        "Bit-packs a dense boolean (..., N, N) mask for the mask / mask_t arguments",
+        py::arg("mask"), py::arg("transposed") = true);
   m.def("forward", &fa_forward, "FlashAttention forward (gfx950)");
   m.def("backward", &fa_backward, "FlashAttention backward (gfx950)");
   m.def("backward_half_dq", &fa_backward_half_dq,
@@ -381,22 +440,26 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "FlashAttention forward (gfx950) on dense (B, N, H, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
-        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0);
+        py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
 }

@@ -67,7 +67,7 @@ class _FlashAttnP100(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None,
-                segs=None, scale=0.0):
+                segs=None, scale=0.0, mask=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -79,17 +79,19 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.alibi = alibi
         ctx.segs = segs
         ctx.scale = scale
+        ctx.mask = mask
         seg_start, seg_end = segs if segs is not None else (None, None)
+        bits, bits_t = mask if mask is not None else (None, None)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
-                                        seg_end, scale)
+                                        seg_end, scale, bits)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
         if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
-                or segs is not None or scale):
+                or segs is not None or scale or mask is not None):
             o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end,
-                                     scale)
+                                     scale, bits)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -98,13 +100,15 @@ class _FlashAttnP100(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_o):
         seg_start, seg_end = ctx.segs if ctx.segs is not None else (None, None)
+        bits, bits_t = ctx.mask if ctx.mask is not None else (None, None)
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
-                                            ctx.window, ctx.alibi, seg_start, seg_end, ctx.scale)
+                                            ctx.window, ctx.alibi, seg_start, seg_end, ctx.scale,
+                                            bits, bits_t)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
-                    None, None, None, None, None, None, None)
+                    None, None, None, None, None, None, None, None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
@@ -112,17 +116,18 @@ class _FlashAttnP100(torch.autograd.Function):
         # and backward_dt to bf16 for bf16 inputs.
         g = grad_o.contiguous()
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
-                or ctx.alibi is not None or ctx.segs is not None or ctx.scale):
+                or ctx.alibi is not None or ctx.segs is not None or ctx.scale
+                or ctx.mask is not None):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
-                                          ctx.alibi, seg_start, seg_end, ctx.scale)
+                                          ctx.alibi, seg_start, seg_end, ctx.scale, bits, bits_t)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
-                None, None)
+                None, None, None)
 
 
 def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-               alibi_slopes=None, segment_ids=None, softmax_scale=None):
+               alibi_slopes=None, segment_ids=None, softmax_scale=None, attn_mask=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -154,7 +159,14 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         makes from such ids, for callers that reuse one packing across calls;
       * softmax_scale: a positive float used in place of 1/sqrt(D) (the
         reference fixes 1/sqrt(D), fa_p100_ext.cu:71); the returned LSE is in
-        units of the scaled logits.
+        units of the scaled logits;
+      * attn_mask, a boolean tensor on q's device of shape (N, N), (B, N, N)
+        or (B or 1, 1 or Hq, N, N): key j is hidden from query i wherever it
+        is False (torch scaled_dot_product_attention's boolean attn_mask),
+        on top of every other mask, causal included. A row left with no key
+        gets o = 0 and zero gradients. Also accepted: the (bits, bits_t)
+        pair pack_mask() makes, for callers that reuse one mask across calls.
+        The mask is a constant: no gradient flows to it.
     """
     window = 0
     if sliding_window is not None:
@@ -179,8 +191,49 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         scale = float(softmax_scale)
         if not (scale > 0.0 and math.isfinite(scale)):
             raise ValueError(f"softmax_scale must be positive and finite, got {softmax_scale}")
+    mask = None
+    if attn_mask is not None:
+        if isinstance(attn_mask, (tuple, list)):
+            mask = tuple(attn_mask)
+            want = (q.size(0), q.size(2), (q.size(2) + 31) // 32)
+            got = tuple(mask[0].shape)
+            if (len(mask) != 2 or len(got) != 4 or (got[0], got[2], got[3]) != want
+                    or got[1] not in (1, q.size(1)) or tuple(mask[1].shape) != got):
+                raise ValueError(f"packed attn_mask must be two ({want[0]}, 1 or {q.size(1)}, "
+                                 f"{want[1]}, {want[2]}) tensors from pack_mask, got "
+                                 f"{[tuple(t.shape) for t in mask]}")
+        else:
+            mask = pack_mask(attn_mask, q.size(0), q.size(1))
     return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes,
-                                segs, scale)
+                                segs, scale, mask)
+
+
+def pack_mask(attn_mask, batch, heads):
+    """(bits, bits_t), int32 (batch, 1 or heads, N, ceil(N/32)) each, of a
+    boolean mask (N, N), (B, N, N) or (B or 1, 1 or heads, N, N).
+
+    Bit j % 32 of bits[b, h, i, j // 32] is set iff query i may attend key j
+    (attn_mask True); bits_t holds the transpose (bit i % 32 of
+    bits_t[b, h, j, i // 32]), which the backward reads. These are the words
+    the kernels take (fa_options.mask / mask_t in the C ABI); one HIP kernel
+    packs them on the mask's device.
+    """
+    m = attn_mask
+    if m.dtype != torch.bool:
+        raise ValueError(f"attn_mask must be a boolean tensor (True = attend), got {m.dtype}")
+    if m.dim() == 2:
+        m = m[None, None]
+    elif m.dim() == 3:
+        m = m[:, None]
+    if m.dim() != 4 or m.size(-1) != m.size(-2) or m.size(0) not in (1, batch) \
+            or m.size(1) not in (1, heads):
+        raise ValueError(f"attn_mask must be (N, N), ({batch}, N, N) or ({batch} or 1, 1 or "
+                         f"{heads}, N, N), got {tuple(attn_mask.shape)}")
+    bits, bits_t = _ext.pack_mask(m, True)
+    if bits.size(0) != batch:  # one plane set shared by the batch
+        shape = (batch,) + tuple(bits.shape[1:])
+        bits, bits_t = bits.expand(shape).contiguous(), bits_t.expand(shape).contiguous()
+    return bits, bits_t
 
 
 def segment_bounds(segment_ids):

@@ -22,7 +22,18 @@ lengths, so every position attends to the real keys only, as with eager
 attention and the same mask. Left (and both-sided) padding is served on
 causal layers too: the pads form a packed sequence of their own (below), so
 every real token attends to the real keys only, as with eager; only the pad
-rows' outputs, which nothing reads, differ.
+rows' outputs, which nothing reads, differ. Any other 2-D mask (holes inside
+a row) goes to the kernels as a bit mask over the keys, on top of the layer's
+causal mask and window, as eager combines them; a query row left with no key
+gets a zero output where eager's is arbitrary.
+
+A 4-D mask handed to the model (boolean, True = attend, or additive with only
+0 and blocking values <= -1e4 or -inf) reaches every layer as it is
+(masking_utils returns 4-D masks unchanged); as with eager and sdpa it alone
+decides which keys each query sees, and it goes to the kernels as a bit mask.
+The causal flag is kept only when the mask allows no key above the diagonal,
+where it changes nothing but the tiles skipped. An additive mask with other
+values is a bias the kernels do not add, and raises.
 
 Also beyond the reference, a causal layer's sliding window (Qwen3's and
 Mistral-style `sliding_window`) runs in the kernels: row i sees keys
@@ -30,32 +41,39 @@ Mistral-style `sliding_window`) runs in the kernels: row i sees keys
 (several sequences in one row, marked by `position_ids` that restart, as
 transformers' DataCollatorWithFlattening produces them) attend within their
 own sequence only, as transformers' packed-sequence mask does for eager and
-sdpa (masking_utils.find_packed_sequence_indices). The reference, which
-ignores position_ids, attended across the packed sequences.
+sdpa (masking_utils.find_packed_sequence_indices) when the model gets no
+attention mask. The reference, which ignores position_ids, attended across the
+packed sequences.
 
 The kernels run in the autocast dtype (fp16 or bf16; bf16 inputs without
 autocast stay bf16); the reference cast everything to fp16.
 
 Every other unsupported request raises NotImplementedError instead of
-degrading (fa_p100_hf.py:24-32): other attention / padding masks,
-output_attentions, head_mask, a window on non-causal attention, dropout,
-head_dim other than 64/128, q_len != kv_len (KV-cache decoding). A scale other
-than 1/sqrt(D), which the reference rejected, goes to the kernels.
+degrading (fa_p100_hf.py:24-32): masks carrying a bias, output_attentions,
+head_mask, a window on non-causal attention, dropout, head_dim other than
+64/128, q_len != kv_len (KV-cache decoding). A scale other than 1/sqrt(D),
+which the reference rejected, goes to the kernels.
 """
 import warnings
 
 import torch
 
-from fa_p100 import flash_attn, segment_bounds
+from fa_p100 import flash_attn, pack_mask, segment_bounds
 
 _IMPL_NAME = "fa_p100"
 _warned_cast = False
 # enable_fa_p100's forward wrapper hands every attention call of a model call
-# the batch's padding and packing as one keyword argument, (kv_len, segs):
+# the batch's padding, packing and mask as one keyword argument,
+# (kv_len, segs, mask):
 #   kv_len: key lengths, int32 (B,) on the model's device, of a padded batch,
 #           or None;
 #   segs:   packed-sequence bounds (seg_start, seg_end), or _NOT_PACKED once
-#           the call's position_ids were found to hold one sequence per row.
+#           the call's position_ids were found to hold one sequence per row;
+#   mask:   None, or (bits, bits_t, causal): the packed words of a mask
+#           (pack_mask's layout) and, for a 4-D mask, whether the causal flag
+#           may stay on (None for a 2-D padding mask, which the layer's causal
+#           mask and window apply on top of).
+# The mask is packed once per model call rather than once per layer.
 # transformers passes a model's **kwargs down to each decoder layer and from
 # there to the attention interface, and gradient checkpointing replays a
 # layer with the same kwargs, so a layer recomputed in the backward pass sees
@@ -124,6 +142,65 @@ def _left_padding_segments(first, n):
     return (idx >= first[:, None].long()).to(torch.int32)
 
 
+# Additive mask values at or below this block a key: exp(s - 1e4) is exactly
+# 0 in fp32 next to any allowed key's logit.
+_BLOCKED = -1.0e4
+
+
+def key_mask_bits(mask):
+    """(bits, bits_t), int32 (B, 1, N, ceil(N/32)) each, of a 2-D padding
+    mask: every query row may attend key j of entry b iff mask[b, j] != 0.
+    Built from the (B, N) mask with a few device ops, without an N x N
+    boolean tensor."""
+    m = mask != 0
+    b, n = m.shape
+    w = (n + 31) // 32
+    flat = torch.zeros(b, w * 32, dtype=torch.int64, device=m.device)
+    flat[:, :n] = m.long()
+    shifts = torch.arange(32, dtype=torch.int64, device=m.device)
+    words = (flat.view(b, w, 32) << shifts).sum(-1)  # in [0, 2^32)
+    bits = _as_int32(words)[:, None, None, :].expand(b, 1, n, w).contiguous()
+    # Transposed: key j's words over the query rows, all set (rows past N
+    # clear) for a real key, none for a pad.
+    full = torch.full((w,), (1 << 32) - 1, dtype=torch.int64, device=m.device)
+    full[-1] = (1 << (n - 32 * (w - 1))) - 1
+    rows = _as_int32(full)
+    bits_t = torch.where(m[:, None, :, None], rows, torch.zeros_like(rows)).contiguous()
+    return bits, bits_t
+
+
+def _as_int32(words):
+    """int64 values in [0, 2^32) as the int32 with the same 32 bits."""
+    return torch.where(words >= (1 << 31), words - (1 << 32), words).to(torch.int32)
+
+
+def dense_mask_bits(mask, batch, heads):
+    """(bits, bits_t, causal) of a 4-D attention mask (B or 1, 1 or heads,
+    N, N) as transformers hands it to the attention interface: boolean
+    (True = attend) or additive (0 = attend; -inf or <= -1e4 = blocked).
+    `causal` tells whether the mask allows no key above the diagonal."""
+    if mask.dim() != 4 or mask.size(-1) != mask.size(-2) or mask.size(0) not in (1, batch) \
+            or mask.size(1) not in (1, heads):
+        raise NotImplementedError(
+            f"fa_p100 takes a 4-D attention mask of shape ({batch} or 1, 1 or {heads}, N, N); "
+            f"got {tuple(mask.shape)}.")
+    if mask.dtype == torch.bool:
+        allowed = mask
+    elif mask.is_floating_point():
+        allowed = mask == 0
+        if not bool((allowed | (mask <= _BLOCKED)).all()):
+            raise NotImplementedError(
+                "fa_p100 got an additive attention mask with values other than 0 and "
+                "blocking ones (-inf, or <= -1e4): that is a bias, which the kernels do not "
+                "add. Pass a boolean mask or use attn_implementation='sdpa'.")
+    else:
+        raise NotImplementedError(
+            f"fa_p100 takes a boolean or floating attention mask, got {mask.dtype}.")
+    causal = not bool(torch.triu(allowed, diagonal=1).any())
+    bits, bits_t = pack_mask(allowed, batch, heads)
+    return bits, bits_t, causal
+
+
 def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout=0.0,
                               scaling=None, is_causal=None, **kwargs):
     """transformers attention-interface entry point (fa_p100_hf.py:46-142).
@@ -134,10 +211,6 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
     """
     global _warned_cast
 
-    if attention_mask is not None:
-        raise NotImplementedError(
-            "fa_p100 got an attention mask, but the kernel has no mask input. "
-            "Pack sequences to one fixed length so no padding is needed.")
     if kwargs.get("output_attentions", False):
         raise NotImplementedError(
             "fa_p100 never forms the attention probabilities, so "
@@ -162,7 +235,15 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
 
     if is_causal is None:
         is_causal = getattr(module, "is_causal", True) and query.size(2) > 1
+    # Padding, packing and mask of the model call (enable_fa_p100's wrapper).
+    kv_len, segs, mask = kwargs.pop(_BOUNDS_KW, None) or (None, None, None)
+    if attention_mask is not None and mask is None:  # a 4-D mask, no wrapper
+        mask = dense_mask_bits(attention_mask, query.size(0), query.size(1))
     sliding_window = kwargs.get("sliding_window")
+    if mask is not None and mask[2] is not None:
+        # A 4-D mask alone decides which keys each query sees (eager adds it
+        # to the logits, sdpa passes it with is_causal=False).
+        is_causal, sliding_window, kv_len, segs = mask[2], None, None, _NOT_PACKED
     if sliding_window is not None and (not is_causal or sliding_window <= 0):
         raise NotImplementedError(
             f"fa_p100 serves sliding windows on causal attention only; this layer asks for "
@@ -192,9 +273,7 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             _warned_cast = True
         query, key, value = query.to(target), key.to(target), value.to(target)
 
-    # Padding and packing of the model call (enable_fa_p100's wrapper); when
-    # the hook runs without it, packed sequences come from position_ids here.
-    kv_len, segs = kwargs.pop(_BOUNDS_KW, None) or (None, None)
+    # Without the wrapper, packed sequences come from position_ids here.
     position_ids = kwargs.get("position_ids")
     if segs is None and position_ids is not None:
         segs = _packed_bounds(position_ids, query.size(0))
@@ -216,7 +295,8 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
                 "attention call's batch.")
     out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
                      kv_len=kv_len, sliding_window=sliding_window, segment_ids=segs,
-                     softmax_scale=softmax_scale)
+                     softmax_scale=softmax_scale,
+                     attn_mask=None if mask is None else mask[:2])
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
 
@@ -241,10 +321,12 @@ def enable_fa_p100(model, full_precision=False):
 
     Mirrors fa_p100_hf.py:161-213: registers the implementation, points every
     config at it, records `full_precision` on every module, turns the KV cache
-    off, and wraps `model.forward` once so that use_cache=True and any
-    padding mask other than right padding raise instead of being silently
-    ignored; a right-padded mask is served through per-entry key lengths and
-    a left-padded one (causal layers) through packed-sequence bounds.
+    off, and wraps `model.forward` once so that use_cache=True raises and the
+    attention mask, which transformers would drop before the attention
+    interface, reaches the kernels: a right-padded mask as per-entry key
+    lengths, a left-padded one (causal layers) as packed-sequence bounds, any
+    other 2-D mask as a key bit mask, and a 4-D mask as a bit mask of its
+    own, each prepared once per model call.
     """
     register()
     _set_impl(model.config, _IMPL_NAME)
@@ -262,21 +344,27 @@ def enable_fa_p100(model, full_precision=False):
         inner = model.forward
 
         def guarded(*args, attention_mask=None, use_cache=None, **kwargs):
-            # transformers drops the mask before the attention interface sees it
-            # for unregistered implementations: this is the last place to catch it.
-            kv_len, left = None, None
-            if attention_mask is not None and not bool(attention_mask.all()):
+            # transformers drops a 2-D mask before the attention interface sees
+            # it for unregistered implementations: this is the last place to
+            # catch it. A 4-D mask reaches every layer; it is packed here once.
+            kv_len, left, mask = None, None, None
+            ref = kwargs.get("input_ids")
+            if ref is None:
+                ref = kwargs.get("inputs_embeds")
+            if ref is None and args:
+                ref = args[0]
+            if attention_mask is not None and attention_mask.dim() == 4:
+                batch = ref.size(0) if ref is not None else attention_mask.size(0)
+                mask = dense_mask_bits(attention_mask, batch, attention_mask.size(1))
+            elif attention_mask is not None and not bool(attention_mask.all()):
                 spans = padding_spans(attention_mask)
                 if spans is None:
-                    raise NotImplementedError(
-                        "fa_p100 serves only padding masks whose ones form one run per row "
-                        "(right, left or both-sided padding); this mask would be discarded "
-                        "silently. Pad at the ends or pack the batch so every position is "
-                        "real.")
-                first, end = spans
-                kv_len = end  # keys past the run exist for no row
-                if bool((first > 0).any()):
-                    left = first
+                    mask = key_mask_bits(attention_mask) + (None,)
+                else:
+                    first, end = spans
+                    kv_len = end  # keys past the run exist for no row
+                    if bool((first > 0).any()):
+                        left = first
             # Rejected up front rather than at the first decode step, after a
             # prefill that would have succeeded.
             if use_cache:
@@ -284,7 +372,8 @@ def enable_fa_p100(model, full_precision=False):
                     "fa_p100 needs q_len == kv_len, so it cannot serve a KV cache; it "
                     "is a training kernel. Set generation_config.use_cache = False for "
                     "cache-free generation.")
-            # Packed sequences: restarting position_ids (checked once per call).
+            # Packed sequences: restarting position_ids (checked once per call)
+            # when the model gets no mask, as transformers' mask creation does.
             # Left padding rides on the same bounds: the pads form a sequence
             # of their own, so real tokens (causal) see real keys only.
             segs = _NOT_PACKED
@@ -303,15 +392,10 @@ def enable_fa_p100(model, full_precision=False):
                             "fa_p100 does not serve left padding and packed sequences "
                             "together.")
                 segs = segment_bounds(_left_padding_segments(left, attention_mask.size(1)))
-            elif position_ids is not None:
-                ref = kwargs.get("input_ids")
-                if ref is None:
-                    ref = kwargs.get("inputs_embeds")
-                if ref is None and args:
-                    ref = args[0]
+            elif position_ids is not None and attention_mask is None:
                 batch = ref.size(0) if ref is not None else position_ids.size(0)
                 segs = _packed_bounds(position_ids, batch)
-            kwargs[_BOUNDS_KW] = (kv_len, segs)
+            kwargs[_BOUNDS_KW] = (kv_len, segs, mask)
             return inner(*args, attention_mask=attention_mask, use_cache=use_cache, **kwargs)
 
         model.forward = guarded

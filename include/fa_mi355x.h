@@ -29,6 +29,7 @@
 #define FA_MI355X_H_
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -48,7 +49,8 @@ enum {
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */
   FA_ERR_SEGMENTS = 10011,   /* packed sequences with only one of the two bound arrays */
   FA_ERR_SCALE = 10012,      /* softmax scale negative or not finite */
-  FA_ERR_SCRATCH = 10013     /* fa_bwd_noalloc: the shape needs more than its scratch */
+  FA_ERR_SCRATCH = 10013,    /* fa_bwd_noalloc: the shape needs more than its scratch */
+  FA_ERR_MASK = 10014        /* mask_heads not 1 or Hq, or a backward mask without mask_t */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -166,7 +168,7 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
 /*
  * Options of the general pair below; a zeroed struct (or a NULL pointer)
  * means fp16, dense (B, H, N, D), no key lengths, no window, no ALiBi, no
- * packed sequences.
+ * packed sequences, no mask.
  *   - dtype: FA_DTYPE_FP16 or FA_DTYPE_BF16 for q, k, v, o, dO, dq, dk, dv
  *     (bf16: products on the bf16 MFMA with fp32 accumulation, P and dS
  *     rounded to bf16 as operands, outputs rounded to nearest even);
@@ -193,7 +195,17 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *   - scale: 0 (the reference's fixed 1/sqrt(D), fa_p100_ext.cu:71, 117), or
  *     a positive softmax scale applied to q . k before the masks; dq and dk
  *     carry it as they carry 1/sqrt(D), and lse is in units of the scaled
- *     logits.
+ *     logits;
+ *   - mask, mask_t, mask_heads: an arbitrary boolean attention mask on top of
+ *     every other one (mask = NULL: none). W = ceil(N / 32) words per row;
+ *     plane p = b * mask_heads + (mask_heads == 1 ? 0 : h) for query head h
+ *     (mask_heads is 1, one plane per batch entry shared by all heads, or Hq).
+ *     Query i may attend key j iff bit j % 32 of mask[(p * N + i) * W + j / 32]
+ *     is set; mask_t holds the same bits transposed, bit i % 32 of
+ *     mask_t[(p * N + j) * W + i / 32]. The forward reads mask, the backward
+ *     both (mask_t is required there). fa_pack_mask writes both from a dense
+ *     boolean mask. A row with no key left gets o = 0, lse = +inf and zero
+ *     gradients.
  */
 typedef struct fa_options {
   int dtype;
@@ -204,16 +216,19 @@ typedef struct fa_options {
   const int* seg_start;
   const int* seg_end;
   float scale;
+  const uint32_t* mask;
+  const uint32_t* mask_t;
+  int mask_heads;
 } fa_options;
 
 /*
  * The general pair: every entry point above is one of its cases, plus bf16,
- * key padding, sliding windows, ALiBi and packed sequences (`opts`).
+ * key padding, sliding windows, ALiBi, packed sequences and masks (`opts`).
  * fa_bwd_ex writes dq in the element format (fp16 or bf16); lse and the
  * workspace as in fa_bwd. No counterpart in the reference, which raises on
  * bf16, masks and windows (README.md:72-75, fa_p100_ext.cu:33,
  * fa_p100_hf.py:64-82) and has no bias or packing input; the HF hook uses key
- * lengths, windows and packed sequences.
+ * lengths, windows, packed sequences and masks.
  */
 int fa_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse,
               int B, int Hq, int Hkv, int N, int D, int causal, const fa_options* opts,
@@ -222,6 +237,18 @@ int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const
               const float* lse, void* dq, void* dk, void* dv, void* workspace,
               size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
               const fa_options* opts, void* stream);
+
+/*
+ * Bit-packs a dense boolean mask for fa_options.mask / mask_t. No counterpart
+ * in the reference, which takes no mask (fa_p100_hf.py:64-70). `dense` is P
+ * planes of N x N bytes, row-major (plane p, query row i, key j at
+ * (p * N + i) * N + j; nonzero = may attend), as a torch.bool tensor holds
+ * them. Writes P * N * ceil(N/32) words to `bits` and, when `bits_t` is not
+ * NULL, as many to `bits_t` (layouts as fa_options.mask / mask_t; bits past N
+ * in a row's last word are 0). Asynchronous on `stream`.
+ */
+int fa_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* bits_t,
+                 void* stream);
 
 /*
  * fa_bwd without a workspace argument and without any allocation. No

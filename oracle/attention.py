@@ -61,7 +61,7 @@ def _group_sum(g, hkv):
 
 
 def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=None,
-            scale=None):
+            scale=None, mask=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
@@ -76,6 +76,10 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
     scaled logit before the masks. With `segments` (B x N ids, another
     extension: packed sequences) each maximal run of equal ids is one
     sequence and key col is masked for row unless both lie in the same run.
+    With `mask` (a boolean array broadcastable to (B, Hq, N, N), another
+    extension) key col is also masked for row wherever mask[b, h, row, col]
+    is False, as torch's scaled_dot_product_attention reads a boolean
+    attn_mask.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
@@ -88,13 +92,13 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
         dist = np.abs(np.arange(n)[:, None] - np.arange(n)[None, :]).astype(np.float64)
         s = (s - (slopes[:, None, None] * dist[None]).astype(dtype)[None]).astype(dtype)
     if causal:
-        mask = np.triu(np.ones((n, n), dtype=bool), 1)
-        s = np.where(mask, -np.inf, s).astype(dtype)
+        above = np.triu(np.ones((n, n), dtype=bool), 1)
+        s = np.where(above, -np.inf, s).astype(dtype)
     if window is not None:
         if not causal:
             raise ValueError("a sliding window needs causal masking")
-        mask = np.tril(np.ones((n, n), dtype=bool), -int(window))
-        s = np.where(mask, -np.inf, s).astype(dtype)
+        outside = np.tril(np.ones((n, n), dtype=bool), -int(window))
+        s = np.where(outside, -np.inf, s).astype(dtype)
     if segments is not None:
         seg = np.asarray(segments).reshape(q.shape[0], n)
         run = np.concatenate([np.zeros((seg.shape[0], 1), dtype=np.int64),
@@ -105,27 +109,31 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
         lens = np.clip(np.asarray(kv_len).reshape(-1), 1, n)
         cols = np.arange(n)[None, :] >= lens[:, None]  # (B, N) masked key columns
         s = np.where(cols[:, None, None, :], -np.inf, s).astype(dtype)
+    if mask is not None:
+        m = np.broadcast_to(np.asarray(mask, dtype=bool), s.shape)
+        s = np.where(m, s, -np.inf).astype(dtype)
     return s
 
 
 def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None,
-                  alibi=None, segments=None, scale=None):
+                  alibi=None, segments=None, scale=None, mask=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
-    (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`, `segments`:
-    optional per-entry key lengths, sliding window, ALiBi slopes and packed
-    sequence ids (see _scores).
+    (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`, `segments`, `mask`:
+    optional per-entry key lengths, sliding window, ALiBi slopes, packed
+    sequence ids and boolean mask (see _scores).
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments, scale)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments, scale, mask)
     m = s.max(axis=-1, keepdims=True)
-    # A row that sees no key at all (only with both key lengths and a window:
-    # pad rows more than W past their entry's length) gets O = 0 and
-    # LSE = +inf, so that the backward's P = exp(S - LSE) is 0 there too.
+    # A row that sees no key at all (key lengths with a window: pad rows more
+    # than W past their entry's length; or a mask row without a set bit) gets
+    # O = 0 and LSE = +inf, so that the backward's P = exp(S - LSE) is 0 there
+    # too.
     empty = m == -np.inf
     m = np.where(empty, 0, m)
     p = np.exp(s - m)
@@ -141,7 +149,7 @@ def bwd_preprocess(o, do, dtype=np.float64):
 
 
 def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
-                  window=None, alibi=None, segments=None, scale=None):
+                  window=None, alibi=None, segments=None, scale=None, mask=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -157,8 +165,9 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     qd = q.astype(dtype)
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
-        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale)
-    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments, scale)
+        o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale,
+                               mask)
+    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments, scale, mask)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     dv = np.matmul(np.swapaxes(p, -1, -2), dod)
     dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
@@ -170,9 +179,9 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
 
 
 def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None,
-                   alibi=None, segments=None, scale=None):
+                   alibi=None, segments=None, scale=None, mask=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale, mask)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

@@ -65,6 +65,8 @@ def load_capi():
     lib.fa_fwd_ex.restype = i
     lib.fa_bwd_ex.argtypes = [vp] * 10 + [sz] + [i] * 6 + [opts, vp]
     lib.fa_bwd_ex.restype = i
+    lib.fa_pack_mask.argtypes = [vp, i, i, vp, vp, vp]
+    lib.fa_pack_mask.restype = i
     if hasattr(lib, "fa_bwd_noalloc"):
         lib.fa_bwd_noalloc.argtypes = [vp] * 9 + [i] * 6 + [vp]
         lib.fa_bwd_noalloc.restype = i
@@ -76,17 +78,19 @@ class FaOptions(ctypes.Structure):
     _fields_ = [("dtype", ctypes.c_int), ("layout", ctypes.c_int),
                 ("kv_len", ctypes.c_void_p), ("window", ctypes.c_int),
                 ("alibi_slopes", ctypes.c_void_p), ("seg_start", ctypes.c_void_p),
-                ("seg_end", ctypes.c_void_p), ("scale", ctypes.c_float)]
+                ("seg_end", ctypes.c_void_p), ("scale", ctypes.c_float),
+                ("mask", ctypes.c_void_p), ("mask_t", ctypes.c_void_p),
+                ("mask_heads", ctypes.c_int)]
 
 
 def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_start=None,
-            seg_end=None, scale=0.0):
+            seg_end=None, scale=0.0, mask=None, mask_t=None, mask_heads=0):
     """A pointer to an FaOptions; the array fields are device addresses (ints)
     or tensors."""
     def addr(x):
         return None if x is None else (x if isinstance(x, int) else x.data_ptr())
     o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes), addr(seg_start),
-                  addr(seg_end), scale)
+                  addr(seg_end), scale, addr(mask), addr(mask_t), mask_heads)
     return ctypes.pointer(o)
 
 

@@ -78,6 +78,24 @@ def test_capi_validation_returns_before_any_launch():
         assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(scale=bad), s) == 10012
     assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, fa_opts(scale=0.3), s) == 10005
     assert b"scale" in lib.fa_error_string(10012)
+    # masks: mask_heads 1 or Hq; the backward needs the transposed words too
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 4, 2, 8, 64, 0, fa_opts(mask=1, mask_heads=2),
+                         s) == 10014
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 4, 2, 8, 64, 0, fa_opts(mask=1, mask_heads=0),
+                         s) == 10014
+    for heads in (1, 4):  # forward: mask alone is enough
+        assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, 64, 1,
+                             fa_opts(mask=1, mask_heads=heads), s) == 10005
+    assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 4, 2, 8, 64, 0,
+                         fa_opts(mask=1, mask_heads=4), s) == 10014
+    assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 4, 2, 8, 64, 0,
+                         fa_opts(mask=1, mask_t=1, mask_heads=4), s) == 10006
+    assert b"mask_t" in lib.fa_error_string(10014)
+    # the packer: N, planes, pointers
+    assert lib.fa_pack_mask(one, 1, 0, one, one, s) == 10002
+    assert lib.fa_pack_mask(one, 0, 8, one, one, s) == 10004
+    assert lib.fa_pack_mask(z, 1, 8, one, None, s) == 10005
+    assert lib.fa_pack_mask(one, 1, 8, z, one, s) == 10005
     # BNHD puts every head of a row in one 32-bit buffer range
     assert lib.fa_fwd_ex(*([one] * 5), 1, 1 << 12, 1, 1 << 14, 128, 0, fa_opts(0, 1), s) == 10007
     assert b"layout" in lib.fa_error_string(10008)
@@ -94,6 +112,15 @@ def test_binding_rejects_host_tensors_with_reference_messages():
         fa_p100._ext.backward(x, x, x, x, x, torch.zeros(1, 2, 8), True)
     with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
         fa_p100.flash_attn(x, x, x, True)
+    # masks: checked on the host before any launch
+    with pytest.raises(RuntimeError, match="mask must be a CUDA tensor"):
+        fa_p100._ext.pack_mask(torch.ones(8, 8, dtype=torch.bool), True)
+    with pytest.raises(ValueError, match="boolean"):
+        fa_p100.flash_attn(x, x, x, True, attn_mask=torch.zeros(8, 8))
+    with pytest.raises(ValueError, match="attn_mask must be"):
+        fa_p100.flash_attn(x, x, x, True, attn_mask=torch.ones(3, 8, 8, dtype=torch.bool))
+    with pytest.raises(ValueError, match="packed attn_mask"):
+        fa_p100.flash_attn(x, x, x, True, attn_mask=(torch.zeros(1, 2, 8, 2, dtype=torch.int32),) * 2)
 
 
 def test_public_api_surface_matches_reference():
@@ -103,9 +130,10 @@ def test_public_api_surface_matches_reference():
     import fa_p100_hf
     sig = inspect.signature(fa_p100.flash_attn)
     # The reference's parameters, in order, with its defaults; the extensions
-    # (key lengths, sliding window, ALiBi slopes) come after them and default
-    # to None, so every reference call binds the same way.
-    extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids", "softmax_scale"]
+    # (key lengths, sliding window, ALiBi slopes, packing, scale, mask) come
+    # after them and default to None, so every reference call binds the same way.
+    extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids", "softmax_scale",
+                  "attn_mask"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False

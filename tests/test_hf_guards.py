@@ -23,7 +23,9 @@ MOD = types.SimpleNamespace(is_causal=True)
 
 
 @pytest.mark.parametrize("kwargs,match", [
-    (dict(attention_mask=torch.ones(1, 1, 4, 4)), "attention mask"),
+    (dict(attention_mask=torch.ones(1, 1, 4, 4)), "additive attention mask"),
+    (dict(attention_mask=torch.ones(1, 3, 4, 4, dtype=torch.bool)), "4-D attention mask"),
+    (dict(attention_mask=torch.ones(1, 1, 4, 4, dtype=torch.int32)), "boolean or floating"),
     (dict(attention_mask=None, output_attentions=True), "output_attentions"),
     (dict(attention_mask=None, head_mask=torch.ones(4)), "head_mask"),
     (dict(attention_mask=None, sliding_window=128, is_causal=False), "a window of 128"),
@@ -87,11 +89,17 @@ def test_register_and_enable():
     assert model.forward is inner
 
     ids = torch.zeros(1, 6, dtype=torch.long)
-    # Holes and all-zero rows still raise; right, left and both-sided padding
-    # are served (tests/test_gpu_kvlen.py runs them against eager with the mask).
+    # Holes and all-zero rows go to the kernels as key bit masks; right, left
+    # and both-sided padding as key lengths / sequence bounds
+    # (tests/test_gpu_kvlen.py and test_gpu_mask.py run them against eager
+    # with the mask). Host tensors stop at the binding's device check.
     for mask in ([[1, 1, 0, 1, 1, 1]], [[0, 0, 0, 0, 0, 0]], [[0, 1, 0, 1, 1, 0]]):
-        with pytest.raises(NotImplementedError, match="one run per row"):
+        with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
             model(ids, attention_mask=torch.tensor(mask))
+    # A 4-D mask is packed once in the wrapper (the packer's device check
+    # stops host tensors).
+    with pytest.raises(RuntimeError, match="mask must be a CUDA tensor"):
+        model(ids, attention_mask=torch.ones(1, 1, 6, 6, dtype=torch.bool).tril())
     assert hf.right_padding_lengths(torch.tensor([[1, 1, 1, 1, 0, 0], [1] * 6])).tolist() == [4, 6]
     assert hf.right_padding_lengths(torch.tensor([[1, 0, 1, 0, 0, 0]])) is None
     first, end = hf.padding_spans(torch.tensor([[0, 0, 1, 1, 1, 1], [1, 1, 1, 0, 0, 0],
@@ -147,10 +155,11 @@ def test_checkpointed_layers_see_the_padding_in_their_recompute(monkeypatch):
     seen = []
 
     def spy(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-            segment_ids=None, softmax_scale=None):
+            segment_ids=None, softmax_scale=None, attn_mask=None):
         seen.append((torch.is_grad_enabled(),
                      None if kv_len is None else kv_len.tolist(),
-                     None if segment_ids is None else segment_ids[0].tolist()))
+                     None if segment_ids is None else segment_ids[0].tolist(),
+                     None if attn_mask is None else attn_mask[0][:, 0, 0].tolist()))
         g = q.size(1) // k.size(1)
         return torch.nn.functional.scaled_dot_product_attention(
             q.float(), k.float().repeat_interleave(g, 1), v.float().repeat_interleave(g, 1),
@@ -166,15 +175,59 @@ def test_checkpointed_layers_see_the_padding_in_their_recompute(monkeypatch):
     model.gradient_checkpointing_enable()
     model.train()
     ids = torch.randint(0, 64, (2, 6))
-    for mask, kv_len, seg_start in (
-            (torch.tensor([[1, 1, 1, 1, 0, 0], [1, 1, 1, 1, 1, 1]]), [4, 6], None),  # right
-            (torch.tensor([[0, 0, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1]]), [6, 6],         # left
-             [[0, 0, 2, 2, 2, 2], [0, 0, 0, 0, 0, 0]])):
+    for mask, kv_len, seg_start, words in (
+            (torch.tensor([[1, 1, 1, 1, 0, 0], [1, 1, 1, 1, 1, 1]]), [4, 6], None, None),  # right
+            (torch.tensor([[0, 0, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1]]), [6, 6],               # left
+             [[0, 0, 2, 2, 2, 2], [0, 0, 0, 0, 0, 0]], None),
+            (torch.tensor([[1, 0, 1, 1, 0, 1], [1, 1, 1, 1, 1, 1]]), None, None,          # holes
+             [[0b101101], [0b111111]])):
         seen.clear()
         loss = model(ids, attention_mask=mask, labels=ids).loss
         first = list(seen)
         loss.backward()
         recompute = seen[len(first):]
         assert len(first) == len(recompute) == 2  # one call per layer, each replayed
-        for _, kl, ss in first + recompute:
-            assert kl == kv_len and ss == seg_start
+        for _, kl, ss, wd in first + recompute:
+            assert kl == kv_len and ss == seg_start and wd == words
+
+
+def test_mask_words_match_a_dense_packing():
+    """key_mask_bits (2-D padding masks with holes) against the bits of the
+    dense mask it stands for, packed on the host with numpy (bit j % 32 of
+    word j // 32, little-endian bit order), and its transpose."""
+    import numpy as np
+    rng = np.random.default_rng(3)
+    for n in (1, 5, 32, 33, 70):
+        m = torch.tensor(rng.random((3, n)) < 0.6)
+        bits, bits_t = hf.key_mask_bits(m)
+        dense = np.broadcast_to(m.numpy()[:, None, None, :], (3, 1, n, n))
+        w = (n + 31) // 32
+
+        def words(a):
+            pad = np.zeros(a.shape[:-1] + (w * 32,), dtype=bool)
+            pad[..., :n] = a
+            packed = np.packbits(pad, axis=-1, bitorder="little")
+            return packed.view("<u4").astype(np.int64)
+
+        got = bits.numpy().astype(np.int64) & 0xFFFFFFFF
+        got_t = bits_t.numpy().astype(np.int64) & 0xFFFFFFFF
+        assert bits.shape == bits_t.shape == (3, 1, n, w)
+        assert np.array_equal(got, words(dense))
+        assert np.array_equal(got_t, words(np.swapaxes(dense, -1, -2)))
+
+
+def test_dense_mask_checks_on_the_host():
+    """4-D masks: boolean, or additive with 0 / blocking values only; the
+    causal flag survives only when nothing above the diagonal is allowed.
+    Host tensors pass the checks and stop at the packer's device check."""
+    n = 6
+    tril = torch.ones(n, n, dtype=torch.bool).tril()[None, None]
+    additive = torch.zeros(1, 1, n, n).masked_fill(~tril, float("-inf"))
+    finfo_min = torch.zeros(1, 1, n, n).masked_fill(~tril, torch.finfo(torch.float32).min)
+    for m in (tril, additive, finfo_min, tril.expand(2, 4, n, n)):
+        with pytest.raises(RuntimeError, match="mask must be a CUDA tensor"):
+            hf.dense_mask_bits(m, 2, 4)
+    with pytest.raises(NotImplementedError, match="bias"):
+        hf.dense_mask_bits(additive + 0.5 * tril, 2, 4)
+    with pytest.raises(NotImplementedError, match="4-D attention mask"):
+        hf.dense_mask_bits(tril.expand(3, 1, n, n), 2, 4)

@@ -482,3 +482,88 @@ def test_softmax_scale_pins(causal):
             fd = (ora.attention_loss(*plus, do, causal, scale=sc)
                   - ora.attention_loss(*minus, do, causal, scale=sc)) / (2 * h)
             assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
+
+
+def _fd_check(rng, grads, q, k, v, do, causal, probes=3, **opts):
+    h = 1e-4
+    for which, g in enumerate(grads):
+        for _ in range(probes):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, causal, **opts)
+                  - ora.attention_loss(*minus, do, causal, **opts)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < 1e-6 * max(1.0, abs(fd))
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_mask_pins(causal):
+    """An arbitrary boolean mask (an extension: the reference takes none,
+    fa_p100_hf.py:64-70). Pinned against torch SDPA with the same boolean
+    attn_mask and autograd in float64 (per-head and head-shared masks); the
+    special masks that reduce to features pinned above (lower triangle =
+    causal, key columns = kv_len, block diagonal = packed sequences); an
+    empty row (o = 0, lse = +inf, no gradient through it); finite
+    differences; and a planted transposed mask that SDPA rejects."""
+    rng = np.random.default_rng(61 + causal)
+    b, hq, hkv, n, d = 2, 4, 2, 21, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    i, j = np.arange(n)[:, None], np.arange(n)[None, :]
+    mask = rng.random((b, hq, n, n)) < 0.4
+    mask |= (i == j)[None, None]  # every row keeps a key (causal too)
+    o, lse = ora.attention_fwd(q, k, v, causal, mask=mask)
+    grads = ora.attention_bwd(q, k, v, do, causal, mask=mask)
+    allowed = mask & (j <= i) if causal else mask
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    ref = F.scaled_dot_product_attention(tq, tk.repeat_interleave(hq // hkv, 1),
+                                         tv.repeat_interleave(hq // hkv, 1),
+                                         attn_mask=torch.tensor(allowed))
+    ref.backward(torch.tensor(do))
+    assert np.allclose(o, ref.detach().numpy(), atol=1e-12)
+    for got, t in zip(grads, (tq, tk, tv)):
+        assert np.allclose(got, t.grad.numpy(), atol=1e-10)
+    s = np.matmul(q, np.swapaxes(np.repeat(k, hq // hkv, 1), -1, -2)) / math.sqrt(d)
+    s = np.where(allowed, s, -np.inf)
+    assert np.allclose(lse, np.log(np.exp(s - s.max(-1, keepdims=True)).sum(-1))
+                       + s.max(-1), atol=1e-12)
+    _fd_check(rng, grads, q, k, v, do, causal, mask=mask)
+    # Planted: the transposed mask gives other values.
+    assert not np.allclose(ora.attention_fwd(q, k, v, causal, mask=np.swapaxes(mask, -1, -2))[0],
+                           o, atol=1e-6)
+    # One plane shared by every head == that plane repeated per head.
+    shared = mask[:, :1]
+    assert np.array_equal(ora.attention_fwd(q, k, v, causal, mask=shared)[0],
+                          ora.attention_fwd(q, k, v, causal,
+                                            mask=np.repeat(shared, hq, 1))[0])
+    # Special masks: the lower triangle is causal; key columns below kv_len
+    # are kv_len; the block diagonal of runs is packed sequences.
+    tril = np.broadcast_to(j <= i, (b, 1, n, n))
+    for got, want in zip(ora.attention_bwd(q, k, v, do, False, mask=tril),
+                         ora.attention_bwd(q, k, v, do, True)):
+        assert np.allclose(got, want, atol=1e-12)
+    lens = np.array([n, 9])
+    cols = (j[None] < lens[:, None, None])[:, None]  # (B, 1, 1, N)
+    assert np.allclose(ora.attention_fwd(q, k, v, causal, mask=cols)[0],
+                       ora.attention_fwd(q, k, v, causal, kv_len=lens)[0], atol=1e-12)
+    seg = np.array([[0] * 6 + [1] * 15, [2] * 13 + [5] * 8])
+    block = (seg[:, :, None] == seg[:, None, :])[:, None]
+    assert np.allclose(ora.attention_fwd(q, k, v, causal, mask=block)[0],
+                       ora.attention_fwd(q, k, v, causal, segments=seg)[0], atol=1e-12)
+    # An empty row: o = 0, lse = +inf; the gradients equal those of a run in
+    # which that row attends everywhere but receives no upstream gradient.
+    e_mask = mask.copy()
+    e_mask[1, 2, 7] = False
+    o_e, lse_e = ora.attention_fwd(q, k, v, causal, mask=e_mask)
+    assert np.all(o_e[1, 2, 7] == 0) and np.isinf(lse_e[1, 2, 7]) and lse_e[1, 2, 7] > 0
+    g_e = ora.attention_bwd(q, k, v, do, causal, mask=e_mask)
+    f_mask, f_do = mask.copy(), do.copy()
+    f_mask[1, 2, 7] = True
+    f_do[1, 2, 7] = 0
+    g_f = ora.attention_bwd(q, k, v, f_do, causal, mask=f_mask)
+    assert np.all(g_e[0][1, 2, 7] == 0)
+    for got, want in zip(g_e, g_f):
+        assert np.allclose(got, want, atol=1e-12)
