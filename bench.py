@@ -76,11 +76,12 @@ QWEN3_C5 = dict(layers=28, hidden=1024, heads=16, kv_heads=8, head_dim=128, inte
                 vocab=151936, seq=8192)
 
 
-def qwen3_bench(steps, warmup):
+def qwen3_bench(steps, warmup, impls=("fa_p100", "sdpa")):
     """a random-init Qwen3-0.6B-shaped decoder, B=1, seq
     8192, token ids uniform over the vocabulary, one forward + backward
     (fp16 autocast) per step, attention through the HF hook ("fa_p100"), and
-    the same step with transformers' "sdpa" attention on the same weights."""
+    the same step with transformers' "sdpa" attention on the same weights
+    (`impls` picks which of the two run, for kernel traces of one)."""
     import torch
     from transformers import Qwen3Config, Qwen3ForCausalLM
     import fa_p100_hf
@@ -105,7 +106,7 @@ def qwen3_bench(steps, warmup):
         return loss
 
     out = {}
-    for impl in ("fa_p100", "sdpa"):
+    for impl in impls:
         if impl == "fa_p100":
             fa_p100_hf.enable_fa_p100(model)
         else:
@@ -387,6 +388,8 @@ def main():
                     help="first run one device copy of MIB MiB (counter calibration)")
     ap.add_argument("--no-d64", action="store_true",
                     help="skip the D=64 leg beside the headline (C3) line")
+    ap.add_argument("--c5-impl", default="both", choices=["both", "fa_p100", "sdpa"],
+                    help="C5: run only the hook's step or only sdpa's (kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU "
@@ -396,7 +399,11 @@ def main():
 
     if args.config == "C5":
         import torch
-        r = qwen3_bench(args.steps, args.warmup)
+        impls = ("fa_p100", "sdpa") if args.c5_impl == "both" else (args.c5_impl,)
+        r = qwen3_bench(args.steps, args.warmup, impls)
+        if args.c5_impl != "both":
+            print(json.dumps({"c5_impl": args.c5_impl, **r[args.c5_impl]}), flush=True)
+            return
         fa, sd = r["fa_p100"], r["sdpa"]
         print(json.dumps({
             "metric": "Qwen3-0.6B-shaped training step (fwd+bwd), attention through the HF hook",

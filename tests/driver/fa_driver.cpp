@@ -18,6 +18,14 @@
 //                           v_mfma_f32_32x32x16_f16 chains on every SIMD, the
 //                           measured ceiling for the roofline (the reference's
 //                           half2 peak sweep measured its SIMT ceiling).
+//   fa_driver dqcost        the dQ traffic a backward without the dQ pass
+//                           would carry (the reference's design,
+//                           flash_bwd.cuh:434-443, accumulates dQ across key
+//                           tiles): one 64 x D fp32 partial per (key tile,
+//                           query step) of the causal C3 shape, sent as
+//                           global fp32 atomics into dQ, or stored to a
+//                           workspace for a later reduction; no compute.
+//                           Timed beside the library's own backward.
 //
 // Inputs come from a fixed-seed splitmix64 + Box-Muller generator, rounded to
 // fp16; the oracle sees exactly those fp16 values.
@@ -27,6 +35,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <string>
 #include <vector>
@@ -394,6 +403,103 @@ int cmd_peak() {
   return 0;
 }
 
+// One item per (head, key tile u, query step i0) of a causal backward with
+// 128-key tiles and 64-row query steps, dealt out evenly over the grid (the
+// library balances its causal work the same way). mode 0: each item adds its
+// 64 x D fp32 partial into dQ rows i0 .. i0+63 with no-return fp32 atomics;
+// mode 1: each item stores the partial to its own workspace slot (the first
+// half of a store-then-reduce scheme). Consecutive threads touch consecutive
+// floats, so every wave's accesses are fully coalesced.
+__global__ __launch_bounds__(256) void dq_traffic_kernel(float* dq, float* ws,
+                                                         const int2* items, int n_items,
+                                                         int per_block, int N, int D,
+                                                         int mode) {
+  const int first = blockIdx.x * per_block;
+  const int last = min(first + per_block, n_items);
+  for (int it = first; it < last; ++it) {
+    const int2 hi = items[it];  // (head, first query row)
+    float* dst = mode == 0 ? dq + ((size_t)hi.x * N + hi.y) * D : ws + (size_t)it * 64 * D;
+    for (int e = threadIdx.x; e < 64 * D; e += 256) {
+      const float v = (float)((e + it) & 7) * 0.125f;
+      if (mode == 0) unsafeAtomicAdd(dst + e, v);
+      else dst[e] = v;
+    }
+  }
+}
+
+int cmd_dqcost() {
+  const int B = 1, H = 8, N = 4096, D = 128, tiles = N / 128;
+  std::vector<int2> items;
+  for (int h = 0; h < H; ++h)
+    for (int u = 0; u < tiles; ++u)
+      for (int i0 = 128 * u; i0 < N; i0 += 64) items.push_back(make_int2(h, i0));
+  const int n_items = (int)items.size();
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, 0));
+  const int blocks = prop.multiProcessorCount;
+  const int per_block = (n_items + blocks - 1) / blocks;
+  int2* d_items = dalloc<int2>(items.size());
+  HIP_OK(hipMemcpy(d_items, items.data(), items.size() * sizeof(int2), hipMemcpyHostToDevice));
+  float* dq = dalloc<float>((size_t)B * H * N * D);
+  float* ws = dalloc<float>((size_t)n_items * 64 * D);
+  HIP_OK(hipMemset(dq, 0, (size_t)B * H * N * D * sizeof(float)));
+  hipEvent_t e0, e1;
+  HIP_OK(hipEventCreate(&e0));
+  HIP_OK(hipEventCreate(&e1));
+  const double bytes = (double)n_items * 64 * D * sizeof(float);
+  const char* names[2] = {"fp32 atomics into dQ", "stores to a workspace"};
+  for (int mode = 0; mode < 2; ++mode) {
+    std::vector<float> ms_all;
+    for (int rep = 0; rep < 12; ++rep) {
+      HIP_OK(hipEventRecord(e0, nullptr));
+      hipLaunchKernelGGL(dq_traffic_kernel, dim3(blocks), dim3(256), 0, nullptr, dq, ws, d_items,
+                         n_items, per_block, N, D, mode);
+      HIP_OK(hipGetLastError());
+      HIP_OK(hipEventRecord(e1, nullptr));
+      HIP_OK(hipEventSynchronize(e1));
+      float ms = 0;
+      HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+      if (rep >= 2) ms_all.push_back(ms);
+    }
+    std::sort(ms_all.begin(), ms_all.end());
+    const double med = ms_all[ms_all.size() / 2];
+    std::printf("dqcost: %d partials of 64 x %d fp32 (%.1f MiB), %s: median %.1f us "
+                "(%.0f GB/s)\n", n_items, D, bytes / 1048576.0, names[mode], med * 1e3,
+                bytes / (med * 1e-3) / 1e9);
+  }
+  // The library's backward on the same shape, for scale (fa_bwd: preprocess +
+  // the one main kernel, whose dQ pass recomputes S and dP instead).
+  Shape s{B, H, H, N, D, true};
+  _Float16 *q = dalloc<_Float16>(s.nq()), *k = dalloc<_Float16>(s.nk()),
+           *v = dalloc<_Float16>(s.nk()), *g = dalloc<_Float16>(s.nq()),
+           *o = dalloc<_Float16>(s.nq()), *dk = dalloc<_Float16>(s.nk()),
+           *dv = dalloc<_Float16>(s.nk());
+  float* lse = dalloc<float>((size_t)B * H * N);
+  Rng rng{77};
+  std::vector<_Float16> h(s.nq());
+  for (_Float16* t : {q, k, v, g}) {  // standard-normal inputs, as bench.py
+    for (auto& x : h) x = (_Float16)rng.normal();
+    HIP_OK(hipMemcpy(t, h.data(), h.size() * sizeof(_Float16), hipMemcpyHostToDevice));
+  }
+  FA_OK_(fa_fwd(q, k, v, o, lse, B, H, H, N, D, 1, 0, nullptr));
+  const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, H, N, D);
+  void* bws = dalloc<char>(ws_bytes);
+  std::vector<float> ms_all;
+  for (int rep = 0; rep < 12; ++rep) {
+    HIP_OK(hipEventRecord(e0, nullptr));
+    FA_OK_(fa_bwd(q, k, v, g, o, lse, dq, dk, dv, bws, ws_bytes, B, H, H, N, D, 1, nullptr));
+    HIP_OK(hipEventRecord(e1, nullptr));
+    HIP_OK(hipEventSynchronize(e1));
+    float ms = 0;
+    HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+    if (rep >= 2) ms_all.push_back(ms);
+  }
+  std::sort(ms_all.begin(), ms_all.end());
+  std::printf("dqcost: fa_bwd (with its dQ pass) on the same shape: median %.1f us\n",
+              ms_all[ms_all.size() / 2] * 1e3);
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -402,6 +508,7 @@ int main(int argc, char** argv) {
   if (cmd == "fd") return cmd_fd();
   if (cmd == "bench") return cmd_bench(argc > 2 && std::string(argv[2]) == "quick");
   if (cmd == "peak") return cmd_peak();
-  std::fprintf(stderr, "usage: %s check | fd | bench [quick] | peak\n", argv[0]);
+  if (cmd == "dqcost") return cmd_dqcost();
+  std::fprintf(stderr, "usage: %s check | fd | bench [quick] | peak | dqcost\n", argv[0]);
   return 2;
 }
