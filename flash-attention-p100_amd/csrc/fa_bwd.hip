@@ -82,7 +82,7 @@ constexpr int kSplitBias = 5;
 // next step's direct loads are filling and does not wait for those loads.
 template <int D>
 struct BwdLds {
-  static constexpr int kTileHalves = Swz<D>::template bytes<kSub>() / 2;  // staged tile
+  static constexpr int kTileHalves = Stream<D>::template bytes<kSub>() / 2;  // staged tile
   static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();  // resident K or V
   // Partial-sum exchange regions (they reuse the tiles once a phase's loop is
   // done): D/32 accumulators x 16 floats per lane for one wave.
@@ -90,6 +90,10 @@ struct BwdLds {
   static_assert(kRegionBytes <= kTileHalves * 2 && 2 * kRegionBytes <= kKVTileHalves * 2,
                 "exchange regions exceed the tiles");
 };
+
+// Lanes per row of the preprocess: D/8 rounded up to a power of two (the
+// row sum is a butterfly over them; lanes past D/8 add zeros).
+constexpr int pre_lanes_per_row(int D) { return D / 8 <= 8 ? 8 : 16; }
 
 // ---------------------------------------------------------------------------
 // Preprocess: dvec[row] = sum_d float(O[row,d]) * float(dO[row,d]) from the
@@ -104,7 +108,7 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
                                                       int Hq, int N, Strides st,
                                                       unsigned* __restrict__ counters,
                                                       int n_counters) {
-  constexpr int kLanesPerRow = D / 8;
+  constexpr int kLanesPerRow = pre_lanes_per_row(D);
   constexpr int kRowsPerBlock = 256 / kLanesPerRow;
   const int tid = threadIdx.x;
   // The main kernel's split-tile counters start at zero (it leaves them zero,
@@ -113,7 +117,7 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
   const long row = (long)blockIdx.x * kRowsPerBlock + tid / kLanesPerRow;
   const int c8 = (tid % kLanesPerRow) * 8;
   float acc = 0.f;
-  if (row < rows) {
+  if (row < rows && c8 < D) {
     // row = (b * Hq + hq) * N + n over the dense (B, Hq, N) vectors.
     const long bh = row / N, n = row - bh * N;
     const size_t off = (size_t)((bh / Hq) * st.b + (bh % Hq) * st.h + n * st.n) + c8;
@@ -213,8 +217,8 @@ struct KVWave {
                                        const float* dvs, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int row_lo, int row_end,
                                        float alibi_raw, uint32_t mtw, int lane, int roff,
-                                       const typename Swz<D>::Offsets& so, float c) {
-    using S = Swz<D>;
+                                       const typename Stream<D>::Offsets& so, float c) {
+    using S = Stream<D>;
     const int h = lane >> 5;
     floatx16 sacc = zero16(), pacc = zero16();
     // Operands read one k-step ahead of their products.
@@ -287,9 +291,9 @@ struct QWave {
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
                                        int i_row, int Nk, int key_lo, float alibi_raw,
                                        uint32_t mw, int lane,
-                                       const typename Swz<D>::Offsets& so, float c,
+                                       const typename Stream<D>::Offsets& so, float c,
                                        const Issue& issue) {
-    using S = Swz<D>;
+    using S = Stream<D>;
     const int h = lane >> 5;
     floatx16 st = zero16(), pt = zero16();
     // Operands are read one k-step ahead of their products, so that no
@@ -435,10 +439,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     return m + ((size_t)b * mask_heads + (mask_heads == 1 ? 0 : hq)) * N * W32;
   };
   const int roff = row_lane_off<D>(lane);  // resident tiles (padded rows)
-  typename Swz<D>::Offsets so;             // staged tiles (swizzled rows), rows 32*half ..
+  typename Stream<D>::Offsets so;          // staged tiles, rows 32*half ..
   so.init(lane, 32 * half);
 
-  SwzPlan<D, kSub, kWaves> plan_q, plan_k;  // staged 64-row tiles of Q/dO (phase 1), K/V (2)
+  StreamPlan<D, kSub, kWaves> plan_q, plan_k;  // staged 64-row tiles of Q/dO (phase 1), K/V (2)
   plan_q.init(wave, lane, stq.n);
   plan_k.init(wave, lane, stk.n);
   using P0 = std::integral_constant<int, 0>;
@@ -750,7 +754,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
 
 template <int D, bool BF>
 hipError_t launch_pre_d(const BwdArgs& a) {
-  constexpr int kRowsPerBlock = 256 / (D / 8);
+  constexpr int kRowsPerBlock = 256 / pre_lanes_per_row(D);
   const long rows = (long)a.B * a.Hq * a.N;
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   hipLaunchKernelGGL((bwd_pre_kernel<D, BF>), grid, dim3(256), 0, (hipStream_t)a.stream,
@@ -795,7 +799,7 @@ hipError_t launch_main_d(const BwdArgs& a) {
 
 unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D) {
   const unsigned long long rows = (unsigned long long)B * Hq * N;
-  const unsigned long long rows_per_block = 256 / (D / 8);
+  const unsigned long long rows_per_block = 256 / pre_lanes_per_row(D);
   const unsigned long long pre = (rows + rows_per_block - 1) / rows_per_block * 256;
   const unsigned long long tiles = ((unsigned long long)N + kTile - 1) / kTile;
   const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hkv;
@@ -804,13 +808,19 @@ unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D) {
 }
 
 hipError_t launch_bwd_preprocess(const BwdArgs& a) {
-  if (a.dtype == kBF16) return a.D == 64 ? launch_pre_d<64, true>(a) : launch_pre_d<128, true>(a);
-  return a.D == 64 ? launch_pre_d<64, false>(a) : launch_pre_d<128, false>(a);
+  if (a.dtype == kBF16)
+    return a.D == 64 ? launch_pre_d<64, true>(a)
+         : a.D == 96 ? launch_pre_d<96, true>(a) : launch_pre_d<128, true>(a);
+  return a.D == 64 ? launch_pre_d<64, false>(a)
+       : a.D == 96 ? launch_pre_d<96, false>(a) : launch_pre_d<128, false>(a);
 }
 
 hipError_t launch_bwd_main(const BwdArgs& a) {
-  if (a.dtype == kBF16) return a.D == 64 ? launch_main_d<64, true>(a) : launch_main_d<128, true>(a);
-  return a.D == 64 ? launch_main_d<64, false>(a) : launch_main_d<128, false>(a);
+  if (a.dtype == kBF16)
+    return a.D == 64 ? launch_main_d<64, true>(a)
+         : a.D == 96 ? launch_main_d<96, true>(a) : launch_main_d<128, true>(a);
+  return a.D == 64 ? launch_main_d<64, false>(a)
+       : a.D == 96 ? launch_main_d<96, false>(a) : launch_main_d<128, false>(a);
 }
 
 }  // namespace fa

@@ -16,7 +16,7 @@
 namespace {
 
 int check_shape(int B, int Hq, int Hkv, int N, int D) {
-  if (D != 64 && D != 128) return FA_ERR_HEAD_DIM;
+  if (D != 64 && D != 96 && D != 128) return FA_ERR_HEAD_DIM;
   if (N <= 0) return FA_ERR_SEQLEN;
   if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return FA_ERR_HEADS;
   if (B <= 0) return FA_ERR_BATCH;
@@ -79,7 +79,7 @@ extern "C" {
 const char* fa_error_string(int err) {
   switch (err) {
     case FA_OK: return "success";
-    case FA_ERR_HEAD_DIM: return "head dim must be 64 or 128";
+    case FA_ERR_HEAD_DIM: return "head dim must be 64, 96 or 128";
     case FA_ERR_SEQLEN: return "N must be positive";
     case FA_ERR_HEADS: return "query heads (H) must be a multiple of key/value heads (Hkv)";
     case FA_ERR_BATCH: return "B must be positive";

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fa {
 
 typedef _Float16 half_t;
@@ -294,6 +296,51 @@ struct SwzPlan {
   }
 };
 
+// The padded-row layout of Tile<D> behind Swz<D>'s interface, for the
+// staged tiles of head dims whose rows do not pack into 1 KB load
+// instructions (2D does not divide 1024, e.g. D = 96). Logical row R sits at
+// LDS row perm16(R) with kStride = D/8 + 1 chunks per row; D/8 even makes
+// kStride odd, so both read patterns stay conflict-free (see Tile).
+template <int D>
+struct Pad {
+  using T = Tile<D>;
+  static_assert((D / 8) % 2 == 0, "odd row stride needs an even chunk count");
+  static constexpr int kRowBytes = T::kRowHalves * 2;
+  template <int ROWS>
+  static constexpr int bytes() { return T::template halves<ROWS>() * 2; }
+  struct Offsets {
+    int rd[D / 16];
+    int tr[D / 32][2];
+    __device__ __forceinline__ void init(int lane, int row0) {
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        rd[kk] = 2 * ((row0 + perm16(lane & 31)) * T::kRowHalves + 16 * kk + 8 * (lane >> 5));
+#pragma unroll
+      for (int cb = 0; cb < D / 32; ++cb) {
+        tr[cb][0] = 2 * (row0 * T::kRowHalves + 32 * cb + tr_lane_off<D>(lane));
+        tr[cb][1] = tr[cb][0] + 4 * T::kRowHalves;
+      }
+    }
+  };
+  __device__ __forceinline__ static half8 read16(const void* tile, const Offsets& o, int kk) {
+    return *reinterpret_cast<const half8*>(reinterpret_cast<const char*>(tile) + o.rd[kk]);
+  }
+  __device__ __forceinline__ static half8 tr_operand(const void* tile, int q, const Offsets& o,
+                                                     int cb) {
+    const char* p = reinterpret_cast<const char*>(tile) + 16 * q * kRowBytes;
+    const half4 lo = lds_read_tr(reinterpret_cast<const half_t*>(p + o.tr[cb][0]));
+    const half4 hi = lds_read_tr(reinterpret_cast<const half_t*>(p + o.tr[cb][1]));
+    return half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+};
+
+// Layout and load plan of tiles streamed every step: the swizzled rows when
+// whole rows fill the 1 KB load instructions, the padded rows otherwise.
+template <int D>
+constexpr bool kSwizzled = 1024 % (2 * D) == 0;
+template <int D>
+using Stream = std::conditional_t<kSwizzled<D>, Swz<D>, Pad<D>>;
+
 // Wait until this wave's direct-to-LDS (and other vector memory) loads landed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -313,6 +360,7 @@ struct TileLoad {
 template <int D, int ROWS, int NW, bool EVEN>
 struct TilePlan {
   using TL = TileLoad<D, ROWS, NW, EVEN>;
+  static constexpr int kParts = TL::kParts;
   uint32_t off[TL::kParts];
   uint32_t row_bytes;  // bytes between consecutive rows in global memory (2*D when dense)
 
@@ -336,6 +384,12 @@ struct TilePlan {
       lds_direct_buf<16>(tile + inst * 512, r, off[u], (uint32_t)r0 * row_bytes);
   }
 };
+
+// Load plan of a streamed tile (Stream<D>): SwzPlan, or TilePlan for the
+// padded rows, with the same kParts / part() interface.
+template <int D, int ROWS, int NW>
+using StreamPlan = std::conditional_t<kSwizzled<D>, SwzPlan<D, ROWS, NW>,
+                                      TilePlan<D, ROWS, NW, false>>;
 
 // Buffer resource over the n_rows rows of one head: rows of D halves
 // row_stride halves apart. Its size ends right after row n_rows-1, so any row

@@ -502,8 +502,11 @@ unsigned long long fwd_launch_items(int B, int Hq, int N, int D) {
 }
 
 hipError_t launch_fwd(const FwdArgs& a) {
-  if (a.dtype == kBF16) return a.D == 64 ? launch_fwd_d<64, true>(a) : launch_fwd_d<128, true>(a);
-  return a.D == 64 ? launch_fwd_d<64, false>(a) : launch_fwd_d<128, false>(a);
+  if (a.dtype == kBF16)
+    return a.D == 64 ? launch_fwd_d<64, true>(a)
+         : a.D == 96 ? launch_fwd_d<96, true>(a) : launch_fwd_d<128, true>(a);
+  return a.D == 64 ? launch_fwd_d<64, false>(a)
+       : a.D == 96 ? launch_fwd_d<96, false>(a) : launch_fwd_d<128, false>(a);
 }
 
 }  // namespace fa

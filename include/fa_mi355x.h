@@ -37,7 +37,7 @@ extern "C" {
 
 enum {
   FA_OK = 0,
-  FA_ERR_HEAD_DIM = 10001,   /* D not in {64, 128} (fa_p100_ext.cu:59, 111) */
+  FA_ERR_HEAD_DIM = 10001,   /* D not in {64, 96, 128} (fa_p100_ext.cu:59, 111: {64, 128}) */
   FA_ERR_SEQLEN = 10002,     /* N <= 0 (fa_p100_ext.cu:60, 112) */
   FA_ERR_HEADS = 10003,      /* Hkv <= 0 or Hq % Hkv != 0 (fa_p100_ext.cu:61, 113) */
   FA_ERR_BATCH = 10004,      /* B <= 0 */

@@ -24,7 +24,7 @@ def test_host_only_helpers():
     lib = load_capi()
     assert lib.fa_version().decode().startswith("fa_mi355x")
     assert lib.fa_error_string(0) == b"success"
-    assert b"64 or 128" in lib.fa_error_string(10001)
+    assert b"64, 96 or 128" in lib.fa_error_string(10001)
     assert b"multiple" in lib.fa_error_string(10003)
     # two (B, Hq, N) float32 vectors, each rounded up to 256 bytes; 0 if invalid.
     # dvec + lse2 (256-aligned), counters per key-tile pair (by Hq), then two
@@ -43,7 +43,7 @@ def test_capi_validation_returns_before_any_launch():
     s = ctypes.c_void_p(0)
     z = ctypes.c_void_p(0)
     # head dim, sequence length, heads, batch, null pointers
-    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 96, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 80, 0, 0, s) == 10001
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 0, 64, 0, 0, s) == 10002
     assert lib.fa_fwd(z, z, z, z, z, 1, 4, 3, 8, 64, 0, 0, s) == 10003
     assert lib.fa_fwd(z, z, z, z, z, 0, 2, 2, 8, 64, 0, 0, s) == 10004

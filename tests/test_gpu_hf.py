@@ -31,7 +31,7 @@ def logits_with(model, impl, ids):
         return model(ids).logits.float()
 
 
-@pytest.mark.parametrize("head_dim,heads,kv", [(64, 8, 2), (128, 4, 4)])
+@pytest.mark.parametrize("head_dim,heads,kv", [(64, 8, 2), (96, 8, 4), (128, 4, 4)])
 def test_hook_logits_within_eager_sdpa_envelope(head_dim, heads, kv):
     import fa_p100_hf
     model = qwen3(2, 512, heads, kv, head_dim, 1024, 1000).eval()

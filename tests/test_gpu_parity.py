@@ -58,7 +58,7 @@ def check_grads(got, ref, what):
 
 
 # ---------------------------------------------------------------------------
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("Hq,Hkv", [(8, 8), (8, 2), (8, 1)])
 @pytest.mark.parametrize("N", [1, 7, 63, 64, 65, 333, 1023])
 def test_forward_matrix(D, Hq, Hkv, N):
@@ -76,7 +76,7 @@ def test_forward_matrix(D, Hq, Hkv, N):
         assert err <= LSE_MAX_ABS, f"lse D{D} {Hq}/{Hkv} N{N} causal={causal}: {err:.3e}"
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 2), (8, 1)])
 @pytest.mark.parametrize("N", [7, 64, 129, 333])
 @pytest.mark.parametrize("causal", [False, True])
@@ -92,7 +92,7 @@ def test_gradient_matrix(D, Hq, Hkv, N, causal):
 
 @pytest.mark.parametrize("regime,scale", [("1 N(0,1)", 1.0), ("2 large x10", 10.0),
                                           ("3 near-uniform", 0.05), ("4 near-one-hot", 3.0)])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_input_regimes(regime, scale, D, causal):
     """test_fa_p100.py:107-139: q, k scaled, v and dO N(0,1), (1,4,256,D).
@@ -159,7 +159,7 @@ def test_capi_rejects_bad_arguments_without_launching():
     lse = torch.zeros(1, 2, 8, device=DEV)
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     s = ctypes.c_void_p(0)
-    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 96, 0, 0, s) == 10001
+    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 80, 0, 0, s) == 10001
     assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 0, 64, 0, 0, s) == 10002
     assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 3, 2, 8, 64, 0, 0, s) == 10003
     assert lib.fa_fwd(None, p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 64, 0, 0, s) == 10005
@@ -176,8 +176,8 @@ def test_reference_error_messages_on_device():
         fa._ext.forward(h(1, 2, 8, 64).float(), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
     with pytest.raises(RuntimeError, match=r"q must be \(B, H, N, D\)"):
         fa._ext.forward(h(2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
-    with pytest.raises(RuntimeError, match="head dim must be 64 or 128, got 96"):
-        fa._ext.forward(h(1, 2, 8, 96), h(1, 2, 8, 96), h(1, 2, 8, 96), False, False)
+    with pytest.raises(RuntimeError, match="head dim must be 64, 96 or 128, got 80"):
+        fa._ext.forward(h(1, 2, 8, 80), h(1, 2, 8, 80), h(1, 2, 8, 80), False, False)
     with pytest.raises(RuntimeError, match="N must be positive"):
         fa._ext.forward(h(1, 2, 0, 64), h(1, 2, 0, 64), h(1, 2, 0, 64), False, False)
     with pytest.raises(RuntimeError, match=r"query heads \(3\) must be a multiple of key/value heads \(2\)"):
@@ -221,7 +221,7 @@ def test_backward_is_deterministic():
         assert np.array_equal(x, y)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("Hq,Hkv,N", [(4, 4, 200), (8, 2, 333), (2, 1, 64)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_half_dq_is_the_rounded_fp32_dq(D, Hq, Hkv, N, causal):
@@ -250,7 +250,7 @@ def test_half_dq_is_the_rounded_fp32_dq(D, Hq, Hkv, N, causal):
     assert torch.equal(dq, dq16) and torch.equal(dk, dk16) and torch.equal(dv, dv16)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("B,Hq,Hkv,N", [(1, 4, 4, 200), (2, 8, 2, 333), (1, 2, 1, 64)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_bnhd_views_match_dense_bit_for_bit(D, B, Hq, Hkv, N, causal):
@@ -303,7 +303,7 @@ def test_bnhd_capi_matches_dense_capi():
         assert torch.equal(tb(a), b)
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [64, 96, 128])
 @pytest.mark.parametrize("B,Hq,Hkv,N", [(1, 4, 4, 1536), (2, 8, 2, 1000)])
 def test_split_key_tiles_share_a_workspace_across_calls(D, B, Hq, Hkv, N):
     """Causal backward: the first key tiles' phase-1 work is split between two
