@@ -107,7 +107,7 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
                                                       float* __restrict__ lse2, long rows,
                                                       int Hq, int N, Strides st,
                                                       unsigned* __restrict__ counters,
-                                                      int n_counters) {
+                                                      int n_counters, int dr) {
   constexpr int kLanesPerRow = pre_lanes_per_row(D);
   constexpr int kRowsPerBlock = 256 / kLanesPerRow;
   const int tid = threadIdx.x;
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(256) void bwd_pre_kernel(const half_t* __restrict__
   const long row = (long)blockIdx.x * kRowsPerBlock + tid / kLanesPerRow;
   const int c8 = (tid % kLanesPerRow) * 8;
   float acc = 0.f;
-  if (row < rows && c8 < D) {
+  if (row < rows && c8 < dr) {
     // row = (b * Hq + hq) * N + n over the dense (B, Hq, N) vectors.
     const long bh = row / N, n = row - bh * N;
     const size_t off = (size_t)((bh / Hq) * st.b + (bh % Hq) * st.h + n * st.n) + c8;
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     int split_num, int split_bias, const int* __restrict__ kv_len, int window,
     const float* __restrict__ alibi, const int* __restrict__ seg_start,
     const int* __restrict__ seg_end, const uint32_t* __restrict__ mask,
-    const uint32_t* __restrict__ mask_t, int mask_heads) {
+    const uint32_t* __restrict__ mask_t, int mask_heads, int dr) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     return packed_nc ? max(0, min(sst[j], j)) : 0;
   };
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
-  const rsrc_t rk = rows_rsrc<D>(K + kv_off, N, stk.n), rv = rows_rsrc<D>(V + kv_off, N, stk.n);
+  const rsrc_t rk = rows_rsrc(K + kv_off, N, stk.n, dr), rv = rows_rsrc(V + kv_off, N, stk.n, dr);
   // Offset of query head hq's row 0 in Q, dO, dQ.
   auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
   // Arbitrary mask (BITMASK instantiation): query head hq's bit plane,
@@ -443,8 +443,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   so.init(lane, 32 * half);
 
   StreamPlan<D, kSub, kWaves> plan_q, plan_k;  // staged 64-row tiles of Q/dO (phase 1), K/V (2)
-  plan_q.init(wave, lane, stq.n);
-  plan_k.init(wave, lane, stk.n);
+  plan_q.init(wave, lane, stq.n, dr);
+  plan_k.init(wave, lane, stk.n, dr);
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
   // 16 KB-class exchange regions: the four staged tiles, then the halves of
@@ -496,7 +496,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     KVWave<D, CAUSAL, BOUNDS, BF> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
-      plan_kv.init(wave, lane, stk.n);
+      plan_kv.init(wave, lane, stk.n, dr);
 #pragma unroll
       for (int u = 0; u < decltype(plan_kv)::TL::kParts; ++u) {
         plan_kv.part(kres, rk, tp0, wave, u);
@@ -520,8 +520,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const int i0 = i_start + (it % n_qt) * kSub;
       const int hq = hkv * group + g;
       const size_t bhq = (size_t)b * Hq + hq;
-      const rsrc_t rq = rows_rsrc<D>(Q + q_off(hq), N, stq.n);
-      const rsrc_t ro = rows_rsrc<D>(dO + q_off(hq), N, stq.n);
+      const rsrc_t rq = rows_rsrc(Q + q_off(hq), N, stq.n, dr);
+      const rsrc_t ro = rows_rsrc(dO + q_off(hq), N, stq.n, dr);
 #pragma unroll
       for (int u = 0; u < decltype(plan_q)::kParts; ++u) {
         plan_q.part(tq, rq, i0, wave, u);
@@ -639,8 +639,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             k4[e] = to16<BF>(w.acc[D / 32 + cb][4 * g4 + e] * scale);
             v4[e] = to16<BF>(w.acc[cb][4 * g4 + e]);
           }
-          *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
-          *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
+          if (cb * 32 + 8 * g4 + 4 * h < dr) {  // columns past the head dim are padding
+            *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
+            *reinterpret_cast<half4*>(dvrow + cb * 32 + 8 * g4 + 4 * h) = v4;
+          }
         }
       }
     }
@@ -674,8 +676,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       QWave<D, CAUSAL, BOUNDS, BF> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
-        w.qb[kk] = as_half8(load16(Qg + (size_t)i_row * stq.n + kk * 16 + h * 8, row_ok));
-        w.ob[kk] = as_half8(load16(dOg + (size_t)i_row * stq.n + kk * 16 + h * 8, row_ok));
+        const bool col_ok = row_ok && kk * 16 + h * 8 < dr;
+        w.qb[kk] = as_half8(load16(Qg + (size_t)i_row * stq.n + kk * 16 + h * 8, col_ok));
+        w.ob[kk] = as_half8(load16(dOg + (size_t)i_row * stq.n + kk * 16 + h * 8, col_ok));
       }
       w.lse2 = row_ok ? Lse2[bhq * N + i_row] : 0.f;
       w.dvv = row_ok ? Dvec[bhq * N + i_row] : 0.f;
@@ -733,7 +736,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
               half4 v4;
 #pragma unroll
               for (int e = 0; e < 4; ++e) v4[e] = to16<BF>(w.acc[cb][4 * g4 + e] * scale);
-              *reinterpret_cast<half4*>(dQh + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
+              if (cb * 32 + 8 * g4 + 4 * h < dr)
+                *reinterpret_cast<half4*>(dQh + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
             }
         } else {
 #pragma unroll
@@ -743,7 +747,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
               floatx4 v4;
 #pragma unroll
               for (int e = 0; e < 4; ++e) v4[e] = w.acc[cb][4 * g4 + e] * scale;
-              *reinterpret_cast<floatx4*>(dQ + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
+              if (cb * 32 + 8 * g4 + 4 * h < dr)
+                *reinterpret_cast<floatx4*>(dQ + row_off + cb * 32 + 8 * g4 + 4 * h) = v4;
             }
         }
       }
@@ -759,7 +764,7 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   const dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
   hipLaunchKernelGGL((bwd_pre_kernel<D, BF>), grid, dim3(256), 0, (hipStream_t)a.stream,
                      (const half_t*)a.o, (const half_t*)a.dO, a.lse, a.dvec, a.lse2, rows, a.Hq,
-                     a.N, make_strides(a.layout, a.Hq, a.N, D), a.counters, a.n_counters);
+                     a.N, make_strides(a.layout, a.Hq, a.N, a.D), a.counters, a.n_counters, a.D);
   return hipGetLastError();
 }
 
@@ -767,15 +772,17 @@ template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
-  const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)D);
+  // D is the tile width; a.D the head dim in memory, which sets the default
+  // scale and the strides.
+  const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D);
   hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
-                     a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D), a.counters, a.slots,
+                     a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, a.D),
+                     make_strides(a.layout, a.Hkv, a.N, a.D), a.counters, a.slots,
                      a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
-                     a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads);
+                     a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.D);
   return hipGetLastError();
 }
 
@@ -799,7 +806,7 @@ hipError_t launch_main_d(const BwdArgs& a) {
 
 unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D) {
   const unsigned long long rows = (unsigned long long)B * Hq * N;
-  const unsigned long long rows_per_block = 256 / pre_lanes_per_row(D);
+  const unsigned long long rows_per_block = 256 / pre_lanes_per_row(padded_head_dim(D));
   const unsigned long long pre = (rows + rows_per_block - 1) / rows_per_block * 256;
   const unsigned long long tiles = ((unsigned long long)N + kTile - 1) / kTile;
   const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hkv;
@@ -808,19 +815,21 @@ unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D) {
 }
 
 hipError_t launch_bwd_preprocess(const BwdArgs& a) {
+  const int w = padded_head_dim(a.D);
   if (a.dtype == kBF16)
-    return a.D == 64 ? launch_pre_d<64, true>(a)
-         : a.D == 96 ? launch_pre_d<96, true>(a) : launch_pre_d<128, true>(a);
-  return a.D == 64 ? launch_pre_d<64, false>(a)
-       : a.D == 96 ? launch_pre_d<96, false>(a) : launch_pre_d<128, false>(a);
+    return w == 32 ? launch_pre_d<32, true>(a) : w == 64 ? launch_pre_d<64, true>(a)
+         : w == 96 ? launch_pre_d<96, true>(a) : launch_pre_d<128, true>(a);
+  return w == 32 ? launch_pre_d<32, false>(a) : w == 64 ? launch_pre_d<64, false>(a)
+       : w == 96 ? launch_pre_d<96, false>(a) : launch_pre_d<128, false>(a);
 }
 
 hipError_t launch_bwd_main(const BwdArgs& a) {
+  const int w = padded_head_dim(a.D);
   if (a.dtype == kBF16)
-    return a.D == 64 ? launch_main_d<64, true>(a)
-         : a.D == 96 ? launch_main_d<96, true>(a) : launch_main_d<128, true>(a);
-  return a.D == 64 ? launch_main_d<64, false>(a)
-       : a.D == 96 ? launch_main_d<96, false>(a) : launch_main_d<128, false>(a);
+    return w == 32 ? launch_main_d<32, true>(a) : w == 64 ? launch_main_d<64, true>(a)
+         : w == 96 ? launch_main_d<96, true>(a) : launch_main_d<128, true>(a);
+  return w == 32 ? launch_main_d<32, false>(a) : w == 64 ? launch_main_d<64, false>(a)
+       : w == 96 ? launch_main_d<96, false>(a) : launch_main_d<128, false>(a);
 }
 
 }  // namespace fa

@@ -16,14 +16,17 @@
 namespace {
 
 int check_shape(int B, int Hq, int Hkv, int N, int D) {
-  if (D != 64 && D != 96 && D != 128) return FA_ERR_HEAD_DIM;
+  if (!fa::valid_head_dim(D)) return FA_ERR_HEAD_DIM;
   if (N <= 0) return FA_ERR_SEQLEN;
   if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return FA_ERR_HEADS;
   if (B <= 0) return FA_ERR_BATCH;
   // Kernels index rows of one (b, h) slice with 32-bit ints and whole tensors
-  // with 64-bit offsets; every launch is a 1-D grid whose work-item count
-  // (workgroups x threads) must fit the dispatch packet's 32-bit field.
-  if ((long long)N * D > INT_MAX) return FA_ERR_TOO_LARGE;
+  // with 64-bit offsets; a head's rows must span at most 2^30 bytes (lane
+  // offsets from 2^31 up mark columns past a narrow head dim as out of range,
+  // and the row offsets added to them stay clear of 2^32);
+  // every launch is a 1-D grid whose work-item count (workgroups x threads)
+  // must fit the dispatch packet's 32-bit field.
+  if ((long long)N * D > (1LL << 29)) return FA_ERR_TOO_LARGE;
   constexpr unsigned long long kMaxItems = 0xFFFFFFFFull;
   if (fa::fwd_launch_items(B, Hq, N, D) > kMaxItems ||
       fa::bwd_launch_items(B, Hq, Hkv, N, D) > kMaxItems)
@@ -31,10 +34,10 @@ int check_shape(int B, int Hq, int Hkv, int N, int D) {
   return FA_OK;
 }
 
-// The (B, N, H, D) layout addresses one head's rows through a 32-bit buffer
-// range that spans all H heads: (N - 1) * H * D + D halves must fit.
+// The (B, N, H, D) layout addresses one head's rows through a buffer range
+// that spans all H heads: (N - 1) * H * D + D halves, at most 2^30 bytes.
 int check_bnhd(int Hq, int N, int D) {
-  return (long long)N * Hq * D > INT_MAX ? FA_ERR_TOO_LARGE : FA_OK;
+  return (long long)N * Hq * D > (1LL << 29) ? FA_ERR_TOO_LARGE : FA_OK;
 }
 
 int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }
@@ -79,7 +82,7 @@ extern "C" {
 const char* fa_error_string(int err) {
   switch (err) {
     case FA_OK: return "success";
-    case FA_ERR_HEAD_DIM: return "head dim must be 64, 96 or 128";
+    case FA_ERR_HEAD_DIM: return "head dim must be a multiple of 8 from 8 to 128";
     case FA_ERR_SEQLEN: return "N must be positive";
     case FA_ERR_HEADS: return "query heads (H) must be a multiple of key/value heads (Hkv)";
     case FA_ERR_BATCH: return "B must be positive";

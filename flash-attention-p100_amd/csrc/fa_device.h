@@ -189,6 +189,11 @@ constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcWord3);
 }
+// A per-lane offset at or above 2^31 is past every resource this library
+// makes (the C ABI keeps a head's byte range within 2^30, so the scalar row
+// offsets added to it cannot carry the sum past 2^32), so the lane reads
+// zeros: the columns past a head dim that is narrower than the tile.
+constexpr uint32_t kOutOfRange = 0x80000000u;
 // Each lane loads `size` bytes (4 or 16) from voff + soff into LDS at
 // lds + size * lane (lds wave-uniform).
 template <int size>
@@ -282,10 +287,12 @@ struct SwzPlan {
   uint32_t base;
   uint32_t row_bytes;  // bytes between consecutive rows in global memory (2*D when dense)
 
-  __device__ __forceinline__ void init(int wave, int lane, int row_stride) {
+  // dr: the head dim in memory (<= D); chunks past it load as zeros.
+  __device__ __forceinline__ void init(int wave, int lane, int row_stride, int dr) {
     row_bytes = 2u * (uint32_t)row_stride;
     const int r = S::kRowsPerInst * wave + lane / S::kChunks;  // row within part 0
-    base = (uint32_t)r * row_bytes + (uint32_t)(((lane % S::kChunks) ^ S::g(r)) * 16);
+    const int c = (lane % S::kChunks) ^ S::g(r);               // global chunk of this lane
+    base = (uint32_t)r * row_bytes + (uint32_t)(c * 16) + (c < dr / 8 ? 0u : kOutOfRange);
   }
   // Part u of the load of rows r0 .. r0+ROWS-1 of the buffer `r` (rows of D
   // halves, row_bytes apart) into `tile`; rows past the buffer's end read as
@@ -334,10 +341,11 @@ struct Pad {
   }
 };
 
-// Layout and load plan of tiles streamed every step: the swizzled rows when
-// whole rows fill the 1 KB load instructions, the padded rows otherwise.
+// Layout and load plan of tiles streamed every step: the swizzled rows for
+// the widths whose rows fill the 1 KB load instructions and whose swizzle g
+// is defined (64, 128), the padded rows otherwise.
 template <int D>
-constexpr bool kSwizzled = 1024 % (2 * D) == 0;
+constexpr bool kSwizzled = D == 64 || D == 128;
 template <int D>
 using Stream = std::conditional_t<kSwizzled<D>, Swz<D>, Pad<D>>;
 
@@ -364,7 +372,8 @@ struct TilePlan {
   uint32_t off[TL::kParts];
   uint32_t row_bytes;  // bytes between consecutive rows in global memory (2*D when dense)
 
-  __device__ __forceinline__ void init(int wave, int lane, int row_stride) {
+  // dr: the head dim in memory (<= D); chunks past it load as zeros.
+  __device__ __forceinline__ void init(int wave, int lane, int row_stride, int dr) {
     using T = Tile<D>;
     row_bytes = 2u * (uint32_t)row_stride;
 #pragma unroll
@@ -373,7 +382,8 @@ struct TilePlan {
       const int rho = p / T::kStride;
       const int c = p - rho * T::kStride;
       const int row = rho < ROWS ? perm16(rho) : 0;
-      off[u] = (uint32_t)row * row_bytes + (uint32_t)(c < T::kChunks ? c * 16 : 0);
+      off[u] = (uint32_t)row * row_bytes + (uint32_t)(c < T::kChunks ? c * 16 : 0) +
+               (c < T::kChunks && c >= dr / 8 ? kOutOfRange : 0u);
     }
   }
   // Loads part u of the tile whose first row is r0 from the buffer `r` (rows
@@ -391,12 +401,12 @@ template <int D, int ROWS, int NW>
 using StreamPlan = std::conditional_t<kSwizzled<D>, SwzPlan<D, ROWS, NW>,
                                       TilePlan<D, ROWS, NW, false>>;
 
-// Buffer resource over the n_rows rows of one head: rows of D halves
+// Buffer resource over the n_rows rows of one head: rows of dr halves
 // row_stride halves apart. Its size ends right after row n_rows-1, so any row
 // index >= n_rows reads as zeros.
-template <int D>
-__device__ __forceinline__ rsrc_t rows_rsrc(const half_t* base, int n_rows, int row_stride) {
-  return make_rsrc(base, ((uint32_t)n_rows - 1u) * 2u * (uint32_t)row_stride + 2u * D);
+__device__ __forceinline__ rsrc_t rows_rsrc(const half_t* base, int n_rows, int row_stride,
+                                            int dr) {
+  return make_rsrc(base, ((uint32_t)n_rows - 1u) * 2u * (uint32_t)row_stride + 2u * (uint32_t)dr);
 }
 
 }  // namespace fa

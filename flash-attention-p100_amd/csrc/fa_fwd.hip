@@ -109,7 +109,7 @@ struct FwdWave {
     floatx16 s = sc;
     floatx16 sn = zero16();
     constexpr int kS = D / 16;  // products of the next S^T
-    constexpr int kFront = 2;  // issued before the row max (covers its latency)
+    constexpr int kFront = kS > 2 ? 2 : 1;  // issued before the row max (covers its latency)
 #pragma unroll
     for (int kk = 0; kk < kFront; ++kk)
       if constexpr (NEXT) {
@@ -190,7 +190,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          float* __restrict__ Lse, int N, int Nk, int W,
                                          const int* __restrict__ sst, const int* __restrict__ sen,
                                          float alibi_raw, const uint32_t* __restrict__ mbase,
-                                         int W32, int sq, int sk,
+                                         int W32, int sq, int sk, int dr,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
@@ -209,7 +209,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const bool row_ok = !BOUNDS || i_row < N;
 #pragma unroll
   for (int kk = 0; kk < D / 16; ++kk)
-    w.qb[kk] = as_half8(load16(Q + (size_t)i_row * sq + kk * 16 + h * 8, row_ok));
+    w.qb[kk] = as_half8(load16(Q + (size_t)i_row * sq + kk * 16 + h * 8,
+                               row_ok && kk * 16 + h * 8 < dr));
 #pragma unroll
   for (int cb = 0; cb < D / 32; ++cb) w.oacc[cb] = zero16();
   w.m_raw = -INFINITY;
@@ -270,8 +271,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // redundant copy lands only in a buffer nobody reads in that step).
   using TL = typename L::TL;
   TilePlan<D, kKV, kWaves, false> plan;
-  plan.init(wave, lane, sk);
-  const rsrc_t rk = rows_rsrc<D>(K, Nk, sk), rv = rows_rsrc<D>(V, Nk, sk);
+  plan.init(wave, lane, sk, dr);
+  const rsrc_t rk = rows_rsrc(K, Nk, sk, dr), rv = rows_rsrc(V, Nk, sk, dr);
   const int k1 = min(j_lo + 1, n_it - 1) * kKV;
 #pragma unroll
   for (int u = 0; u < TL::kParts; ++u) {
@@ -389,7 +390,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     // A row that saw no key (key lengths with a window: pad rows past the
     // window) gets O = 0 and LSE = +inf, so its backward P is 0 as well.
     const float inv_l = l_star > 0.f ? 1.f / l_star : 0.f;
-    if (row_ok) {
+    if (row_ok && cb * 32 < dr) {  // d-blocks past the head dim hold padding
       half_t* orow = O + (size_t)i_row * sq + cb * 32;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -404,7 +405,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
         half4 o4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) o4[e] = to16<BF>(acc[e] * inv_l);
-        *reinterpret_cast<half4*>(orow + 8 * g + 4 * h) = o4;
+        if (cb * 32 + 8 * g + 4 * h < dr) *reinterpret_cast<half4*>(orow + 8 * g + 4 * h) = o4;
       }
       if (cb == 0 && h == 0)
         Lse[i_row] = l_star > 0.f ? (m_star * c + __log2f(l_star)) * kLn2 : INFINITY;
@@ -420,7 +421,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
     Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi,
     const int* __restrict__ seg_start, const int* __restrict__ seg_end,
-    const uint32_t* __restrict__ mask, int mask_heads) {
+    const uint32_t* __restrict__ mask, int mask_heads, int dr) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -454,7 +455,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
                                 Lse + (size_t)bh * N, N, Nk, window,
                                 seg_start ? seg_start + (size_t)b * N : nullptr,
                                 seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, mbase,
-                                W32, stq.n, stk.n,
+                                W32, stq.n, stk.n, dr,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
@@ -466,13 +467,15 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
   const int BH = a.B * a.Hq;
   dim3 grid(xcd_grid(gx * BH));
-  const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)D));
+  // D is the tile width; a.D the head dim in memory, which sets the default
+  // scale and the strides.
+  const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D));
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
-                     n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, D),
-                     make_strides(a.layout, a.Hkv, a.N, D), a.kv_len, a.window, a.alibi,
-                     a.seg_start, a.seg_end, a.mask, a.mask_heads);
+                     n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
+                     make_strides(a.layout, a.Hkv, a.N, a.D), a.kv_len, a.window, a.alibi,
+                     a.seg_start, a.seg_end, a.mask, a.mask_heads, a.D);
   return hipGetLastError();
 }
 
@@ -502,11 +505,12 @@ unsigned long long fwd_launch_items(int B, int Hq, int N, int D) {
 }
 
 hipError_t launch_fwd(const FwdArgs& a) {
+  const int w = padded_head_dim(a.D);
   if (a.dtype == kBF16)
-    return a.D == 64 ? launch_fwd_d<64, true>(a)
-         : a.D == 96 ? launch_fwd_d<96, true>(a) : launch_fwd_d<128, true>(a);
-  return a.D == 64 ? launch_fwd_d<64, false>(a)
-       : a.D == 96 ? launch_fwd_d<96, false>(a) : launch_fwd_d<128, false>(a);
+    return w == 32 ? launch_fwd_d<32, true>(a) : w == 64 ? launch_fwd_d<64, true>(a)
+         : w == 96 ? launch_fwd_d<96, true>(a) : launch_fwd_d<128, true>(a);
+  return w == 32 ? launch_fwd_d<32, false>(a) : w == 64 ? launch_fwd_d<64, false>(a)
+       : w == 96 ? launch_fwd_d<96, false>(a) : launch_fwd_d<128, false>(a);
 }
 
 }  // namespace fa

@@ -58,13 +58,22 @@ struct FwdArgs {
 //   the preprocess kernel zeroes (sized by Hq, which bounds Hkv, so that the
 //   preprocess needs no Hkv);
 //   two fp32 partial dK/dV slots per such pair and (b, kv head).
+// Head dims: any multiple of 8 from 8 to 128 (the `D` of the argument
+// structs, the row length in memory). The kernels are compiled for the
+// widths 32, 64, 96 and 128 and run a head dim on the smallest that holds
+// it: the extra columns load as zeros and are never stored.
+inline int padded_head_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128; }
+inline bool valid_head_dim(int D) { return D >= 8 && D <= 128 && D % 8 == 0; }
+
 constexpr int kBwdTile = 128;  // key rows of one backward workgroup
 struct BwdWorkspace {
   size_t dvec, lse2, counters, slots, total;
   int n_counters;
 };
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
-inline size_t bwd_slot_floats(int D) { return (size_t)kBwdTile * D * 2; }  // dK^T, dV^T
+inline size_t bwd_slot_floats(int D) {  // dK^T, dV^T at the padded width
+  return (size_t)kBwdTile * padded_head_dim(D) * 2;
+}
 inline BwdWorkspace bwd_workspace(int B, int Hq, int Hkv, int N, int D) {
   BwdWorkspace w;
   const size_t vec = align256((size_t)B * Hq * N * sizeof(float));

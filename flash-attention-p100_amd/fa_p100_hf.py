@@ -51,7 +51,7 @@ autocast stay bf16); the reference cast everything to fp16.
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): masks carrying a bias, output_attentions,
 head_mask, a window on non-causal attention, dropout, head_dim other than
-64/96/128, q_len != kv_len (KV-cache decoding). A scale other than 1/sqrt(D),
+not a multiple of 8 up to 128, q_len != kv_len (KV-cache decoding). A scale other than 1/sqrt(D),
 which the reference rejected, goes to the kernels.
 """
 import warnings
@@ -221,8 +221,9 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
         raise NotImplementedError(f"fa_p100 has no attention dropout (got {dropout}).")
 
     head_dim = query.size(-1)
-    if head_dim not in (64, 96, 128):
-        raise NotImplementedError(f"fa_p100 supports head_dim 64, 96 or 128, got {head_dim}.")
+    if not (8 <= head_dim <= 128 and head_dim % 8 == 0):
+        raise NotImplementedError(
+            f"fa_p100 supports head_dim multiples of 8 up to 128, got {head_dim}.")
     # The reference fixed scale = 1/sqrt(D) and raised on anything else; the
     # kernels take the model's scale (softmax_scale) when it differs.
     softmax_scale = None

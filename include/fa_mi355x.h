@@ -37,13 +37,13 @@ extern "C" {
 
 enum {
   FA_OK = 0,
-  FA_ERR_HEAD_DIM = 10001,   /* D not in {64, 96, 128} (fa_p100_ext.cu:59, 111: {64, 128}) */
+  FA_ERR_HEAD_DIM = 10001,   /* D not a multiple of 8 in [8, 128] (fa_p100_ext.cu:59, 111: {64, 128}) */
   FA_ERR_SEQLEN = 10002,     /* N <= 0 (fa_p100_ext.cu:60, 112) */
   FA_ERR_HEADS = 10003,      /* Hkv <= 0 or Hq % Hkv != 0 (fa_p100_ext.cu:61, 113) */
   FA_ERR_BATCH = 10004,      /* B <= 0 */
   FA_ERR_NULL = 10005,       /* a required pointer is NULL */
   FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
-  FA_ERR_TOO_LARGE = 10007,  /* N*D, or a launch's work-item count, exceeds 32 bits */
+  FA_ERR_TOO_LARGE = 10007,  /* N*D (BNHD: N*H*D) over 2^29, or a launch's work items over 2^32 */
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */

@@ -24,7 +24,7 @@ def test_host_only_helpers():
     lib = load_capi()
     assert lib.fa_version().decode().startswith("fa_mi355x")
     assert lib.fa_error_string(0) == b"success"
-    assert b"64, 96 or 128" in lib.fa_error_string(10001)
+    assert b"multiple of 8 from 8 to 128" in lib.fa_error_string(10001)
     assert b"multiple" in lib.fa_error_string(10003)
     # two (B, Hq, N) float32 vectors, each rounded up to 256 bytes; 0 if invalid.
     # dvec + lse2 (256-aligned), counters per key-tile pair (by Hq), then two
@@ -35,7 +35,10 @@ def test_host_only_helpers():
         2 * 768256 + 2 * 32 * 12 * 4 + 2 * 8 * 12 * 2 * 128 * 128 * 2 * 4)
     assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 512  # one key tile: no pairs
     assert lib.fa_bwd_workspace_bytes(1, 8, 3, 4096, 128) == 0
-    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 80) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 100) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 136) == 0
+    # narrower head dims take the slots of the tile width they run on (80 -> 96)
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 80) == lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 96)
 
 
 def test_capi_validation_returns_before_any_launch():
@@ -43,7 +46,9 @@ def test_capi_validation_returns_before_any_launch():
     s = ctypes.c_void_p(0)
     z = ctypes.c_void_p(0)
     # head dim, sequence length, heads, batch, null pointers
-    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 80, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 100, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 4, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 136, 0, 0, s) == 10001
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 0, 64, 0, 0, s) == 10002
     assert lib.fa_fwd(z, z, z, z, z, 1, 4, 3, 8, 64, 0, 0, s) == 10003
     assert lib.fa_fwd(z, z, z, z, z, 0, 2, 2, 8, 64, 0, 0, s) == 10004
@@ -57,7 +62,7 @@ def test_capi_validation_returns_before_any_launch():
     bf16 = 1
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(bf16, 2), s) == 10008
     assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 0, fa_opts(2, 0), s) == 10009
-    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 80, 0, fa_opts(bf16), s) == 10001
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 100, 0, fa_opts(bf16), s) == 10001
     assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, fa_opts(bf16, 1), s) == 10005
     assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 0, None, s) == 10005  # NULL: defaults
     assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 2, 2, 8, 64, 0, fa_opts(bf16), s) == 10006
@@ -186,12 +191,14 @@ def test_shape_limits_follow_the_one_dimensional_grids():
     """Every launch is a 1-D grid, so B*Hq is not bounded by a 65535 grid.y
     any more: B*Hq = 65536 (and well beyond) passes validation. What is
     bounded is each launch's work-item count (workgroups x threads), which
-    the dispatch packet holds in 32 bits, and N*D (32-bit row offsets);
+    the dispatch packet holds in 32 bits, and N*D (a head's rows within 2^30
+    bytes);
     fa_bwd_workspace_bytes returns 0 exactly for a shape validation rejects."""
     lib = load_capi()
     for B, Hq, Hkv, N, D in [(1, 65536, 65536, 64, 64), (2, 32768, 8, 128, 128),
-                             (65536, 1, 1, 1, 64), (1, 1, 1, 1 << 20, 128)]:
+                             (65536, 1, 1, 1, 64), (1, 1, 1, 1 << 20, 128),
+                             (1, 1, 1, 1 << 22, 128)]:
         assert lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D) > 0, (B, Hq, Hkv, N, D)
     # 2^23 query heads of 4096 rows need more than 2^32 forward work-items.
     assert lib.fa_bwd_workspace_bytes(1 << 13, 1 << 10, 1 << 10, 4096, 128) == 0
-    assert lib.fa_bwd_workspace_bytes(1, 1, 1, (1 << 31) // 64, 128) == 0  # N*D > 2^31-1
+    assert lib.fa_bwd_workspace_bytes(1, 1, 1, (1 << 22) + 1, 128) == 0  # N*D > 2^29

@@ -1,12 +1,15 @@
-"""Head dim 96 (beyond the reference, which takes 64 or 128 only,
-fa_p100_ext.cu:59, 111; Phi-3-style models use 96). The staged tiles of the
-backward use padded rows at this width (192-byte rows do not pack into the
-1 KB direct loads); the plain matrices run in test_gpu_parity.py with D=96
-added. Here: every option at D=96 against the float64 oracle (key lengths,
-window, ALiBi, packed sequences, mask, softmax scale), split key tiles over
-long causal rows, bf16, the (B, N, H, D) views and the C ABI bit-identical to
-the dense op. Bars: the fp16 ones (helpers.py), bf16's from
-test_gpu_bf16.py."""
+"""Head dims other than 64 and 128 (the reference takes those two only,
+fa_p100_ext.cu:59, 111). The kernels run at the tile widths 32, 64, 96 and
+128; a head dim between them runs on the next wider one, its extra columns
+loaded as zeros and never stored. At width 96 (and 32) the backward's staged
+tiles use padded rows (192-byte rows do not pack into the 1 KB direct
+loads). The plain matrices run in test_gpu_parity.py with D=96 added. Here:
+every multiple of 8 from 8 to 128 against the float64 oracle; every option
+at D=96 and D=80 (key lengths, window, ALiBi, packed sequences, mask,
+softmax scale); split key tiles over long causal rows; bf16, the
+(B, N, H, D) views and the C ABI bit-identical to the dense op; and Qwen3
+with head_dim 80 through the hook. Bars: the fp16 ones (helpers.py),
+bf16's from test_gpu_bf16.py."""
 import ctypes
 
 import numpy as np
@@ -40,6 +43,23 @@ def check(o, lse, grads, q, k, v, do, causal, what, **opts):
 
 
 @pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("Dh", list(range(8, 129, 8)))
+def test_every_head_dim_matches_oracle(Dh, causal):
+    """Each multiple of 8 up to 128 on a ragged shape with GQA and two key
+    tiles per workgroup (the causal split included)."""
+    import fa_p100
+    B, Hq, Hkv, N = 2, 4, 2, 397
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, Dh, seed=Dh + causal)
+    qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    o = fa_p100.flash_attn(qg, kg, vg, causal)
+    o.backward(do.to(DEV))
+    _, lse = fa_p100._ext.forward(qg.detach(), kg.detach(), vg.detach(), causal, False)
+    torch.cuda.synchronize()
+    assert o.shape == q.shape and qg.grad.shape == q.shape and kg.grad.shape == k.shape
+    check(o, lse, (qg.grad, kg.grad, vg.grad), q, k, v, do, causal, f"D{Dh} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("B,Hq,Hkv,N", [(1, 4, 4, 2048), (2, 8, 2, 1000), (1, 2, 1, 4096)])
 def test_d96_long_rows_match_oracle(B, Hq, Hkv, N, causal):
     """Long rows: several key tiles per workgroup, the causal split of key
@@ -55,8 +75,9 @@ def test_d96_long_rows_match_oracle(B, Hq, Hkv, N, causal):
           f"D96 {B},{Hq}/{Hkv},N{N} causal={causal}")
 
 
+@pytest.mark.parametrize("D", [96, 80])
 @pytest.mark.parametrize("causal", [True, False])
-def test_d96_every_option_matches_oracle(causal):
+def test_d96_every_option_matches_oracle(causal, D):
     """Key lengths, ALiBi, a softmax scale, packed sequences, a mask, and a
     window when causal, all at once."""
     import fa_p100
@@ -87,10 +108,11 @@ def test_d96_every_option_matches_oracle(causal):
                                      window, kw["alibi_slopes"], s0, s1, 0.09, bits)
     torch.cuda.synchronize()
     check(o, lse, (qg.grad, kg.grad, vg.grad), q, k, v, do, causal,
-          f"D96 options causal={causal}", **opts)
+          f"D{D} options causal={causal}", **opts)
 
 
-def test_d96_bf16_bnhd_and_capi():
+@pytest.mark.parametrize("D", [96, 40])
+def test_d96_bf16_bnhd_and_capi(D):
     """bf16 against the oracle; (B, N, H, D) views bit-identical to the dense
     op; fa_fwd / fa_bwd (fp16) and fa_fwd_ex / fa_bwd_ex (bf16) through the C
     ABI bit-identical to the op."""
@@ -148,3 +170,17 @@ def test_d96_bf16_bnhd_and_capi():
     assert torch.equal(oh, o_ref) and torch.equal(lh, l_ref)
     dq_ref, dk_ref, dv_ref = fa_p100._ext.backward(qh, kh, vh, gh, oh, lh, True)
     assert torch.equal(dq32, dq_ref) and torch.equal(dkh, dk_ref) and torch.equal(dvh, dv_ref)
+
+
+def test_hf_hook_head_dim_80_matches_eager():
+    """Qwen3 with head_dim 80 (a width between the tiles) through the hook:
+    logits within the eager-vs-sdpa envelope."""
+    import fa_p100_hf
+    from test_gpu_hf import logits_with, qwen3
+    model = qwen3(2, 640, 8, 4, 80, 1024, 1000).eval()
+    ids = torch.randint(0, 1000, (2, 300), device=DEV, generator=torch.Generator(DEV).manual_seed(2))
+    eager, sdpa = logits_with(model, "eager", ids), logits_with(model, "sdpa", ids)
+    fa_p100_hf.enable_fa_p100(model)
+    fa = logits_with(model, "fa_p100", ids)
+    env, gap = (sdpa - eager).abs(), (fa - eager).abs()
+    assert gap.mean() <= 2 * env.mean() + 1e-4, (gap.mean().item(), env.mean().item())

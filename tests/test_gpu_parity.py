@@ -159,7 +159,7 @@ def test_capi_rejects_bad_arguments_without_launching():
     lse = torch.zeros(1, 2, 8, device=DEV)
     p = lambda t: ctypes.c_void_p(t.data_ptr())
     s = ctypes.c_void_p(0)
-    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 80, 0, 0, s) == 10001
+    assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 100, 0, 0, s) == 10001
     assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 2, 2, 0, 64, 0, 0, s) == 10002
     assert lib.fa_fwd(p(x), p(x), p(x), p(x), p(lse), 1, 3, 2, 8, 64, 0, 0, s) == 10003
     assert lib.fa_fwd(None, p(x), p(x), p(x), p(lse), 1, 2, 2, 8, 64, 0, 0, s) == 10005
@@ -176,8 +176,8 @@ def test_reference_error_messages_on_device():
         fa._ext.forward(h(1, 2, 8, 64).float(), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
     with pytest.raises(RuntimeError, match=r"q must be \(B, H, N, D\)"):
         fa._ext.forward(h(2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
-    with pytest.raises(RuntimeError, match="head dim must be 64, 96 or 128, got 80"):
-        fa._ext.forward(h(1, 2, 8, 80), h(1, 2, 8, 80), h(1, 2, 8, 80), False, False)
+    with pytest.raises(RuntimeError, match="head dim must be a multiple of 8 from 8 to 128, got 100"):
+        fa._ext.forward(h(1, 2, 8, 100), h(1, 2, 8, 100), h(1, 2, 8, 100), False, False)
     with pytest.raises(RuntimeError, match="N must be positive"):
         fa._ext.forward(h(1, 2, 0, 64), h(1, 2, 0, 64), h(1, 2, 0, 64), False, False)
     with pytest.raises(RuntimeError, match=r"query heads \(3\) must be a multiple of key/value heads \(2\)"):

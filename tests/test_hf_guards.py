@@ -39,8 +39,8 @@ def test_unsupported_requests_raise(kwargs, match):
 
 
 def test_head_dim_scale_and_kv_len_guards():
-    q, k, v = qkv(d=80)
-    with pytest.raises(NotImplementedError, match="head_dim 64, 96 or 128, got 80"):
+    q, k, v = qkv(d=100)
+    with pytest.raises(NotImplementedError, match="multiples of 8 up to 128, got 100"):
         hf.fa_p100_attention_forward(MOD, q, k, v, None)
     q, k, v = qkv(d=128)
     # Another scale passes the guards now (the host tensors then stop at the
