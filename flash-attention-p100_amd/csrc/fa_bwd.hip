@@ -216,7 +216,8 @@ struct KVWave {
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int row_lo, int row_end,
-                                       float alibi_raw, uint32_t mtw, int lane, int roff,
+                                       float alibi_raw, uint32_t mtw, uint32_t ztw, float zs,
+                                       int lane, int roff,
                                        const typename Stream<D>::Offsets& so, float c) {
     using S = Stream<D>;
     const int h = lane >> 5;
@@ -263,8 +264,11 @@ struct KVWave {
         float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
         if (CAUSAL || BOUNDS) p = (idx >= lo) ? p : 0.f;
         if (BOUNDS) p = (idx < hi && ((mtw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
-        pb[r >> 3][r & 7] = to16<BF>(p);
-        sb[r >> 3][r & 7] = to16<BF>(p * (pacc[r] - d4[e]));
+        // Dropout (keep bits ztw, scale zs): dV sees the kept P, and the
+        // gradient of P is the kept dP scaled.
+        const bool keep = (ztw >> (idx + 4 * h)) & 1u;
+        pb[r >> 3][r & 7] = to16<BF>(keep ? p : 0.f);
+        sb[r >> 3][r & 7] = to16<BF>(p * ((keep ? pacc[r] * zs : 0.f) - d4[e]));
       }
     }
     // dV^T += dO^T P, dK^T += Q^T dS; k-step q = query rows 32m+16q .. +15.
@@ -290,7 +294,7 @@ struct QWave {
   template <class Issue>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
                                        int i_row, int Nk, int key_lo, float alibi_raw,
-                                       uint32_t mw, int lane,
+                                       uint32_t mw, uint32_t zw, float zs, int lane,
                                        const typename Stream<D>::Offsets& so, float c,
                                        const Issue& issue) {
     using S = Stream<D>;
@@ -332,7 +336,9 @@ struct QWave {
       float p = fast_exp2(fmaf(st[r], c, -lse2));
       if (CAUSAL) p = (idx <= lo) ? p : 0.f;
       if (BOUNDS) p = (idx < hi && idx >= lw && ((mw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
-      sb[r >> 3][r & 7] = to16<BF>(p * (pt[r] - dvv));
+      // Dropout: the gradient of P is the kept dP scaled by zs.
+      const bool keep = (zw >> (idx + 4 * h)) & 1u;
+      sb[r >> 3][r & 7] = to16<BF>(p * ((keep ? pt[r] * zs : 0.f) - dvv));
     }
     // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15 (operands one ahead).
     half8 kt = S::tr_operand(Ks, 0, so, 0);
@@ -363,7 +369,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     int split_num, int split_bias, const int* __restrict__ kv_len, int window,
     const float* __restrict__ alibi, const int* __restrict__ seg_start,
     const int* __restrict__ seg_end, const uint32_t* __restrict__ mask,
-    const uint32_t* __restrict__ mask_t, int mask_heads, int dr) {
+    const uint32_t* __restrict__ mask_t, int mask_heads, const uint32_t* __restrict__ drop,
+    const uint32_t* __restrict__ drop_t, float drop_scale, int dr) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -438,6 +445,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   auto plane = [&](const uint32_t* m, int hq) {
     return m + ((size_t)b * mask_heads + (mask_heads == 1 ? 0 : hq)) * N * W32;
   };
+  // Dropout keep bits (BITMASK instantiation): one plane per (b, query head),
+  // in the mask's two layouts; zs scales the kept probabilities.
+  auto zplane = [&](const uint32_t* z, int hq) { return z + ((size_t)b * Hq + hq) * N * W32; };
+  const float zs = BITMASK ? drop_scale : 1.f;
   const int roff = row_lane_off<D>(lane);  // resident tiles (padded rows)
   typename Stream<D>::Offsets so;          // staged tiles, rows 32*half ..
   so.init(lane, 32 * half);
@@ -545,12 +556,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           BOUNDS && alibi ? alibi[hkv * group + (it / n_qt)] / scale : 0.f;  // step's query head
       // Key j_col's mask word for the step's query rows (clamped: rows past N
       // are masked by row_end, keys past N have row_end = 0).
+      const size_t tword =
+          (size_t)min(j_col, N - 1) * W32 + min((i0 + 32 * half) >> 5, W32 - 1);
       const uint32_t mtw =
-          BITMASK ? plane(mask_t, hkv * group + it / n_qt)[(size_t)min(j_col, N - 1) * W32 +
-                                                            min((i0 + 32 * half) >> 5, W32 - 1)]
-                   : ~0u;
+          BITMASK && mask_t ? plane(mask_t, hkv * group + it / n_qt)[tword] : ~0u;
+      const uint32_t ztw =
+          BITMASK && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
       w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
-             alibi_raw, mtw, lane, roff, so, scale_log2);
+             alibi_raw, mtw, ztw, zs, lane, roff, so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -637,7 +650,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             k4[e] = to16<BF>(w.acc[D / 32 + cb][4 * g4 + e] * scale);
-            v4[e] = to16<BF>(w.acc[cb][4 * g4 + e]);
+            v4[e] = to16<BF>(w.acc[cb][4 * g4 + e] * zs);  // dropout: dV of the scaled P
           }
           if (cb * 32 + 8 * g4 + 4 * h < dr) {  // columns past the head dim are padding
             *reinterpret_cast<half4*>(dkrow + cb * 32 + 8 * g4 + 4 * h) = k4;
@@ -672,7 +685,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const half_t* Qg = Q + q_off(hq);
       const half_t* dOg = dO + q_off(hq);
       // This lane's row of the mask (rows past N are never stored).
-      const uint32_t* mrow = BITMASK ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
+      const uint32_t* mrow =
+          BITMASK && mask ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
+      const uint32_t* zrow =
+          BITMASK && drop ? zplane(drop, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
       QWave<D, CAUSAL, BOUNDS, BF> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
@@ -706,10 +722,11 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
             else plan_k.part(P ? ta0 : ta1, rk, jn, wave, q >> 1);
           }
         };
-        const uint32_t mw =
-            BITMASK ? mrow[min(t * (kSub / 32) + half, W32 - 1)] : ~0u;  // keys t*kSub + 32*half ..
+        const int word = min(t * (kSub / 32) + half, W32 - 1);  // keys t*kSub + 32*half ..
+        const uint32_t mw = mrow ? mrow[word] : ~0u;
+        const uint32_t zw = zrow ? zrow[word] : ~0u;
         w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, mw,
-               lane, so, scale_log2, issue);
+               zw, zs, lane, so, scale_log2, issue);
         wait_vmem();
         __syncthreads();
       };
@@ -782,17 +799,18 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, a.D),
                      make_strides(a.layout, a.Hkv, a.N, a.D), a.counters, a.slots,
                      a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
-                     a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.D);
+                     a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.drop,
+                     a.drop_t, a.drop_scale, a.D);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
-  // Key lengths, windows, packed sequences, ALiBi and masks need the masked
-  // instantiation (kTile is a multiple of kSub).
+  // Key lengths, windows, packed sequences and ALiBi need the masked
+  // instantiation (kTile is a multiple of kSub), masks and dropout the bit one.
   const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
-  if (a.mask)
+  if (a.mask || a.drop)
     return a.causal ? launch_main_t<D, true, true, true, BF>(a)
                     : launch_main_t<D, false, true, true, BF>(a);
   if (a.causal)

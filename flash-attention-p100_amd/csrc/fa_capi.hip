@@ -97,6 +97,9 @@ const char* fa_error_string(int err) {
     case FA_ERR_SCALE: return "softmax scale must be 0 (1/sqrt(D)) or positive and finite";
     case FA_ERR_MASK:
       return "mask_heads must be 1 or Hq, and the backward needs mask_t with mask";
+    case FA_ERR_DROPOUT:
+      return "dropout p must lie in [0, 1) and its scale be positive and finite; the backward "
+             "needs drop_t with drop";
     case FA_ERR_SCRATCH:
       return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
              "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
@@ -109,7 +112,8 @@ const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 // Options: every field checked; the defaults are fp16, (B, H, N, D), no key
 // lengths, no window, no ALiBi, no packed sequences, no mask.
 constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0,       nullptr,
-                                     nullptr,   nullptr,   0.f,     nullptr, nullptr, 0};
+                                     nullptr,   nullptr,   0.f,     nullptr, nullptr,
+                                     0,         nullptr,   nullptr, 0.f};
 
 // `backward`: the pass reads mask_t too.
 static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
@@ -122,7 +126,17 @@ static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
     if (op.mask_heads != 1 && op.mask_heads != Hq) return FA_ERR_MASK;
     if (backward && op.mask_t == nullptr) return FA_ERR_MASK;
   }
+  if (op.drop != nullptr) {
+    if (!(op.drop_scale > 0.f) || !std::isfinite(op.drop_scale)) return FA_ERR_DROPOUT;
+    if (backward && op.drop_t == nullptr) return FA_ERR_DROPOUT;
+  }
   return FA_OK;
+}
+
+// Keep threshold of a drop probability: 16-bit draws >= t are kept.
+static uint32_t dropout_threshold(float p) {
+  const double t = std::nearbyint((double)p * 65536.0);
+  return (uint32_t)(t < 0.0 ? 0.0 : t > 65535.0 ? 65535.0 : t);
 }
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
@@ -155,6 +169,8 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.scale = op.scale;
   a.mask = op.mask;
   a.mask_heads = op.mask_heads;
+  a.drop = op.drop;
+  a.drop_scale = op.drop ? op.drop_scale : 1.f;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -263,6 +279,9 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.mask = op.mask;
   a.mask_t = op.mask_t;
   a.mask_heads = op.mask_heads;
+  a.drop = op.drop;
+  a.drop_t = op.drop_t;
+  a.drop_scale = op.drop ? op.drop_scale : 1.f;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -336,6 +355,20 @@ int fa_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* b
   if (P <= 0) return FA_ERR_BATCH;
   if (!dense || !bits) return FA_ERR_NULL;
   return to_code(fa::launch_pack_mask(dense, P, N, bits, bits_t, stream));
+}
+
+int fa_dropout_bits(uint64_t seed, float p, int P, int N, uint32_t* bits, uint32_t* bits_t,
+                    void* stream) {
+  if (!(p >= 0.f && p < 1.f)) return FA_ERR_DROPOUT;
+  if (N <= 0) return FA_ERR_SEQLEN;
+  if (P <= 0) return FA_ERR_BATCH;
+  if (!bits) return FA_ERR_NULL;
+  return to_code(fa::launch_dropout_bits(seed, dropout_threshold(p), P, N, bits, bits_t, stream));
+}
+
+float fa_dropout_scale(float p) {
+  if (!(p >= 0.f && p < 1.f)) return 0.f;
+  return (float)(65536.0 / (65536.0 - (double)dropout_threshold(p)));
 }
 
 int fa_bwd_noalloc(const void* q, const void* k, const void* v, const void* dO, const void* o,

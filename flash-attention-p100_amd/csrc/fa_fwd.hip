@@ -103,7 +103,7 @@ struct FwdWave {
   template <bool MASK, bool NEXT, class Issue>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
                                        bool masked, int i_row, int N, int w_lo, float alibi_raw,
-                                       uint32_t mw, int lane, int roff,
+                                       uint32_t mw, uint32_t zw, int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
@@ -166,7 +166,9 @@ struct FwdWave {
         if (r < 16) {
           const float p = fast_exp2(fmaf(s[r], c, neg));
           l += p;
-          pb[r >> 3][r & 7] = to16<BF>(p);
+          // Dropout: the row sum keeps every key, P V only the kept ones.
+          const int jj = 8 * (r >> 2) + 4 * h + (r & 3);
+          pb[r >> 3][r & 7] = to16<BF>(((zw >> jj) & 1u) ? p : 0.f);
         }
       }
     }
@@ -190,6 +192,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          float* __restrict__ Lse, int N, int Nk, int W,
                                          const int* __restrict__ sst, const int* __restrict__ sen,
                                          float alibi_raw, const uint32_t* __restrict__ mbase,
+                                         const uint32_t* __restrict__ zbase, float o_scale,
                                          int W32, int sq, int sk, int dr,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
@@ -260,9 +263,13 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // then takes the mask. Word w covers keys 32w .. 32w+31, and a wave's 32
   // keys of step j are word (kKV / 32) j + kq (clamped: keys past N are
   // masked anyway).
-  const uint32_t* mrow = BITMASK ? mbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
+  // Dropout keep bits (BITMASK instantiation; zbase null: keep all) in the
+  // same layout, one plane per (b, query head).
+  const uint32_t* mrow = BITMASK && mbase ? mbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
+  const uint32_t* zrow = BITMASK && zbase ? zbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
   if (BITMASK) n_full = 0;
-  auto mword = [&](int j) { return BITMASK ? mrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
+  auto mword = [&](int j) { return mrow ? mrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
+  auto zword = [&](int j) { return zrow ? zrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
 
   // Software pipeline over steps j = 0 .. n_it-1. Step j reads K_{j+1} (for
   // the next S^T) from K buffer (j+1)%2 and V_j from V buffer j%2, while it
@@ -289,12 +296,16 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // compiler sees that the step's reads never touch the buffers its direct
   // loads fill and does not wait for those loads before them).
   uint32_t mw = mword(j_lo);  // mask bits of the next step to run
+  uint32_t zw = zword(j_lo);  // its dropout keep bits
   auto run = [&](int j, auto par_tag, auto mask_tag, auto next_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
-    const uint32_t mw_now = mw;
-    if (BITMASK && NEXT) mw = mword(j + 1);
+    const uint32_t mw_now = mw, zw_now = zw;
+    if (BITMASK && NEXT) {
+      mw = mword(j + 1);
+      zw = zword(j + 1);
+    }
     half_t* lk = P ? kt1 : kt0;  // receives K_{j+2}
     half_t* lv = P ? vt0 : vt1;  // receives V_{j+1}
     const int jk = min(j + 2, n_it - 1) * kKV;
@@ -312,7 +323,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
-                                lane_hi, w_lo, alibi_raw, mw_now, lane,
+                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -389,7 +400,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     }
     // A row that saw no key (key lengths with a window: pad rows past the
     // window) gets O = 0 and LSE = +inf, so its backward P is 0 as well.
-    const float inv_l = l_star > 0.f ? 1.f / l_star : 0.f;
+    const float inv_l = l_star > 0.f ? o_scale / l_star : 0.f;  // o_scale: dropout's 1/(1-p)
     if (row_ok && cb * 32 < dr) {  // d-blocks past the head dim hold padding
       half_t* orow = O + (size_t)i_row * sq + cb * 32;
 #pragma unroll
@@ -421,7 +432,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
     Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi,
     const int* __restrict__ seg_start, const int* __restrict__ seg_end,
-    const uint32_t* __restrict__ mask, int mask_heads, int dr) {
+    const uint32_t* __restrict__ mask, int mask_heads, const uint32_t* __restrict__ drop,
+    float drop_scale, int dr) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -445,8 +457,11 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const float alibi_raw = alibi ? alibi[hq] * kLog2e / scale_log2 : 0.f;
   // This (b, head)'s mask plane (a plane shared by all heads when mask_heads == 1).
   const int W32 = (N + 31) >> 5;
-  const uint32_t* mbase =
-      BITMASK ? mask + ((size_t)b * mask_heads + (mask_heads == 1 ? 0 : hq)) * N * W32 : nullptr;
+  const uint32_t* mbase = BITMASK && mask ? mask + ((size_t)b * mask_heads +
+                                                   (mask_heads == 1 ? 0 : hq)) * N * W32
+                                           : nullptr;
+  // ... and its dropout keep bits (one plane per (b, query head)).
+  const uint32_t* zbase = BITMASK && drop ? drop + (size_t)bh * N * W32 : nullptr;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
@@ -455,7 +470,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
                                 Lse + (size_t)bh * N, N, Nk, window,
                                 seg_start ? seg_start + (size_t)b * N : nullptr,
                                 seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, mbase,
-                                W32, stq.n, stk.n, dr,
+                                zbase, BITMASK ? drop_scale : 1.f, W32, stq.n, stk.n, dr,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
@@ -475,17 +490,17 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
                      make_strides(a.layout, a.Hkv, a.N, a.D), a.kv_len, a.window, a.alibi,
-                     a.seg_start, a.seg_end, a.mask, a.mask_heads, a.D);
+                     a.seg_start, a.seg_end, a.mask, a.mask_heads, a.drop, a.drop_scale, a.D);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
-  // Key lengths, windows, packed sequences, ALiBi and masks need the masked
-  // instantiation (kKV is a multiple of kBR).
+  // Key lengths, windows, packed sequences and ALiBi need the masked
+  // instantiation (kKV is a multiple of kBR), masks and dropout the bit one.
   const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
-  if (a.mask)
+  if (a.mask || a.drop)
     return a.causal ? launch_fwd_t<D, true, true, true, BF>(a)
                     : launch_fwd_t<D, false, true, true, BF>(a);
   if (a.causal)

@@ -50,6 +50,12 @@ struct FwdArgs {
   // 0 when mask_heads == 1). Applied on top of every other mask.
   const uint32_t* mask = nullptr;
   int mask_heads = 0;
+  // Attention dropout: keep bits in the mask's row layout with one plane per
+  // (b, query head) (bit set = keep), and the factor kept probabilities are
+  // scaled by (1 / (1 - p)). P stays normalised over every key; only P V
+  // sees the dropped probabilities.
+  const uint32_t* drop = nullptr;
+  float drop_scale = 1.f;
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -122,6 +128,9 @@ struct BwdArgs {
   // j) * W + i / 32 (set iff query i may attend key j); required with mask.
   const uint32_t* mask_t = nullptr;
   int mask_heads = 0;              // as FwdArgs::mask_heads
+  const uint32_t* drop = nullptr;  // as FwdArgs::drop
+  const uint32_t* drop_t = nullptr;  // its transpose (as mask_t); required with drop
+  float drop_scale = 1.f;          // as FwdArgs::drop_scale
 };
 
 hipError_t launch_fwd(const FwdArgs& a);
@@ -131,6 +140,11 @@ hipError_t launch_bwd_main(const BwdArgs& a);
 // FwdArgs::mask (bits) and BwdArgs::mask_t (bits_t, skipped when null).
 hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* bits_t,
                             void* stream);
+// Dropout keep bits for P planes of N x N (bits and, when not null, bits_t;
+// layouts as the mask's): key j of row i in plane p is kept iff its 16-bit
+// draw is at least `threshold` (see fa_dropout_bits).
+hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, uint32_t* bits,
+                               uint32_t* bits_t, void* stream);
 
 // Work-items (workgroups x threads) of the largest launch each pass makes for
 // a shape (either masking). An AMD dispatch packet counts its grid in

@@ -1,11 +1,14 @@
-// Bit-packing of a dense boolean attention mask into the two layouts the
-// kernels read: rows of W = ceil(N / 32) words per query (the forward and the
-// backward's dQ phase, one word per lane and 32-key step) and the transpose,
-// rows of W words per key (the backward's dK/dV phase, whose lanes own keys).
-// No counterpart in the reference, which takes no mask (fa_p100_hf.py:64-70).
+// Bit-packing of a dense boolean attention mask, and generation of dropout
+// keep bits, into the two layouts the kernels read: rows of W = ceil(N / 32)
+// words per query (the forward and the backward's dQ phase, one word per
+// lane and 32-key step) and the transpose, rows of W words per key (the
+// backward's dK/dV phase, whose lanes own keys). No counterpart in the
+// reference, which takes no mask and raises on dropout (fa_p100_hf.py:64-70, 83-85).
 //
-// Both kernels are HBM-bound byte work: N*N bytes in, N*N/8 bytes out per
-// plane. Grid-stride loops over 64-bit word indices keep the grid small.
+// The packers are HBM-bound byte work: N*N bytes in, N*N/8 bytes out per
+// plane; grid-stride loops over 64-bit word indices keep their grid small.
+// The dropout generator writes N*N/8 bytes per layout and plane and spends
+// one hash (two 32-bit multiplies) per two keys.
 #include <hip/hip_runtime.h>
 
 #include "fa_launch.h"
@@ -72,6 +75,62 @@ __global__ __launch_bounds__(kPackThreads) void pack_cols_kernel(const uint8_t* 
   }
 }
 
+// Integer hash `lowbias32` (C. Wellons, hash-prospector): xorshift-multiply
+// rounds with full avalanche, 2 multiplies per 32-bit output.
+__device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// Dropout keep bits. Draws: row key r = h(h(h(h(seed_lo) ^ seed_hi) ^ plane)
+// ^ row); keys 2k and 2k+1 of the row draw the low and high 16 bits of
+// h(r ^ k) (h = lowbias32); a key is kept iff its draw >= thr. Each wave
+// owns 64 consecutive rows of one plane and walks their words: lane l packs
+// row i0 + l's word, then 32 ballots transpose the 64 x 32 block (lane j
+// collects key j's bits of the wave's 64 rows, two transposed words).
+// Rows and keys past N get zero bits.
+__global__ __launch_bounds__(kPackThreads) void dropout_bits_kernel(
+    uint32_t seed_lo, uint32_t seed_hi, uint32_t thr, int N, int W, int row_blocks,
+    uint32_t* __restrict__ bits, uint32_t* __restrict__ bits_t) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int plane = blockIdx.x / row_blocks;
+  const int i0 = ((blockIdx.x % row_blocks) * (kPackThreads / 64) + wave) * 64;
+  if (i0 >= N) return;  // wave-uniform; no barriers below
+  const int i = i0 + lane;
+  const bool row_ok = i < N;
+  const uint32_t key =
+      lowbias32(lowbias32(lowbias32(lowbias32(seed_lo) ^ seed_hi) ^ (uint32_t)plane) ^ (uint32_t)i);
+  uint32_t* row_out = bits + ((size_t)plane * N + (row_ok ? i : 0)) * W;
+  for (int w = 0; w < W; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint32_t u = lowbias32(key ^ (uint32_t)(16 * w + k));
+      word |= (uint32_t)((u & 0xffffu) >= thr) << (2 * k);
+      word |= (uint32_t)((u >> 16) >= thr) << (2 * k + 1);
+    }
+    const int nk = N - 32 * w;  // keys of this word that exist (>= 1)
+    if (nk < 32) word &= (1u << nk) - 1u;
+    if (!row_ok) word = 0u;
+    if (row_ok) row_out[w] = word;
+    if (bits_t) {
+      uint32_t mine = 0u;
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const unsigned long long b = __ballot((word >> j) & 1u);
+        if ((lane & 31) == j) mine = lane < 32 ? (uint32_t)b : (uint32_t)(b >> 32);
+      }
+      const int kj = 32 * w + (lane & 31);  // this lane's key
+      const int rw = (i0 >> 5) + (lane >> 5);  // its word of query rows
+      if (kj < N && rw < W) bits_t[((size_t)plane * N + kj) * W + rw] = mine;
+    }
+  }
+}
+
 unsigned blocks_for(long long items) {
   const long long b = (items + kPackThreads - 1) / kPackThreads;
   return (unsigned)(b < kPackMaxBlocks ? (b > 0 ? b : 1) : kPackMaxBlocks);
@@ -94,6 +153,16 @@ hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, 
   if (e != hipSuccess || bits_t == nullptr) return e;
   hipLaunchKernelGGL(pack_cols_kernel, dim3(blocks_for(rows * W)), dim3(kPackThreads), 0,
                      (hipStream_t)stream, dense, bits_t, (long long)P, N, W);
+  return hipGetLastError();
+}
+
+hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, uint32_t* bits,
+                               uint32_t* bits_t, void* stream) {
+  const int W = (N + 31) / 32;
+  const int row_blocks = (N + kPackThreads - 1) / kPackThreads;
+  hipLaunchKernelGGL(dropout_bits_kernel, dim3((unsigned)((long long)P * row_blocks)),
+                     dim3(kPackThreads), 0, (hipStream_t)stream, (uint32_t)seed,
+                     (uint32_t)(seed >> 32), threshold, N, W, row_blocks, bits, bits_t);
   return hipGetLastError();
 }
 

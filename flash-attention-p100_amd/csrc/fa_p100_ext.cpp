@@ -11,7 +11,8 @@
 // Function: backward_half_dq (dq as fp16), forward_bnhd / backward_bnhd
 // (dense (B, N, H, D) tensors) and forward_dt / backward_dt (fp16 or bf16);
 // the last four take bf16 as well as fp16; pack_mask bit-packs a boolean
-// mask for their `mask` / `mask_t` arguments.
+// mask for their `mask` / `mask_t` arguments and dropout_bits draws the keep
+// bits for `drop` / `drop_t`.
 //
 // Plain C++ (no device code): every launch goes through the C ABI of
 // libfa_mi355x.so (include/fa_mi355x.h). Unlike the reference, which uses the
@@ -102,7 +103,10 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
                      const c10::optional<at::Tensor>& seg_start,
                      const c10::optional<at::Tensor>& seg_end, double scale,
                      const c10::optional<at::Tensor>& mask,
-                     const c10::optional<at::Tensor>& mask_t, int B, int H, int N) {
+                     const c10::optional<at::Tensor>& mask_t,
+                     const c10::optional<at::Tensor>& drop,
+                     const c10::optional<at::Tensor>& drop_t, double drop_scale, int B, int H,
+                     int N) {
   fa_options op{};
   op.dtype = dtype_code(q);
   op.layout = layout;
@@ -117,6 +121,12 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
   op.mask_t = mask_ptr(mask_t, q, B, H, N, "mask_t", &heads_t);
   TORCH_CHECK(!op.mask_t || (op.mask && heads_t == heads), "mask_t must come with a mask of its shape");
   op.mask_heads = heads;
+  int dheads = 0, dheads_t = 0;
+  op.drop = mask_ptr(drop, q, B, H, N, "drop", &dheads);
+  op.drop_t = mask_ptr(drop_t, q, B, H, N, "drop_t", &dheads_t);
+  TORCH_CHECK(!op.drop || dheads == H, "drop must hold one plane per query head");
+  TORCH_CHECK(!op.drop_t || (op.drop && dheads_t == H), "drop_t must come with drop");
+  op.drop_scale = (float)drop_scale;
   return op;
 }
 
@@ -240,7 +250,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
                                         c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -262,7 +273,7 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -275,7 +286,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
                                          bool causal, c10::optional<at::Tensor> kv_len,
                                          int64_t window, c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -301,7 +313,7 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -321,7 +333,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
                                       c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -346,7 +359,7 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -359,7 +372,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
                                        c10::optional<at::Tensor> kv_len, int64_t window,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
-    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t) {
+    double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -390,7 +404,7 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -428,7 +442,36 @@ std::vector<at::Tensor> fa_pack_mask_t(at::Tensor dense, bool transposed) {
   return {bits, bits_t};
 }
 
+// Dropout keep bits for `drop` / `drop_t`: int32 (B, H, N, ceil(N/32)) each on
+// the given device, drawn from `seed` with drop probability p (see
+// fa_dropout_bits), and the matching scale of the kept probabilities.
+std::vector<at::Tensor> fa_dropout_bits_t(int64_t seed, double p, int64_t B, int64_t H, int64_t N,
+                                          int64_t device) {
+  TORCH_CHECK(p >= 0.0 && p < 1.0, "dropout p must lie in [0, 1), got ", p);
+  TORCH_CHECK(B > 0 && H > 0 && N > 0 && B * H <= INT32_MAX && N <= INT32_MAX,
+              "dropout bits need positive B, H, N");
+  const at::Device dev(at::kCUDA, (c10::DeviceIndex)device);
+  c10::DeviceGuard guard(dev);
+  auto opts = at::TensorOptions().dtype(at::kInt).device(dev);
+  const int64_t W = (N + 31) / 32;
+  auto bits = at::empty({B, H, N, W}, opts);
+  auto bits_t = at::empty({B, H, N, W}, opts);
+  check_rc(fa_dropout_bits((uint64_t)seed, (float)p, (int)(B * H), (int)N,
+                           reinterpret_cast<uint32_t*>(bits.data_ptr<int>()),
+                           reinterpret_cast<uint32_t*>(bits_t.data_ptr<int>()),
+                           current_stream(bits)),
+           "fa_dropout_bits");
+  return {bits, bits_t};
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.def("dropout_bits", &fa_dropout_bits_t,
+        "Dropout keep bits (B, H, N, ceil(N/32)) and their transpose for drop / drop_t",
+        py::arg("seed"), py::arg("p"), py::arg("B"), py::arg("H"), py::arg("N"),
+        py::arg("device"));
+  m.def("dropout_scale", [](double p) { return (double)fa_dropout_scale((float)p); },
+        "Scale of the kept probabilities for dropout_bits(p): 1 / (1 - the drawn rate)",
+        py::arg("p"));
   m.def("pack_mask", &fa_pack_mask_t,
         "Bit-packs a dense boolean (..., N, N) mask for the mask / mask_t arguments",
         py::arg("mask"), py::arg("transposed") = true);
@@ -441,25 +484,29 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
-        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
-        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
-        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
         py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
-        py::arg("mask") = py::none(), py::arg("mask_t") = py::none());
+        py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
 }

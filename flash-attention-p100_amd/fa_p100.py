@@ -68,7 +68,7 @@ class _FlashAttnP100(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None,
-                segs=None, scale=0.0, mask=None):
+                segs=None, scale=0.0, mask=None, drop=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -81,18 +81,20 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.segs = segs
         ctx.scale = scale
         ctx.mask = mask
+        ctx.drop = drop
         seg_start, seg_end = segs if segs is not None else (None, None)
         bits, bits_t = mask if mask is not None else (None, None)
+        z, z_t, z_scale = drop if drop is not None else (None, None, 1.0)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
-                                        seg_end, scale, bits)
+                                        seg_end, scale, bits, drop=z, drop_scale=z_scale)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
         if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
-                or segs is not None or scale or mask is not None):
+                or segs is not None or scale or mask is not None or drop is not None):
             o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end,
-                                     scale, bits)
+                                     scale, bits, drop=z, drop_scale=z_scale)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -102,14 +104,15 @@ class _FlashAttnP100(torch.autograd.Function):
     def backward(ctx, grad_o):
         seg_start, seg_end = ctx.segs if ctx.segs is not None else (None, None)
         bits, bits_t = ctx.mask if ctx.mask is not None else (None, None)
+        z, z_t, z_scale = ctx.drop if ctx.drop is not None else (None, None, 1.0)
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
                                             ctx.window, ctx.alibi, seg_start, seg_end, ctx.scale,
-                                            bits, bits_t)
+                                            bits, bits_t, z, z_t, z_scale)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
-                    None, None, None, None, None, None, None, None)
+                    None, None, None, None, None, None, None, None, None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
@@ -118,17 +121,19 @@ class _FlashAttnP100(torch.autograd.Function):
         g = grad_o.contiguous()
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
                 or ctx.alibi is not None or ctx.segs is not None or ctx.scale
-                or ctx.mask is not None):
+                or ctx.mask is not None or ctx.drop is not None):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
-                                          ctx.alibi, seg_start, seg_end, ctx.scale, bits, bits_t)
+                                          ctx.alibi, seg_start, seg_end, ctx.scale, bits, bits_t,
+                                          z, z_t, z_scale)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
-                None, None, None)
+                None, None, None, None)
 
 
 def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-               alibi_slopes=None, segment_ids=None, softmax_scale=None, attn_mask=None):
+               alibi_slopes=None, segment_ids=None, softmax_scale=None, attn_mask=None,
+               dropout_p=None, dropout_seed=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -168,7 +173,17 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         on top of every other mask, causal included. A row left with no key
         gets o = 0 and zero gradients. Also accepted: the (bits, bits_t)
         pair pack_mask() makes, for callers that reuse one mask across calls.
-        The mask is a constant: no gradient flows to it.
+        The mask is a constant: no gradient flows to it;
+      * dropout_p in [0, 1): attention dropout. Each probability of the
+        softmax (normalised over every key) is dropped with that
+        probability and the kept ones are scaled by 1 / (1 - p); the
+        returned o is (P * Z / (1 - p)) V and the gradients are those of
+        that o. The keep bits Z come from a counter-based hash of
+        dropout_seed (64-bit; drawn from torch's default CPU generator when
+        None, so torch.manual_seed makes runs repeat) through
+        dropout_bits(), and the backward reuses the forward's bits. The
+        drawn rate is p rounded to a multiple of 1/65536, and the scale
+        matches it exactly.
     """
     window = 0
     if sliding_window is not None:
@@ -206,8 +221,35 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
                                  f"{[tuple(t.shape) for t in mask]}")
         else:
             mask = pack_mask(attn_mask, q.size(0), q.size(1))
+    drop = None
+    if dropout_p:
+        p = float(dropout_p)
+        if not 0.0 <= p < 1.0:
+            raise ValueError(f"dropout_p must lie in [0, 1), got {dropout_p}")
+        if not q.is_cuda:  # the binding's own check and message, before any drawing
+            raise RuntimeError("q must be a CUDA tensor")
+        if dropout_seed is None:
+            dropout_seed = int(torch.randint(0, 2 ** 63 - 1, (), dtype=torch.int64))
+        drop = dropout_bits(dropout_seed, p, q.size(0), q.size(1), q.size(2), q.device)
     return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes,
-                                segs, scale, mask)
+                                segs, scale, mask, drop)
+
+
+def dropout_bits(seed, p, batch, heads, n, device):
+    """(bits, bits_t, scale) of attention dropout: int32 keep bits
+    (batch, heads, n, ceil(n/32)) in the mask layout and its transpose (bit
+    set = keep), drawn by one HIP kernel from the 64-bit `seed` with drop
+    probability p (fa_dropout_bits in the C ABI states the draw), and the
+    scale 1 / (1 - drawn rate) of the kept probabilities."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError(f"dropout bits are drawn on the GPU, got device {device}")
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    seed = int(seed) % (1 << 64)
+    if seed >= 1 << 63:  # the binding takes a signed 64-bit value with the same bits
+        seed -= 1 << 64
+    bits, bits_t = _ext.dropout_bits(seed, float(p), batch, heads, n, index)
+    return bits, bits_t, _ext.dropout_scale(float(p))
 
 
 def pack_mask(attn_mask, batch, heads):

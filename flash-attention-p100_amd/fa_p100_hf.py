@@ -48,9 +48,13 @@ packed sequences.
 The kernels run in the autocast dtype (fp16 or bf16; bf16 inputs without
 autocast stay bf16); the reference cast everything to fp16.
 
+Attention dropout (a layer's `attention_dropout` in training), which the
+reference rejects (fa_p100_hf.py:83-85), runs in the kernels with keep bits
+drawn per call from torch's default generator (fa_p100.dropout_bits).
+
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): masks carrying a bias, output_attentions,
-head_mask, a window on non-causal attention, dropout, head_dim other than
+head_mask, a window on non-causal attention, head_dim other than
 not a multiple of 8 up to 128, q_len != kv_len (KV-cache decoding). A scale other than 1/sqrt(D),
 which the reference rejected, goes to the kernels.
 """
@@ -217,8 +221,6 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             "output_attentions=True is not available; use attn_implementation='eager'.")
     if kwargs.get("head_mask") is not None:
         raise NotImplementedError("fa_p100 does not support head_mask.")
-    if dropout:
-        raise NotImplementedError(f"fa_p100 has no attention dropout (got {dropout}).")
 
     head_dim = query.size(-1)
     if not (8 <= head_dim <= 128 and head_dim % 8 == 0):
@@ -294,10 +296,12 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             raise NotImplementedError(
                 "fa_p100: the padding mask given to the model does not match this "
                 "attention call's batch.")
+    # transformers passes the layer's attention_dropout in training, 0 in eval.
     out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
                      kv_len=kv_len, sliding_window=sliding_window, segment_ids=segs,
                      softmax_scale=softmax_scale,
-                     attn_mask=None if mask is None else mask[:2])
+                     attn_mask=None if mask is None else mask[:2],
+                     dropout_p=float(dropout) if dropout else None)
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
 

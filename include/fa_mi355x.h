@@ -50,7 +50,9 @@ enum {
   FA_ERR_SEGMENTS = 10011,   /* packed sequences with only one of the two bound arrays */
   FA_ERR_SCALE = 10012,      /* softmax scale negative or not finite */
   FA_ERR_SCRATCH = 10013,    /* fa_bwd_noalloc: the shape needs more than its scratch */
-  FA_ERR_MASK = 10014        /* mask_heads not 1 or Hq, or a backward mask without mask_t */
+  FA_ERR_MASK = 10014,       /* mask_heads not 1 or Hq, or a backward mask without mask_t */
+  FA_ERR_DROPOUT = 10015     /* dropout p not in [0, 1), a scale not positive and finite, or
+                                a backward with drop but without drop_t */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -168,7 +170,7 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
 /*
  * Options of the general pair below; a zeroed struct (or a NULL pointer)
  * means fp16, dense (B, H, N, D), no key lengths, no window, no ALiBi, no
- * packed sequences, no mask.
+ * packed sequences, no mask, no dropout.
  *   - dtype: FA_DTYPE_FP16 or FA_DTYPE_BF16 for q, k, v, o, dO, dq, dk, dv
  *     (bf16: products on the bf16 MFMA with fp32 accumulation, P and dS
  *     rounded to bf16 as operands, outputs rounded to nearest even);
@@ -205,7 +207,15 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *     mask_t[(p * N + j) * W + i / 32]. The forward reads mask, the backward
  *     both (mask_t is required there). fa_pack_mask writes both from a dense
  *     boolean mask. A row with no key left gets o = 0, lse = +inf and zero
- *     gradients.
+ *     gradients;
+ *   - drop, drop_t, drop_scale: attention dropout (drop = NULL: none). Keep
+ *     bits in the layouts of mask and mask_t with one plane per (b, query
+ *     head) (plane b * Hq + h; bit set = keep), and the factor drop_scale
+ *     (1 / (1 - p)) the kept probabilities are scaled by: o = (P * Z *
+ *     drop_scale) v with P the softmax over every key, lse that softmax's
+ *     (dropout does not touch it). The forward reads drop, the backward both
+ *     (drop_t is required there) with the same bits and scale as the
+ *     forward. fa_dropout_bits draws them.
  */
 typedef struct fa_options {
   int dtype;
@@ -219,6 +229,9 @@ typedef struct fa_options {
   const uint32_t* mask;
   const uint32_t* mask_t;
   int mask_heads;
+  const uint32_t* drop;
+  const uint32_t* drop_t;
+  float drop_scale;
 } fa_options;
 
 /*
@@ -249,6 +262,24 @@ int fa_bwd_ex(const void* q, const void* k, const void* v, const void* dO, const
  */
 int fa_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* bits_t,
                  void* stream);
+
+/*
+ * Dropout keep bits for fa_options.drop / drop_t. No counterpart in the
+ * reference, whose hook raises on dropout (fa_p100_hf.py:83-85). For each of
+ * the P = B * H planes, row i and key j < N: with h the 32-bit integer hash
+ * lowbias32 (C. Wellons: x ^= x >> 16; x *= 0x7feb352d; x ^= x >> 15;
+ * x *= 0x846ca68b; x ^= x >> 16), the row key r = h(h(h(h(lo) ^ hi) ^ plane)
+ * ^ i) of the seed's low and high words, and u = h(r ^ (j / 2)), key j draws
+ * the low (j even) or high (j odd) 16 bits of u and is kept iff that draw is
+ * at least t = min(65535, round(p * 65536)). The drop probability is then
+ * t / 65536 and fa_dropout_scale(p) = 65536 / (65536 - t) the matching
+ * scale. Writes P * N * ceil(N/32) words to bits and, when bits_t is not
+ * NULL, as many to bits_t; bits past N are 0. p must lie in [0, 1)
+ * (FA_ERR_DROPOUT otherwise; fa_dropout_scale then returns 0).
+ */
+int fa_dropout_bits(uint64_t seed, float p, int P, int N, uint32_t* bits, uint32_t* bits_t,
+                    void* stream);
+float fa_dropout_scale(float p);
 
 /*
  * fa_bwd without a workspace argument and without any allocation. No

@@ -38,7 +38,7 @@ import numpy as np
 __all__ = [
     "expand_kv", "attention_fwd", "bwd_preprocess", "attention_bwd",
     "attention_loss", "rel_max_rms", "rel_l2", "max_abs", "fwd_flops",
-    "bwd_flops",
+    "bwd_flops", "lowbias32", "dropout_threshold", "dropout_keep",
 ]
 
 
@@ -115,15 +115,64 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
     return s
 
 
+def lowbias32(x):
+    """C. Wellons' 32-bit integer hash (hash-prospector's `lowbias32`), on
+    uint32 arrays with wrap-around multiplies."""
+    m32 = np.uint64(0xFFFFFFFF)
+    x = np.asarray(x, dtype=np.uint32).astype(np.uint64)
+    x = x ^ (x >> np.uint64(16))
+    x = (x * np.uint64(0x7FEB352D)) & m32
+    x = x ^ (x >> np.uint64(15))
+    x = (x * np.uint64(0x846CA68B)) & m32
+    return (x ^ (x >> np.uint64(16))).astype(np.uint32)
+
+
+def dropout_threshold(p):
+    """16-bit keep threshold of a drop probability p (a float32, as the C ABI
+    takes it): draws >= t are kept; the drop rate is t / 65536."""
+    t = np.rint(np.float64(np.float32(p)) * 65536.0)
+    return int(min(max(t, 0.0), 65535.0))
+
+
+def dropout_keep(seed, p, planes, n):
+    """Keep mask (planes, n, n) of attention dropout, restating the draw that
+    include/fa_mi355x.h states for fa_dropout_bits (an extension: the
+    reference has no dropout, fa_p100_hf.py:83-85): row key
+    r = h(h(h(h(lo) ^ hi) ^ plane) ^ row) of the seed's 32-bit halves, key j
+    draws the low (j even) or high (j odd) 16 bits of h(r ^ (j // 2)), and
+    is kept iff the draw >= dropout_threshold(p). Returns (keep, scale), the
+    scale 65536 / (65536 - t) of the kept probabilities."""
+    t = dropout_threshold(p)
+    seed = int(seed) % (1 << 64)
+    lo, hi = np.uint32(seed & 0xFFFFFFFF), np.uint32(seed >> 32)
+    base = lowbias32(lowbias32(lowbias32(lo) ^ hi) ^ np.arange(planes, dtype=np.uint32))
+    rows = lowbias32(base[:, None] ^ np.arange(n, dtype=np.uint32)[None, :])
+    u = lowbias32(rows[:, :, None] ^ np.arange((n + 1) // 2, dtype=np.uint32)[None, None, :])
+    draws = np.stack([u & np.uint32(0xFFFF), u >> np.uint32(16)], axis=-1).reshape(planes, n, -1)
+    return draws[:, :, :n] >= t, 65536.0 / (65536 - t)
+
+
+def _drop_factor(dropout, shape):
+    """Z / (1 - p) over (B, Hq, N, N) from dropout = (keep (B*Hq, N, N) or
+    broadcastable to (B, Hq, N, N), scale)."""
+    keep, zs = dropout
+    keep = np.asarray(keep, dtype=bool)
+    if keep.ndim == 3:
+        keep = keep.reshape(shape)
+    return np.broadcast_to(keep, shape) * np.float64(zs)
+
+
 def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None,
-                  alibi=None, segments=None, scale=None, mask=None):
+                  alibi=None, segments=None, scale=None, mask=None, dropout=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
     (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`, `segments`, `mask`:
     optional per-entry key lengths, sliding window, ALiBi slopes, packed
-    sequence ids and boolean mask (see _scores).
+    sequence ids and boolean mask (see _scores). `dropout` = (keep, scale)
+    (an extension): O = (P * keep * scale) V with P the softmax over every
+    key; LSE is that softmax's, unchanged by dropout.
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
@@ -138,7 +187,10 @@ def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=N
     m = np.where(empty, 0, m)
     p = np.exp(s - m)
     l = p.sum(axis=-1, keepdims=True)
-    o = np.matmul(p / np.where(empty, 1, l), v.astype(dtype))
+    pn = p / np.where(empty, 1, l)
+    if dropout is not None:
+        pn = pn * _drop_factor(dropout, pn.shape)
+    o = np.matmul(pn, v.astype(dtype))
     lse = np.where(empty, np.inf, m + np.log(np.where(empty, 1, l)))[..., 0]
     return o, lse
 
@@ -149,12 +201,14 @@ def bwd_preprocess(o, do, dtype=np.float64):
 
 
 def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
-                  window=None, alibi=None, segments=None, scale=None, mask=None):
+                  window=None, alibi=None, segments=None, scale=None, mask=None, dropout=None):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
     kernels do, flash_bwd.cuh:278); otherwise they are recomputed here.
     dK and dQ carry the scale; dV does not (flash_bwd.cuh:442, 457).
+    With `dropout` = (keep, scale), F = keep * scale: dV = (P F)^T dO,
+    dP = (dO V^T) F, dS = P (dP - rowsum(dO O)) with O the dropped output.
     """
     q = np.asarray(q)
     hq, hkv = q.shape[1], np.asarray(k).shape[1]
@@ -166,11 +220,12 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
         o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale,
-                               mask)
+                               mask, dropout)
     s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments, scale, mask)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
-    dv = np.matmul(np.swapaxes(p, -1, -2), dod)
-    dp = np.matmul(dod, np.swapaxes(ve, -1, -2))
+    f = 1.0 if dropout is None else _drop_factor(dropout, p.shape)
+    dv = np.matmul(np.swapaxes(p * f, -1, -2), dod)
+    dp = np.matmul(dod, np.swapaxes(ve, -1, -2)) * f
     dvec = bwd_preprocess(o, dod, dtype)
     ds = p * (dp - dvec[..., None])
     dq = np.matmul(ds, ke) * sc
@@ -179,9 +234,10 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
 
 
 def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None,
-                   alibi=None, segments=None, scale=None, mask=None):
+                   alibi=None, segments=None, scale=None, mask=None, dropout=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
-    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale, mask)
+    o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale, mask,
+                         dropout)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

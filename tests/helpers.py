@@ -67,6 +67,10 @@ def load_capi():
     lib.fa_bwd_ex.restype = i
     lib.fa_pack_mask.argtypes = [vp, i, i, vp, vp, vp]
     lib.fa_pack_mask.restype = i
+    lib.fa_dropout_bits.argtypes = [ctypes.c_uint64, ctypes.c_float, i, i, vp, vp, vp]
+    lib.fa_dropout_bits.restype = i
+    lib.fa_dropout_scale.argtypes = [ctypes.c_float]
+    lib.fa_dropout_scale.restype = ctypes.c_float
     if hasattr(lib, "fa_bwd_noalloc"):
         lib.fa_bwd_noalloc.argtypes = [vp] * 9 + [i] * 6 + [vp]
         lib.fa_bwd_noalloc.restype = i
@@ -80,17 +84,20 @@ class FaOptions(ctypes.Structure):
                 ("alibi_slopes", ctypes.c_void_p), ("seg_start", ctypes.c_void_p),
                 ("seg_end", ctypes.c_void_p), ("scale", ctypes.c_float),
                 ("mask", ctypes.c_void_p), ("mask_t", ctypes.c_void_p),
-                ("mask_heads", ctypes.c_int)]
+                ("mask_heads", ctypes.c_int), ("drop", ctypes.c_void_p),
+                ("drop_t", ctypes.c_void_p), ("drop_scale", ctypes.c_float)]
 
 
 def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_start=None,
-            seg_end=None, scale=0.0, mask=None, mask_t=None, mask_heads=0):
+            seg_end=None, scale=0.0, mask=None, mask_t=None, mask_heads=0, drop=None,
+            drop_t=None, drop_scale=0.0):
     """A pointer to an FaOptions; the array fields are device addresses (ints)
     or tensors."""
     def addr(x):
         return None if x is None else (x if isinstance(x, int) else x.data_ptr())
     o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes), addr(seg_start),
-                  addr(seg_end), scale, addr(mask), addr(mask_t), mask_heads)
+                  addr(seg_end), scale, addr(mask), addr(mask_t), mask_heads, addr(drop),
+                  addr(drop_t), drop_scale)
     return ctypes.pointer(o)
 
 

@@ -96,6 +96,24 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_bwd_ex(*([one] * 10), 0, 1, 4, 2, 8, 64, 0,
                          fa_opts(mask=1, mask_t=1, mask_heads=4), s) == 10006
     assert b"mask_t" in lib.fa_error_string(10014)
+    # dropout: a positive finite scale; the backward needs the transposed bits
+    for bad in (0.0, -1.0, float("inf"), float("nan")):
+        assert lib.fa_fwd_ex(*([one] * 5), 1, 4, 2, 8, 64, 0, fa_opts(drop=1, drop_scale=bad),
+                             s) == 10015
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, 64, 1, fa_opts(drop=1, drop_scale=1.25),
+                         s) == 10005
+    assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 4, 2, 8, 64, 0,
+                         fa_opts(drop=1, drop_scale=1.25), s) == 10015
+    assert b"drop_t" in lib.fa_error_string(10015)
+    # the dropout generator: p in [0, 1), shape, pointers; the scale of the drawn rate
+    for bad in (-0.1, 1.0, 1.5, float("nan")):
+        assert lib.fa_dropout_bits(7, bad, 1, 8, one, one, s) == 10015
+        assert lib.fa_dropout_scale(bad) == 0.0
+    assert lib.fa_dropout_bits(7, 0.1, 1, 0, one, one, s) == 10002
+    assert lib.fa_dropout_bits(7, 0.1, 0, 8, one, one, s) == 10004
+    assert lib.fa_dropout_bits(7, 0.1, 1, 8, z, one, s) == 10005
+    for p, t in ((0.0, 0), (0.1, 6554), (0.5, 32768), (0.999999, 65535)):
+        assert abs(lib.fa_dropout_scale(p) - 65536.0 / (65536 - t)) < 1e-6 * 65536 / (65536 - t)
     # the packer: N, planes, pointers
     assert lib.fa_pack_mask(one, 1, 0, one, one, s) == 10002
     assert lib.fa_pack_mask(one, 0, 8, one, one, s) == 10004
@@ -138,7 +156,7 @@ def test_public_api_surface_matches_reference():
     # (key lengths, sliding window, ALiBi slopes, packing, scale, mask) come
     # after them and default to None, so every reference call binds the same way.
     extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids", "softmax_scale",
-                  "attn_mask"]
+                  "attn_mask", "dropout_p", "dropout_seed"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False

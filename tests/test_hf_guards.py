@@ -30,12 +30,19 @@ MOD = types.SimpleNamespace(is_causal=True)
     (dict(attention_mask=None, head_mask=torch.ones(4)), "head_mask"),
     (dict(attention_mask=None, sliding_window=128, is_causal=False), "a window of 128"),
     (dict(attention_mask=None, sliding_window=0), "a window of 0"),
-    (dict(attention_mask=None, dropout=0.1), "dropout"),
 ])
 def test_unsupported_requests_raise(kwargs, match):
     q, k, v = qkv()
     with pytest.raises(NotImplementedError, match=match):
         hf.fa_p100_attention_forward(MOD, q, k, v, **kwargs)
+
+
+def test_dropout_reaches_the_kernel():
+    """Attention dropout passes the hook (the reference raised,
+    fa_p100_hf.py:83-85); host tensors then stop at the device check."""
+    q, k, v = qkv()
+    with pytest.raises(RuntimeError, match="q must be a CUDA tensor"):
+        hf.fa_p100_attention_forward(MOD, q, k, v, None, dropout=0.1)
 
 
 def test_head_dim_scale_and_kv_len_guards():
@@ -155,7 +162,7 @@ def test_checkpointed_layers_see_the_padding_in_their_recompute(monkeypatch):
     seen = []
 
     def spy(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-            segment_ids=None, softmax_scale=None, attn_mask=None):
+            segment_ids=None, softmax_scale=None, attn_mask=None, dropout_p=None):
         seen.append((torch.is_grad_enabled(),
                      None if kv_len is None else kv_len.tolist(),
                      None if segment_ids is None else segment_ids[0].tolist(),

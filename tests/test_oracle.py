@@ -567,3 +567,95 @@ def test_mask_pins(causal):
     assert np.all(g_e[0][1, 2, 7] == 0)
     for got, want in zip(g_e, g_f):
         assert np.allclose(got, want, atol=1e-12)
+
+
+def _h32(x):
+    """lowbias32 on Python integers (mod 2^32), written out independently."""
+    x &= 0xFFFFFFFF
+    x ^= x >> 16
+    x = (x * 0x7FEB352D) & 0xFFFFFFFF
+    x ^= x >> 15
+    x = (x * 0x846CA68B) & 0xFFFFFFFF
+    return x ^ (x >> 16)
+
+
+def test_dropout_draw_pins():
+    """The dropout keep-bit draw (an extension; the reference has no
+    dropout, fa_p100_hf.py:83-85). The vectorised hash equals plain integer
+    arithmetic; it avalanches (each input bit flips each output bit about
+    half the time); the row keys and draws follow the stated recipe on a few
+    hand-computed entries; keep rates match 1 - t/65536 within 5 sigma; and
+    neighbouring keys, rows, planes and seeds are uncorrelated."""
+    rng = np.random.default_rng(8)
+    xs = rng.integers(0, 1 << 32, 4000, dtype=np.uint64).astype(np.uint32)
+    got = ora.lowbias32(xs)
+    assert all(int(g) == _h32(int(x)) for g, x in zip(got[:500], xs[:500]))
+    for bit in range(32):
+        flipped = ora.lowbias32(xs ^ np.uint32(1 << bit)) ^ got
+        frac = np.unpackbits(flipped.view(np.uint8)).reshape(-1, 32).mean(axis=0)
+        assert np.all((frac > 0.4) & (frac < 0.6)), (bit, frac.min(), frac.max())
+    # Hand-computed entries of the recipe.
+    seed, p, planes, n = 0x0123456789ABCDEF, 0.3, 3, 37
+    keep, zs = ora.dropout_keep(seed, p, planes, n)
+    t = ora.dropout_threshold(p)
+    assert t == round(float(np.float32(0.3)) * 65536) and zs == 65536 / (65536 - t)
+    for plane, i, j in [(0, 0, 0), (2, 36, 36), (1, 5, 17), (2, 11, 2)]:
+        r = _h32(_h32(_h32(_h32(seed & 0xFFFFFFFF) ^ (seed >> 32)) ^ plane) ^ i)
+        u = _h32(r ^ (j // 2))
+        draw = (u >> 16) if j % 2 else (u & 0xFFFF)
+        assert keep[plane, i, j] == (draw >= t)
+    assert ora.dropout_threshold(0.0) == 0 and ora.dropout_threshold(0.9999999) == 65535
+    # Statistics over ~1M draws per rate.
+    for p in (0.1, 0.5, 0.9):
+        keep, _ = ora.dropout_keep(99, p, 4, 512)
+        q_keep = 1 - ora.dropout_threshold(p) / 65536
+        n_all = keep.size
+        assert abs(keep.mean() - q_keep) < 5 * math.sqrt(q_keep * (1 - q_keep) / n_all)
+        z = keep.astype(np.float64) - keep.mean()
+        lim = 5 / math.sqrt(n_all / 2)
+        for a, b in ((z[:, :, 1:], z[:, :, :-1]), (z[:, 1:], z[:, :-1]), (z[1:], z[:-1])):
+            corr = (a * b).mean() / z.var()
+            assert abs(corr) < lim, (p, corr)
+    k1, _ = ora.dropout_keep(1, 0.5, 2, 256)
+    k2, _ = ora.dropout_keep(2, 0.5, 2, 256)
+    agree = (k1 == k2).mean()
+    assert abs(agree - 0.5) < 0.01
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_dropout_attention_pins(causal):
+    """Attention with a fixed dropout keep mask: forward and backward
+    against torch autograd through o = (softmax(S) * Z * s) V in float64
+    (the backward formula of attention_bwd is derived by hand; autograd
+    derives its own), GQA included; keep-all with scale 1 equals no
+    dropout; finite differences; and a planted slip (dP not dropped) fails."""
+    rng = np.random.default_rng(13 + causal)
+    b, hq, hkv, n, d = 2, 4, 2, 19, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    keep, zs = ora.dropout_keep(2024, 0.25, b * hq, n)
+    drop = (keep, zs)
+    o, lse = ora.attention_fwd(q, k, v, causal, dropout=drop)
+    grads = ora.attention_bwd(q, k, v, do, causal, dropout=drop)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    s = tq @ tk.repeat_interleave(hq // hkv, 1).transpose(-1, -2) / math.sqrt(d)
+    if causal:
+        s = s.masked_fill(torch.triu(torch.ones(n, n, dtype=torch.bool), 1), float("-inf"))
+    pt = torch.softmax(s, -1)
+    ref = (pt * torch.tensor(keep.reshape(b, hq, n, n)) * zs) @ tv.repeat_interleave(hq // hkv, 1)
+    ref.backward(torch.tensor(do))
+    assert np.allclose(o, ref.detach().numpy(), atol=1e-12)
+    assert np.allclose(lse, torch.logsumexp(s, -1).detach().numpy(), atol=1e-12)
+    for got, t in zip(grads, (tq, tk, tv)):
+        assert np.allclose(got, t.grad.numpy(), atol=1e-10)
+    ones = (np.ones_like(keep), 1.0)
+    for got, want in zip(ora.attention_bwd(q, k, v, do, causal, dropout=ones),
+                         ora.attention_bwd(q, k, v, do, causal)):
+        assert np.allclose(got, want, atol=1e-13)
+    _fd_check(rng, grads, q, k, v, do, causal, dropout=drop)
+    # Planted: dS from the undropped dP misses autograd's dQ.
+    p = np.exp(ora._scores(q, ora.expand_kv(k, hq), causal, np.float64) - lse[..., None])
+    dp = do @ np.swapaxes(ora.expand_kv(v, hq), -1, -2)
+    ds = p * (dp - (o * do).sum(-1)[..., None])
+    wrong_dq = ds @ ora.expand_kv(k, hq) / math.sqrt(d)
+    assert not np.allclose(wrong_dq, tq.grad.numpy(), atol=1e-6)
