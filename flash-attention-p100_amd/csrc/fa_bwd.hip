@@ -217,7 +217,7 @@ struct KVWave {
                                        const float* dvs, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int row_lo, int row_end,
                                        float alibi_raw, uint32_t mtw, uint32_t ztw, float zs,
-                                       int lane, int roff,
+                                       const floatx16& bv, float bias_raw, int lane, int roff,
                                        const typename Stream<D>::Offsets& so, float c) {
     using S = Stream<D>;
     const int h = lane >> 5;
@@ -252,6 +252,10 @@ struct KVWave {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         sacc[r] = fmaf(-alibi_raw, fabsf(d0 + (float)(8 * (r >> 2) + (r & 3))), sacc[r]);
+    }
+    if (BOUNDS && bias_raw != 0.f) {  // attention bias of the 16 (row, j_col) in raw units
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sacc[r] = fmaf(bv[r], bias_raw, sacc[r]);
     }
     half8 pb[2], sb[2];
 #pragma unroll
@@ -294,7 +298,8 @@ struct QWave {
   template <class Issue>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
                                        int i_row, int Nk, int key_lo, float alibi_raw,
-                                       uint32_t mw, uint32_t zw, float zs, int lane,
+                                       uint32_t mw, uint32_t zw, float zs, const floatx16& bv,
+                                       float bias_raw, float* dbrow, int lane,
                                        const typename Stream<D>::Offsets& so, float c,
                                        const Issue& issue) {
     using S = Stream<D>;
@@ -329,6 +334,10 @@ struct QWave {
       for (int r = 0; r < 16; ++r)
         st[r] = fmaf(-alibi_raw, fabsf(d0 - (float)(8 * (r >> 2) + (r & 3))), st[r]);
     }
+    if (BOUNDS && bias_raw != 0.f) {  // attention bias of the 16 (i_row, key) in raw units
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st[r] = fmaf(bv[r], bias_raw, st[r]);
+    }
     half8 sb[2];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -338,7 +347,10 @@ struct QWave {
       if (BOUNDS) p = (idx < hi && idx >= lw && ((mw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
       // Dropout: the gradient of P is the kept dP scaled by zs.
       const bool keep = (zw >> (idx + 4 * h)) & 1u;
-      sb[r >> 3][r & 7] = to16<BF>(p * ((keep ? pt[r] * zs : 0.f) - dvv));
+      const float ds = p * ((keep ? pt[r] * zs : 0.f) - dvv);
+      sb[r >> 3][r & 7] = to16<BF>(ds);
+      // The bias's gradient is dS itself (keys past N are not stored).
+      if (BOUNDS && dbrow && idx < hi) dbrow[base + idx] = ds;
     }
     // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15 (operands one ahead).
     half8 kt = S::tr_operand(Ks, 0, so, 0);
@@ -355,9 +367,12 @@ struct QWave {
 };
 
 // ---------------------------------------------------------------------------
-// BITMASK: the arbitrary-mask instantiation (with BOUNDS); its bit tests stay out
-// of the others, whose D = 128 copies have no registers to spare.
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
+// BITMASK: the arbitrary-mask and dropout instantiation (with BOUNDS); its bit
+// tests stay out of the others, whose D = 128 copies have no registers to
+// spare. BIAS (with BITMASK): the one that also adds an attention bias and
+// writes its gradient, whose 16 prefetched values per step would otherwise
+// cost the mask and dropout paths their registers too.
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
@@ -370,7 +385,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const float* __restrict__ alibi, const int* __restrict__ seg_start,
     const int* __restrict__ seg_end, const uint32_t* __restrict__ mask,
     const uint32_t* __restrict__ mask_t, int mask_heads, const uint32_t* __restrict__ drop,
-    const uint32_t* __restrict__ drop_t, float drop_scale, int dr) {
+    const uint32_t* __restrict__ drop_t, float drop_scale, const float* __restrict__ bias,
+    long long bias_sb, long long bias_sh, float bias_raw, float* __restrict__ dbias, int dr) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -449,6 +465,11 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // in the mask's two layouts; zs scales the kept probabilities.
   auto zplane = [&](const uint32_t* z, int hq) { return z + ((size_t)b * Hq + hq) * N * W32; };
   const float zs = BITMASK ? drop_scale : 1.f;
+  // Attention bias (BIAS instantiation; bias null: none), raw-score factor
+  // bias_raw = 1/scale; its gradient dbias, dense (B, Hq, N, N).
+  const bool has_bias = BIAS && bias != nullptr;
+  const float braw = has_bias ? bias_raw : 0.f;
+  auto bplane = [&](int hq) { return bias + b * bias_sb + hq * bias_sh; };
   const int roff = row_lane_off<D>(lane);  // resident tiles (padded rows)
   typename Stream<D>::Offsets so;          // staged tiles, rows 32*half ..
   so.init(lane, 32 * half);
@@ -541,11 +562,29 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       if (wave == 0) vec_load64(tv, make_rsrc(Lse2 + bhq * N, (uint32_t)N * 4), i0, lane);
       if (wave == 1) vec_load64(tv + kSub, make_rsrc(Dvec + bhq * N, (uint32_t)N * 4), i0, lane);
     };
+    // Bias values of step `it` for this lane's key and its 16 query rows
+    // (rows or keys past N read as 0: masked anyway); loaded one step ahead.
+    auto bload1 = [&](int it) {
+      floatx16 v = zero16();
+      if (has_bias) {
+        const float* pl = bplane(hkv * group + it / n_qt);
+        const int r0 = i_start + (it % n_qt) * kSub + 32 * half + 4 * (lane >> 5);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = r0 + 8 * (r >> 2) + (r & 3);
+          v[r] = row < N && j_col < N ? pl[(size_t)row * N + j_col] : 0.f;
+        }
+      }
+      return v;
+    };
+    floatx16 bv1 = bload1(it_begin);
     // One step over the stage of parity P, while the next step's tiles load
     // into the other stage.
     auto step = [&](int it, auto par) {
       constexpr int P = decltype(par)::value;
       fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
+      const floatx16 bv_now = bv1;
+      if (has_bias) bv1 = bload1(min(it + 1, it_end - 1));
       const half_t* Qs = P ? ta1 : ta0;
       const half_t* Os = P ? tb1 : tb0;
       const float* lse2s = P ? vec1 : vec0;
@@ -563,7 +602,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const uint32_t ztw =
           BITMASK && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
       w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
-             alibi_raw, mtw, ztw, zs, lane, roff, so, scale_log2);
+             alibi_raw, mtw, ztw, zs, bv_now, braw, lane, roff, so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -689,6 +728,23 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           BITMASK && mask ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
       const uint32_t* zrow =
           BITMASK && drop ? zplane(drop, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
+      // This lane's bias row and gradient row (rows past N: none).
+      const float* brow =
+          has_bias ? bplane(hq) + (size_t)min(i_row, N - 1) * N : nullptr;
+      float* dbrow = BIAS && dbias && row_ok ? dbias + (bhq * N + i_row) * N : nullptr;
+      auto bload2 = [&](int t) {  // bias of key step t for this row's 16 keys
+        floatx16 v = zero16();
+        if (brow) {
+          const int key0 = t * kSub + 32 * half + 4 * (lane >> 5);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = key0 + 8 * (r >> 2) + (r & 3);
+            v[r] = key < N ? brow[key] : 0.f;
+          }
+        }
+        return v;
+      };
+      floatx16 bv2 = bload2(t_lo);
       QWave<D, CAUSAL, BOUNDS, BF> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
@@ -725,8 +781,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         const int word = min(t * (kSub / 32) + half, W32 - 1);  // keys t*kSub + 32*half ..
         const uint32_t mw = mrow ? mrow[word] : ~0u;
         const uint32_t zw = zrow ? zrow[word] : ~0u;
+        const floatx16 bv_now = bv2;
+        if (has_bias) bv2 = bload2(min(t + 1, n_kt - 1));
         w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, mw,
-               zw, zs, lane, so, scale_log2, issue);
+               zw, zs, bv_now, braw, dbrow, lane, so, scale_log2, issue);
         wait_vmem();
         __syncthreads();
       };
@@ -785,14 +843,14 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D);
-  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BIAS, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
@@ -800,24 +858,29 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      make_strides(a.layout, a.Hkv, a.N, a.D), a.counters, a.slots,
                      a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
                      a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.drop,
-                     a.drop_t, a.drop_scale, a.D);
+                     a.drop_t, a.drop_scale, a.bias, a.bias_sb, a.bias_sh,
+                     a.bias ? 1.f / scale : 0.f, a.dbias, a.D);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
   // Key lengths, windows, packed sequences and ALiBi need the masked
-  // instantiation (kTile is a multiple of kSub), masks and dropout the bit one.
+  // instantiation (kTile is a multiple of kSub), masks and dropout the bit
+  // one, a bias (with or without them) the bias one.
   const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
+  if (a.bias)
+    return a.causal ? launch_main_t<D, true, true, true, true, BF>(a)
+                    : launch_main_t<D, false, true, true, true, BF>(a);
   if (a.mask || a.drop)
-    return a.causal ? launch_main_t<D, true, true, true, BF>(a)
-                    : launch_main_t<D, false, true, true, BF>(a);
+    return a.causal ? launch_main_t<D, true, true, true, false, BF>(a)
+                    : launch_main_t<D, false, true, true, false, BF>(a);
   if (a.causal)
-    return bounds ? launch_main_t<D, true, true, false, BF>(a)
-                  : launch_main_t<D, true, false, false, BF>(a);
-  return bounds ? launch_main_t<D, false, true, false, BF>(a)
-                : launch_main_t<D, false, false, false, BF>(a);
+    return bounds ? launch_main_t<D, true, true, false, false, BF>(a)
+                  : launch_main_t<D, true, false, false, false, BF>(a);
+  return bounds ? launch_main_t<D, false, true, false, false, BF>(a)
+                : launch_main_t<D, false, false, false, false, BF>(a);
 }
 
 }  // namespace

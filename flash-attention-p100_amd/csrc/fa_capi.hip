@@ -100,6 +100,7 @@ const char* fa_error_string(int err) {
     case FA_ERR_DROPOUT:
       return "dropout p must lie in [0, 1) and its scale be positive and finite; the backward "
              "needs drop_t with drop";
+    case FA_ERR_BIAS: return "bias strides must not be negative, and dbias needs a bias";
     case FA_ERR_SCRATCH:
       return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
              "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
@@ -113,7 +114,8 @@ const char* fa_version(void) { return "fa_mi355x 1.0 gfx950"; }
 // lengths, no window, no ALiBi, no packed sequences, no mask.
 constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0,       nullptr,
                                      nullptr,   nullptr,   0.f,     nullptr, nullptr,
-                                     0,         nullptr,   nullptr, 0.f};
+                                     0,         nullptr,   nullptr, 0.f,
+                                     nullptr,   0,         0,       nullptr};
 
 // `backward`: the pass reads mask_t too.
 static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
@@ -130,6 +132,8 @@ static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
     if (!(op.drop_scale > 0.f) || !std::isfinite(op.drop_scale)) return FA_ERR_DROPOUT;
     if (backward && op.drop_t == nullptr) return FA_ERR_DROPOUT;
   }
+  if (op.bias_stride_b < 0 || op.bias_stride_h < 0) return FA_ERR_BIAS;
+  if (op.dbias != nullptr && op.bias == nullptr) return FA_ERR_BIAS;
   return FA_OK;
 }
 
@@ -171,6 +175,9 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.mask_heads = op.mask_heads;
   a.drop = op.drop;
   a.drop_scale = op.drop ? op.drop_scale : 1.f;
+  a.bias = op.bias;
+  a.bias_sb = op.bias_stride_b;
+  a.bias_sh = op.bias_stride_h;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -282,6 +289,10 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.drop = op.drop;
   a.drop_t = op.drop_t;
   a.drop_scale = op.drop ? op.drop_scale : 1.f;
+  a.bias = op.bias;
+  a.bias_sb = op.bias_stride_b;
+  a.bias_sh = op.bias_stride_h;
+  a.dbias = op.dbias;
   return to_code(fa::launch_bwd_main(a));
 }
 

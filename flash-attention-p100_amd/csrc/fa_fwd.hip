@@ -103,7 +103,8 @@ struct FwdWave {
   template <bool MASK, bool NEXT, class Issue>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
                                        bool masked, int i_row, int N, int w_lo, float alibi_raw,
-                                       uint32_t mw, uint32_t zw, int lane, int roff,
+                                       uint32_t mw, uint32_t zw, const floatx16& bv,
+                                       float bias_raw, int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
@@ -123,6 +124,12 @@ struct FwdWave {
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         s[r] = fmaf(-alibi_raw, fabsf(d0 - (float)(8 * (r >> 2) + (r & 3))), s[r]);
+    }
+    // Additive attention bias (bit instantiation only; bias_raw = 1/scale
+    // puts it in raw-score units): bv holds this row's 16 values of the step.
+    if (BOUNDS && bias_raw != 0.f) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s[r] = fmaf(bv[r], bias_raw, s[r]);
     }
     if (MASK && masked) {
 #pragma unroll
@@ -184,15 +191,19 @@ struct FwdWave {
   }
 };
 
-// BITMASK: the arbitrary-mask instantiation (with BOUNDS); its bit tests stay out
-// of the others, whose D = 128 copies have no registers to spare.
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
+// BITMASK: the arbitrary-mask and dropout instantiation (with BOUNDS); its bit
+// tests stay out of the others, whose D = 128 copies have no registers to
+// spare. BIAS (with BITMASK): the one that also adds an attention bias, whose
+// 16 prefetched values per step would otherwise cost the mask and dropout
+// paths their registers too.
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int Nk, int W,
                                          const int* __restrict__ sst, const int* __restrict__ sen,
                                          float alibi_raw, const uint32_t* __restrict__ mbase,
                                          const uint32_t* __restrict__ zbase, float o_scale,
+                                         const float* __restrict__ bbase, float bias_raw,
                                          int W32, int sq, int sk, int dr,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
@@ -270,6 +281,21 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   if (BITMASK) n_full = 0;
   auto mword = [&](int j) { return mrow ? mrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
   auto zword = [&](int j) { return zrow ? zrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
+  // Attention bias (BIAS instantiation; bbase null: none): this row's values
+  // for the wave's 16 keys of step j, keys past N read as 0 (masked anyway).
+  const float* brow = BIAS && bbase ? bbase + (size_t)min(i_row, N - 1) * N : nullptr;
+  auto bload = [&](int j) {
+    floatx16 v = zero16();
+    if (brow) {
+      const int key0 = j * kKV + kq * 32 + 4 * (lane >> 5);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = key0 + 8 * (r >> 2) + (r & 3);
+        v[r] = key < N ? brow[key] : 0.f;
+      }
+    }
+    return v;
+  };
 
   // Software pipeline over steps j = 0 .. n_it-1. Step j reads K_{j+1} (for
   // the next S^T) from K buffer (j+1)%2 and V_j from V buffer j%2, while it
@@ -297,14 +323,17 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // loads fill and does not wait for those loads before them).
   uint32_t mw = mword(j_lo);  // mask bits of the next step to run
   uint32_t zw = zword(j_lo);  // its dropout keep bits
+  floatx16 bv = bload(j_lo);  // its bias values
   auto run = [&](int j, auto par_tag, auto mask_tag, auto next_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
     const uint32_t mw_now = mw, zw_now = zw;
+    const floatx16 bv_now = bv;
     if (BITMASK && NEXT) {
       mw = mword(j + 1);
       zw = zword(j + 1);
+      bv = bload(j + 1);
     }
     half_t* lk = P ? kt1 : kt0;  // receives K_{j+2}
     half_t* lv = P ? vt0 : vt1;  // receives V_{j+1}
@@ -323,7 +352,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
-                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, lane,
+                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv_now,
+                                BIAS ? bias_raw : 0.f, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
       wait_vmem();
@@ -425,7 +455,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   __syncthreads();  // the LDS is reused by the next tile
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
@@ -433,7 +463,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     Strides stk, const int* __restrict__ kv_len, int window, const float* __restrict__ alibi,
     const int* __restrict__ seg_start, const int* __restrict__ seg_end,
     const uint32_t* __restrict__ mask, int mask_heads, const uint32_t* __restrict__ drop,
-    float drop_scale, int dr) {
+    float drop_scale, const float* __restrict__ bias, long long bias_sb, long long bias_sh,
+    float bias_raw, int dr) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -462,21 +493,24 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
                                            : nullptr;
   // ... and its dropout keep bits (one plane per (b, query head)).
   const uint32_t* zbase = BITMASK && drop ? drop + (size_t)bh * N * W32 : nullptr;
+  // ... and its attention bias plane (element (i, j) at i * N + j).
+  const float* bbase = BIAS && bias ? bias + b * bias_sb + hq * bias_sh : nullptr;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
-    fwd_tile<D, CAUSAL, BOUNDS, BITMASK, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
+    fwd_tile<D, CAUSAL, BOUNDS, BITMASK, BIAS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
                                 Lse + (size_t)bh * N, N, Nk, window,
                                 seg_start ? seg_start + (size_t)b * N : nullptr,
                                 seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, mbase,
-                                zbase, BITMASK ? drop_scale : 1.f, W32, stq.n, stk.n, dr,
+                                zbase, BITMASK ? drop_scale : 1.f, bbase, bias_raw, W32, stq.n,
+                                stk.n, dr,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
 hipError_t launch_fwd_t(const FwdArgs& a) {
   const int n_qtiles = (a.N + kBR - 1) / kBR;
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
@@ -485,29 +519,35 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D));
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BIAS, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
                      make_strides(a.layout, a.Hkv, a.N, a.D), a.kv_len, a.window, a.alibi,
-                     a.seg_start, a.seg_end, a.mask, a.mask_heads, a.drop, a.drop_scale, a.D);
+                     a.seg_start, a.seg_end, a.mask, a.mask_heads, a.drop, a.drop_scale, a.bias,
+                     a.bias_sb, a.bias_sh,
+                     a.bias ? 1.f / (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D)) : 0.f, a.D);
   return hipGetLastError();
 }
 
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
   // Key lengths, windows, packed sequences and ALiBi need the masked
-  // instantiation (kKV is a multiple of kBR), masks and dropout the bit one.
+  // instantiation (kKV is a multiple of kBR), masks and dropout the bit one,
+  // a bias (with or without them) the bias one.
   const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
+  if (a.bias)
+    return a.causal ? launch_fwd_t<D, true, true, true, true, BF>(a)
+                    : launch_fwd_t<D, false, true, true, true, BF>(a);
   if (a.mask || a.drop)
-    return a.causal ? launch_fwd_t<D, true, true, true, BF>(a)
-                    : launch_fwd_t<D, false, true, true, BF>(a);
+    return a.causal ? launch_fwd_t<D, true, true, true, false, BF>(a)
+                    : launch_fwd_t<D, false, true, true, false, BF>(a);
   if (a.causal)
-    return bounds ? launch_fwd_t<D, true, true, false, BF>(a)
-                  : launch_fwd_t<D, true, false, false, BF>(a);
-  return bounds ? launch_fwd_t<D, false, true, false, BF>(a)
-                : launch_fwd_t<D, false, false, false, BF>(a);
+    return bounds ? launch_fwd_t<D, true, true, false, false, BF>(a)
+                  : launch_fwd_t<D, true, false, false, false, BF>(a);
+  return bounds ? launch_fwd_t<D, false, true, false, false, BF>(a)
+                : launch_fwd_t<D, false, false, false, false, BF>(a);
 }
 
 }  // namespace

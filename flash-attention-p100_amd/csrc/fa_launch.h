@@ -56,6 +56,11 @@ struct FwdArgs {
   // sees the dropped probabilities.
   const uint32_t* drop = nullptr;
   float drop_scale = 1.f;
+  // Additive attention bias, fp32, added to the scaled logits: element
+  // (b, h, i, j) at bias[b * bias_sb + h * bias_sh + i * N + j] (strides in
+  // elements; 0 broadcasts over that dimension).
+  const float* bias = nullptr;
+  long long bias_sb = 0, bias_sh = 0;
 };
 
 // Backward workspace, in this order (each part 256-byte aligned):
@@ -131,6 +136,12 @@ struct BwdArgs {
   const uint32_t* drop = nullptr;  // as FwdArgs::drop
   const uint32_t* drop_t = nullptr;  // its transpose (as mask_t); required with drop
   float drop_scale = 1.f;          // as FwdArgs::drop_scale
+  const float* bias = nullptr;     // as FwdArgs::bias
+  long long bias_sb = 0, bias_sh = 0;
+  // Gradient of the bias: dS (the gradient of the scaled logits), dense
+  // (B, Hq, N, N) fp32; written where a row meets a key, so the caller
+  // zeroes it first. Null: not computed.
+  float* dbias = nullptr;
 };
 
 hipError_t launch_fwd(const FwdArgs& a);

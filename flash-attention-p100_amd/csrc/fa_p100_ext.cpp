@@ -12,7 +12,8 @@
 // (dense (B, N, H, D) tensors) and forward_dt / backward_dt (fp16 or bf16);
 // the last four take bf16 as well as fp16; pack_mask bit-packs a boolean
 // mask for their `mask` / `mask_t` arguments and dropout_bits draws the keep
-// bits for `drop` / `drop_t`.
+// bits for `drop` / `drop_t`; they also take an fp32 attention `bias` (and
+// the backward its gradient buffer `dbias`).
 //
 // Plain C++ (no device code): every launch goes through the C ABI of
 // libfa_mi355x.so (include/fa_mi355x.h). Unlike the reference, which uses the
@@ -105,8 +106,9 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
                      const c10::optional<at::Tensor>& mask,
                      const c10::optional<at::Tensor>& mask_t,
                      const c10::optional<at::Tensor>& drop,
-                     const c10::optional<at::Tensor>& drop_t, double drop_scale, int B, int H,
-                     int N) {
+                     const c10::optional<at::Tensor>& drop_t, double drop_scale,
+                     const c10::optional<at::Tensor>& bias,
+                     const c10::optional<at::Tensor>& dbias, int B, int H, int N) {
   fa_options op{};
   op.dtype = dtype_code(q);
   op.layout = layout;
@@ -127,6 +129,28 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
   TORCH_CHECK(!op.drop || dheads == H, "drop must hold one plane per query head");
   TORCH_CHECK(!op.drop_t || (op.drop && dheads_t == H), "drop_t must come with drop");
   op.drop_scale = (float)drop_scale;
+  if (bias.has_value()) {
+    // fp32 (B or 1, Hq or 1, N, N) with dense rows; a dimension of size 1 is
+    // shared (stride 0).
+    const at::Tensor& t = *bias;
+    TORCH_CHECK(t.is_cuda() && t.device() == q.device(), "bias must be on q's device");
+    TORCH_CHECK(t.scalar_type() == at::kFloat, "bias must be fp32");
+    TORCH_CHECK(t.dim() == 4 && (t.size(0) == B || t.size(0) == 1) &&
+                    (t.size(1) == H || t.size(1) == 1) && t.size(2) == N && t.size(3) == N &&
+                    t.stride(3) == 1 && t.stride(2) == N,
+                "bias must be (B or 1, Hq or 1, N, N) with dense rows");
+    op.bias = t.data_ptr<float>();
+    op.bias_stride_b = t.size(0) == 1 ? 0 : t.stride(0);
+    op.bias_stride_h = t.size(1) == 1 ? 0 : t.stride(1);
+  }
+  if (dbias.has_value()) {
+    const at::Tensor& t = *dbias;
+    TORCH_CHECK(t.is_cuda() && t.device() == q.device(), "dbias must be on q's device");
+    TORCH_CHECK(t.scalar_type() == at::kFloat && t.dim() == 4 && t.size(0) == B &&
+                    t.size(1) == H && t.size(2) == N && t.size(3) == N && t.is_contiguous(),
+                "dbias must be fp32 (B, Hq, N, N), contiguous");
+    op.dbias = t.data_ptr<float>();
+  }
   return op;
 }
 
@@ -251,7 +275,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
-    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -273,7 +298,7 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -287,7 +312,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
                                          int64_t window, c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
-    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -313,7 +339,7 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -334,7 +360,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
-    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -359,7 +386,7 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -373,7 +400,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
     c10::optional<at::Tensor> alibi_slopes,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
-    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale) {
+    c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -404,7 +432,7 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   const fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -485,7 +513,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
-        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
@@ -493,14 +522,16 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
-        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
-        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
@@ -508,5 +539,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("alibi_slopes") = py::none(), py::arg("seg_start") = py::none(),
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
-        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0);
+        py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
 }

@@ -68,7 +68,7 @@ class _FlashAttnP100(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None,
-                segs=None, scale=0.0, mask=None, drop=None):
+                segs=None, scale=0.0, mask=None, drop=None, bias=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -82,19 +82,23 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.scale = scale
         ctx.mask = mask
         ctx.drop = drop
+        # bias: fp32 (B|1, Hq|1, N, N) view with dense rows (see flash_attn).
+        ctx.bias = bias.detach() if bias is not None else None
         seg_start, seg_end = segs if segs is not None else (None, None)
         bits, bits_t = mask if mask is not None else (None, None)
         z, z_t, z_scale = drop if drop is not None else (None, None, 1.0)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
-                                        seg_end, scale, bits, drop=z, drop_scale=z_scale)
+                                        seg_end, scale, bits, drop=z, drop_scale=z_scale,
+                                        bias=ctx.bias)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
         if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
-                or segs is not None or scale or mask is not None or drop is not None):
+                or segs is not None or scale or mask is not None or drop is not None
+                or bias is not None):
             o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end,
-                                     scale, bits, drop=z, drop_scale=z_scale)
+                                     scale, bits, drop=z, drop_scale=z_scale, bias=ctx.bias)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -105,14 +109,19 @@ class _FlashAttnP100(torch.autograd.Function):
         seg_start, seg_end = ctx.segs if ctx.segs is not None else (None, None)
         bits, bits_t = ctx.mask if ctx.mask is not None else (None, None)
         z, z_t, z_scale = ctx.drop if ctx.drop is not None else (None, None, 1.0)
+        dbias = None
+        if ctx.bias is not None and ctx.needs_input_grad[12]:  # bias is input 12
+            B, H, N = grad_o.size(0), grad_o.size(1), grad_o.size(2)
+            dbias = torch.zeros(B, H, N, N, dtype=torch.float32, device=grad_o.device)
         if ctx.bnhd:
             qb, kb, vb, ob, lse = ctx.saved_tensors
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
                                             ctx.window, ctx.alibi, seg_start, seg_end, ctx.scale,
-                                            bits, bits_t, z, z_t, z_scale)
+                                            bits, bits_t, z, z_t, z_scale, ctx.bias, dbias)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
-                    None, None, None, None, None, None, None, None, None)
+                    None, None, None, None, None, None, None, None, None,
+                    _reduce_bias_grad(dbias, ctx.bias))
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
@@ -121,19 +130,28 @@ class _FlashAttnP100(torch.autograd.Function):
         g = grad_o.contiguous()
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
                 or ctx.alibi is not None or ctx.segs is not None or ctx.scale
-                or ctx.mask is not None or ctx.drop is not None):
+                or ctx.mask is not None or ctx.drop is not None or ctx.bias is not None):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
                                           ctx.alibi, seg_start, seg_end, ctx.scale, bits, bits_t,
-                                          z, z_t, z_scale)
+                                          z, z_t, z_scale, ctx.bias, dbias)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
-                None, None, None, None)
+                None, None, None, None, _reduce_bias_grad(dbias, ctx.bias))
+
+
+def _reduce_bias_grad(dbias, bias):
+    """The full (B, Hq, N, N) gradient summed over the dimensions the bias
+    shares (size 1), in the bias's shape."""
+    if dbias is None:
+        return None
+    dims = [d for d in (0, 1) if bias.size(d) == 1 and dbias.size(d) != 1]
+    return dbias.sum(dim=dims, keepdim=True) if dims else dbias
 
 
 def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
                alibi_slopes=None, segment_ids=None, softmax_scale=None, attn_mask=None,
-               dropout_p=None, dropout_seed=None):
+               dropout_p=None, dropout_seed=None, attn_bias=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -183,7 +201,13 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         None, so torch.manual_seed makes runs repeat) through
         dropout_bits(), and the backward reuses the forward's bits. The
         drawn rate is p rounded to a multiple of 1/65536, and the scale
-        matches it exactly.
+        matches it exactly;
+      * attn_bias, a floating tensor of shape (N, N), (B, N, N) or
+        (B|1, Hq|1, N, N) on q's device: added to the scaled scores before
+        the masks and the softmax (torch scaled_dot_product_attention's
+        float attn_mask), in fp32. When it requires grad its gradient (the
+        gradient of the scaled scores, summed over the dimensions it
+        shares) comes back in its own shape and dtype.
     """
     window = 0
     if sliding_window is not None:
@@ -231,8 +255,25 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         if dropout_seed is None:
             dropout_seed = int(torch.randint(0, 2 ** 63 - 1, (), dtype=torch.int64))
         drop = dropout_bits(dropout_seed, p, q.size(0), q.size(1), q.size(2), q.device)
+    bias = None
+    if attn_bias is not None:
+        bias = attn_bias
+        if not bias.is_floating_point():
+            raise ValueError(f"attn_bias must be a floating tensor, got {bias.dtype}")
+        if bias.dim() == 2:
+            bias = bias[None, None]
+        elif bias.dim() == 3:
+            bias = bias[:, None]
+        n = q.size(2)
+        if bias.dim() != 4 or tuple(bias.shape[2:]) != (n, n) \
+                or bias.size(0) not in (1, q.size(0)) or bias.size(1) not in (1, q.size(1)):
+            raise ValueError(f"attn_bias must be (N, N), (B, N, N) or (B|1, Hq|1, N, N) with "
+                             f"N = {n}, got {tuple(attn_bias.shape)}")
+        bias = bias.float()
+        if bias.stride(-1) != 1 or bias.stride(-2) != n:
+            bias = bias.contiguous()
     return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes,
-                                segs, scale, mask, drop)
+                                segs, scale, mask, drop, bias)
 
 
 def dropout_bits(seed, p, batch, heads, n, device):

@@ -27,13 +27,14 @@ a row) goes to the kernels as a bit mask over the keys, on top of the layer's
 causal mask and window, as eager combines them; a query row left with no key
 gets a zero output where eager's is arbitrary.
 
-A 4-D mask handed to the model (boolean, True = attend, or additive with only
-0 and blocking values <= -1e4 or -inf) reaches every layer as it is
-(masking_utils returns 4-D masks unchanged); as with eager and sdpa it alone
-decides which keys each query sees, and it goes to the kernels as a bit mask.
-The causal flag is kept only when the mask allows no key above the diagonal,
-where it changes nothing but the tiles skipped. An additive mask with other
-values is a bias the kernels do not add, and raises.
+A 4-D mask handed to the model (boolean, True = attend, or additive) reaches
+every layer as it is (masking_utils returns 4-D masks unchanged); as with
+eager and sdpa it alone decides which keys each query sees. Boolean masks and
+additive ones with only 0 and blocking values (<= -1e4 or -inf) go to the
+kernels as a bit mask; any other additive mask is an attention bias and goes
+to them as such (fp32), added to the scaled scores as eager adds it. The
+causal flag is kept only when the mask allows no key above the diagonal,
+where it changes nothing but the tiles skipped.
 
 Also beyond the reference, a causal layer's sliding window (Qwen3's and
 Mistral-style `sliding_window`) runs in the kernels: row i sees keys
@@ -53,7 +54,7 @@ reference rejects (fa_p100_hf.py:83-85), runs in the kernels with keep bits
 drawn per call from torch's default generator (fa_p100.dropout_bits).
 
 Every other unsupported request raises NotImplementedError instead of
-degrading (fa_p100_hf.py:24-32): masks carrying a bias, output_attentions,
+degrading (fa_p100_hf.py:24-32): output_attentions,
 head_mask, a window on non-causal attention, head_dim other than
 not a multiple of 8 up to 128, q_len != kv_len (KV-cache decoding). A scale other than 1/sqrt(D),
 which the reference rejected, goes to the kernels.
@@ -73,10 +74,11 @@ _warned_cast = False
 #           or None;
 #   segs:   packed-sequence bounds (seg_start, seg_end), or _NOT_PACKED once
 #           the call's position_ids were found to hold one sequence per row;
-#   mask:   None, or (bits, bits_t, causal): the packed words of a mask
-#           (pack_mask's layout) and, for a 4-D mask, whether the causal flag
-#           may stay on (None for a 2-D padding mask, which the layer's causal
-#           mask and window apply on top of).
+#   mask:   None, or (bits, bits_t, causal, bias): the packed words of a
+#           mask (pack_mask's layout; None for a bias), for a 4-D mask
+#           whether the causal flag may stay on (None for a 2-D padding mask,
+#           which the layer's causal mask and window apply on top of), and
+#           an additive 4-D mask that carries a bias (fp32), or None.
 # The mask is packed once per model call rather than once per layer.
 # transformers passes a model's **kwargs down to each decoder layer and from
 # there to the attention interface, and gradient checkpointing replays a
@@ -179,30 +181,34 @@ def _as_int32(words):
 
 
 def dense_mask_bits(mask, batch, heads):
-    """(bits, bits_t, causal) of a 4-D attention mask (B or 1, 1 or heads,
-    N, N) as transformers hands it to the attention interface: boolean
-    (True = attend) or additive (0 = attend; -inf or <= -1e4 = blocked).
-    `causal` tells whether the mask allows no key above the diagonal."""
+    """(bits, bits_t, causal, bias) of a 4-D attention mask (B or 1, 1 or
+    heads, N, N) as transformers hands it to the attention interface:
+    boolean (True = attend), or additive. An additive mask whose values are
+    only 0 (attend) and blocking ones (-inf, or <= -1e4) becomes bits like a
+    boolean one (bias None); any other additive mask is a bias: it goes to
+    the kernels as fp32 `attn_bias` (bits None), blocking values included
+    (exp underflows to exactly 0 there). `causal` tells whether the mask
+    allows no key above the diagonal."""
     if mask.dim() != 4 or mask.size(-1) != mask.size(-2) or mask.size(0) not in (1, batch) \
             or mask.size(1) not in (1, heads):
         raise NotImplementedError(
             f"fa_p100 takes a 4-D attention mask of shape ({batch} or 1, 1 or {heads}, N, N); "
             f"got {tuple(mask.shape)}.")
+    bias = None
     if mask.dtype == torch.bool:
         allowed = mask
     elif mask.is_floating_point():
-        allowed = mask == 0
-        if not bool((allowed | (mask <= _BLOCKED)).all()):
-            raise NotImplementedError(
-                "fa_p100 got an additive attention mask with values other than 0 and "
-                "blocking ones (-inf, or <= -1e4): that is a bias, which the kernels do not "
-                "add. Pass a boolean mask or use attn_implementation='sdpa'.")
+        allowed = mask > _BLOCKED
+        if not bool((mask[allowed] == 0).all()):
+            bias = mask.float()
     else:
         raise NotImplementedError(
             f"fa_p100 takes a boolean or floating attention mask, got {mask.dtype}.")
     causal = not bool(torch.triu(allowed, diagonal=1).any())
+    if bias is not None:
+        return None, None, causal, bias
     bits, bits_t = pack_mask(allowed, batch, heads)
-    return bits, bits_t, causal
+    return bits, bits_t, causal, None
 
 
 def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout=0.0,
@@ -300,7 +306,8 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
     out = flash_attn(query, key, value, causal=bool(is_causal), full_precision=full_precision,
                      kv_len=kv_len, sliding_window=sliding_window, segment_ids=segs,
                      softmax_scale=softmax_scale,
-                     attn_mask=None if mask is None else mask[:2],
+                     attn_mask=None if mask is None or mask[0] is None else mask[:2],
+                     attn_bias=None if mask is None else mask[3],
                      dropout_p=float(dropout) if dropout else None)
     return out.transpose(1, 2).contiguous().to(orig_dtype), None
 
@@ -364,7 +371,7 @@ def enable_fa_p100(model, full_precision=False):
             elif attention_mask is not None and not bool(attention_mask.all()):
                 spans = padding_spans(attention_mask)
                 if spans is None:
-                    mask = key_mask_bits(attention_mask) + (None,)
+                    mask = key_mask_bits(attention_mask) + (None, None)
                 else:
                     first, end = spans
                     kv_len = end  # keys past the run exist for no row

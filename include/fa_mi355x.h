@@ -51,8 +51,9 @@ enum {
   FA_ERR_SCALE = 10012,      /* softmax scale negative or not finite */
   FA_ERR_SCRATCH = 10013,    /* fa_bwd_noalloc: the shape needs more than its scratch */
   FA_ERR_MASK = 10014,       /* mask_heads not 1 or Hq, or a backward mask without mask_t */
-  FA_ERR_DROPOUT = 10015     /* dropout p not in [0, 1), a scale not positive and finite, or
+  FA_ERR_DROPOUT = 10015,    /* dropout p not in [0, 1), a scale not positive and finite, or
                                 a backward with drop but without drop_t */
+  FA_ERR_BIAS = 10016        /* a negative bias stride, or dbias without bias */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -170,7 +171,7 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
 /*
  * Options of the general pair below; a zeroed struct (or a NULL pointer)
  * means fp16, dense (B, H, N, D), no key lengths, no window, no ALiBi, no
- * packed sequences, no mask, no dropout.
+ * packed sequences, no mask, no dropout, no bias.
  *   - dtype: FA_DTYPE_FP16 or FA_DTYPE_BF16 for q, k, v, o, dO, dq, dk, dv
  *     (bf16: products on the bf16 MFMA with fp32 accumulation, P and dS
  *     rounded to bf16 as operands, outputs rounded to nearest even);
@@ -215,7 +216,16 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *     drop_scale) v with P the softmax over every key, lse that softmax's
  *     (dropout does not touch it). The forward reads drop, the backward both
  *     (drop_t is required there) with the same bits and scale as the
- *     forward. fa_dropout_bits draws them.
+ *     forward. fa_dropout_bits draws them;
+ *   - bias, bias_stride_b, bias_stride_h, dbias: an additive attention bias
+ *     (bias = NULL: none), fp32, added to the scaled logits before the masks
+ *     and the softmax: element (b, h, i, j) of query head h at
+ *     bias[b * bias_stride_b + h * bias_stride_h + i * N + j] (strides in
+ *     elements, 0 to share one plane over batch entries or heads; rows are
+ *     dense). The backward writes the bias's gradient, dS of the scaled
+ *     logits, to dbias when it is not NULL: dense (B, Hq, N, N) fp32, only
+ *     where a query row meets a key it may attend (the caller zeroes dbias
+ *     first; reduce over shared dimensions afterwards).
  */
 typedef struct fa_options {
   int dtype;
@@ -232,6 +242,10 @@ typedef struct fa_options {
   const uint32_t* drop;
   const uint32_t* drop_t;
   float drop_scale;
+  const float* bias;
+  long long bias_stride_b;
+  long long bias_stride_h;
+  float* dbias;
 } fa_options;
 
 /*

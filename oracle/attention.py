@@ -61,7 +61,7 @@ def _group_sum(g, hkv):
 
 
 def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=None,
-            scale=None, mask=None):
+            scale=None, mask=None, bias=None):
     """Scaled logits S*scale with the causal upper triangle set to -inf.
 
     The scale is applied to the logit after the product, never to Q
@@ -79,7 +79,9 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
     With `mask` (a boolean array broadcastable to (B, Hq, N, N), another
     extension) key col is also masked for row wherever mask[b, h, row, col]
     is False, as torch's scaled_dot_product_attention reads a boolean
-    attn_mask.
+    attn_mask. With `bias` (a float array broadcastable to (B, Hq, N, N),
+    another extension) it is added to the scaled logits before the masks, as
+    SDPA reads a float attn_mask.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
@@ -91,6 +93,8 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
             raise ValueError("alibi needs one slope per query head")
         dist = np.abs(np.arange(n)[:, None] - np.arange(n)[None, :]).astype(np.float64)
         s = (s - (slopes[:, None, None] * dist[None]).astype(dtype)[None]).astype(dtype)
+    if bias is not None:
+        s = (s + np.broadcast_to(np.asarray(bias, dtype=np.float64), s.shape)).astype(dtype)
     if causal:
         above = np.triu(np.ones((n, n), dtype=bool), 1)
         s = np.where(above, -np.inf, s).astype(dtype)
@@ -163,21 +167,22 @@ def _drop_factor(dropout, shape):
 
 
 def attention_fwd(q, k, v, causal=False, dtype=np.float64, kv_len=None, window=None,
-                  alibi=None, segments=None, scale=None, mask=None, dropout=None):
+                  alibi=None, segments=None, scale=None, mask=None, dropout=None, bias=None):
     """Forward: returns (O, LSE) computed in `dtype`.
 
     q: (B,Hq,N,D); k, v: (B,Hkv,N,D). O is (B,Hq,N,D) and LSE is (B,Hq,N),
     both in `dtype`. LSE is in natural-log units of the scaled logits
     (flash_fwd.cuh:324-329). `kv_len`, `window`, `alibi`, `segments`, `mask`:
     optional per-entry key lengths, sliding window, ALiBi slopes, packed
-    sequence ids and boolean mask (see _scores). `dropout` = (keep, scale)
+    sequence ids, boolean mask and float bias (see _scores). `dropout` = (keep, scale)
     (an extension): O = (P * keep * scale) V with P the softmax over every
     key; LSE is that softmax's, unchanged by dropout.
     """
     hq = q.shape[1]
     k = expand_kv(np.asarray(k), hq)
     v = expand_kv(np.asarray(v), hq)
-    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments, scale, mask)
+    s = _scores(np.asarray(q), k, causal, dtype, kv_len, window, alibi, segments, scale, mask,
+                bias)
     m = s.max(axis=-1, keepdims=True)
     # A row that sees no key at all (key lengths with a window: pad rows more
     # than W past their entry's length; or a mask row without a set bit) gets
@@ -201,7 +206,8 @@ def bwd_preprocess(o, do, dtype=np.float64):
 
 
 def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64, kv_len=None,
-                  window=None, alibi=None, segments=None, scale=None, mask=None, dropout=None):
+                  window=None, alibi=None, segments=None, scale=None, mask=None, dropout=None,
+                  bias=None, dbias=False):
     """Analytic backward: returns (dQ, dK, dV) in `dtype`.
 
     When `o`/`lse` are given they are used as the saved forward state (as the
@@ -209,6 +215,8 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     dK and dQ carry the scale; dV does not (flash_bwd.cuh:442, 457).
     With `dropout` = (keep, scale), F = keep * scale: dV = (P F)^T dO,
     dP = (dO V^T) F, dS = P (dP - rowsum(dO O)) with O the dropped output.
+    With dbias=True a fourth result is dS (B, Hq, N, N), the gradient of
+    the scaled logits and hence of an additive `bias`.
     """
     q = np.asarray(q)
     hq, hkv = q.shape[1], np.asarray(k).shape[1]
@@ -220,8 +228,8 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     dod = np.asarray(do).astype(dtype)
     if o is None or lse is None:
         o, lse = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale,
-                               mask, dropout)
-    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments, scale, mask)
+                               mask, dropout, bias)
+    s = _scores(q, ke, causal, dtype, kv_len, window, alibi, segments, scale, mask, bias)
     p = np.exp(s - np.asarray(lse).astype(dtype)[..., None])
     f = 1.0 if dropout is None else _drop_factor(dropout, p.shape)
     dv = np.matmul(np.swapaxes(p * f, -1, -2), dod)
@@ -230,14 +238,16 @@ def attention_bwd(q, k, v, do, causal=False, o=None, lse=None, dtype=np.float64,
     ds = p * (dp - dvec[..., None])
     dq = np.matmul(ds, ke) * sc
     dk = np.matmul(np.swapaxes(ds, -1, -2), qd) * sc
+    if dbias:
+        return dq, _group_sum(dk, hkv), _group_sum(dv, hkv), ds
     return dq, _group_sum(dk, hkv), _group_sum(dv, hkv)
 
 
 def attention_loss(q, k, v, do, causal=False, dtype=np.float64, kv_len=None, window=None,
-                   alibi=None, segments=None, scale=None, mask=None, dropout=None):
+                   alibi=None, segments=None, scale=None, mask=None, dropout=None, bias=None):
     """Scalar loss sum(dO * O) whose gradient is attention_bwd (bwd.cu:73-105)."""
     o, _ = attention_fwd(q, k, v, causal, dtype, kv_len, window, alibi, segments, scale, mask,
-                         dropout)
+                         dropout, bias)
     return float((o * np.asarray(do).astype(dtype)).sum())
 
 

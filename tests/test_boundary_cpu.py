@@ -105,6 +105,13 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 4, 2, 8, 64, 0,
                          fa_opts(drop=1, drop_scale=1.25), s) == 10015
     assert b"drop_t" in lib.fa_error_string(10015)
+    # bias: strides not negative; dbias only with a bias
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 4, 2, 8, 64, 0,
+                         fa_opts(bias=1, bias_stride_b=-1), s) == 10016
+    assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 4, 2, 8, 64, 0, fa_opts(dbias=1), s) == 10016
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, 64, 1,
+                         fa_opts(bias=1, bias_stride_b=0, bias_stride_h=64), s) == 10005
+    assert b"dbias" in lib.fa_error_string(10016)
     # the dropout generator: p in [0, 1), shape, pointers; the scale of the drawn rate
     for bad in (-0.1, 1.0, 1.5, float("nan")):
         assert lib.fa_dropout_bits(7, bad, 1, 8, one, one, s) == 10015
@@ -156,7 +163,7 @@ def test_public_api_surface_matches_reference():
     # (key lengths, sliding window, ALiBi slopes, packing, scale, mask) come
     # after them and default to None, so every reference call binds the same way.
     extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids", "softmax_scale",
-                  "attn_mask", "dropout_p", "dropout_seed"]
+                  "attn_mask", "dropout_p", "dropout_seed", "attn_bias"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False

@@ -23,7 +23,6 @@ MOD = types.SimpleNamespace(is_causal=True)
 
 
 @pytest.mark.parametrize("kwargs,match", [
-    (dict(attention_mask=torch.ones(1, 1, 4, 4)), "additive attention mask"),
     (dict(attention_mask=torch.ones(1, 3, 4, 4, dtype=torch.bool)), "4-D attention mask"),
     (dict(attention_mask=torch.ones(1, 1, 4, 4, dtype=torch.int32)), "boolean or floating"),
     (dict(attention_mask=None, output_attentions=True), "output_attentions"),
@@ -162,7 +161,8 @@ def test_checkpointed_layers_see_the_padding_in_their_recompute(monkeypatch):
     seen = []
 
     def spy(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
-            segment_ids=None, softmax_scale=None, attn_mask=None, dropout_p=None):
+            segment_ids=None, softmax_scale=None, attn_mask=None, dropout_p=None,
+            attn_bias=None):
         seen.append((torch.is_grad_enabled(),
                      None if kv_len is None else kv_len.tolist(),
                      None if segment_ids is None else segment_ids[0].tolist(),
@@ -234,7 +234,11 @@ def test_dense_mask_checks_on_the_host():
     for m in (tril, additive, finfo_min, tril.expand(2, 4, n, n)):
         with pytest.raises(RuntimeError, match="mask must be a CUDA tensor"):
             hf.dense_mask_bits(m, 2, 4)
-    with pytest.raises(NotImplementedError, match="bias"):
-        hf.dense_mask_bits(additive + 0.5 * tril, 2, 4)
+    # An additive mask with other values is a bias: no bits, the fp32 values.
+    bits, bits_t, causal, bias = hf.dense_mask_bits(additive + 0.5 * tril, 2, 4)
+    assert bits is None and causal and bias.dtype == torch.float32
+    assert torch.equal(bias, additive + 0.5 * tril)
+    _, _, causal, _ = hf.dense_mask_bits(torch.full((1, 1, n, n), 0.25), 2, 4)
+    assert not causal
     with pytest.raises(NotImplementedError, match="4-D attention mask"):
         hf.dense_mask_bits(tril.expand(3, 1, n, n), 2, 4)

@@ -659,3 +659,56 @@ def test_dropout_attention_pins(causal):
     ds = p * (dp - (o * do).sum(-1)[..., None])
     wrong_dq = ds @ ora.expand_kv(k, hq) / math.sqrt(d)
     assert not np.allclose(wrong_dq, tq.grad.numpy(), atol=1e-6)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_bias_pins(causal):
+    """An additive attention bias (an extension; the reference has no bias
+    input, HANDOFF.md:281): against torch SDPA with the same float attn_mask
+    and autograd in float64, the bias's own gradient included (per-head and
+    shared planes, with a boolean mask and ALiBi beside it); a zero bias
+    equals none; a bias of -slope |i - j| equals ALiBi; finite differences in
+    the bias; and a planted transposed bias fails."""
+    rng = np.random.default_rng(71 + causal)
+    b, hq, hkv, n, d = 2, 4, 2, 17, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, n, d), rnd(rng, b, hkv, n, d)
+    i, j = np.arange(n)[:, None], np.arange(n)[None, :]
+    for shape in ((b, hq, n, n), (1, hq, n, n), (b, 1, n, n)):
+        bias = rnd(rng, *shape, scale=2.0)
+        mask = rng.random((b, 1, n, n)) < 0.8
+        mask |= (i == j)[None, None]
+        o, lse = ora.attention_fwd(q, k, v, causal, bias=bias, mask=mask)
+        dq, dk, dv, ds = ora.attention_bwd(q, k, v, do, causal, bias=bias, mask=mask, dbias=True)
+        tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+        tb = torch.tensor(bias, requires_grad=True)
+        allowed = torch.tensor(mask & (j <= i) if causal else mask)
+        fb = tb.masked_fill(~allowed, float("-inf"))
+        ref = F.scaled_dot_product_attention(tq, tk.repeat_interleave(hq // hkv, 1),
+                                             tv.repeat_interleave(hq // hkv, 1), attn_mask=fb)
+        ref.backward(torch.tensor(do))
+        assert np.allclose(o, ref.detach().numpy(), atol=1e-12)
+        for got, t in zip((dq, dk, dv), (tq, tk, tv)):
+            assert np.allclose(got, t.grad.numpy(), atol=1e-10)
+        red = ds.sum(axis=tuple(a for a in (0, 1) if shape[a] == 1), keepdims=True)
+        assert np.allclose(red, tb.grad.numpy(), atol=1e-10), shape
+    zero = np.zeros((1, 1, n, n))
+    assert np.array_equal(ora.attention_fwd(q, k, v, causal, bias=zero)[0],
+                          ora.attention_fwd(q, k, v, causal)[0])
+    slopes = np.array([0.3, 0.1, 0.05, 0.02])
+    as_bias = -slopes[None, :, None, None] * np.abs(i - j)[None, None]
+    assert np.allclose(ora.attention_fwd(q, k, v, causal, bias=as_bias)[0],
+                       ora.attention_fwd(q, k, v, causal, alibi=slopes)[0], atol=1e-12)
+    bias = rnd(rng, b, hq, n, n)
+    _, _, _, ds = ora.attention_bwd(q, k, v, do, causal, bias=bias, dbias=True)
+    h = 1e-5
+    for _ in range(6):
+        idx = tuple(int(rng.integers(x)) for x in bias.shape)
+        plus, minus = bias.copy(), bias.copy()
+        plus[idx] += h
+        minus[idx] -= h
+        fd = (ora.attention_loss(q, k, v, do, causal, bias=plus)
+              - ora.attention_loss(q, k, v, do, causal, bias=minus)) / (2 * h)
+        assert abs(fd - ds[idx]) < 1e-6 * max(1.0, abs(fd))
+    assert not np.allclose(ora.attention_fwd(q, k, v, causal, bias=np.swapaxes(bias, -1, -2))[0],
+                           ora.attention_fwd(q, k, v, causal, bias=bias)[0], atol=1e-6)
