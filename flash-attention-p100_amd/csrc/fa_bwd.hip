@@ -213,11 +213,15 @@ struct KVWave {
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
   // mtw: the mask bits of key j_col for this step's 32 query rows i0 + 32m ..
   // (bit = row offset; all set without a mask).
+  // bv: the step's bias values, replaced by `bnext()` (the next step's) as
+  // soon as they are added, so one set of registers carries the prefetch.
+  template <class BiasNext>
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
                                        const float* dvs, const half_t* Vt,
                                        int m, int kr0, int i0, int j_col, int row_lo, int row_end,
                                        float alibi_raw, uint32_t mtw, uint32_t ztw, float zs,
-                                       const floatx16& bv, float bias_raw, int lane, int roff,
+                                       floatx16& bv, const BiasNext& bnext, float bias_raw,
+                                       int lane, int roff,
                                        const typename Stream<D>::Offsets& so, float c) {
     using S = Stream<D>;
     const int h = lane >> 5;
@@ -256,6 +260,7 @@ struct KVWave {
     if (BOUNDS && bias_raw != 0.f) {  // attention bias of the 16 (row, j_col) in raw units
 #pragma unroll
       for (int r = 0; r < 16; ++r) sacc[r] = fmaf(bv[r], bias_raw, sacc[r]);
+      bv = bnext();
     }
     half8 pb[2], sb[2];
 #pragma unroll
@@ -295,11 +300,13 @@ struct QWave {
 
   // Keys j0 + 32s .. +31 (s = this wave's half of the staged 64-key tile).
   // mw: row i_row's mask bits for keys j0 + 32s .. (all set without a mask).
-  template <class Issue>
+  // bv: as in KVWave::step.
+  template <class Issue, class BiasNext>
   __device__ __forceinline__ void step(const half_t* Ks, const half_t* Vs, int s, int j0,
                                        int i_row, int Nk, int key_lo, float alibi_raw,
-                                       uint32_t mw, uint32_t zw, float zs, const floatx16& bv,
-                                       float bias_raw, float* dbrow, int lane,
+                                       uint32_t mw, uint32_t zw, float zs, floatx16& bv,
+                                       const BiasNext& bnext, float bias_raw, float* dbrow,
+                                       bool db_x4, int lane,
                                        const typename Stream<D>::Offsets& so, float c,
                                        const Issue& issue) {
     using S = Stream<D>;
@@ -337,8 +344,10 @@ struct QWave {
     if (BOUNDS && bias_raw != 0.f) {  // attention bias of the 16 (i_row, key) in raw units
 #pragma unroll
       for (int r = 0; r < 16; ++r) st[r] = fmaf(bv[r], bias_raw, st[r]);
+      bv = bnext();
     }
     half8 sb[2];
+    floatx4 ds4;  // the current run of four keys' dS (16-byte dbias stores)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int idx = 8 * (r >> 2) + (r & 3);
@@ -349,8 +358,19 @@ struct QWave {
       const bool keep = (zw >> (idx + 4 * h)) & 1u;
       const float ds = p * ((keep ? pt[r] * zs : 0.f) - dvv);
       sb[r >> 3][r & 7] = to16<BF>(ds);
-      // The bias's gradient is dS itself (keys past N are not stored).
-      if (BOUNDS && dbrow && idx < hi) dbrow[base + idx] = ds;
+      // The bias's gradient is dS itself; keys from the key length on are not
+      // stored, except that a 16-byte run (db_x4: N % 4 == 0 and an aligned
+      // plane, so no run crosses N) starting before it stores its masked
+      // keys' zeros.
+      ds4[r & 3] = ds;
+      if (BOUNDS && dbrow) {
+        if (db_x4) {
+          if ((r & 3) == 3 && idx - 3 < hi)
+            *reinterpret_cast<floatx4*>(dbrow + base + idx - 3) = ds4;
+        } else if (idx < hi) {
+          dbrow[base + idx] = ds;
+        }
+      }
     }
     // dQ^T += K^T dS^T; k-step q = keys 32s+16q .. +15 (operands one ahead).
     half8 kt = S::tr_operand(Ks, 0, so, 0);
@@ -562,18 +582,18 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       if (wave == 0) vec_load64(tv, make_rsrc(Lse2 + bhq * N, (uint32_t)N * 4), i0, lane);
       if (wave == 1) vec_load64(tv + kSub, make_rsrc(Dvec + bhq * N, (uint32_t)N * 4), i0, lane);
     };
-    // Bias values of step `it` for this lane's key and its 16 query rows
-    // (rows or keys past N read as 0: masked anyway); loaded one step ahead.
+    // Bias values of step `it` for this lane's key and its 16 query rows,
+    // through a resource over the wave's 32 rows (rows past N read zeros, a
+    // key past N the next row: both masked); loaded one step ahead.
+    const uint32_t bvoff1 = (uint32_t)(4 * h * N + j_col) * 4u;
     auto bload1 = [&](int it) {
       floatx16 v = zero16();
       if (has_bias) {
-        const float* pl = bplane(hkv * group + it / n_qt);
-        const int r0 = i_start + (it % n_qt) * kSub + 32 * half + 4 * (lane >> 5);
+        const rsrc_t rb = bias_rows_rsrc(bplane(hkv * group + it / n_qt),
+                                         i_start + (it % n_qt) * kSub + 32 * half, N);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = r0 + 8 * (r >> 2) + (r & 3);
-          v[r] = row < N && j_col < N ? pl[(size_t)row * N + j_col] : 0.f;
-        }
+        for (int r = 0; r < 16; ++r)
+          v[r] = buf_load_f32(rb, bvoff1, (uint32_t)((8 * (r >> 2) + (r & 3)) * N) * 4u);
       }
       return v;
     };
@@ -583,8 +603,6 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     auto step = [&](int it, auto par) {
       constexpr int P = decltype(par)::value;
       fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
-      const floatx16 bv_now = bv1;
-      if (has_bias) bv1 = bload1(min(it + 1, it_end - 1));
       const half_t* Qs = P ? ta1 : ta0;
       const half_t* Os = P ? tb1 : tb0;
       const float* lse2s = P ? vec1 : vec0;
@@ -602,7 +620,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const uint32_t ztw =
           BITMASK && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
       w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
-             alibi_raw, mtw, ztw, zs, bv_now, braw, lane, roff, so, scale_log2);
+             alibi_raw, mtw, ztw, zs, bv1, [&] { return bload1(min(it + 1, it_end - 1)); },
+             braw, lane, roff, so, scale_log2);
       wait_vmem();
       __syncthreads();
     };
@@ -728,18 +747,32 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           BITMASK && mask ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
       const uint32_t* zrow =
           BITMASK && drop ? zplane(drop, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
-      // This lane's bias row and gradient row (rows past N: none).
-      const float* brow =
-          has_bias ? bplane(hq) + (size_t)min(i_row, N - 1) * N : nullptr;
+      // This lane's bias values of key step t (four runs of four keys, read
+      // as in the forward: a resource over the wave's 32 rows, 16-byte loads
+      // when N % 4 == 0 on a 16-byte aligned plane) and its gradient row
+      // (rows past N: none).
+      const float* bpl = has_bias ? bplane(hq) : nullptr;
+      const rsrc_t rb2 = bias_rows_rsrc(bpl, iw, N);
+      const bool bias_x4 =
+          has_bias && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(bpl) & 15u) == 0;
+      const uint32_t bvoff2 = (uint32_t)(l32 * N + 32 * half + 4 * h) * 4u;
       float* dbrow = BIAS && dbias && row_ok ? dbias + (bhq * N + i_row) * N : nullptr;
-      auto bload2 = [&](int t) {  // bias of key step t for this row's 16 keys
+      const bool db_x4 =
+          BIAS && dbias && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(dbias) & 15u) == 0;
+      auto bload2 = [&](int t) {
         floatx16 v = zero16();
-        if (brow) {
-          const int key0 = t * kSub + 32 * half + 4 * (lane >> 5);
+        if (has_bias) {
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = key0 + 8 * (r >> 2) + (r & 3);
-            v[r] = key < N ? brow[key] : 0.f;
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const uint32_t soff = (uint32_t)(t * kSub + 8 * g4) * 4u;
+            if (bias_x4) {
+              const floatx4 x = buf_load_f32x4(rb2, bvoff2, soff);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[4 * g4 + e] = x[e];
+            } else {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[4 * g4 + e] = buf_load_f32(rb2, bvoff2 + 4u * e, soff);
+            }
           }
         }
         return v;
@@ -781,10 +814,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         const int word = min(t * (kSub / 32) + half, W32 - 1);  // keys t*kSub + 32*half ..
         const uint32_t mw = mrow ? mrow[word] : ~0u;
         const uint32_t zw = zrow ? zrow[word] : ~0u;
-        const floatx16 bv_now = bv2;
-        if (has_bias) bv2 = bload2(min(t + 1, n_kt - 1));
         w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, mw,
-               zw, zs, bv_now, braw, dbrow, lane, so, scale_log2, issue);
+               zw, zs, bv2, [&] { return bload2(min(t + 1, n_kt - 1)); }, braw, dbrow, db_x4,
+               lane, so, scale_log2, issue);
         wait_vmem();
         __syncthreads();
       };

@@ -100,7 +100,7 @@ const char* fa_error_string(int err) {
     case FA_ERR_DROPOUT:
       return "dropout p must lie in [0, 1) and its scale be positive and finite; the backward "
              "needs drop_t with drop";
-    case FA_ERR_BIAS: return "bias strides must not be negative, and dbias needs a bias";
+    case FA_ERR_BIAS: return "bias strides must not be negative, dbias needs a bias, and a bias needs N <= 2^22";
     case FA_ERR_SCRATCH:
       return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
              "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
@@ -118,7 +118,12 @@ constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0,       nul
                                      nullptr,   0,         0,       nullptr};
 
 // `backward`: the pass reads mask_t too.
-static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
+// Largest sequence length with a bias: the kernels read the bias through
+// buffer resources of 32 rows of N fp32 values, whose sizes stay below 2^32.
+// (One N x N fp32 plane at this N is 64 TiB, so no real caller meets it.)
+static constexpr int kMaxBiasN = 1 << 22;
+
+static int check_opts(const fa_options& op, int causal, int Hq, int N, bool backward) {
   if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
   if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
@@ -134,6 +139,7 @@ static int check_opts(const fa_options& op, int causal, int Hq, bool backward) {
   }
   if (op.bias_stride_b < 0 || op.bias_stride_h < 0) return FA_ERR_BIAS;
   if (op.dbias != nullptr && op.bias == nullptr) return FA_ERR_BIAS;
+  if (op.bias != nullptr && N > kMaxBiasN) return FA_ERR_BIAS;
   return FA_OK;
 }
 
@@ -145,7 +151,7 @@ static uint32_t dropout_threshold(float p) {
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
                int Hkv, int N, int D, int causal, const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal, Hq, false);
+  int rc = check_opts(op, causal, Hq, N, false);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -246,7 +252,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
                     const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal, Hq, true);
+  int rc = check_opts(op, causal, Hq, N, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc != FA_OK) return rc;
@@ -301,7 +307,7 @@ static int bwd_16(const void* q, const void* k, const void* v, const void* dO, c
                   const float* lse, void* dq, void* dk, void* dv, void* workspace,
                   size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                   const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal, Hq, true);
+  int rc = check_opts(op, causal, Hq, N, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!workspace || !dq) return FA_ERR_NULL;

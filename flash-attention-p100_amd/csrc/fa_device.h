@@ -194,6 +194,22 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 // offsets added to it cannot carry the sum past 2^32), so the lane reads
 // zeros: the columns past a head dim that is narrower than the tile.
 constexpr uint32_t kOutOfRange = 0x80000000u;
+// One and four fp32 values at voff + soff of a resource (zeros past its size).
+__device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+__device__ __forceinline__ floatx4 buf_load_f32x4(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+// Attention bias reads from an fp32 plane of N rows of N values: a resource
+// over the 32 rows from row0 (fewer at the plane's end, none past it), so
+// reads past the plane's last row return zeros, while a key past N in an
+// earlier row reads the next row's value, which every caller masks. The C
+// ABI keeps N <= 2^22 with a bias, so 32 rows stay below 2^32 bytes.
+__device__ __forceinline__ rsrc_t bias_rows_rsrc(const float* plane, int row0, int N) {
+  const int rows = max(0, min(32, N - row0));
+  return make_rsrc(plane + (size_t)min(row0, N) * N, (uint32_t)rows * (uint32_t)N * 4u);
+}
 // Each lane loads `size` bytes (4 or 16) from voff + soff into LDS at
 // lds + size * lane (lds wave-uniform).
 template <int size>

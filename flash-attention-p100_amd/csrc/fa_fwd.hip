@@ -100,11 +100,13 @@ struct FwdWave {
   // S^T is computed from its K tile Kn. `issue(s)` is called at issue points
   // s = 0 .. D/8 - 1 (after each product).
   // MASK: the step may need the causal / ragged mask, applied when `masked`.
-  template <bool MASK, bool NEXT, class Issue>
+  // bv: this step's bias values, replaced by `bnext()` (the next step's) as
+  // soon as they are added, so one set of registers carries the prefetch.
+  template <bool MASK, bool NEXT, class Issue, class BiasNext>
   __device__ __forceinline__ void step(const half_t* Kn, const half_t* Vs, int kq, int j0,
                                        bool masked, int i_row, int N, int w_lo, float alibi_raw,
-                                       uint32_t mw, uint32_t zw, const floatx16& bv,
-                                       float bias_raw, int lane, int roff,
+                                       uint32_t mw, uint32_t zw, floatx16& bv,
+                                       const BiasNext& bnext, float bias_raw, int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
     floatx16 s = sc;
@@ -130,6 +132,7 @@ struct FwdWave {
     if (BOUNDS && bias_raw != 0.f) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[r] = fmaf(bv[r], bias_raw, s[r]);
+      if constexpr (NEXT) bv = bnext();
     }
     if (MASK && masked) {
 #pragma unroll
@@ -282,16 +285,29 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   auto mword = [&](int j) { return mrow ? mrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
   auto zword = [&](int j) { return zrow ? zrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
   // Attention bias (BIAS instantiation; bbase null: none): this row's values
-  // for the wave's 16 keys of step j, keys past N read as 0 (masked anyway).
-  const float* brow = BIAS && bbase ? bbase + (size_t)min(i_row, N - 1) * N : nullptr;
+  // for the wave's 16 keys of step j, four runs of four keys, through a
+  // resource over the wave's 32 rows (keys past N read the next row or zeros
+  // and are masked). Rows of N % 4 == 0 values from a 16-byte aligned plane
+  // take one 16-byte load per run; a run never crosses the resource's end.
+  const bool has_bias = BIAS && bbase != nullptr;
+  const rsrc_t rbias = bias_rows_rsrc(bbase, i_base, N);
+  const bool bias_x4 =
+      has_bias && (N & 3) == 0 && (reinterpret_cast<uintptr_t>(bbase) & 15u) == 0;
+  const uint32_t bvoff = (uint32_t)(l32 * N + kq * 32 + 4 * h) * 4u;
   auto bload = [&](int j) {
     floatx16 v = zero16();
-    if (brow) {
-      const int key0 = j * kKV + kq * 32 + 4 * (lane >> 5);
+    if (has_bias) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = key0 + 8 * (r >> 2) + (r & 3);
-        v[r] = key < N ? brow[key] : 0.f;
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t soff = (uint32_t)(j * kKV + 8 * g) * 4u;
+        if (bias_x4) {
+          const floatx4 x = buf_load_f32x4(rbias, bvoff, soff);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * g + e] = x[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * g + e] = buf_load_f32(rbias, bvoff + 4u * e, soff);
+        }
       }
     }
     return v;
@@ -329,11 +345,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
     const uint32_t mw_now = mw, zw_now = zw;
-    const floatx16 bv_now = bv;
     if (BITMASK && NEXT) {
       mw = mword(j + 1);
       zw = zword(j + 1);
-      bv = bload(j + 1);
     }
     half_t* lk = P ? kt1 : kt0;  // receives K_{j+2}
     half_t* lv = P ? vt0 : vt1;  // receives V_{j+1}
@@ -352,7 +366,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
-                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv_now,
+                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv, [&] { return bload(j + 1); },
                                 BIAS ? bias_raw : 0.f, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {

@@ -53,7 +53,8 @@ enum {
   FA_ERR_MASK = 10014,       /* mask_heads not 1 or Hq, or a backward mask without mask_t */
   FA_ERR_DROPOUT = 10015,    /* dropout p not in [0, 1), a scale not positive and finite, or
                                 a backward with drop but without drop_t */
-  FA_ERR_BIAS = 10016        /* a negative bias stride, or dbias without bias */
+  FA_ERR_BIAS = 10016        /* a negative bias stride, dbias without bias, or a bias with
+                                N > 2^22 */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
