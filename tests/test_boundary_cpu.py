@@ -105,9 +105,12 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 4, 2, 8, 64, 0,
                          fa_opts(drop=1, drop_scale=1.25), s) == 10015
     assert b"drop_t" in lib.fa_error_string(10015)
-    # bias: strides not negative; dbias only with a bias
+    # bias: strides not negative; dbias only with a bias; N <= 2^22 with a bias
     assert lib.fa_fwd_ex(*([one] * 5), 1, 4, 2, 8, 64, 0,
                          fa_opts(bias=1, bias_stride_b=-1), s) == 10016
+    big = (1 << 22) + 8  # N * D within 2^29 at D = 8: only the bias bound applies
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 1, 1, big, 8, 0, fa_opts(bias=1), s) == 10016
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 1, 1, big, 8, 0, fa_opts(), s) == 10005
     assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 4, 2, 8, 64, 0, fa_opts(dbias=1), s) == 10016
     assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, 64, 1,
                          fa_opts(bias=1, bias_stride_b=0, bias_stride_h=64), s) == 10005
