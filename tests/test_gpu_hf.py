@@ -154,3 +154,62 @@ def test_hook_runs_bf16_under_bf16_autocast():
         rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
         env_g = ((grads["sdpa"][n] - g).norm() / g.norm()).item()
         assert rel <= max(5e-2, 2 * env_g), (n, rel, env_g)
+
+
+def test_qwen3_0p6b_full_depth_step_matches_eager_and_sdpa():
+    """The Qwen3-0.6B shape at its full depth (28 layers, hidden 1024, 16/8
+    heads of 128, SwiGLU 3072, vocab 151936) at seq 2048 (eager's stored
+    attention weights stay ~10 GB): one fp16-autocast training step through
+    the hook against eager and sdpa on the same weights and ids. The loss,
+    every layer's q/k/v/o projection gradients and the whole gradient vector
+    stay within a small multiple of the eager-vs-sdpa envelope, so the
+    kernel's error does not grow through 28 layers of backward."""
+    import fa_p100_hf
+    g = torch.Generator("cuda").manual_seed(4)
+    ids = torch.randint(0, 151936, (1, 2048), device="cuda", generator=g)
+    losses, grads = {}, {}
+    for impl in ("eager", "sdpa", "fa_p100"):
+        model = qwen3(28, 1024, 16, 8, 128, 3072, 151936, seed=5)
+        model.train()
+        if impl == "fa_p100":
+            fa_p100_hf.enable_fa_p100(model)
+        else:
+            model.config._attn_implementation = impl
+        with torch.autocast("cuda", torch.float16):
+            out = model(ids, labels=ids)
+        out.loss.backward()
+        torch.cuda.synchronize()
+        losses[impl] = out.loss.item()
+        grads[impl] = {n: p.grad.float() for n, p in model.named_parameters()
+                       if p.grad is not None}
+        del model, out
+        torch.cuda.empty_cache()
+    env_loss = abs(losses["sdpa"] - losses["eager"])
+    assert abs(losses["fa_p100"] - losses["eager"]) <= 3 * env_loss + 1e-4 * losses["eager"], losses
+
+    def rel(a, b):
+        return ((a - b).norm() / b.norm()).item()
+
+    worst = []
+    for n, ge in grads["eager"].items():
+        gf, gs = grads["fa_p100"][n], grads["sdpa"][n]
+        assert torch.isfinite(gf).all(), n
+        if "self_attn" in n and n.endswith("proj.weight"):
+            r_fa, r_env = rel(gf, ge), rel(gs, ge)
+            worst.append((r_fa / (r_env + 1e-6), n, r_fa, r_env))
+            assert r_fa <= 3 * r_env + 2e-3, (n, r_fa, r_env)
+    flat = lambda d: torch.cat([d[n].flatten() for n in grads["eager"]])
+    r_all, r_all_env = rel(flat(grads["fa_p100"]), flat(grads["eager"])), rel(
+        flat(grads["sdpa"]), flat(grads["eager"]))
+    assert r_all <= 3 * r_all_env + 1e-3, (r_all, r_all_env)
+    # Tighter: the hook against sdpa (both fused, fp32 softmax and
+    # accumulation) differs less than eager does from sdpa.
+    r_fs = rel(flat(grads["fa_p100"]), flat(grads["sdpa"]))
+    r_attn = max(rel(grads["fa_p100"][n], grads["sdpa"][n]) /
+                 (rel(grads["eager"][n], grads["sdpa"][n]) + 1e-6)
+                 for n in grads["eager"] if "self_attn" in n and n.endswith("proj.weight"))
+    print(f"loss {losses}; all-grad rel vs eager {r_all:.2e} (sdpa {r_all_env:.2e}), "
+          f"vs sdpa {r_fs:.2e}; worst attention ratio vs eager {max(worst)[:2]}, "
+          f"vs sdpa {r_attn:.3f}")
+    assert r_fs <= r_all_env, (r_fs, r_all_env)
+    assert r_attn <= 1.5, r_attn
