@@ -387,12 +387,8 @@ struct QWave {
 };
 
 // ---------------------------------------------------------------------------
-// BITMASK: the arbitrary-mask and dropout instantiation (with BOUNDS); its bit
-// tests stay out of the others, whose D = 128 copies have no registers to
-// spare. BIAS (with BITMASK): the one that also adds an attention bias and
-// writes its gradient, whose 16 prefetched values per step would otherwise
-// cost the mask and dropout paths their registers too.
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
+// FEAT: the optional per-score inputs compiled in (Feat, with BOUNDS).
+template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
@@ -474,17 +470,18 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const rsrc_t rk = rows_rsrc(K + kv_off, N, stk.n, dr), rv = rows_rsrc(V + kv_off, N, stk.n, dr);
   // Offset of query head hq's row 0 in Q, dO, dQ.
   auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
-  // Arbitrary mask (BITMASK instantiation): query head hq's bit plane,
+  constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
+  // Arbitrary mask (MASKB instantiations): query head hq's bit plane,
   // rows of W32 words, row-major (phase 2: row = query) or transposed (phase
   // 1: row = key). Word indices are clamped (bits past N are masked anyway).
   const int W32 = (N + 31) >> 5;
   auto plane = [&](const uint32_t* m, int hq) {
     return m + ((size_t)b * mask_heads + (mask_heads == 1 ? 0 : hq)) * N * W32;
   };
-  // Dropout keep bits (BITMASK instantiation): one plane per (b, query head),
+  // Dropout keep bits (DROPB instantiations): one plane per (b, query head),
   // in the mask's two layouts; zs scales the kept probabilities.
   auto zplane = [&](const uint32_t* z, int hq) { return z + ((size_t)b * Hq + hq) * N * W32; };
-  const float zs = BITMASK ? drop_scale : 1.f;
+  const float zs = DROPB ? drop_scale : 1.f;
   // Attention bias (BIAS instantiation; bias null: none), raw-score factor
   // bias_raw = 1/scale; its gradient dbias, dense (B, Hq, N, N).
   const bool has_bias = BIAS && bias != nullptr;
@@ -616,9 +613,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const size_t tword =
           (size_t)min(j_col, N - 1) * W32 + min((i0 + 32 * half) >> 5, W32 - 1);
       const uint32_t mtw =
-          BITMASK && mask_t ? plane(mask_t, hkv * group + it / n_qt)[tword] : ~0u;
+          MASKB && mask_t ? plane(mask_t, hkv * group + it / n_qt)[tword] : ~0u;
       const uint32_t ztw =
-          BITMASK && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
+          DROPB && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
       w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
              alibi_raw, mtw, ztw, zs, bv1, [&] { return bload1(min(it + 1, it_end - 1)); },
              braw, lane, roff, so, scale_log2);
@@ -744,9 +741,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       const half_t* dOg = dO + q_off(hq);
       // This lane's row of the mask (rows past N are never stored).
       const uint32_t* mrow =
-          BITMASK && mask ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
+          MASKB && mask ? plane(mask, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
       const uint32_t* zrow =
-          BITMASK && drop ? zplane(drop, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
+          DROPB && drop ? zplane(drop, hq) + (size_t)min(i_row, N - 1) * W32 : nullptr;
       // This lane's bias values of key step t (four runs of four keys, read
       // as in the forward: a resource over the wave's 32 rows, 16-byte loads
       // when N % 4 == 0 on a 16-byte aligned plane) and its gradient row
@@ -875,14 +872,14 @@ hipError_t launch_pre_d(const BwdArgs& a) {
   return hipGetLastError();
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
   const int n_tiles = (a.N + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D);
-  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BIAS, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
@@ -898,21 +895,27 @@ hipError_t launch_main_t(const BwdArgs& a) {
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
   // Key lengths, windows, packed sequences and ALiBi need the masked
-  // instantiation (kTile is a multiple of kSub), masks and dropout the bit
-  // one, a bias (with or without them) the bias one.
+  // instantiation (kTile is a multiple of kSub); a mask, dropout or a bias
+  // one of its copies with those inputs compiled in (Feat).
   const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
-  if (a.bias)
-    return a.causal ? launch_main_t<D, true, true, true, true, BF>(a)
-                    : launch_main_t<D, false, true, true, true, BF>(a);
-  if (a.mask || a.drop)
-    return a.causal ? launch_main_t<D, true, true, true, false, BF>(a)
-                    : launch_main_t<D, false, true, true, false, BF>(a);
+  auto with = [&](auto feat) {
+    constexpr int F = decltype(feat)::value;
+    return a.causal ? launch_main_t<D, true, true, F, BF>(a)
+                    : launch_main_t<D, false, true, F, BF>(a);
+  };
+  switch (feat_of(a.mask != nullptr, a.drop != nullptr, a.bias != nullptr)) {
+    case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
+    case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
+    case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});
+    case kFeatBias: return with(std::integral_constant<int, kFeatBias>{});
+    default: break;
+  }
   if (a.causal)
-    return bounds ? launch_main_t<D, true, true, false, false, BF>(a)
-                  : launch_main_t<D, true, false, false, false, BF>(a);
-  return bounds ? launch_main_t<D, false, true, false, false, BF>(a)
-                : launch_main_t<D, false, false, false, false, BF>(a);
+    return bounds ? launch_main_t<D, true, true, 0, BF>(a)
+                  : launch_main_t<D, true, false, 0, BF>(a);
+  return bounds ? launch_main_t<D, false, true, 0, BF>(a)
+                : launch_main_t<D, false, false, 0, BF>(a);
 }
 
 }  // namespace

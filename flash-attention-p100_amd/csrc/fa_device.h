@@ -194,6 +194,24 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 // offsets added to it cannot carry the sum past 2^32), so the lane reads
 // zeros: the columns past a head dim that is narrower than the tile.
 constexpr uint32_t kOutOfRange = 0x80000000u;
+
+// Optional per-score inputs of a masked (BOUNDS) instantiation: a bit-packed
+// mask, dropout keep bits, or an additive bias. Each costs registers in every
+// step of the D = 128 copies (the mask or the dropout bits alone ~90 bytes of
+// spills per lane, both ~180), so each set the launchers meet has its own
+// copy: FEAT = kFeatMask, kFeatDrop, both, or kFeatBias (a bias, with a mask
+// and dropout as run-time options).
+enum : int { kFeatMask = 1, kFeatDrop = 2, kFeatBias = 4 };
+template <int FEAT>
+struct Feat {
+  static constexpr bool kMask = (FEAT & (kFeatMask | kFeatBias)) != 0;
+  static constexpr bool kDrop = (FEAT & (kFeatDrop | kFeatBias)) != 0;
+  static constexpr bool kBias = (FEAT & kFeatBias) != 0;
+};
+// The instantiation serving a set of options (mask, dropout, bias present).
+__host__ __device__ constexpr int feat_of(bool mask, bool drop, bool bias) {
+  return bias ? kFeatBias : (mask ? kFeatMask : 0) | (drop ? kFeatDrop : 0);
+}
 // One and four fp32 values at voff + soff of a resource (zeros past its size).
 __device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));

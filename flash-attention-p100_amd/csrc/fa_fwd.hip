@@ -127,7 +127,7 @@ struct FwdWave {
       for (int r = 0; r < 16; ++r)
         s[r] = fmaf(-alibi_raw, fabsf(d0 - (float)(8 * (r >> 2) + (r & 3))), s[r]);
     }
-    // Additive attention bias (bit instantiation only; bias_raw = 1/scale
+    // Additive attention bias (the bias instantiation only; bias_raw = 1/scale
     // puts it in raw-score units): bv holds this row's 16 values of the step.
     if (BOUNDS && bias_raw != 0.f) {
 #pragma unroll
@@ -194,12 +194,8 @@ struct FwdWave {
   }
 };
 
-// BITMASK: the arbitrary-mask and dropout instantiation (with BOUNDS); its bit
-// tests stay out of the others, whose D = 128 copies have no registers to
-// spare. BIAS (with BITMASK): the one that also adds an attention bias, whose
-// 16 prefetched values per step would otherwise cost the mask and dropout
-// paths their registers too.
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
+// FEAT: the optional per-score inputs compiled in (Feat, with BOUNDS).
+template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const half_t* __restrict__ K,
                                          const half_t* __restrict__ V, half_t* __restrict__ O,
                                          float* __restrict__ Lse, int N, int Nk, int W,
@@ -212,6 +208,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml) {
   using L = FwdLds<D>;
+  constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
   __builtin_assume(wave >= 0 && wave < kWaves);
@@ -273,15 +270,20 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int k_hi = row_hi(i_base);  // smallest key bound of this wave's rows
   if (BOUNDS) n_full = min(n_full, k_hi - 32 - kq * 32 >= 0 ? (k_hi - 32 - kq * 32) / kKV + 1 : 0);
   const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
-  // Arbitrary mask (BITMASK instantiation): this row's bit words; every step
+  // Arbitrary mask (MASKB instantiations): this row's bit words; every step
   // then takes the mask. Word w covers keys 32w .. 32w+31, and a wave's 32
   // keys of step j are word (kKV / 32) j + kq (clamped: keys past N are
   // masked anyway).
-  // Dropout keep bits (BITMASK instantiation; zbase null: keep all) in the
+  // Dropout keep bits (DROPB instantiations; zbase null: keep all) in the
   // same layout, one plane per (b, query head).
-  const uint32_t* mrow = BITMASK && mbase ? mbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
-  const uint32_t* zrow = BITMASK && zbase ? zbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
-  if (BITMASK) n_full = 0;
+  const uint32_t* mrow = MASKB && mbase ? mbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
+  const uint32_t* zrow = DROPB && zbase ? zbase + (size_t)min(i_row, N - 1) * W32 : nullptr;
+  // With a mask every step runs in the masked loops below, and a step takes
+  // the mask only at the bounds above or when some row of the wave's block
+  // hides a key (bits past N are zero, so a ragged last word never passes);
+  // dropout bits apply in either loop. The bias copy masks every step (one
+  // step form: measured 5% faster there).
+  if (BIAS) n_full = 0;
   auto mword = [&](int j) { return mrow ? mrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
   auto zword = [&](int j) { return zrow ? zrow[min(j * (kKV / 32) + kq, W32 - 1)] : ~0u; };
   // Attention bias (BIAS instantiation; bbase null: none): this row's values
@@ -345,7 +347,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
     const uint32_t mw_now = mw, zw_now = zw;
-    if (BITMASK && NEXT) {
+    if ((MASKB || DROPB) && NEXT) {
       mw = mword(j + 1);
       zw = zword(j + 1);
     }
@@ -365,7 +367,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     };
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
-    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32, j < n_head || j >= n_full, i_row,
+    const bool hidden = MASKB && mrow && __builtin_amdgcn_ballot_w64(mw_now != ~0u) != 0;
+    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32,
+                                j < n_head || j >= n_full || hidden, i_row,
                                 lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv, [&] { return bload(j + 1); },
                                 BIAS ? bias_raw : 0.f, lane,
                                 roff, troff, c, thr_raw, issue);
@@ -378,7 +382,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   using P1 = std::integral_constant<int, 1>;
   using T = std::true_type;
   using F = std::false_type;
-  const int n_plain = min(n_full, n_it - 1);  // unmasked steps with a next step
+  const int n_plain = MASKB ? 0 : min(n_full, n_it - 1);  // unmasked steps with a next step
   // Buffer parity counts from j_lo. Every wave runs steps j_lo .. n_it-1, one
   // barrier each; only which of them are masked differs between waves.
   int j = j_lo;
@@ -469,7 +473,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   __syncthreads();  // the LDS is reused by the next tile
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
@@ -502,29 +506,30 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const float alibi_raw = alibi ? alibi[hq] * kLog2e / scale_log2 : 0.f;
   // This (b, head)'s mask plane (a plane shared by all heads when mask_heads == 1).
   const int W32 = (N + 31) >> 5;
-  const uint32_t* mbase = BITMASK && mask ? mask + ((size_t)b * mask_heads +
+  constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
+  const uint32_t* mbase = MASKB && mask ? mask + ((size_t)b * mask_heads +
                                                    (mask_heads == 1 ? 0 : hq)) * N * W32
                                            : nullptr;
   // ... and its dropout keep bits (one plane per (b, query head)).
-  const uint32_t* zbase = BITMASK && drop ? drop + (size_t)bh * N * W32 : nullptr;
+  const uint32_t* zbase = DROPB && drop ? drop + (size_t)bh * N * W32 : nullptr;
   // ... and its attention bias plane (element (i, j) at i * N + j).
   const float* bbase = BIAS && bias ? bias + b * bias_sb + hq * bias_sh : nullptr;
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
   for (int t = 0; t < n_tiles; ++t)
-    fwd_tile<D, CAUSAL, BOUNDS, BITMASK, BIAS, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
+    fwd_tile<D, CAUSAL, BOUNDS, FEAT, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
                                 Lse + (size_t)bh * N, N, Nk, window,
                                 seg_start ? seg_start + (size_t)b * N : nullptr,
                                 seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, mbase,
-                                zbase, BITMASK ? drop_scale : 1.f, bbase, bias_raw, W32, stq.n,
+                                zbase, DROPB ? drop_scale : 1.f, bbase, bias_raw, W32, stq.n,
                                 stk.n, dr,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml);
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BITMASK, bool BIAS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 hipError_t launch_fwd_t(const FwdArgs& a) {
   const int n_qtiles = (a.N + kBR - 1) / kBR;
   const int gx = CAUSAL ? (n_qtiles + 1) / 2 : n_qtiles;
@@ -533,7 +538,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D));
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, BITMASK, BIAS, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid, dim3(kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
@@ -547,21 +552,27 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
 template <int D, bool BF>
 hipError_t launch_fwd_d(const FwdArgs& a) {
   // Key lengths, windows, packed sequences and ALiBi need the masked
-  // instantiation (kKV is a multiple of kBR), masks and dropout the bit one,
-  // a bias (with or without them) the bias one.
+  // instantiation (kKV is a multiple of kBR); a mask, dropout or a bias one
+  // of its copies with those inputs compiled in (Feat).
   const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr;
-  if (a.bias)
-    return a.causal ? launch_fwd_t<D, true, true, true, true, BF>(a)
-                    : launch_fwd_t<D, false, true, true, true, BF>(a);
-  if (a.mask || a.drop)
-    return a.causal ? launch_fwd_t<D, true, true, true, false, BF>(a)
-                    : launch_fwd_t<D, false, true, true, false, BF>(a);
+  auto with = [&](auto feat) {
+    constexpr int F = decltype(feat)::value;
+    return a.causal ? launch_fwd_t<D, true, true, F, BF>(a)
+                    : launch_fwd_t<D, false, true, F, BF>(a);
+  };
+  switch (feat_of(a.mask != nullptr, a.drop != nullptr, a.bias != nullptr)) {
+    case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
+    case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
+    case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});
+    case kFeatBias: return with(std::integral_constant<int, kFeatBias>{});
+    default: break;
+  }
   if (a.causal)
-    return bounds ? launch_fwd_t<D, true, true, false, false, BF>(a)
-                  : launch_fwd_t<D, true, false, false, false, BF>(a);
-  return bounds ? launch_fwd_t<D, false, true, false, false, BF>(a)
-                : launch_fwd_t<D, false, false, false, false, BF>(a);
+    return bounds ? launch_fwd_t<D, true, true, 0, BF>(a)
+                  : launch_fwd_t<D, true, false, 0, BF>(a);
+  return bounds ? launch_fwd_t<D, false, true, 0, BF>(a)
+                : launch_fwd_t<D, false, false, 0, BF>(a);
 }
 
 }  // namespace
