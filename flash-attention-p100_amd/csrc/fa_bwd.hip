@@ -204,10 +204,15 @@ __device__ __forceinline__ void slot_add(rsrc_t r, floatx16 (&acc)[n], int w4, i
 
 // ------------------------------- phase 1 -----------------------------------
 // acc[0 .. D/32) = dV^T blocks, acc[D/32 .. 2D/32) = dK^T blocks.
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+// KREG: K's operands stay in registers (kb); otherwise each step reads them
+// from the resident K tile, as V's. The copies with a mask, dropout or a bias
+// read K from LDS: with it in registers they spill half of kb at D = 128,
+// and each reload's wait (loads complete in issue order) also waits for the
+// next stage's loads.
+template <int D, bool CAUSAL, bool BOUNDS, bool BF, bool KREG = true>
 struct KVWave {
   floatx16 acc[2 * (D / 32)];
-  half8 kb[D / 16];  // this wave's 32 key rows of K as B operands (loop-invariant)
+  half8 kb[KREG ? D / 16 : 1];  // this wave's 32 key rows of K as B operands (loop-invariant)
 
   // Query rows i0 + 32m .. +31 (m = this wave's half of the staged tile)
   // against key rows kr0 .. kr0+31 (K from kb, V from the resident tile Vt).
@@ -217,7 +222,7 @@ struct KVWave {
   // soon as they are added, so one set of registers carries the prefetch.
   template <class BiasNext>
   __device__ __forceinline__ void step(const half_t* Qs, const half_t* Os, const float* lse2s,
-                                       const float* dvs, const half_t* Vt,
+                                       const float* dvs, const half_t* Vt, const half_t* Kt,
                                        int m, int kr0, int i0, int j_col, int row_lo, int row_end,
                                        float alibi_raw, uint32_t mtw, uint32_t ztw, float zs,
                                        floatx16& bv, const BiasNext& bnext, float bias_raw,
@@ -229,20 +234,23 @@ struct KVWave {
     // Operands read one k-step ahead of their products.
     half8 qa = S::read16(Qs, so, 0), oa = S::read16(Os, so, 0);
     half8 va = tile_read16<D>(Vt, kr0, 0, roff);
+    half8 ka = KREG ? kb[0] : tile_read16<D>(Kt, kr0, 0, roff);
 #pragma unroll
     for (int kk = 0; kk < D / 16; ++kk) {
-      half8 qn = qa, on = oa, vn = va;
+      half8 qn = qa, on = oa, vn = va, kn = ka;
       if (kk + 1 < D / 16) {
         qn = S::read16(Qs, so, kk + 1);
         on = S::read16(Os, so, kk + 1);
         vn = tile_read16<D>(Vt, kr0, kk + 1, roff);
+        if constexpr (!KREG) kn = tile_read16<D>(Kt, kr0, kk + 1, roff);
       }
       __builtin_amdgcn_sched_barrier(0);
-      sacc = mfma16<BF>(qa, kb[kk], sacc);
+      sacc = mfma16<BF>(qa, KREG ? kb[kk] : ka, sacc);
       pacc = mfma16<BF>(oa, va, pacc);
       qa = qn;
       oa = on;
       va = vn;
+      ka = kn;
     }
     // P and dS. A lane holds key column j_col and the 16 query rows
     // i = i0 + 32m + 8*g4 + 4h + e; rows from row_end on are masked: past N,
@@ -542,7 +550,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int it_begin = helping ? n_it - x_help : 0;
     const int it_end = helping ? n_it : n_it - x_own;
     const bool shared = helping || x_own > 0;
-    KVWave<D, CAUSAL, BOUNDS, BF> w;
+    KVWave<D, CAUSAL, BOUNDS, BF, FEAT == 0> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
       plan_kv.init(wave, lane, stk.n, dr);
@@ -599,7 +607,6 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     // into the other stage.
     auto step = [&](int it, auto par) {
       constexpr int P = decltype(par)::value;
-      fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
       const half_t* Qs = P ? ta1 : ta0;
       const half_t* Os = P ? tb1 : tb0;
       const float* lse2s = P ? vec1 : vec0;
@@ -616,7 +623,11 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
           MASKB && mask_t ? plane(mask_t, hkv * group + it / n_qt)[tword] : ~0u;
       const uint32_t ztw =
           DROPB && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, half, w4 * 32, i0, j_col, row_lo, row_end,
+      // The next stage's loads go out after the step's mask and dropout words:
+      // loads complete in issue order, so words loaded after them would hold
+      // the softmax until the whole next stage had landed.
+      fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, kres, half, w4 * 32, i0, j_col, row_lo, row_end,
              alibi_raw, mtw, ztw, zs, bv1, [&] { return bload1(min(it + 1, it_end - 1)); },
              braw, lane, roff, so, scale_log2);
       wait_vmem();
@@ -626,8 +637,10 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     fetch(it_begin, ta0, tb0, vec0);
     wait_vmem();
     __syncthreads();
+    if constexpr (FEAT == 0) {
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) w.kb[kk] = tile_read16<D>(kres, w4 * 32, kk, roff);
+      for (int kk = 0; kk < D / 16; ++kk) w.kb[kk] = tile_read16<D>(kres, w4 * 32, kk, roff);
+    }
     int it = it_begin;
     for (; it + 2 <= it_end; it += 2) {
       step(it, P0{});
