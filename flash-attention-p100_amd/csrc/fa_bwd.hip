@@ -271,6 +271,9 @@ struct KVWave {
       bv = bnext();
     }
     half8 pb[2], sb[2];
+    // This lane's rows are bits idx + 4h of the mask and dropout words:
+    // shifted once, every per-score bit position is a constant.
+    const uint32_t mth = mtw >> (4 * h), zth = ztw >> (4 * h);
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const floatx4 l4 = *reinterpret_cast<const floatx4*>(lse2s + 32 * m + 8 * g4 + 4 * h);
@@ -280,10 +283,10 @@ struct KVWave {
         const int r = 4 * g4 + e, idx = 8 * g4 + e;
         float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
         if (CAUSAL || BOUNDS) p = (idx >= lo) ? p : 0.f;
-        if (BOUNDS) p = (idx < hi && ((mtw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
+        if (BOUNDS) p = (idx < hi && ((mth >> idx) & 1u)) ? p : 0.f;
         // Dropout (keep bits ztw, scale zs): dV sees the kept P, and the
         // gradient of P is the kept dP scaled.
-        const bool keep = (ztw >> (idx + 4 * h)) & 1u;
+        const bool keep = (zth >> idx) & 1u;
         pb[r >> 3][r & 7] = to16<BF>(keep ? p : 0.f);
         sb[r >> 3][r & 7] = to16<BF>(p * ((keep ? pacc[r] * zs : 0.f) - d4[e]));
       }
@@ -356,14 +359,15 @@ struct QWave {
     }
     half8 sb[2];
     floatx4 ds4;  // the current run of four keys' dS (16-byte dbias stores)
+    const uint32_t mwh = mw >> (4 * h), zwh = zw >> (4 * h);  // as in KVWave::step
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int idx = 8 * (r >> 2) + (r & 3);
       float p = fast_exp2(fmaf(st[r], c, -lse2));
       if (CAUSAL) p = (idx <= lo) ? p : 0.f;
-      if (BOUNDS) p = (idx < hi && idx >= lw && ((mw >> (idx + 4 * h)) & 1u)) ? p : 0.f;
+      if (BOUNDS) p = (idx < hi && idx >= lw && ((mwh >> idx) & 1u)) ? p : 0.f;
       // Dropout: the gradient of P is the kept dP scaled by zs.
-      const bool keep = (zw >> (idx + 4 * h)) & 1u;
+      const bool keep = (zwh >> idx) & 1u;
       const float ds = p * ((keep ? pt[r] * zs : 0.f) - dvv);
       sb[r >> 3][r & 7] = to16<BF>(ds);
       // The bias's gradient is dS itself; keys from the key length on are not

@@ -109,6 +109,10 @@ struct FwdWave {
                                        const BiasNext& bnext, float bias_raw, int lane, int roff,
                                        int troff, float c, float thr_raw, const Issue& issue) {
     const int h = lane >> 5;
+    // This lane's keys are bits 8g + 4h + e of the step's mask and dropout
+    // words: shifted once, every per-score bit position is a constant (with
+    // 4h inside it the compiler kept 16 per-lane bit masks in registers).
+    const uint32_t mwh = mw >> (4 * h), zwh = zw >> (4 * h);
     floatx16 s = sc;
     floatx16 sn = zero16();
     constexpr int kS = D / 16;  // products of the next S^T
@@ -137,11 +141,11 @@ struct FwdWave {
     if (MASK && masked) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int jj = 8 * (r >> 2) + 4 * h + (r & 3);
-        const int j = j0 + jj;
+        const int bit = 8 * (r >> 2) + (r & 3);
+        const int j = j0 + bit + 4 * h;
         // w_lo: the last key left of this row's sliding window (INT_MIN if none);
         // mw: this row's mask bits for keys j0 .. j0+31 (all set without a mask)
-        if ((CAUSAL && j > i_row) || (BOUNDS && (j >= N || j <= w_lo || !((mw >> jj) & 1u))))
+        if ((CAUSAL && j > i_row) || (BOUNDS && (j >= N || j <= w_lo || !((mwh >> bit) & 1u))))
           s[r] = -INFINITY;
       }
     }
@@ -177,8 +181,8 @@ struct FwdWave {
           const float p = fast_exp2(fmaf(s[r], c, neg));
           l += p;
           // Dropout: the row sum keeps every key, P V only the kept ones.
-          const int jj = 8 * (r >> 2) + 4 * h + (r & 3);
-          pb[r >> 3][r & 7] = to16<BF>(((zw >> jj) & 1u) ? p : 0.f);
+          const int bit = 8 * (r >> 2) + (r & 3);
+          pb[r >> 3][r & 7] = to16<BF>(((zwh >> bit) & 1u) ? p : 0.f);
         }
       }
     }
