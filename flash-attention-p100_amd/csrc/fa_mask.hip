@@ -89,23 +89,28 @@ __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
 // Dropout keep bits. Draws: row key r = h(h(h(h(seed_lo) ^ seed_hi) ^ plane)
 // ^ row); keys 2k and 2k+1 of the row draw the low and high 16 bits of
 // h(r ^ k) (h = lowbias32); a key is kept iff its draw >= thr. Each wave
-// owns 64 consecutive rows of one plane and walks their words: lane l packs
-// row i0 + l's word, then 32 ballots transpose the 64 x 32 block (lane j
-// collects key j's bits of the wave's 64 rows, two transposed words).
-// Rows and keys past N get zero bits.
+// owns 64 consecutive rows of one plane and kDropWords of their words (a
+// wave per 64 rows alone left half the SIMDs idle at B*H = 8, N = 4096, and
+// the hash chains exposed: 140 us): lane l packs row i0 + l's word, then 32
+// ballots transpose the 64 x 32 block (lane j collects key j's bits of the
+// wave's 64 rows, two transposed words). Rows and keys past N get zero bits.
+constexpr int kDropWords = 8;
 __global__ __launch_bounds__(kPackThreads) void dropout_bits_kernel(
     uint32_t seed_lo, uint32_t seed_hi, uint32_t thr, int N, int W, int row_blocks,
-    uint32_t* __restrict__ bits, uint32_t* __restrict__ bits_t) {
+    int word_chunks, uint32_t* __restrict__ bits, uint32_t* __restrict__ bits_t) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int plane = blockIdx.x / row_blocks;
-  const int i0 = ((blockIdx.x % row_blocks) * (kPackThreads / 64) + wave) * 64;
+  const int chunk = blockIdx.x % word_chunks;
+  const int rest = blockIdx.x / word_chunks;
+  const int plane = rest / row_blocks;
+  const int i0 = ((rest % row_blocks) * (kPackThreads / 64) + wave) * 64;
   if (i0 >= N) return;  // wave-uniform; no barriers below
   const int i = i0 + lane;
   const bool row_ok = i < N;
   const uint32_t key =
       lowbias32(lowbias32(lowbias32(lowbias32(seed_lo) ^ seed_hi) ^ (uint32_t)plane) ^ (uint32_t)i);
   uint32_t* row_out = bits + ((size_t)plane * N + (row_ok ? i : 0)) * W;
-  for (int w = 0; w < W; ++w) {
+  const int w_end = min(W, (chunk + 1) * kDropWords);
+  for (int w = chunk * kDropWords; w < w_end; ++w) {
     uint32_t word = 0;
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -160,9 +165,12 @@ hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, 
                                uint32_t* bits_t, void* stream) {
   const int W = (N + 31) / 32;
   const int row_blocks = (N + kPackThreads - 1) / kPackThreads;
-  hipLaunchKernelGGL(dropout_bits_kernel, dim3((unsigned)((long long)P * row_blocks)),
-                     dim3(kPackThreads), 0, (hipStream_t)stream, (uint32_t)seed,
-                     (uint32_t)(seed >> 32), threshold, N, W, row_blocks, bits, bits_t);
+  const int word_chunks = (W + kDropWords - 1) / kDropWords;
+  const long long blocks = (long long)P * row_blocks * word_chunks;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dropout_bits_kernel, dim3((unsigned)blocks), dim3(kPackThreads), 0,
+                     (hipStream_t)stream, (uint32_t)seed, (uint32_t)(seed >> 32), threshold, N,
+                     W, row_blocks, word_chunks, bits, bits_t);
   return hipGetLastError();
 }
 
