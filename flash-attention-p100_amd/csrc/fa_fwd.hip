@@ -79,20 +79,32 @@ __device__ __forceinline__ float max_halves(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+// QLDS: Q's operands are read from a staged LDS tile (qt, rows qrow ..) at
+// each product instead of being held in registers (qb); the bias copy does
+// this, as its 16 prefetched bias values per lane left no registers for Q.
+template <int D, bool CAUSAL, bool BOUNDS, bool BF, bool QLDS = false>
 struct FwdWave {
   // Per-wave state for one 32-row query block.
-  half8 qb[D / 16];
+  half8 qb[QLDS ? 1 : D / 16];
+  const half_t* qt;
+  int qrow;
   floatx16 oacc[D / 32];
   floatx16 sc;  // raw logits S^T of the current step (this wave's 32 keys x 32 rows)
   float m_raw;  // running max of the raw (unscaled) logits; -inf before any key
   float l;      // this lane's partial row sum of p (its 16 of every 32 keys)
 
+  // Q's operand of k-step kk: this wave's rows, columns 16kk .. 16kk+15.
+  __device__ __forceinline__ half8 qop(int kk, int roff) const {
+    if constexpr (QLDS) return tile_read16<D>(qt, qrow, kk, roff);
+    else return qb[kk];
+  }
+
   // S^T = K Q^T for this wave's 32 keys of a staged K tile.
   __device__ __forceinline__ void s_product(const half_t* Ks, int kq, int roff) {
     sc = zero16();
 #pragma unroll
-    for (int kk = 0; kk < D / 16; ++kk) sc = mfma16<BF>(tile_read16<D>(Ks, kq * 32, kk, roff), qb[kk], sc);
+    for (int kk = 0; kk < D / 16; ++kk)
+      sc = mfma16<BF>(tile_read16<D>(Ks, kq * 32, kk, roff), qop(kk, roff), sc);
   }
 
   // One software-pipelined step: softmax of sc (the keys j0 .. j0+31 of this
@@ -120,7 +132,7 @@ struct FwdWave {
 #pragma unroll
     for (int kk = 0; kk < kFront; ++kk)
       if constexpr (NEXT) {
-        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
+        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qop(kk, roff), sn);
         issue(kk);
       }
     // ALiBi (masked instantiation only): -slope |i - j| in raw-score units,
@@ -169,7 +181,7 @@ struct FwdWave {
 #pragma unroll
     for (int kk = kFront; kk < kS; ++kk) {
       if constexpr (NEXT) {
-        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qb[kk], sn);
+        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qop(kk, roff), sn);
         issue(kk);
       }
       // 16 exponentials spread over the remaining products.
@@ -210,7 +222,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          int W32, int sq, int sk, int dr,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
-                                         half_t* kt1, half_t* vt1, float2* ml) {
+                                         half_t* kt1, half_t* vt1, float2* ml, half_t* qt) {
   using L = FwdLds<D>;
   constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -222,13 +234,18 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int i_base = q0 + rb * 32;
   const int i_row = i_base + l32;
 
-  FwdWave<D, CAUSAL, BOUNDS, BF> w;
+  FwdWave<D, CAUSAL, BOUNDS, BF, BIAS> w;
   const int roff = row_lane_off<D>(lane), troff = tr_lane_off<D>(lane);
   const bool row_ok = !BOUNDS || i_row < N;
+  if constexpr (!BIAS) {
 #pragma unroll
-  for (int kk = 0; kk < D / 16; ++kk)
-    w.qb[kk] = as_half8(load16(Q + (size_t)i_row * sq + kk * 16 + h * 8,
-                               row_ok && kk * 16 + h * 8 < dr));
+    for (int kk = 0; kk < D / 16; ++kk)
+      w.qb[kk] = as_half8(load16(Q + (size_t)i_row * sq + kk * 16 + h * 8,
+                                 row_ok && kk * 16 + h * 8 < dr));
+  } else {
+    w.qt = qt;
+    w.qrow = rb * 32;
+  }
 #pragma unroll
   for (int cb = 0; cb < D / 32; ++cb) w.oacc[cb] = zero16();
   w.m_raw = -INFINITY;
@@ -334,6 +351,13 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     plan.part(kt0, rk, j_lo * kKV, wave, u);
     plan.part(vt0, rv, j_lo * kKV, wave, u);
     plan.part(kt1, rk, k1, wave, u);
+  }
+  if constexpr (BIAS) {  // the tile's 64 query rows (rows past N read zeros)
+    TilePlan<D, kBR, kWaves, false> plan_q;
+    plan_q.init(wave, lane, sq, dr);
+    const rsrc_t rq = rows_rsrc(Q, N, sq, dr);
+#pragma unroll
+    for (int u = 0; u < decltype(plan_q)::kParts; ++u) plan_q.part(qt, rq, q0, wave, u);
   }
   wait_vmem();
   __syncthreads();
@@ -494,6 +518,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   __shared__ __align__(16) half_t kt1[FwdLds<D>::kTileHalves];
   __shared__ __align__(16) half_t vt1[FwdLds<D>::kTileHalves];
   __shared__ float2 ml[FwdLds<D>::kMLFloat2];
+  // The bias copy's staged Q tile (64 rows; a placeholder elsewhere).
+  __shared__ __align__(16) half_t qt[Feat<FEAT>::kBias ? Tile<D>::template halves<kBR>() : 8];
   const int w = xcd_work_index(gx * BH);
   if (w < 0) return;
   const int bh = w / gx;       // over B*Hq
@@ -530,7 +556,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
                                 stk.n, dr,
                                 t ? second : first,
                                 scale_log2, thr_raw,
-                                kt0, vt0, kt1, vt1, ml);
+                                kt0, vt0, kt1, vt1, ml, qt);
 }
 
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>

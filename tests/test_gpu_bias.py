@@ -8,8 +8,8 @@ test_oracle.py against SDPA with the same float attn_mask and autograd,
 the bias's own gradient included, and finite differences): per-head,
 batch-shared, head-shared and (N, N) biases with their gradients reduced
 to the bias's shape; a bias beside a mask, dropout, key lengths, ALiBi and
-a window; bf16; the (B, N, H, D) views and the C ABI bit-identical to the
-op; and Qwen3 through the hook with an additive 4-D mask carrying a bias
+a window; head dims 8, 40 and 96; bf16; the (B, N, H, D) views and the C
+ABI bit-identical to the op; and Qwen3 through the hook with an additive 4-D mask carrying a bias
 against eager and sdpa. Bars: the fp16 ones (helpers.py) for o, LSE and
 every gradient, dbias included."""
 import ctypes
@@ -93,6 +93,19 @@ def test_bias_matches_oracle(B, Hq, Hkv, N, shape, D, causal):
     got = run(q, k, v, do, bias, causal)
     check(got, lse_of(q, k, v, causal, as4(bias, B, Hq)), q, k, v, do, bias, causal,
           f"bias {shape} {B},{Hq}/{Hkv},N{N} D{D} causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("D", [8, 40, 96])
+def test_bias_other_head_dims(D, causal):
+    """Head dims on the widths 32, 64 and 96 (columns past the head dim
+    are padding in the staged Q, K and V tiles), GQA, a ragged N."""
+    B, Hq, Hkv, N = 2, 4, 2, 301
+    q, k, v, do = make_inputs(B, Hq, Hkv, N, D, seed=D + causal)
+    bias = torch.randn(B, 1, N, N, generator=torch.Generator().manual_seed(D)) * 1.5
+    got = run(q, k, v, do, bias, causal)
+    check(got, lse_of(q, k, v, causal, bias), q, k, v, do, bias, causal,
+          f"bias D{D} causal={causal}")
 
 
 @pytest.mark.parametrize("causal", [True, False])
