@@ -5,8 +5,10 @@
 // backward's dK/dV phase, whose lanes own keys). No counterpart in the
 // reference, which takes no mask and raises on dropout (fa_p100_hf.py:64-70, 83-85).
 //
-// The packers are HBM-bound byte work: N*N bytes in, N*N/8 bytes out per
-// plane; grid-stride loops over 64-bit word indices keep their grid small.
+// The row packer is HBM-bound byte work: N*N bytes in, N*N/8 bytes out per
+// plane (a grid-stride loop over 64-bit word indices keeps its grid small);
+// the transposed words are then built from the packed rows (N*N/8 bytes
+// each way) by the wave-ballot transpose the dropout generator uses.
 // The dropout generator writes N*N/8 bytes per layout and plane and spends
 // one hash (two 32-bit multiplies) per two keys.
 #include <hip/hip_runtime.h>
@@ -52,27 +54,45 @@ __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(const uint8_t* 
   }
 }
 
-// One 32-query word of one key per thread. Consecutive threads take
-// consecutive keys of the same 32 query rows, so each of the 32 byte loads is
-// contiguous across the wave; the word stores are W words apart.
-__global__ __launch_bounds__(kPackThreads) void pack_cols_kernel(const uint8_t* __restrict__ dense,
-                                                                 uint32_t* __restrict__ bits_t,
-                                                                 long long planes, int N, int W) {
-  const long long total = planes * W * N;
-  const long long stride = (long long)gridDim.x * blockDim.x;
-  for (long long g = (long long)blockIdx.x * blockDim.x + threadIdx.x; g < total; g += stride) {
-    // g = (p * W + w) * N + j: key j fastest.
-    const long long pw = g / N;
-    const int j = (int)(g - pw * N);
-    const long long p = pw / W;
-    const int w = (int)(pw - p * W);
-    const int i0 = 32 * w;
-    const int n = min(32, N - i0);  // query rows of this word that exist
-    const uint8_t* src = dense + (p * N + i0) * (long long)N + j;
-    uint32_t word = 0;
-    for (int e = 0; e < n; ++e) word |= (uint32_t)(src[(long long)e * N] != 0) << e;
-    bits_t[(p * N + j) * W + w] = word;
+// Transpose of one 64-row x 32-key block of bit words: lane l holds row
+// i0 + l's word w (bits = keys 32w ..); 32 ballots give lane j < 32 key
+// 32w + j's bits of rows i0 .. i0+31 and lane 32 + j those of rows i0+32 ..
+// i0+63, which it stores as that key's transposed word (rows i0/32 and
+// i0/32 + 1). Keys past N and words past W are not stored.
+__device__ __forceinline__ void store_transposed(uint32_t word, int lane, int w, int i0, int N,
+                                                 int W, uint32_t* __restrict__ plane_t) {
+  uint32_t mine = 0u;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) {
+    const unsigned long long b = __ballot((word >> j) & 1u);
+    if ((lane & 31) == j) mine = lane < 32 ? (uint32_t)b : (uint32_t)(b >> 32);
   }
+  const int kj = 32 * w + (lane & 31);  // this lane's key
+  const int rw = (i0 >> 5) + (lane >> 5);  // its word of query rows
+  if (kj < N && rw < W) plane_t[(size_t)kj * W + rw] = mine;
+}
+
+// Words per wave of the ballot-transpose kernels (a wave per 64 rows alone
+// left half the SIMDs idle at B*H = 8, N = 4096).
+constexpr int kDropWords = 8;
+
+// The transposed words of packed rows: each wave owns 64 rows of one plane
+// and kDropWords of their words (rows past N read as zero words).
+__global__ __launch_bounds__(kPackThreads) void pack_cols_kernel(
+    const uint32_t* __restrict__ bits, uint32_t* __restrict__ bits_t, int N, int W,
+    int row_blocks, int word_chunks) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunk = blockIdx.x % word_chunks;
+  const int rest = blockIdx.x / word_chunks;
+  const int plane = rest / row_blocks;
+  const int i0 = ((rest % row_blocks) * (kPackThreads / 64) + wave) * 64;
+  if (i0 >= N) return;  // wave-uniform; no barriers below
+  const int i = i0 + lane;
+  const uint32_t* row = bits + ((size_t)plane * N + (i < N ? i : 0)) * W;
+  uint32_t* plane_t = bits_t + (size_t)plane * N * W;
+  const int w_end = min(W, (chunk + 1) * kDropWords);
+  for (int w = chunk * kDropWords; w < w_end; ++w)
+    store_transposed(i < N ? row[w] : 0u, lane, w, i0, N, W, plane_t);
 }
 
 // Integer hash `lowbias32` (C. Wellons, hash-prospector): xorshift-multiply
@@ -89,12 +109,10 @@ __device__ __forceinline__ uint32_t lowbias32(uint32_t x) {
 // Dropout keep bits. Draws: row key r = h(h(h(h(seed_lo) ^ seed_hi) ^ plane)
 // ^ row); keys 2k and 2k+1 of the row draw the low and high 16 bits of
 // h(r ^ k) (h = lowbias32); a key is kept iff its draw >= thr. Each wave
-// owns 64 consecutive rows of one plane and kDropWords of their words (a
-// wave per 64 rows alone left half the SIMDs idle at B*H = 8, N = 4096, and
-// the hash chains exposed: 140 us): lane l packs row i0 + l's word, then 32
-// ballots transpose the 64 x 32 block (lane j collects key j's bits of the
-// wave's 64 rows, two transposed words). Rows and keys past N get zero bits.
-constexpr int kDropWords = 8;
+// owns 64 consecutive rows of one plane and kDropWords of their words (one
+// wave per 64 rows also left the hash chains exposed: 140 us): lane l packs
+// row i0 + l's word, then store_transposed writes the block's transposed
+// words. Rows and keys past N get zero bits.
 __global__ __launch_bounds__(kPackThreads) void dropout_bits_kernel(
     uint32_t seed_lo, uint32_t seed_hi, uint32_t thr, int N, int W, int row_blocks,
     int word_chunks, uint32_t* __restrict__ bits, uint32_t* __restrict__ bits_t) {
@@ -122,17 +140,7 @@ __global__ __launch_bounds__(kPackThreads) void dropout_bits_kernel(
     if (nk < 32) word &= (1u << nk) - 1u;
     if (!row_ok) word = 0u;
     if (row_ok) row_out[w] = word;
-    if (bits_t) {
-      uint32_t mine = 0u;
-#pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        const unsigned long long b = __ballot((word >> j) & 1u);
-        if ((lane & 31) == j) mine = lane < 32 ? (uint32_t)b : (uint32_t)(b >> 32);
-      }
-      const int kj = 32 * w + (lane & 31);  // this lane's key
-      const int rw = (i0 >> 5) + (lane >> 5);  // its word of query rows
-      if (kj < N && rw < W) bits_t[((size_t)plane * N + kj) * W + rw] = mine;
-    }
+    if (bits_t) store_transposed(word, lane, w, i0, N, W, bits_t + (size_t)plane * N * W);
   }
 }
 
@@ -156,8 +164,12 @@ hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, 
                        (hipStream_t)stream, dense, bits, rows, N, W);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || bits_t == nullptr) return e;
-  hipLaunchKernelGGL(pack_cols_kernel, dim3(blocks_for(rows * W)), dim3(kPackThreads), 0,
-                     (hipStream_t)stream, dense, bits_t, (long long)P, N, W);
+  const int row_blocks = (N + kPackThreads - 1) / kPackThreads;
+  const int word_chunks = (W + kDropWords - 1) / kDropWords;
+  const long long blocks = (long long)P * row_blocks * word_chunks;
+  if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_cols_kernel, dim3((unsigned)blocks), dim3(kPackThreads), 0,
+                     (hipStream_t)stream, bits, bits_t, N, W, row_blocks, word_chunks);
   return hipGetLastError();
 }
 
