@@ -395,7 +395,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     };
     const half_t* Kn = P ? kt0 : kt1;  // K_{j+1}
     const half_t* Vs = P ? vt1 : vt0;  // V_j
-    const bool hidden = MASKB && mrow && __builtin_amdgcn_ballot_w64(mw_now != ~0u) != 0;
+    // (every lane takes the ballot: without a mask mw_now is all ones)
+    const bool hidden = MASKB && __builtin_amdgcn_ballot_w64(mw_now != ~0u) != 0;
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32,
                                 j < n_head || j >= n_full || hidden, i_row,
                                 lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv, [&] { return bload(j + 1); },
