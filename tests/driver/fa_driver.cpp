@@ -7,7 +7,11 @@
 //                           (oracle/attention_ref.c): the reference's 4 input
 //                           regimes x D x causal (attention.cu:120-160,
 //                           test_fa_p100.py:107-139), plus GQA, ragged N and
-//                           split-key-tile shapes. Exit status 1 on any miss.
+//                           split-key-tile shapes, and the general pair's
+//                           options (key lengths, window, ALiBi, scale,
+//                           packed sequences, mask, dropout, bias) against
+//                           the oracle's ora_fwd_ex / ora_bwd_ex. Exit
+//                           status 1 on any miss.
 //   fa_driver fd            central finite differences of the oracle's loss
 //                           against its analytic backward (bwd.cu:136-160,
 //                           h = 1e-4, bar 1e-4). CPU only.
@@ -216,6 +220,227 @@ bool check_case(const char* name, const Shape& s, double scale_qk, uint64_t seed
   return ok;
 }
 
+// The C ABI's options (fa_fwd_ex / fa_bwd_ex) against the C oracle's
+// ora_fwd_ex / ora_bwd_ex on the same options: key lengths, a window, ALiBi,
+// a scale, packed sequences, a mask (packed on the GPU by fa_pack_mask from
+// the dense bytes the oracle reads), dropout (bits drawn on the GPU by
+// fa_dropout_bits, first checked bit for bit in both layouts against the C
+// draw ora_dropout_keep) and a bias with its gradient. The backward's
+// reference takes the GPU's saved o and lse, as the kernels do.
+enum OptBits { kOptKvLen = 1, kOptWindow = 2, kOptAlibi = 4, kOptScale = 8, kOptSegs = 16,
+               kOptMask1 = 32, kOptMaskH = 64, kOptDrop = 128, kOptBias = 256 };
+
+template <class T>
+T* dcopy(const std::vector<T>& h) {
+  T* p = dalloc<T>(h.size());
+  HIP_OK(hipMemcpy(p, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice));
+  return p;
+}
+template <class T>
+std::vector<T> hcopy(const T* p, size_t n) {
+  std::vector<T> h(n);
+  HIP_OK(hipMemcpy(h.data(), p, n * sizeof(T), hipMemcpyDeviceToHost));
+  return h;
+}
+
+// Bit j % 32 of words[(p * N + i) * W + j / 32] == keep[(p * N + i) * N + j]
+// (and the transposed words with i and j swapped) over P planes.
+bool bits_match(const std::vector<uint32_t>& words, const std::vector<uint32_t>& words_t,
+                const std::vector<unsigned char>& keep, int P, int N) {
+  const int W = (N + 31) / 32;
+  for (int pl = 0; pl < P; ++pl)
+    for (int i = 0; i < N; ++i)
+      for (int j = 0; j < N; ++j) {
+        const bool k = keep[((size_t)pl * N + i) * N + j] != 0;
+        const bool a = (words[((size_t)pl * N + i) * W + j / 32] >> (j % 32)) & 1u;
+        const bool b = (words_t[((size_t)pl * N + j) * W + i / 32] >> (i % 32)) & 1u;
+        if (a != k || b != k) return false;
+      }
+  return true;
+}
+
+bool check_options_case(const char* name, const Shape& s, int opts, uint64_t seed) {
+  Rng r{seed};
+  Host16 q, k, v, g;
+  q.fill(s.nq(), r, 1.0);
+  k.fill(s.nk(), r, 1.0);
+  v.fill(s.nk(), r, 1.0);
+  g.fill(s.nq(), r, 1.0);
+  const int B = s.B, Hq = s.Hq, N = s.N, W = (N + 31) / 32;
+  const size_t plane_nn = (size_t)N * N;
+  fa_options fo{};
+  ora_opts oo{};
+  std::vector<void*> owned;  // device buffers of this case
+  std::vector<int> lens, s0, s1;
+  std::vector<float> slopes_f, bias_f;
+  std::vector<double> slopes_d, bias_d;
+  std::vector<unsigned char> mask, keep;
+  bool bits_ok = true;
+  if (opts & kOptKvLen) {
+    for (int b = 0; b < B; ++b) lens.push_back(1 + (int)(r.next() % (uint64_t)N));
+    int* d = dcopy(lens);
+    owned.push_back(d);
+    fo.kv_len = d;
+    oo.kv_len = lens.data();
+  }
+  if (opts & kOptWindow) fo.window = oo.window = 1 + (int)(r.next() % (uint64_t)N);
+  if (opts & kOptAlibi) {
+    for (int h = 0; h < Hq; ++h) slopes_f.push_back((float)(0.02 + 0.4 * r.uniform()));
+    for (float x : slopes_f) slopes_d.push_back(x);
+    float* d = dcopy(slopes_f);
+    owned.push_back(d);
+    fo.alibi_slopes = d;
+    oo.alibi = slopes_d.data();
+  }
+  if (opts & kOptScale) {
+    fo.scale = 0.17f;
+    oo.scale = (double)fo.scale;
+  }
+  if (opts & kOptSegs) {  // up to four sequences per entry, random lengths
+    s0.resize((size_t)B * N);
+    s1.resize((size_t)B * N);
+    for (int b = 0; b < B; ++b) {
+      int i = 0;
+      while (i < N) {
+        const int len = 1 + (int)(r.next() % (uint64_t)(N / 4 + 1));
+        const int e = std::min(N, i + len);
+        for (int t = i; t < e; ++t) {
+          s0[(size_t)b * N + t] = i;
+          s1[(size_t)b * N + t] = e;
+        }
+        i = e;
+      }
+    }
+    int *d0 = dcopy(s0), *d1 = dcopy(s1);
+    owned.push_back(d0);
+    owned.push_back(d1);
+    fo.seg_start = d0;
+    fo.seg_end = d1;
+    oo.seg_start = s0.data();
+    oo.seg_end = s1.data();
+  }
+  if (opts & (kOptMask1 | kOptMaskH)) {
+    const int mh = (opts & kOptMaskH) ? Hq : 1;
+    mask.resize((size_t)B * mh * plane_nn);
+    for (auto& x : mask) x = r.uniform() < 0.8;
+    for (int j = 0; j < N; ++j) mask[(size_t)2 * N + j] = 0;  // row 2 of plane 0 sees nothing
+    unsigned char* dm = dcopy(mask);
+    uint32_t *bits = dalloc<uint32_t>((size_t)B * mh * N * W),
+             *bits_t = dalloc<uint32_t>((size_t)B * mh * N * W);
+    owned.insert(owned.end(), {dm, bits, bits_t});
+    FA_OK_(fa_pack_mask(dm, B * mh, N, bits, bits_t, nullptr));
+    fo.mask = bits;
+    fo.mask_t = bits_t;
+    fo.mask_heads = mh;
+    oo.mask = mask.data();
+    oo.mask_heads = mh;
+  }
+  if (opts & kOptDrop) {
+    const float p = 0.2f;
+    const unsigned long long dseed = r.next();
+    const int P = B * Hq;
+    uint32_t *bits = dalloc<uint32_t>((size_t)P * N * W), *bits_t = dalloc<uint32_t>((size_t)P * N * W);
+    owned.push_back(bits);
+    owned.push_back(bits_t);
+    FA_OK_(fa_dropout_bits(dseed, p, P, N, bits, bits_t, nullptr));
+    keep.resize((size_t)P * plane_nn);
+    ora_dropout_keep(dseed, ora_dropout_threshold(p), P, N, keep.data());
+    bits_ok = bits_match(hcopy(bits, (size_t)P * N * W), hcopy(bits_t, (size_t)P * N * W), keep,
+                         P, N);
+    fo.drop = bits;
+    fo.drop_t = bits_t;
+    fo.drop_scale = fa_dropout_scale(p);
+    oo.keep = keep.data();
+    oo.drop_scale = 65536.0 / (65536.0 - ora_dropout_threshold(p));
+  }
+  float* dbias = nullptr;
+  if (opts & kOptBias) {
+    bias_f.resize((size_t)B * Hq * plane_nn);
+    for (auto& x : bias_f) x = (float)r.normal();
+    for (float x : bias_f) bias_d.push_back(x);
+    float* d = dcopy(bias_f);
+    dbias = dalloc<float>(bias_f.size());
+    HIP_OK(hipMemset(dbias, 0, bias_f.size() * sizeof(float)));
+    owned.push_back(d);
+    owned.push_back(dbias);
+    fo.bias = d;
+    fo.bias_stride_b = (long long)Hq * plane_nn;
+    fo.bias_stride_h = (long long)plane_nn;
+    fo.dbias = dbias;
+    oo.bias = bias_d.data();
+  }
+  // GPU forward + backward through the general pair.
+  _Float16 *dq_in = dcopy(q.h), *dk_in = dcopy(k.h), *dv_in = dcopy(v.h), *dgo = dcopy(g.h);
+  _Float16 *dout = dalloc<_Float16>(s.nq()), *ddq = dalloc<_Float16>(s.nq()),
+           *ddk = dalloc<_Float16>(s.nk()), *ddv = dalloc<_Float16>(s.nk());
+  float* dlse = dalloc<float>(s.nl());
+  const size_t ws_bytes = fa_bwd_workspace_bytes(B, Hq, s.Hkv, N, s.D);
+  char* ws = dalloc<char>(ws_bytes);
+  owned.insert(owned.end(), {dq_in, dk_in, dv_in, dgo, dout, ddq, ddk, ddv, dlse, ws});
+  FA_OK_(fa_fwd_ex(dq_in, dk_in, dv_in, dout, dlse, B, Hq, s.Hkv, N, s.D, s.causal, &fo,
+                   nullptr));
+  FA_OK_(fa_bwd_ex(dq_in, dk_in, dv_in, dgo, dout, dlse, ddq, ddk, ddv, ws, ws_bytes, B, Hq,
+                   s.Hkv, N, s.D, s.causal, &fo, nullptr));
+  HIP_OK(hipDeviceSynchronize());
+  auto to_d = [](const auto& src) {
+    std::vector<double> out(src.size());
+    for (size_t i = 0; i < src.size(); ++i) out[i] = (double)src[i];
+    return out;
+  };
+  const std::vector<double> go = to_d(hcopy(dout, s.nq())), glse = to_d(hcopy(dlse, s.nl())),
+                            gdq = to_d(hcopy(ddq, s.nq())), gdk = to_d(hcopy(ddk, s.nk())),
+                            gdv = to_d(hcopy(ddv, s.nk()));
+  std::vector<double> gdb;
+  if (dbias) gdb = to_d(hcopy(dbias, bias_f.size()));
+  for (void* p : owned) HIP_OK(hipFree(p));
+
+  // The oracle: forward, then the backward from the GPU's saved o and lse.
+  std::vector<double> o(s.nq()), lse(s.nl()), dq(s.nq()), dk(s.nk()), dv(s.nk()), db;
+  ora_fwd_ex(q.d.data(), k.d.data(), v.d.data(), o.data(), lse.data(), B, Hq, s.Hkv, N, s.D,
+             s.causal, &oo);
+  oo.o = go.data();
+  oo.lse = glse.data();
+  if (dbias) {
+    db.resize(bias_f.size());
+    oo.dbias = db.data();
+  }
+  ora_bwd_ex(q.d.data(), k.d.data(), v.d.data(), g.d.data(), dq.data(), dk.data(), dv.data(), B,
+             Hq, s.Hkv, N, s.D, s.causal, &oo);
+
+  const double zs = (opts & kOptDrop) ? oo.drop_scale : 1.0;
+  const double fo_abs = max_abs(go, o), fo_rel = rel_max_rms(go, o);
+  double fl = 0;
+  bool lse_ok = true;
+  for (size_t i = 0; i < lse.size(); ++i) {
+    if (std::isinf(lse[i])) {
+      lse_ok &= std::isinf(glse[i]);
+      continue;
+    }
+    fl = std::fmax(fl, std::fabs(glse[i] - lse[i]));
+  }
+  auto grad_ok = [](const std::vector<double>& got, const std::vector<double>& ref, double& l2) {
+    bool zero = true;
+    for (double x : ref) zero &= x == 0.0;
+    if (zero) {  // e.g. every row left with one key: dS cancels exactly in float64
+      l2 = max_abs(got, ref);
+      return l2 <= 1e-4;
+    }
+    l2 = rel_l2(got, ref);
+    return l2 <= kGradRelL2 && rel_max_rms(got, ref) < kRefRel;
+  };
+  double q2, k2, v2, b2 = 0;
+  const bool gq = grad_ok(gdq, dq, q2), gk = grad_ok(gdk, dk, k2), gv = grad_ok(gdv, dv, v2);
+  const bool gb = !dbias || grad_ok(gdb, db, b2);
+  const bool ok = bits_ok && fo_abs <= kFwdMaxAbs * zs && fo_rel < kRefRel && lse_ok &&
+                  fl <= kLseMaxAbs && gq && gk && gv && gb;
+  std::printf("%-22s B%d Hq%-2d Hkv%-2d N%-5d D%-3d %s | o %.1e (%.1e) lse %.1e | dQ %.1e dK %.1e"
+              " dV %.1e dbias %.1e%s | %s\n",
+              name, B, Hq, s.Hkv, N, s.D, s.causal ? "causal" : "dense ", fo_abs, fo_rel, fl, q2,
+              k2, v2, b2, bits_ok ? "" : " | dropout bits differ", ok ? "ok" : "FAIL");
+  std::fflush(stdout);
+  return ok;
+}
+
 int cmd_check() {
   bool ok = true;
   struct Regime {
@@ -232,6 +457,19 @@ int cmd_check() {
   ok &= check_case("MQA split tiles", {1, 4, 1, 1000, 64, 1}, 1.0, seed++);
   ok &= check_case("MHA split tiles", {1, 2, 2, 1536, 128, 1}, 1.0, seed++);
   ok &= check_case("N=1", {1, 2, 1, 1, 64, 1}, 1.0, seed++);
+  // The options of the general pair (fa_fwd_ex / fa_bwd_ex).
+  ok &= check_options_case("kv_len+window+alibi", {2, 4, 2, 300, 64, 1},
+                           kOptKvLen | kOptWindow | kOptAlibi, seed++);
+  ok &= check_options_case("scale+segments", {2, 4, 2, 257, 128, 0}, kOptScale | kOptSegs, seed++);
+  ok &= check_options_case("shared mask", {1, 4, 2, 333, 80, 1}, kOptMask1, seed++);
+  ok &= check_options_case("per-head mask+dropout", {2, 4, 4, 200, 64, 0}, kOptMaskH | kOptDrop,
+                           seed++);
+  ok &= check_options_case("dropout", {1, 8, 2, 512, 128, 1}, kOptDrop, seed++);
+  ok &= check_options_case("bias", {2, 4, 2, 300, 128, 1}, kOptBias, seed++);
+  ok &= check_options_case("every option", {2, 4, 2, 301, 64, 1},
+                           kOptKvLen | kOptWindow | kOptAlibi | kOptScale | kOptSegs | kOptMaskH |
+                               kOptDrop | kOptBias,
+                           seed++);
   std::printf("check: %s\n", ok ? "all ok" : "FAILED");
   return ok ? 0 : 1;
 }

@@ -1,7 +1,11 @@
 """The torch-free driver (tests/driver/fa_driver) on the GPU: the C ABI with
 caller-owned hipMalloc buffers and no torch in the process, checked against
 the float64 C oracle over the reference's 4 input regimes and the GQA,
-ragged and split-tile shapes; a benchmark line; the MFMA throughput probe."""
+ragged and split-tile shapes, and fa_fwd_ex / fa_bwd_ex with every option
+(key lengths, window, ALiBi, scale, packed sequences, a mask packed by
+fa_pack_mask, dropout bits from fa_dropout_bits checked against the C draw,
+a bias and its gradient) against the C oracle's ora_fwd_ex / ora_bwd_ex; a
+benchmark line; the MFMA throughput probe."""
 import os
 import re
 import subprocess
@@ -27,7 +31,7 @@ def test_driver_check_against_c_oracle():
     p = _run("check")
     assert p.returncode == 0, p.stdout + p.stderr
     assert "check: all ok" in p.stdout
-    assert p.stdout.count("| ok") == 21
+    assert p.stdout.count("| ok") == 28  # 21 plain cases, 7 of the general pair's options
 
 
 def test_driver_bench_quick():
