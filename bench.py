@@ -154,6 +154,111 @@ def load_capi():
     return lib
 
 
+class FaOptions(ctypes.Structure):
+    """struct fa_options of include/fa_mi355x.h (same field order and types)."""
+    _fields_ = [("dtype", ctypes.c_int), ("layout", ctypes.c_int),
+                ("kv_len", ctypes.c_void_p), ("window", ctypes.c_int),
+                ("alibi_slopes", ctypes.c_void_p), ("seg_start", ctypes.c_void_p),
+                ("seg_end", ctypes.c_void_p), ("scale", ctypes.c_float),
+                ("mask", ctypes.c_void_p), ("mask_t", ctypes.c_void_p),
+                ("mask_heads", ctypes.c_int), ("drop", ctypes.c_void_p),
+                ("drop_t", ctypes.c_void_p), ("drop_scale", ctypes.c_float),
+                ("bias", ctypes.c_void_p), ("bias_stride_b", ctypes.c_longlong),
+                ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p)]
+
+
+def feature_paths(c, steps, warmup):
+    """fwd+bwd ms per step through the general pair (fa_fwd_ex, fa_bwd_ex) on
+    the same inputs, with each optional input the reference lacks: the step
+    as timed above but with options (plain, for comparison), an all-true
+    boolean mask packed once (the packing is per model call, not per layer),
+    dropout 0.1 with its keep bits drawn in every step (fa_dropout_bits, as
+    in training), both, and an fp32 (1, Hq, N, N) bias with and without its
+    gradient (dbias zeroed in every step). Back-to-back steps on one stream,
+    wall clock over `steps` after `warmup`. The block runs after the headline
+    and D=64 measurements, whose load lowers the clock a little, so its own
+    plain_ex, measured in the same state, is what the others compare to (in
+    a fresh process fa_fwd_ex + fa_bwd_ex without options take the same time
+    as the headline step)."""
+    import torch
+    lib = load_capi()
+    vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+    opts_t = ctypes.POINTER(FaOptions)
+    lib.fa_fwd_ex.argtypes = [vp] * 5 + [i] * 6 + [opts_t, vp]
+    lib.fa_bwd_ex.argtypes = [vp] * 10 + [sz] + [i] * 6 + [opts_t, vp]
+    lib.fa_pack_mask.argtypes = [vp, i, i, vp, vp, vp]
+    lib.fa_dropout_bits.argtypes = [ctypes.c_uint64, ctypes.c_float, i, i, vp, vp, vp]
+    lib.fa_dropout_scale.argtypes = [ctypes.c_float]
+    lib.fa_dropout_scale.restype = ctypes.c_float
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, N, D, causal = c["B"], c["Hq"], c["Hkv"], c["N"], c["D"], int(c["causal"])
+    q, k, v, do = (t.to(dev) for t in make_inputs(c, torch))
+    o, lse = torch.empty_like(q), torch.empty(B, Hq, N, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)
+    ws = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    W = (N + 31) // 32
+    mask = torch.ones(B, N, N, dtype=torch.uint8, device=dev)
+    m, m_t = (torch.empty(B, N, W, dtype=torch.int32, device=dev) for _ in range(2))
+    z, z_t = (torch.empty(B * Hq, N, W, dtype=torch.int32, device=dev) for _ in range(2))
+    bias = torch.randn(1, Hq, N, N, device=dev)
+    dbias = torch.empty(B, Hq, N, N, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    s = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+
+    def check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: {lib.fa_error_string(rc).decode()}")
+
+    check(lib.fa_pack_mask(P(mask), B, N, P(m), P(m_t), s), "fa_pack_mask")
+    zs = lib.fa_dropout_scale(0.1)
+
+    def opts(with_mask=False, with_drop=False, with_bias=False, grad=False):
+        f = FaOptions()
+        if with_mask:
+            f.mask, f.mask_t, f.mask_heads = m.data_ptr(), m_t.data_ptr(), 1
+        if with_drop:
+            f.drop, f.drop_t, f.drop_scale = z.data_ptr(), z_t.data_ptr(), zs
+        if with_bias:
+            f.bias, f.bias_stride_b, f.bias_stride_h = bias.data_ptr(), 0, N * N
+            if grad:
+                f.dbias = dbias.data_ptr()
+        return f
+
+    cases = {"plain_ex": opts(), "mask_all_true": opts(with_mask=True),
+             "dropout_0.1": opts(with_drop=True),
+             "mask_and_dropout": opts(with_mask=True, with_drop=True),
+             "bias": opts(with_bias=True), "bias_with_grad": opts(with_bias=True, grad=True)}
+    out = {}
+    # Arguments built once, so that the host stays well ahead of the GPU.
+    pz, pzt = P(z), P(z_t)
+    fwd_args = (P(q), P(k), P(v), P(o), P(lse), B, Hq, Hkv, N, D, causal)
+    bwd_args = (P(q), P(k), P(v), P(do), P(o), P(lse), P(dq), P(dk), P(dv), P(ws), ws_bytes,
+                B, Hq, Hkv, N, D, causal)
+    for name, f in cases.items():
+        fp = ctypes.pointer(f)
+        draw, zero = bool(f.drop), bool(f.dbias)
+
+        def step(seed):
+            if draw:
+                check(lib.fa_dropout_bits(seed, 0.1, B * Hq, N, pz, pzt, s), "fa_dropout_bits")
+            if zero:
+                dbias.zero_()
+            check(lib.fa_fwd_ex(*fwd_args, fp, s), "fa_fwd_ex")
+            check(lib.fa_bwd_ex(*bwd_args, fp, s), "fa_bwd_ex")
+
+        for n in range(warmup):
+            step(n)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for n in range(steps):
+            step(warmup + n)
+        torch.cuda.synchronize()
+        out[name + "_ms"] = round((time.perf_counter() - t0) * 1e3 / steps, 4)
+    return out
+
+
 def gpu_bench(c, steps, warmup, copy_mib=0, compare=True):
     import torch
     import fa_p100  # noqa: F401  (fails loudly if the binding is not built)
@@ -386,6 +491,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="first run one device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--no-features", action="store_true",
+                    help="skip the optional-input timings (feature_paths)")
     ap.add_argument("--no-d64", action="store_true",
                     help="skip the D=64 leg beside the headline (C3) line")
     ap.add_argument("--c5-impl", default="both", choices=["both", "fa_p100", "sdpa"],
@@ -470,6 +577,9 @@ def main():
             "kernel_ms": {"fwd": round(rd["fwd_ms"], 4), "bwd_preprocess": round(rd["pre_ms"], 4),
                           "bwd_main": round(rd["main_ms"], 4)},
             "p100_reference_ms": 29.596}
+    if args.config == "C3" and not args.no_features:
+        out["feature_paths"] = {"workload": "C3 shape through fa_fwd_ex + fa_bwd_ex (dq in fp16)",
+                                **feature_paths(c, min(args.steps, 50), 20)}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(c)
     print(json.dumps(out), flush=True)

@@ -4,13 +4,14 @@
 
 T is the output directory of
     rocprofv3 --kernel-trace --stats -d T -o trace --output-format csv -- \
-        python3 bench.py --no-cpu --no-d64
+        python3 bench.py --no-cpu --no-d64 --no-features
 F and W are the output directories of the two counter runs
     rocprofv3 --pmc FETCH_SIZE -d F -o fetch --output-format csv -- \
-        python3 bench.py --no-cpu --no-d64 --steps 3 --warmup 1 --copy-calibration 256
+        python3 bench.py --no-cpu --no-d64 --no-features --steps 3 --warmup 1 --copy-calibration 256
     rocprofv3 --pmc WRITE_SIZE -d W -o write --output-format csv -- (same bench command)
 and each optional S a counter run with up to 8 SQ counters (the two sets the
-summaries list). --no-d64 keeps the traces to the headline shape's kernels.
+summaries list). --no-d64 and --no-features keep the traces to the headline
+shape's plain kernels.
 
 FETCH_SIZE / WRITE_SIZE are reported in KiB per dispatch. The 256 MiB device
 copy that --copy-calibration runs first must read and write 256 MiB; the ratio
@@ -99,10 +100,10 @@ def main():
                 sq[k][n] = sum(vals) / len(vals)
 
     os.makedirs(a.out, exist_ok=True)
-    cmd_bench = "python3 bench.py --no-cpu --no-d64"
-    cmd_cnt = ("python3 bench.py --no-cpu --no-d64 --steps 3 --warmup 1 --copy-calibration %d"
+    cmd_bench = "python3 bench.py --no-cpu --no-d64 --no-features"
+    cmd_cnt = ("python3 bench.py --no-cpu --no-d64 --no-features --steps 3 --warmup 1 --copy-calibration %d"
                % a.copy_mib)
-    cmd_sq = "python3 bench.py --no-cpu --no-d64 --steps 3 --warmup 1"
+    cmd_sq = "python3 bench.py --no-cpu --no-d64 --no-features --steps 3 --warmup 1"
     sq_sets = [
         "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS "
         "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
