@@ -40,6 +40,17 @@ def test_dropout_bits_match_the_oracle_draw(planes, N, p):
         assert abs(scale - zs) <= 1e-6 * zs
 
 
+def test_dropout_bits_match_the_oracle_draw_on_long_rows():
+    """N = 4096 (128 words per row, 16 of the generator's 8-word chunks) and
+    N = 4095 (a partial last word), both layouts bit for bit."""
+    import fa_p100
+    for planes, n, seed in ((2, 4096, 77), (1, 4095, (1 << 63) + 5)):
+        bits, bits_t, _ = fa_p100.dropout_bits(seed, 0.1, 1, planes, n, DEV)
+        keep, _ = ora.dropout_keep(seed, 0.1, planes, n)
+        assert np.array_equal(as_u32(bits[0]), host_words(keep)), (planes, n)
+        assert np.array_equal(as_u32(bits_t[0]), host_words(np.swapaxes(keep, -1, -2))), (planes, n)
+
+
 def run(q, k, v, do, causal, p, seed, **kw):
     import fa_p100
     qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
