@@ -22,6 +22,16 @@
 //                           v_mfma_f32_32x32x16_f16 chains on every SIMD, the
 //                           measured ceiling for the roofline (the reference's
 //                           half2 peak sweep measured its SIMT ceiling).
+//   fa_driver mix           the same products as one dependent chain per wave
+//                           at two waves per SIMD, each followed by the
+//                           softmax's kind of VALU work (fp32 FMAs,
+//                           v_exp_f32), and the VALU work alone: cycles per
+//                           product per SIMD, what the kernels' instruction
+//                           mix allows at best.
+//   fa_driver lds           LDS read throughput per CU of the kernels' operand
+//                           reads (16-byte and transpose reads of padded and
+//                           swizzled D = 128 tiles, through fa_device.h's
+//                           layout helpers) at two waves per SIMD.
 //   fa_driver dqcost        the dQ traffic a backward without the dQ pass
 //                           would carry (the reference's design,
 //                           flash_bwd.cuh:434-443, accumulates dQ across key
@@ -44,6 +54,7 @@
 #include <string>
 #include <vector>
 
+#include "../../flash-attention-p100_amd/csrc/fa_device.h"
 #include "../../include/fa_mi355x.h"
 #include "../../oracle/attention_ref.h"
 
@@ -641,6 +652,207 @@ int cmd_peak() {
   return 0;
 }
 
+// Issue mix of one wave: one dependent chain of 32x32x16 fp16 MFMAs (the
+// shape of an S^T product: every product accumulates into the last), each
+// followed by NF fp32 FMAs and NE v_exp_f32 on 16 independent values (the
+// softmax's work per product), in that order by scheduling groups. NM = 0
+// leaves the VALU work alone. The wave's shader clock comes from s_memtime
+// against the 100 MHz s_memrealtime.
+template <int NM, int NF, int NE>
+__global__ __launch_bounds__(256) void mix_kernel(float* out, int iters, long long* clk) {
+  const int t = threadIdx.x;
+  half8_t a, b;
+  for (int e = 0; e < 8; ++e) {
+    a[e] = (_Float16)(((t + e) & 7) * 0.001f);
+    b[e] = (_Float16)(((t * 3 + e) & 7) * 0.001f);
+  }
+  floatx16_t c = {};
+  float x[16];
+  for (int r = 0; r < 16; ++r) x[r] = (t + r) * 1e-3f;
+  const long long t0 = clock64(), r0 = wall_clock64();
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      if (NM) c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < NF; ++v) x[(m * NF + v) & 15] = fmaf(x[(m * NF + v) & 15], 0.5f, -0.25f);
+#pragma unroll
+      for (int v = 0; v < NE; ++v) x[(m * NE + v + 8) & 15] = __builtin_amdgcn_exp2f(x[(m * NE + v + 8) & 15]);
+      if (NM) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // the product
+      if (NF + NE) __builtin_amdgcn_sched_group_barrier(0x002, NF + NE, 0);  // its VALU work
+    }
+  }
+  const long long t1 = clock64(), r1 = wall_clock64();
+  float s = 0;
+  for (int e = 0; e < 16; ++e) s += c[e] + x[e];
+  out[blockIdx.x * blockDim.x + t] = s;
+  if (t == 0 && blockIdx.x == 0) {
+    clk[0] = t1 - t0;
+    clk[1] = r1 - r0;
+  }
+}
+
+// Cycles per SIMD for each (product + its VALU work) at two waves per SIMD
+// (the kernels' occupancy), and the VALU instructions alone: what the
+// softmax's FMAs and exponentials cost beside the products.
+int cmd_mix() {
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, 0));
+  const int cus = prop.multiProcessorCount;
+  const int blocks = cus * 2;  // blocks of 4 waves: 2 waves per SIMD
+  const int iters = 4000;
+  float* out = dalloc<float>((size_t)blocks * 256);
+  long long* clk = dalloc<long long>(2);
+  hipEvent_t e0, e1;
+  HIP_OK(hipEventCreate(&e0));
+  HIP_OK(hipEventCreate(&e1));
+  struct Case {
+    const char* name;
+    void (*k)(float*, int, long long*);
+    int nm, nvalu;
+  };
+  const Case cases[] = {
+      {"MFMA chain alone", mix_kernel<1, 0, 0>, 1, 0},
+      {"MFMA + 4 FMA", mix_kernel<1, 4, 0>, 1, 4},
+      {"MFMA + 6 FMA", mix_kernel<1, 6, 0>, 1, 6},
+      {"MFMA + 2 exp", mix_kernel<1, 0, 2>, 1, 2},
+      {"MFMA + 2 FMA + 2 exp", mix_kernel<1, 2, 2>, 1, 4},
+      {"MFMA + 4 exp", mix_kernel<1, 0, 4>, 1, 4},
+      {"16 FMA alone", mix_kernel<0, 16, 0>, 0, 16},
+      {"16 exp alone", mix_kernel<0, 0, 16>, 0, 16},
+  };
+  for (const Case& cs : cases) {
+    hipLaunchKernelGGL(cs.k, dim3(blocks), dim3(256), 0, nullptr, out, 10, clk);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipDeviceSynchronize());
+    float best = 1e30f;
+    long long hc[2] = {0, 0};
+    for (int rep = 0; rep < 3; ++rep) {
+      HIP_OK(hipEventRecord(e0, nullptr));
+      hipLaunchKernelGGL(cs.k, dim3(blocks), dim3(256), 0, nullptr, out, iters, clk);
+      HIP_OK(hipGetLastError());
+      HIP_OK(hipEventRecord(e1, nullptr));
+      HIP_OK(hipEventSynchronize(e1));
+      float ms = 0;
+      HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+      if (ms < best) {
+        best = ms;
+        HIP_OK(hipMemcpy(hc, clk, sizeof(hc), hipMemcpyDeviceToHost));
+      }
+    }
+    const double ghz = hc[1] > 0 ? (double)hc[0] / (double)hc[1] * 0.1 : 0.0;
+    const double kernel_cycles = best * 1e-3 * ghz * 1e9;
+    const double groups = 2.0 * iters * 8;  // per SIMD: 2 waves x iters x 8 groups
+    if (cs.nm) {
+      const double tf = (double)blocks * 4 * iters * 8 * 32768.0 / (best * 1e-3) / 1e12;
+      std::printf("mix: %-22s %7.1f TFLOP/s, %5.1f cycles per product per SIMD at %.2f GHz\n",
+                  cs.name, tf, kernel_cycles / groups, ghz);
+    } else {
+      std::printf("mix: %-22s %5.2f cycles per wave64 instruction per SIMD at %.2f GHz\n", cs.name,
+                  kernel_cycles / (groups * cs.nvalu), ghz);
+    }
+  }
+  HIP_OK(hipFree(out));
+  HIP_OK(hipFree(clk));
+  return 0;
+}
+
+// LDS operand reads of the kernels' D = 128 tiles, through the kernels' own
+// layout helpers (fa_device.h): PAT 0 16-byte reads of a padded tile
+// (tile_read16), 1 16-byte reads of swizzled 256-byte rows (Swz::read16),
+// 2 transpose reads of a padded tile (tile_tr_operand), 3 transpose reads of
+// swizzled rows (Swz::tr_operand). Each iteration reads eight operands of one
+// 32-row block (rows 0-31 or 32-63 of a 64-row tile); the empty asm with a
+// memory clobber keeps the compiler from hoisting the reads out of the loop.
+template <int PAT>
+__global__ __launch_bounds__(256) void lds_kernel(float* out, int iters, long long* clk) {
+  using T = fa::Tile<128>;
+  using S = fa::Swz<128>;
+  constexpr int kHalves = 64 * T::kRowHalves;  // 64 padded rows (17 KB) >= 64 swizzled rows
+  __shared__ __align__(16) fa::half_t tile[kHalves];
+  const int t = threadIdx.x, lane = t & 63;
+  for (int i = t; i < kHalves; i += 256) tile[i] = (fa::half_t)(float)(i & 63);
+  __syncthreads();
+  const int roff = fa::row_lane_off<128>(lane), troff = fa::tr_lane_off<128>(lane);
+  typename S::Offsets so0, so1;
+  so0.init(lane, 0);
+  so1.init(lane, 32);
+  float acc = 0.f;
+  const long long t0 = clock64(), r0 = wall_clock64();
+  for (int i = 0; i < iters; ++i) {
+    const int rb = (i & 1) * 32;
+    const typename S::Offsets& so = (i & 1) ? so1 : so0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+      fa::half8 v;
+      if (PAT == 0) v = fa::tile_read16<128>(tile, rb, m, roff);
+      if (PAT == 1) v = S::read16(tile, so, m);
+      if (PAT == 2) v = fa::tile_tr_operand<128>(tile, rb + 16 * (m & 1), 32 * (m >> 1), troff);
+      if (PAT == 3) v = S::tr_operand(tile, m & 1, so, m >> 1);
+      acc += (float)v[0] + (float)v[7];
+    }
+    asm volatile("" ::: "memory");
+  }
+  const long long t1 = clock64(), r1 = wall_clock64();
+  out[blockIdx.x * blockDim.x + t] = acc;
+  if (t == 0 && blockIdx.x == 0) {
+    clk[0] = t1 - t0;
+    clk[1] = r1 - r0;
+  }
+}
+
+// LDS read throughput of those patterns per CU at two waves per SIMD (the
+// kernels' occupancy): what the operand reads of a step cost.
+int cmd_lds() {
+  hipDeviceProp_t prop;
+  HIP_OK(hipGetDeviceProperties(&prop, 0));
+  const int cus = prop.multiProcessorCount;
+  const int blocks = cus * 2;
+  const int iters = 4000;
+  float* out = dalloc<float>((size_t)blocks * 256);
+  long long* clk = dalloc<long long>(2);
+  hipEvent_t e0, e1;
+  HIP_OK(hipEventCreate(&e0));
+  HIP_OK(hipEventCreate(&e1));
+  struct Case {
+    const char* name;
+    void (*k)(float*, int, long long*);
+  };
+  const Case cases[] = {
+      {"16-byte reads, padded rows", lds_kernel<0>},
+      {"16-byte reads, swizzled rows", lds_kernel<1>},
+      {"transpose reads, padded rows", lds_kernel<2>},
+      {"transpose reads, swizzled rows", lds_kernel<3>},
+  };
+  for (const Case& cs : cases) {
+    hipLaunchKernelGGL(cs.k, dim3(blocks), dim3(256), 0, nullptr, out, 10, clk);
+    HIP_OK(hipGetLastError());
+    HIP_OK(hipDeviceSynchronize());
+    float best = 1e30f;
+    long long hc[2] = {0, 0};
+    for (int rep = 0; rep < 3; ++rep) {
+      HIP_OK(hipEventRecord(e0, nullptr));
+      hipLaunchKernelGGL(cs.k, dim3(blocks), dim3(256), 0, nullptr, out, iters, clk);
+      HIP_OK(hipGetLastError());
+      HIP_OK(hipEventRecord(e1, nullptr));
+      HIP_OK(hipEventSynchronize(e1));
+      float ms = 0;
+      HIP_OK(hipEventElapsedTime(&ms, e0, e1));
+      if (ms < best) {
+        best = ms;
+        HIP_OK(hipMemcpy(hc, clk, sizeof(hc), hipMemcpyDeviceToHost));
+      }
+    }
+    const double ghz = hc[1] > 0 ? (double)hc[0] / (double)hc[1] * 0.1 : 0.0;
+    const double bytes_per_cu = 8.0 * 64 * iters * 8 * 16.0;  // 8 waves x 64 lanes x 16 B per operand
+    std::printf("lds: %-32s %6.1f B/clk per CU at %.2f GHz\n", cs.name,
+                bytes_per_cu / (best * 1e-3 * ghz * 1e9), ghz);
+  }
+  HIP_OK(hipFree(out));
+  HIP_OK(hipFree(clk));
+  return 0;
+}
+
 // One item per (head, key tile u, query step i0) of a causal backward with
 // 128-key tiles and 64-row query steps, dealt out evenly over the grid (the
 // library balances its causal work the same way). mode 0: each item adds its
@@ -746,7 +958,9 @@ int main(int argc, char** argv) {
   if (cmd == "fd") return cmd_fd();
   if (cmd == "bench") return cmd_bench(argc > 2 && std::string(argv[2]) == "quick");
   if (cmd == "peak") return cmd_peak();
+  if (cmd == "mix") return cmd_mix();
+  if (cmd == "lds") return cmd_lds();
   if (cmd == "dqcost") return cmd_dqcost();
-  std::fprintf(stderr, "usage: %s check | fd | bench [quick] | peak | dqcost\n", argv[0]);
+  std::fprintf(stderr, "usage: %s check | fd | bench [quick] | peak | mix | lds | dqcost\n", argv[0]);
   return 2;
 }

@@ -5,7 +5,7 @@ ragged and split-tile shapes, and fa_fwd_ex / fa_bwd_ex with every option
 (key lengths, window, ALiBi, scale, packed sequences, a mask packed by
 fa_pack_mask, dropout bits from fa_dropout_bits checked against the C draw,
 a bias and its gradient) against the C oracle's ora_fwd_ex / ora_bwd_ex; a
-benchmark line; the MFMA throughput probe."""
+benchmark line; the MFMA throughput, MFMA + VALU issue and LDS read probes."""
 import os
 import re
 import subprocess
@@ -47,3 +47,23 @@ def test_driver_mfma_peak_probe():
     assert p.returncode == 0, p.stdout + p.stderr
     tf = float(re.search(r"sustained ([0-9.]+) TFLOP/s", p.stdout).group(1))
     assert 500.0 < tf <= 2600.0, tf
+
+
+def test_driver_issue_mix_probe():
+    p = _run("mix")
+    assert p.returncode == 0, p.stdout + p.stderr
+    lines = [l for l in p.stdout.splitlines() if l.startswith("mix:")]
+    assert len(lines) == 8, p.stdout
+    tf = float(re.search(r"chain alone\s+([0-9.]+) TFLOP/s", p.stdout).group(1))
+    assert 500.0 < tf <= 2600.0, tf
+    for l in lines:
+        cyc = float(re.search(r"([0-9.]+) cycles per", l).group(1))
+        assert 0.5 < cyc < 400.0, l
+
+
+def test_driver_lds_read_probe():
+    p = _run("lds")
+    assert p.returncode == 0, p.stdout + p.stderr
+    rates = [float(x) for x in re.findall(r"([0-9.]+) B/clk per CU", p.stdout)]
+    assert len(rates) == 4, p.stdout
+    assert all(8.0 < r <= 512.0 for r in rates), rates
