@@ -55,8 +55,10 @@ drawn per call from torch's default generator (fa_p100.dropout_bits).
 
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): output_attentions,
-head_mask, a window on non-causal attention, head_dim other than
-not a multiple of 8 up to 128, q_len != kv_len (KV-cache decoding). A scale other than 1/sqrt(D),
+head_mask, attention sinks (s_aux) and logit soft-capping (softcap), which
+other models pass to the attention interface, a window on non-causal
+attention, a head_dim that is not a multiple of 8 up to 128, q_len != kv_len
+(KV-cache decoding). A scale other than 1/sqrt(D),
 which the reference rejected, goes to the kernels.
 """
 import warnings
@@ -227,6 +229,18 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             "output_attentions=True is not available; use attn_implementation='eager'.")
     if kwargs.get("head_mask") is not None:
         raise NotImplementedError("fa_p100 does not support head_mask.")
+    # Terms of other models' attention that the kernels do not compute:
+    # learnable attention sinks (gpt-oss and others pass them as s_aux, an
+    # extra logit per head in the softmax denominator) and logit soft-capping
+    # (Gemma 2: softcap * tanh(s / softcap)). Ignoring either would change the
+    # output without an error.
+    if kwargs.get("s_aux") is not None:
+        raise NotImplementedError(
+            "fa_p100 does not support attention sinks (s_aux); use attn_implementation='eager'.")
+    if kwargs.get("softcap") is not None:
+        raise NotImplementedError(
+            "fa_p100 does not support logit soft-capping (softcap); "
+            "use attn_implementation='eager'.")
 
     head_dim = query.size(-1)
     if not (8 <= head_dim <= 128 and head_dim % 8 == 0):

@@ -29,6 +29,8 @@ MOD = types.SimpleNamespace(is_causal=True)
     (dict(attention_mask=None, head_mask=torch.ones(4)), "head_mask"),
     (dict(attention_mask=None, sliding_window=128, is_causal=False), "a window of 128"),
     (dict(attention_mask=None, sliding_window=0), "a window of 0"),
+    (dict(attention_mask=None, s_aux=torch.zeros(4)), "attention sinks"),
+    (dict(attention_mask=None, softcap=50.0), "soft-capping"),
 ])
 def test_unsupported_requests_raise(kwargs, match):
     q, k, v = qkv()
