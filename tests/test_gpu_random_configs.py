@@ -1,7 +1,7 @@
 """Seeded random configurations that cross every option at once.
 
 The other GPU tests cover each option on its own and in hand-picked sets;
-here 160 seeded draws combine them: batch 1-2, MHA/GQA/MQA, N from 1 to 320,
+here 560 seeded draws combine them: batch 1-2, MHA/GQA/MQA, N from 1 to 320,
 any head dim that is a multiple of 8 up to 128, causal or not, fp16 or bf16,
 dense (B, H, N, D) tensors or views of (B, N, H, D) storage, and a random
 subset of key lengths, a sliding window (causal only), ALiBi, a softmax
@@ -20,7 +20,7 @@ from test_gpu_bf16 import BF_ELEM_REL, BF_FWD_MAX_ABS, BF_GRAD_REL_L2, BF_LSE_MA
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-N_CASES = 160
+N_CASES = 560
 OPTIONS = ("kv_len", "window", "alibi", "scale", "segments", "mask", "dropout", "bias")
 
 
