@@ -73,8 +73,11 @@ static_assert(kTile == kBwdTile, "workspace layout assumes this key tile");
 // 76..86 for B=1 H=8 N=4096 D=128, 66..76 for H=16 N=2048 D=64 and 76 for
 // H=16 N=8192 D=128; 110 lost everywhere (the best rate had been ~50 before
 // phase-2 steps got cheaper). With phase 1's operands read ahead too, 66 beat
-// 76 and 86 on all three shapes by 0.4-1.7%.
-constexpr int kSplitNum = 66;
+// 76 and 86 on all three shapes by 0.4-1.7%. Re-swept (56..96) once phase 2
+// (and phase 1 at D <= 64) took the causal test on diagonal steps only: 86
+// beat 66 by 1.8% at B=1 H=8 N=4096 D=128, within noise at H=16 N=4096
+// D=64, H=16 N=8192 D=128 and H=16 N=2048 D=64.
+constexpr int kSplitNum = 86;
 constexpr int kSplitBias = 5;
 
 // LDS: every tile is its own __shared__ object (declared in bwd_kernel), so
