@@ -32,6 +32,13 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + INCLUDE, "-Wno-unused-result",
 ]
+# Per-file additions. The forward's kernels schedule for instruction-level
+# parallelism: same-box A/B, bit-identical output, 2-4% faster at D = 64 and
+# D = 96 and on non-causal shapes, neutral at B=1 H=8 N=4096 D=128 causal and
+# at H=16/8 N=8192; the backward's lost 3-10% with it, so it stays default.
+FILE_FLAGS = {
+    "fa_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+}
 
 
 def lib_path():
@@ -59,7 +66,8 @@ def build_kernels(jobs=8):
     for src in KERNEL_SOURCES:
         obj = os.path.join(OBJ, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([hipcc, *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(jobs, len(cmds))) as ex:
         list(ex.map(_run, cmds))
     tmp = lib_path() + ".tmp"
