@@ -32,12 +32,16 @@ HIPCC_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + INCLUDE, "-Wno-unused-result",
 ]
-# Per-file additions. The forward's kernels schedule for instruction-level
-# parallelism: same-box A/B, bit-identical output, 2-4% faster at D = 64 and
-# D = 96 and on non-causal shapes, neutral at B=1 H=8 N=4096 D=128 causal and
-# at H=16/8 N=8192; the backward's lost 3-10% with it, so it stays default.
+# Per-file additions (same-box A/B timings, bit-identical output each). The
+# forward's kernels schedule for instruction-level parallelism: 2-4% faster
+# at D = 64 and D = 96 and on non-causal shapes, neutral at B=1 H=8 N=4096
+# D=128 causal and at H=16/8 N=8192 (the backward lost 3-11% with it). The
+# backward's scheduler uses the register-pressure trackers: 2.3% faster at
+# B=2 H=32/8 N=3001 D=128 dense, neutral at the causal shapes (the forward
+# gains nothing from them).
 FILE_FLAGS = {
     "fa_fwd.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "fa_bwd.hip": ["-mllvm", "-amdgpu-use-amdgpu-trackers=1"],
 }
 
 
