@@ -718,7 +718,13 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         __syncthreads();
       }
       if (!finish) {
-        if (!half) slot_store<2 * (D / 32)>(mine, w.acc, w4, lane);
+        if (!half) {
+          slot_store<2 * (D / 32)>(mine, w.acc, w4, lane);
+          // Each storing wave waits for its own slot stores to complete
+          // before the barrier, so the counter bump below cannot overtake
+          // them whatever the compiler does for a workgroup-scope barrier.
+          wait_vmem();
+        }
         __syncthreads();
         if (tid == 0)
           xflag = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);

@@ -15,18 +15,27 @@
 
 namespace {
 
+// Largest span of one head's rows, in elements: N rows of row_elems 16-bit
+// values (D, or H*D in the (B, N, H, D) layout). Buffer resources hold 32-bit
+// byte ranges, and a staged tile addresses up to 255 rows past a head's last
+// row, which must read as zeros, so their byte offsets must not wrap:
+// (N + 256) rows stay below 2^32 bytes. A head dim narrower than its tile
+// width marks the extra columns with lane offsets from 2^31 up, so there the
+// rows (and the scalar offsets added to those lanes) stay below 2^30 bytes.
+bool rows_fit(int N, long long row_elems, int D) {
+  const long long limit = fa::padded_head_dim(D) == D ? (long long)INT_MAX : (1LL << 29);
+  return (long long)(N + 256) * row_elems <= limit;
+}
+
 int check_shape(int B, int Hq, int Hkv, int N, int D) {
   if (!fa::valid_head_dim(D)) return FA_ERR_HEAD_DIM;
   if (N <= 0) return FA_ERR_SEQLEN;
   if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return FA_ERR_HEADS;
   if (B <= 0) return FA_ERR_BATCH;
   // Kernels index rows of one (b, h) slice with 32-bit ints and whole tensors
-  // with 64-bit offsets; a head's rows must span at most 2^30 bytes (lane
-  // offsets from 2^31 up mark columns past a narrow head dim as out of range,
-  // and the row offsets added to them stay clear of 2^32);
-  // every launch is a 1-D grid whose work-item count (workgroups x threads)
-  // must fit the dispatch packet's 32-bit field.
-  if ((long long)N * D > (1LL << 29)) return FA_ERR_TOO_LARGE;
+  // with 64-bit offsets; every launch is a 1-D grid whose work-item count
+  // (workgroups x threads) must fit the dispatch packet's 32-bit field.
+  if (!rows_fit(N, D, D)) return FA_ERR_TOO_LARGE;
   constexpr unsigned long long kMaxItems = 0xFFFFFFFFull;
   if (fa::fwd_launch_items(B, Hq, N, D) > kMaxItems ||
       fa::bwd_launch_items(B, Hq, Hkv, N, D) > kMaxItems)
@@ -35,9 +44,9 @@ int check_shape(int B, int Hq, int Hkv, int N, int D) {
 }
 
 // The (B, N, H, D) layout addresses one head's rows through a buffer range
-// that spans all H heads: (N - 1) * H * D + D halves, at most 2^30 bytes.
+// that spans all H heads: rows of H * D halves.
 int check_bnhd(int Hq, int N, int D) {
-  return (long long)N * Hq * D > (1LL << 29) ? FA_ERR_TOO_LARGE : FA_OK;
+  return rows_fit(N, (long long)Hq * D, D) ? FA_OK : FA_ERR_TOO_LARGE;
 }
 
 int to_code(hipError_t e) { return e == hipSuccess ? FA_OK : (int)e; }

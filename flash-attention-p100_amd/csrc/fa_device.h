@@ -189,10 +189,11 @@ constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, 32-bit data format
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kRsrcWord3);
 }
-// A per-lane offset at or above 2^31 is past every resource this library
-// makes (the C ABI keeps a head's byte range within 2^30, so the scalar row
-// offsets added to it cannot carry the sum past 2^32), so the lane reads
-// zeros: the columns past a head dim that is narrower than the tile.
+// A per-lane offset at or above 2^31 marks the columns past a head dim that
+// is narrower than the tile: only such head dims use it, and for them the C
+// ABI keeps a head's byte range within 2^30, so the offset is past every
+// resource and the scalar row offsets added to it cannot carry the sum past
+// 2^32. The lane reads zeros.
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
 // Optional per-score inputs of a masked (BOUNDS) instantiation: a bit-packed

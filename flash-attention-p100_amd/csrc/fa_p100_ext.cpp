@@ -472,9 +472,10 @@ std::vector<at::Tensor> fa_pack_mask_t(at::Tensor dense, bool transposed) {
 
 // Dropout keep bits for `drop` / `drop_t`: int32 (B, H, N, ceil(N/32)) each on
 // the given device, drawn from `seed` with drop probability p (see
-// fa_dropout_bits), and the matching scale of the kept probabilities.
+// fa_dropout_bits). Without `transposed` only `drop` is drawn (the forward
+// reads no other) and the second tensor is undefined (None in Python).
 std::vector<at::Tensor> fa_dropout_bits_t(int64_t seed, double p, int64_t B, int64_t H, int64_t N,
-                                          int64_t device) {
+                                          int64_t device, bool transposed) {
   TORCH_CHECK(p >= 0.0 && p < 1.0, "dropout p must lie in [0, 1), got ", p);
   TORCH_CHECK(B > 0 && H > 0 && N > 0 && B * H <= INT32_MAX && N <= INT32_MAX,
               "dropout bits need positive B, H, N");
@@ -483,10 +484,12 @@ std::vector<at::Tensor> fa_dropout_bits_t(int64_t seed, double p, int64_t B, int
   auto opts = at::TensorOptions().dtype(at::kInt).device(dev);
   const int64_t W = (N + 31) / 32;
   auto bits = at::empty({B, H, N, W}, opts);
-  auto bits_t = at::empty({B, H, N, W}, opts);
+  at::Tensor bits_t;
+  if (transposed) bits_t = at::empty({B, H, N, W}, opts);
   check_rc(fa_dropout_bits((uint64_t)seed, (float)p, (int)(B * H), (int)N,
                            reinterpret_cast<uint32_t*>(bits.data_ptr<int>()),
-                           reinterpret_cast<uint32_t*>(bits_t.data_ptr<int>()),
+                           transposed ? reinterpret_cast<uint32_t*>(bits_t.data_ptr<int>())
+                                      : nullptr,
                            current_stream(bits)),
            "fa_dropout_bits");
   return {bits, bits_t};
@@ -496,7 +499,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dropout_bits", &fa_dropout_bits_t,
         "Dropout keep bits (B, H, N, ceil(N/32)) and their transpose for drop / drop_t",
         py::arg("seed"), py::arg("p"), py::arg("B"), py::arg("H"), py::arg("N"),
-        py::arg("device"));
+        py::arg("device"), py::arg("transposed") = true);
   m.def("dropout_scale", [](double p) { return (double)fa_dropout_scale((float)p); },
         "Scale of the kept probabilities for dropout_bits(p): 1 / (1 - the drawn rate)",
         py::arg("p"));

@@ -81,12 +81,19 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.segs = segs
         ctx.scale = scale
         ctx.mask = mask
+        # drop: (seed, p, scale). Only the seed is kept for the backward, which
+        # draws the keep bits again (the draw is a pure function of the seed):
+        # keeping the forward's bit planes would hold B*Hq*N*ceil(N/32)*4 bytes
+        # per call from the forward to the backward.
         ctx.drop = drop
         # bias: fp32 (B|1, Hq|1, N, N) view with dense rows (see flash_attn).
         ctx.bias = bias.detach() if bias is not None else None
         seg_start, seg_end = segs if segs is not None else (None, None)
         bits, bits_t = mask if mask is not None else (None, None)
-        z, z_t, z_scale = drop if drop is not None else (None, None, 1.0)
+        z, z_scale = None, 1.0
+        if drop is not None:
+            z, _, z_scale = dropout_bits(drop[0], drop[1], q.size(0), q.size(1), q.size(2),
+                                         q.device, transposed=False)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
@@ -108,7 +115,10 @@ class _FlashAttnP100(torch.autograd.Function):
     def backward(ctx, grad_o):
         seg_start, seg_end = ctx.segs if ctx.segs is not None else (None, None)
         bits, bits_t = ctx.mask if ctx.mask is not None else (None, None)
-        z, z_t, z_scale = ctx.drop if ctx.drop is not None else (None, None, 1.0)
+        z, z_t, z_scale = None, None, 1.0
+        if ctx.drop is not None:  # the forward's keep bits, drawn again from its seed
+            z, z_t, z_scale = dropout_bits(ctx.drop[0], ctx.drop[1], grad_o.size(0),
+                                           grad_o.size(1), grad_o.size(2), grad_o.device)
         dbias = None
         if ctx.bias is not None and ctx.needs_input_grad[12]:  # bias is input 12
             B, H, N = grad_o.size(0), grad_o.size(1), grad_o.size(2)
@@ -198,10 +208,15 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         returned o is (P * Z / (1 - p)) V and the gradients are those of
         that o. The keep bits Z come from a counter-based hash of
         dropout_seed (64-bit; drawn from torch's default CPU generator when
-        None, so torch.manual_seed makes runs repeat) through
-        dropout_bits(), and the backward reuses the forward's bits. The
-        drawn rate is p rounded to a multiple of 1/65536, and the scale
-        matches it exactly;
+        None, so torch.manual_seed makes runs repeat, and checkpoint
+        recomputation, which replays that generator, draws the same seed)
+        through dropout_bits(). The backward draws the same bits again
+        from the seed rather than keeping the forward's, so no bit planes
+        are held between the passes. Under HIP graph capture the seed must
+        be given (a seed drawn on the host at capture time would be
+        replayed unchanged by every replay): every replay then uses that
+        seed's bits. The drawn rate is p rounded to a multiple of 1/65536,
+        and the scale matches it exactly;
       * attn_bias, a floating tensor of shape (N, N), (B, N, N) or
         (B|1, Hq|1, N, N) on q's device: added to the scaled scores before
         the masks and the softmax (torch scaled_dot_product_attention's
@@ -253,8 +268,12 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         if not q.is_cuda:  # the binding's own check and message, before any drawing
             raise RuntimeError("q must be a CUDA tensor")
         if dropout_seed is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError(
+                    "dropout under HIP graph capture needs an explicit dropout_seed: a seed "
+                    "drawn on the host now would repeat in every replay")
             dropout_seed = int(torch.randint(0, 2 ** 63 - 1, (), dtype=torch.int64))
-        drop = dropout_bits(dropout_seed, p, q.size(0), q.size(1), q.size(2), q.device)
+        drop = (int(dropout_seed), p, _ext.dropout_scale(p))
     bias = None
     if attn_bias is not None:
         bias = attn_bias
@@ -276,12 +295,13 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
                                 segs, scale, mask, drop, bias)
 
 
-def dropout_bits(seed, p, batch, heads, n, device):
+def dropout_bits(seed, p, batch, heads, n, device, transposed=True):
     """(bits, bits_t, scale) of attention dropout: int32 keep bits
     (batch, heads, n, ceil(n/32)) in the mask layout and its transpose (bit
-    set = keep), drawn by one HIP kernel from the 64-bit `seed` with drop
-    probability p (fa_dropout_bits in the C ABI states the draw), and the
-    scale 1 / (1 - drawn rate) of the kept probabilities."""
+    set = keep; None when `transposed` is False), drawn by one HIP kernel from
+    the 64-bit `seed` with drop probability p (fa_dropout_bits in the C ABI
+    states the draw), and the scale 1 / (1 - drawn rate) of the kept
+    probabilities."""
     device = torch.device(device)
     if device.type != "cuda":
         raise ValueError(f"dropout bits are drawn on the GPU, got device {device}")
@@ -289,7 +309,7 @@ def dropout_bits(seed, p, batch, heads, n, device):
     seed = int(seed) % (1 << 64)
     if seed >= 1 << 63:  # the binding takes a signed 64-bit value with the same bits
         seed -= 1 << 64
-    bits, bits_t = _ext.dropout_bits(seed, float(p), batch, heads, n, index)
+    bits, bits_t = _ext.dropout_bits(seed, float(p), batch, heads, n, index, bool(transposed))
     return bits, bits_t, _ext.dropout_scale(float(p))
 
 

@@ -23,7 +23,10 @@
  *     asynchronous on it; the call returns after enqueueing.
  *   - Return value: FA_OK (0), an FA_ERR_* validation code (nothing was
  *     launched), or a hipError_t value reported by the HIP runtime.
- *   - Entry points are reentrant and thread-safe: they keep no state.
+ *   - Entry points are reentrant and thread-safe: they keep no state, with
+ *     one exception, fa_bwd_noalloc, whose built-in device scratch (16 MiB
+ *     per GPU, resident while the library is loaded) is shared by its calls
+ *     on one GPU, so calls of it that overlap on one GPU race.
  */
 #ifndef FA_MI355X_H_
 #define FA_MI355X_H_

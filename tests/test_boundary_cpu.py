@@ -229,4 +229,30 @@ def test_shape_limits_follow_the_one_dimensional_grids():
         assert lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D) > 0, (B, Hq, Hkv, N, D)
     # 2^23 query heads of 4096 rows need more than 2^32 forward work-items.
     assert lib.fa_bwd_workspace_bytes(1 << 13, 1 << 10, 1 << 10, 4096, 128) == 0
-    assert lib.fa_bwd_workspace_bytes(1, 1, 1, (1 << 22) + 1, 128) == 0  # N*D > 2^29
+    # At a tile width (32, 64, 96, 128) a head's rows, with the 256 rows a
+    # staged tile may address past them, stay within 2^32 bytes: (N+256)*D
+    # <= INT_MAX; narrower head dims keep (N+256)*D <= 2^29.
+    for D in (32, 64, 96, 128):
+        n_max = (2**31 - 1) // D - 256
+        assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max, D) > 0, D
+        assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max + 1, D) == 0, D
+    for D in (8, 40, 120):
+        n_max = 2**29 // D - 256
+        assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max, D) > 0, D
+        assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max + 1, D) == 0, D
+
+
+def test_bnhd_limit_spans_every_head_of_a_row():
+    """The (B, N, H, D) layout reads a head through one buffer range over all
+    H heads of each row. At a tile width the limit is (N+256)*H*D <= INT_MAX:
+    32 heads of 128 at N = 262144 (N*H*D = 2^30, above the 2^29 bound that
+    narrow head dims keep) pass validation and stop at the null pointers."""
+    lib = load_capi()
+    s = ctypes.c_void_p(0)
+    z = ctypes.c_void_p(0)
+    assert lib.fa_fwd_bnhd(z, z, z, z, z, 1, 32, 8, 1 << 18, 128, 1, s) == 10005
+    assert lib.fa_fwd_bnhd(z, z, z, z, z, 1, 64, 8, 1 << 18, 128, 1, s) == 10007
+    assert lib.fa_fwd_bnhd(z, z, z, z, z, 1, 32, 8, 1 << 18, 120, 1, s) == 10007
+    n_max = (2**31 - 1) // (32 * 128) - 256
+    assert lib.fa_fwd_bnhd(z, z, z, z, z, 1, 32, 8, n_max, 128, 1, s) == 10005
+    assert lib.fa_fwd_bnhd(z, z, z, z, z, 1, 32, 8, n_max + 1, 128, 1, s) == 10007
