@@ -46,7 +46,9 @@ enum {
   FA_ERR_BATCH = 10004,      /* B <= 0 */
   FA_ERR_NULL = 10005,       /* a required pointer is NULL */
   FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
-  FA_ERR_TOO_LARGE = 10007,  /* N*D (BNHD: N*H*D) over 2^29, or a launch's work items over 2^32 */
+  FA_ERR_TOO_LARGE = 10007,  /* (N+256)*D (BNHD: (N+256)*H*D) over 2^31-1, or over 2^29 for a
+                                head dim that is not 32, 64, 96 or 128; or a launch's work
+                                items over 2^32 */
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
   FA_ERR_WINDOW = 10010,     /* sliding window < 0, or > 0 without causal masking */

@@ -90,24 +90,17 @@ def test_hook_training_step_grads_match_eager():
 
 
 def test_qwen3_0p6b_shaped_training_step_through_hook():
-    """Qwen3-0.6B-shaped decoder, random init, B=1, seq 8192,
-    token ids uniform over the vocab, one fwd+bwd step (fp16 autocast) with
-    attention through the hook, unmodified transformers code."""
-    import fa_p100_hf
-    model = qwen3(28, 1024, 16, 8, 128, 3072, 151936)
-    model.train()
-    fa_p100_hf.enable_fa_p100(model)
-    g = torch.Generator("cuda").manual_seed(0)
-    ids = torch.randint(0, 151936, (1, 8192), device="cuda", generator=g)
-    with torch.autocast("cuda", torch.float16):
-        out = model(ids, labels=ids)
-    out.loss.backward()
-    torch.cuda.synchronize()
-    assert torch.isfinite(out.loss)
-    # Random init predicts ~uniformly: the loss sits near log(vocab).
-    assert abs(out.loss.item() - torch.log(torch.tensor(151936.0)).item()) < 1.0
-    q_grad = model.model.layers[0].self_attn.q_proj.weight.grad
-    assert q_grad is not None and torch.isfinite(q_grad).all() and q_grad.abs().sum() > 0
+    """BASELINE config 5 at its real length: the Qwen3-0.6B-shaped decoder
+    (28 layers, hidden 1024, 16/8 heads of 128, SwiGLU 3072, vocab 151936),
+    random init, B=1, seq 8192, token ids uniform over the vocab, one fwd+bwd
+    step (fp16 autocast) with attention through the hook, unmodified
+    transformers code, against the same step through transformers' sdpa and
+    eager attention on the same weights and ids (the verify_hf.py:78-154
+    method). Eager's attention weights at this length would hold ~6 GB per
+    layer until the backward, so the eager run recomputes each layer in the
+    backward (gradient checkpointing; eager draws no random numbers, so the
+    gradients are those of the plain step)."""
+    _full_depth_step(8192, eager_checkpointed=True)
 
 
 def test_hook_runs_bf16_under_bf16_autocast():
@@ -158,15 +151,19 @@ def test_hook_runs_bf16_under_bf16_autocast():
 
 def test_qwen3_0p6b_full_depth_step_matches_eager_and_sdpa():
     """The Qwen3-0.6B shape at its full depth (28 layers, hidden 1024, 16/8
-    heads of 128, SwiGLU 3072, vocab 151936) at seq 2048 (eager's stored
-    attention weights stay ~10 GB): one fp16-autocast training step through
-    the hook against eager and sdpa on the same weights and ids. The loss,
-    every layer's q/k/v/o projection gradients and the whole gradient vector
-    stay within a small multiple of the eager-vs-sdpa envelope, so the
-    kernel's error does not grow through 28 layers of backward."""
+    heads of 128, SwiGLU 3072, vocab 151936) at seq 2048: one fp16-autocast
+    training step through the hook against eager and sdpa on the same
+    weights and ids. The loss, every layer's q/k/v/o projection gradients and
+    the whole gradient vector stay within a small multiple of the
+    eager-vs-sdpa envelope, so the kernel's error does not grow through 28
+    layers of backward."""
+    _full_depth_step(2048, eager_checkpointed=False)
+
+
+def _full_depth_step(seq, eager_checkpointed):
     import fa_p100_hf
     g = torch.Generator("cuda").manual_seed(4)
-    ids = torch.randint(0, 151936, (1, 2048), device="cuda", generator=g)
+    ids = torch.randint(0, 151936, (1, seq), device="cuda", generator=g)
     losses, grads = {}, {}
     for impl in ("eager", "sdpa", "fa_p100"):
         model = qwen3(28, 1024, 16, 8, 128, 3072, 151936, seed=5)
@@ -175,6 +172,8 @@ def test_qwen3_0p6b_full_depth_step_matches_eager_and_sdpa():
             fa_p100_hf.enable_fa_p100(model)
         else:
             model.config._attn_implementation = impl
+        if impl == "eager" and eager_checkpointed:
+            model.gradient_checkpointing_enable()
         with torch.autocast("cuda", torch.float16):
             out = model(ids, labels=ids)
         out.loss.backward()
@@ -184,8 +183,11 @@ def test_qwen3_0p6b_full_depth_step_matches_eager_and_sdpa():
                        if p.grad is not None}
         del model, out
         torch.cuda.empty_cache()
+    # Random init predicts ~uniformly: the loss sits near log(vocab).
+    assert abs(losses["fa_p100"] - torch.log(torch.tensor(151936.0)).item()) < 1.0
     env_loss = abs(losses["sdpa"] - losses["eager"])
     assert abs(losses["fa_p100"] - losses["eager"]) <= 3 * env_loss + 1e-4 * losses["eager"], losses
+    assert abs(losses["fa_p100"] - losses["sdpa"]) <= 3 * env_loss + 1e-4 * losses["eager"], losses
 
     def rel(a, b):
         return ((a - b).norm() / b.norm()).item()
@@ -208,8 +210,48 @@ def test_qwen3_0p6b_full_depth_step_matches_eager_and_sdpa():
     r_attn = max(rel(grads["fa_p100"][n], grads["sdpa"][n]) /
                  (rel(grads["eager"][n], grads["sdpa"][n]) + 1e-6)
                  for n in grads["eager"] if "self_attn" in n and n.endswith("proj.weight"))
-    print(f"loss {losses}; all-grad rel vs eager {r_all:.2e} (sdpa {r_all_env:.2e}), "
+    print(f"seq {seq}: loss {losses}; all-grad rel vs eager {r_all:.2e} (sdpa {r_all_env:.2e}), "
           f"vs sdpa {r_fs:.2e}; worst attention ratio vs eager {max(worst)[:2]}, "
           f"vs sdpa {r_attn:.3f}")
     assert r_fs <= r_all_env, (r_fs, r_all_env)
     assert r_attn <= 1.5, r_attn
+
+
+def test_hook_dropout_under_gradient_checkpointing_redraws_the_same_bits():
+    """Attention dropout through the hook with gradient checkpointing (the
+    reference fine-tunes with it, finetune_hf.py:67, 79): each layer's keep
+    bits come from a seed drawn from torch's CPU generator at call time, and
+    the checkpoint's recompute replays that generator, so a checkpointed step
+    under one torch.manual_seed gives the same loss and gradients, bit for
+    bit, as the plain step. A different seed changes them (dropout is live)."""
+    import fa_p100_hf
+
+    def step(seed, checkpointed):
+        model = qwen3(3, 256, 4, 2, 64, 512, 500, seed=7)
+        model.config.attention_dropout = 0.2
+        for layer in model.model.layers:
+            layer.self_attn.attention_dropout = 0.2
+        model.train()
+        fa_p100_hf.enable_fa_p100(model)
+        if checkpointed:
+            model.gradient_checkpointing_enable()
+        ids = torch.randint(0, 500, (2, 200), device="cuda",
+                            generator=torch.Generator("cuda").manual_seed(3))
+        torch.manual_seed(seed)
+        with torch.autocast("cuda", torch.float16):
+            out = model(ids, labels=ids)
+        out.loss.backward()
+        torch.cuda.synchronize()
+        return out.loss.detach(), {n: p.grad.clone() for n, p in model.named_parameters()
+                                   if p.grad is not None}
+
+    loss_plain, g_plain = step(11, False)
+    loss_ckpt, g_ckpt = step(11, True)
+    assert torch.equal(loss_plain, loss_ckpt), (loss_plain.item(), loss_ckpt.item())
+    assert g_plain.keys() == g_ckpt.keys()
+    for n in g_plain:
+        assert torch.equal(g_plain[n], g_ckpt[n]), n
+    loss_other, g_other = step(12, True)
+    assert not torch.equal(loss_other, loss_plain)
+    n = "model.layers.0.self_attn.q_proj.weight"
+    assert ((g_other[n] - g_plain[n]).norm() / g_plain[n].norm()).item() > 1e-3
