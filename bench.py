@@ -164,7 +164,8 @@ class FaOptions(ctypes.Structure):
                 ("mask_heads", ctypes.c_int), ("drop", ctypes.c_void_p),
                 ("drop_t", ctypes.c_void_p), ("drop_scale", ctypes.c_float),
                 ("bias", ctypes.c_void_p), ("bias_stride_b", ctypes.c_longlong),
-                ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p)]
+                ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p),
+                ("kv_rows", ctypes.c_int)]
 
 
 def feature_paths(c, steps, warmup):

@@ -436,7 +436,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int* __restrict__ seg_end, const uint32_t* __restrict__ mask,
     const uint32_t* __restrict__ mask_t, int mask_heads, const uint32_t* __restrict__ drop,
     const uint32_t* __restrict__ drop_t, float drop_scale, const float* __restrict__ bias,
-    long long bias_sb, long long bias_sh, float bias_raw, float* __restrict__ dbias, int dr) {
+    long long bias_sb, long long bias_sh, float bias_raw, float* __restrict__ dbias, int dr,
+    int NK) {
   using L = BwdLds<D>;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
@@ -463,8 +464,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int bkv = wi / n_tiles;  // over B*Hkv
   const int Hkv = Hq / group;
   const int b = bkv / Hkv, hkv = bkv % Hkv;
-  // Per-entry key length (key padding), clamped to [1, N].
-  const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
+  // Per-entry key length (key padding), clamped to [1, NK] (NK: key rows, N:
+  // query rows). kofs = NK - N: causal masking aligns the last query row with
+  // the last key row, so query i sees key j iff j <= i + kofs. Workgroup t
+  // runs phase 1 for key tile t when there is one and phase 2 for query
+  // tile t when there is one.
+  const int Nk = kv_len ? min(max(kv_len[b], 1), NK) : NK;
+  const int kofs = NK - N;
+  const int n_ktiles = (NK + kTile - 1) / kTile, n_qtiles = (N + kTile - 1) / kTile;
   // Causal sliding window (only in the masked instantiation): row i sees keys
   // (i - Wb, i]; 0 = none.
   const int Wb = BOUNDS ? window : 0;
@@ -477,14 +484,14 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int* const sen = BOUNDS && seg_end ? seg_end + (size_t)b * N : nullptr;
   const bool narrowed = BOUNDS && (Wb > 0 || sst != nullptr);
   auto upper = [&](int j) {
-    j = min(j, N - 1);
-    int hi = Wb > 0 ? min(N, j + Wb) : N;
+    j = min(j, NK - 1);
+    int hi = Wb > 0 ? min(N, j - kofs + Wb) : N;
     if (sen) hi = min(hi, max(sen[j], j + 1));
     return hi;
   };
   auto lower = [&](int i) {
     i = min(i, N - 1);
-    int lo = Wb > 0 ? i - Wb + 1 : 0;
+    int lo = Wb > 0 ? i + kofs - Wb + 1 : 0;
     if (sst) lo = max(lo, min(sst[i], i));
     return max(lo, 0);
   };
@@ -501,7 +508,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     return packed_nc ? max(0, min(sst[j], j)) : 0;
   };
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
-  const rsrc_t rk = rows_rsrc(K + kv_off, N, stk.n, dr), rv = rows_rsrc(V + kv_off, N, stk.n, dr);
+  const rsrc_t rk = rows_rsrc(K + kv_off, NK, stk.n, dr), rv = rows_rsrc(V + kv_off, NK, stk.n, dr);
   // Offset of query head hq's row 0 in Q, dO, dQ.
   auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
   constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
@@ -553,11 +560,15 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   auto q_end = [&](int u) { return narrowed ? upper(u * kTile + kTile - 1) : N; };
   // ... and from its diagonal (causal) or the start of its first key's
   // sequence, rounded down to a streamed tile (u * kTile is a multiple of kSub).
-  auto q_start = [&](int u) { return CAUSAL ? u * kTile : col_lo(u * kTile) / kSub * kSub; };
+  auto q_start = [&](int u) {
+    return CAUSAL ? max(0, u * kTile - kofs) / kSub * kSub : col_lo(u * kTile) / kSub * kSub;
+  };
   auto n_iters = [&](int u) { return group * ((q_end(u) - q_start(u) + kSub - 1) / kSub); };
   auto split = [&](int u) {
     const int m = n_tiles - 1 - 2 * u;
-    if (!CAUSAL || m <= 0 || narrowed) return 0;  // windows leave the tiles' work equal
+    // windows leave the tiles' work equal; with kofs != 0 the key and query
+    // tiles do not pair up
+    if (!CAUSAL || m <= 0 || narrowed || kofs != 0) return 0;
     return max(0, min((group * m * split_num - split_bias) >> 8, n_iters(u) - 1));
   };
   const int tw = wi % n_tiles;
@@ -590,7 +601,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
 
     const int i_start = q_start(tile);
-    const int row_lo = CAUSAL ? j_col : packed_nc ? col_lo(j_col) : -(1 << 30);
+    const int row_lo = CAUSAL ? j_col - kofs : packed_nc ? col_lo(j_col) : -(1 << 30);
     const int n_qt = (q_end(tile) - i_start + kSub - 1) / kSub;
     // Rows this wave's key column reaches (see KVWave::step).
     const int row_end = j_col < Nk ? (narrowed ? upper(j_col) : N) : 0;
@@ -653,7 +664,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       // loads complete in issue order, so words loaded after them would hold
       // the softmax until the whole next stage had landed.
       fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, kres, half, w4 * 32, i0, j_col, row_lo, row_end,
+      // (j_col - kofs: the ALiBi distance counts from the aligned diagonal)
+      w.step(Qs, Os, lse2s, lse2s + kSub, vres, kres, half, w4 * 32, i0, j_col - kofs, row_lo,
+             row_end,
              alibi_raw, mtw, ztw, zs, bv1, [&] { return bload1(min(it + 1, it_end - 1)); },
              braw, lane, roff, so, scale_log2);
       wait_vmem();
@@ -739,7 +752,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       }
     }
     // dK (scaled) and dV leave as fp16.
-    if (finish && !half && (!BOUNDS || j_col < N)) {
+    if (finish && !half && (!BOUNDS || j_col < NK)) {
       half_t* dkrow = dK + kv_off + (size_t)j_col * stk.n;
       half_t* dvrow = dV + kv_off + (size_t)j_col * stk.n;
 #pragma unroll
@@ -761,18 +774,22 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     }
     __syncthreads();  // the exchange regions are the next item's or phase's staging memory
   };
-  if (x_help > 0) run_item(true);
-  run_item(false);
+  if (tw < n_ktiles) {
+    if (x_help > 0) run_item(true);
+    run_item(false);
+  }
   const int t0 = tw * kTile;  // query rows of phase 2
 
   // ============================== phase 2: dQ ==============================
-  {
+  if (tw < n_qtiles) {
     const int iw = t0 + w4 * 32;  // this wave's query rows
     const int i_row = iw + l32;
     const bool row_ok = !BOUNDS || i_row < N;
-    const int kv_end = CAUSAL ? min(Nk, t0 + kTile) : row_hi(t0 + kTile - 1);
+    const int kv_end = CAUSAL ? min(Nk, t0 + kTile + kofs) : row_hi(t0 + kTile - 1);
     const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
-    const int n_kt = (kv_end + kSub - 1) / kSub;
+    // (at least one step: rows above the first key, when there are more query
+    // rows than key rows, mask every key)
+    const int n_kt = max(1, (kv_end + kSub - 1) / kSub);
     // With a window, key tiles left of every row's window are skipped, and
     // each row masks the keys left of its own.
     const int t_lo = narrowed ? lower(t0) / kSub : 0;
@@ -856,7 +873,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         const int word = min(t * (kSub / 32) + half, W32 - 1);  // keys t*kSub + 32*half ..
         const uint32_t mw = mrow ? mrow[word] : ~0u;
         const uint32_t zw = zrow ? zrow[word] : ~0u;
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row, lane_hi, key_lo, alibi_raw, mw,
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row + kofs, lane_hi, key_lo, alibi_raw, mw,
                zw, zs, bv2, [&] { return bload2(min(t + 1, n_kt - 1)); }, braw, dbrow, db_x4,
                lane, so, scale_log2, issue);
         wait_vmem();
@@ -919,7 +936,8 @@ hipError_t launch_pre_d(const BwdArgs& a) {
 
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 hipError_t launch_main_t(const BwdArgs& a) {
-  const int n_tiles = (a.N + kTile - 1) / kTile;
+  const int NK = key_rows(a.N, a.Nkv);
+  const int n_tiles = (max(a.N, NK) + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
@@ -929,11 +947,11 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, a.D),
-                     make_strides(a.layout, a.Hkv, a.N, a.D), a.counters, a.slots,
+                     make_strides(a.layout, a.Hkv, NK, a.D), a.counters, a.slots,
                      a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
                      a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.drop,
                      a.drop_t, a.drop_scale, a.bias, a.bias_sb, a.bias_sh,
-                     a.bias ? 1.f / scale : 0.f, a.dbias, a.D);
+                     a.bias ? 1.f / scale : 0.f, a.dbias, a.D, NK);
   return hipGetLastError();
 }
 
@@ -943,7 +961,8 @@ hipError_t launch_main_d(const BwdArgs& a) {
   // instantiation (kTile is a multiple of kSub); a mask, dropout or a bias
   // one of its copies with those inputs compiled in (Feat).
   const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
-                      a.alibi != nullptr || a.seg_start != nullptr;
+                      a.alibi != nullptr || a.seg_start != nullptr ||
+                      key_rows(a.N, a.Nkv) != a.N;
   auto with = [&](auto feat) {
     constexpr int F = decltype(feat)::value;
     return a.causal ? launch_main_t<D, true, true, F, BF>(a)
@@ -965,11 +984,12 @@ hipError_t launch_main_d(const BwdArgs& a) {
 
 }  // namespace
 
-unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D) {
+unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D, int Nkv) {
   const unsigned long long rows = (unsigned long long)B * Hq * N;
   const unsigned long long rows_per_block = 256 / pre_lanes_per_row(padded_head_dim(D));
   const unsigned long long pre = (rows + rows_per_block - 1) / rows_per_block * 256;
-  const unsigned long long tiles = ((unsigned long long)N + kTile - 1) / kTile;
+  const unsigned long long tiles =
+      ((unsigned long long)(N > key_rows(N, Nkv) ? N : key_rows(N, Nkv)) + kTile - 1) / kTile;
   const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hkv;
   const unsigned long long main = (wgs + kXcds - 1) / kXcds * kXcds * kThreads;
   return pre > main ? pre : main;

@@ -110,6 +110,9 @@ const char* fa_error_string(int err) {
       return "dropout p must lie in [0, 1) and its scale be positive and finite; the backward "
              "needs drop_t with drop";
     case FA_ERR_BIAS: return "bias strides must not be negative, dbias needs a bias, and a bias needs N <= 2^22";
+    case FA_ERR_KV_ROWS:
+      return "kv_rows must be >= 0, and key rows that differ from the query rows do not combine "
+             "with packed sequences, a mask, dropout or a bias";
     case FA_ERR_SCRATCH:
       return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
              "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
@@ -149,6 +152,20 @@ static int check_opts(const fa_options& op, int causal, int Hq, int N, bool back
   if (op.bias_stride_b < 0 || op.bias_stride_h < 0) return FA_ERR_BIAS;
   if (op.dbias != nullptr && op.bias == nullptr) return FA_ERR_BIAS;
   if (op.bias != nullptr && N > kMaxBiasN) return FA_ERR_BIAS;
+  if (op.kv_rows < 0) return FA_ERR_KV_ROWS;
+  if (op.kv_rows > 0 && op.kv_rows != N &&
+      (op.seg_start != nullptr || op.mask != nullptr || op.drop != nullptr || op.bias != nullptr))
+    return FA_ERR_KV_ROWS;
+  return FA_OK;
+}
+
+// The k/v side of a shape whose key rows differ from the query rows
+// (fa_options.kv_rows): the same row-span and launch-size limits.
+static int check_kv_rows(const fa_options& op, int B, int Hq, int Hkv, int N, int D) {
+  if (op.kv_rows <= 0 || op.kv_rows == N) return FA_OK;
+  const int NK = op.kv_rows;
+  if (!rows_fit(NK, op.layout == fa::kBNHD ? (long long)Hkv * D : D, D)) return FA_ERR_TOO_LARGE;
+  if (fa::bwd_launch_items(B, Hq, Hkv, N, D, NK) > 0xFFFFFFFFull) return FA_ERR_TOO_LARGE;
   return FA_OK;
 }
 
@@ -163,6 +180,7 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   int rc = check_opts(op, causal, Hq, N, false);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
+  if (rc == FA_OK) rc = check_kv_rows(op, B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !o || !lse) return FA_ERR_NULL;
   fa::FwdArgs a{};
@@ -193,6 +211,7 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.bias = op.bias;
   a.bias_sb = op.bias_stride_b;
   a.bias_sh = op.bias_stride_h;
+  a.Nkv = op.kv_rows;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -264,6 +283,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   int rc = check_opts(op, causal, Hq, N, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
+  if (rc == FA_OK) rc = check_kv_rows(op, B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!q || !k || !v || !dO || !workspace || !(dq || dq16) || !dk || !dv) return FA_ERR_NULL;
   const fa::BwdWorkspace w = fa::bwd_workspace(B, Hq, Hkv, N, D);
@@ -308,6 +328,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.bias_sb = op.bias_stride_b;
   a.bias_sh = op.bias_stride_h;
   a.dbias = op.dbias;
+  a.Nkv = op.kv_rows;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -318,6 +339,7 @@ static int bwd_16(const void* q, const void* k, const void* v, const void* dO, c
                   const fa_options& op, void* stream) {
   int rc = check_opts(op, causal, Hq, N, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
+  if (rc == FA_OK) rc = check_kv_rows(op, B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;
   if (!workspace || !dq) return FA_ERR_NULL;
   if (workspace_bytes < fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)) return FA_ERR_WORKSPACE;

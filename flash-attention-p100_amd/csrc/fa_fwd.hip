@@ -219,7 +219,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          float alibi_raw, const uint32_t* __restrict__ mbase,
                                          const uint32_t* __restrict__ zbase, float o_scale,
                                          const float* __restrict__ bbase, float bias_raw,
-                                         int W32, int sq, int sk, int dr,
+                                         int W32, int sq, int sk, int dr, int kofs,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml, half_t* qt) {
@@ -251,8 +251,10 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   w.m_raw = -INFINITY;
   w.l = 0.f;
 
-  // Keys [0, Nk) exist for this batch entry (Nk = N unless key lengths are
-  // given); later keys are masked like keys past a ragged N. Without causal
+  // Keys [0, Nk) exist for this batch entry (Nk = the key rows unless key
+  // lengths are given); later keys are masked like keys past a ragged N.
+  // kofs = key rows - query rows: causal masking aligns the last query row
+  // with the last key row, so row i's diagonal key is i + kofs. Without causal
   // masking, packed sequences also end each row's keys at row_hi(i) =
   // min(Nk, sen[i]) (at least i + 1), which does not decrease with i.
   const bool packed_nc = BOUNDS && !CAUSAL && sen != nullptr;
@@ -260,8 +262,10 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     i = min(i, N - 1);
     return packed_nc ? min(Nk, max(sen[i], i + 1)) : Nk;
   };
-  const int kv_end = CAUSAL ? min(Nk, q0 + kBR) : row_hi(q0 + kBR - 1);
-  const int n_it = (kv_end + kKV - 1) / kKV;
+  const int kv_end = CAUSAL ? min(Nk, q0 + kBR + kofs) : row_hi(q0 + kBR - 1);
+  // (at least one step: a tile whose rows all lie above the first key, when
+  // there are more query rows than key rows, masks every key)
+  const int n_it = max(1, (kv_end + kKV - 1) / kKV);
   // Leading steps in which this wave's 32x32 block needs no mask. The later
   // ones run masked; blocks wholly past the diagonal or past N give exact
   // zeros there (their few products are not skipped, so every wave issues its
@@ -278,7 +282,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const bool narrowed = BOUNDS && (Wb > 0 || sst != nullptr);
   auto lower = [&](int i) {
     i = min(i, N - 1);
-    int lo = Wb > 0 ? i - Wb + 1 : 0;
+    int lo = Wb > 0 ? i + kofs - Wb + 1 : 0;
     if (sst) lo = max(lo, min(sst[i], i));
     return max(lo, 0);
   };
@@ -287,7 +291,10 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   const int n_head = win_last >= 0 ? max(j_lo, win_last / kKV + 1) : j_lo;
   const int w_lo = narrowed ? lower(i_row) - 1 : INT_MIN;
   int n_full = n_it;
-  if (CAUSAL) n_full = min(n_full, i_base - 31 - kq * 32 >= 0 ? (i_base - 31 - kq * 32) / kKV + 1 : 0);
+  if (CAUSAL) {
+    const int e = i_base + kofs - 31 - kq * 32;  // the wave's blocks stay unmasked up to key e
+    n_full = min(n_full, e >= 0 ? e / kKV + 1 : 0);
+  }
   const int k_hi = row_hi(i_base);  // smallest key bound of this wave's rows
   if (BOUNDS) n_full = min(n_full, k_hi - 32 - kq * 32 >= 0 ? (k_hi - 32 - kq * 32) / kKV + 1 : 0);
   const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
@@ -398,7 +405,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     // (every lane takes the ballot: without a mask mw_now is all ones)
     const bool hidden = MASKB && __builtin_amdgcn_ballot_w64(mw_now != ~0u) != 0;
     w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32,
-                                j < n_head || j >= n_full || hidden, i_row,
+                                j < n_head || j >= n_full || hidden, i_row + kofs,
                                 lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv, [&] { return bload(j + 1); },
                                 BIAS ? bias_raw : 0.f, lane,
                                 roff, troff, c, thr_raw, issue);
@@ -511,7 +518,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
     const int* __restrict__ seg_start, const int* __restrict__ seg_end,
     const uint32_t* __restrict__ mask, int mask_heads, const uint32_t* __restrict__ drop,
     float drop_scale, const float* __restrict__ bias, long long bias_sb, long long bias_sh,
-    float bias_raw, int dr) {
+    float bias_raw, int dr, int NK) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -531,8 +538,8 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
   const size_t q_off = (size_t)(b * stq.b + hq * stq.h);
   const size_t kv_off = (size_t)(b * stk.b + hkv * stk.h);
   const float thr_raw = kRescaleLog2 / scale_log2;
-  // Per-entry key length (key padding), clamped to [1, N].
-  const int Nk = kv_len ? min(max(kv_len[b], 1), N) : N;
+  // Per-entry key length (key padding), clamped to [1, NK] (NK: key rows).
+  const int Nk = kv_len ? min(max(kv_len[b], 1), NK) : NK;
   // ALiBi slope of this query head in raw-score units (slope / scale).
   const float alibi_raw = alibi ? alibi[hq] * kLog2e / scale_log2 : 0.f;
   // This (b, head)'s mask plane (a plane shared by all heads when mask_heads == 1).
@@ -554,7 +561,7 @@ __global__ __launch_bounds__(kThreads) void fwd_kernel(
                                 seg_start ? seg_start + (size_t)b * N : nullptr,
                                 seg_end ? seg_end + (size_t)b * N : nullptr, alibi_raw, mbase,
                                 zbase, DROPB ? drop_scale : 1.f, bbase, bias_raw, W32, stq.n,
-                                stk.n, dr,
+                                stk.n, dr, NK - N,
                                 t ? second : first,
                                 scale_log2, thr_raw,
                                 kt0, vt0, kt1, vt1, ml, qt);
@@ -573,10 +580,12 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
-                     make_strides(a.layout, a.Hkv, a.N, a.D), a.kv_len, a.window, a.alibi,
+                     make_strides(a.layout, a.Hkv, key_rows(a.N, a.Nkv), a.D), a.kv_len,
+                     a.window, a.alibi,
                      a.seg_start, a.seg_end, a.mask, a.mask_heads, a.drop, a.drop_scale, a.bias,
                      a.bias_sb, a.bias_sh,
-                     a.bias ? 1.f / (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D)) : 0.f, a.D);
+                     a.bias ? 1.f / (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D)) : 0.f, a.D,
+                     key_rows(a.N, a.Nkv));
   return hipGetLastError();
 }
 
@@ -586,7 +595,8 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
   // instantiation (kKV is a multiple of kBR); a mask, dropout or a bias one
   // of its copies with those inputs compiled in (Feat).
   const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
-                      a.alibi != nullptr || a.seg_start != nullptr;
+                      a.alibi != nullptr || a.seg_start != nullptr ||
+                      key_rows(a.N, a.Nkv) != a.N;
   auto with = [&](auto feat) {
     constexpr int F = decltype(feat)::value;
     return a.causal ? launch_fwd_t<D, true, true, F, BF>(a)

@@ -61,7 +61,15 @@ struct FwdArgs {
   // elements; 0 broadcasts over that dimension).
   const float* bias = nullptr;
   long long bias_sb = 0, bias_sh = 0;
+  // Rows of k and v when they differ from q's N (0: N). Causal masking then
+  // aligns the last query row with the last key row: query i sees key j iff
+  // j <= i + Nkv - N, and windows and ALiBi distances count from that
+  // diagonal. Only without packed sequences, a mask, dropout or a bias.
+  int Nkv = 0;
 };
+
+// Key rows of a launch: Nkv, or N when Nkv is 0.
+inline int key_rows(int N, int Nkv) { return Nkv > 0 ? Nkv : N; }
 
 // Backward workspace, in this order (each part 256-byte aligned):
 //   dvec = rowsum(dO * O) and lse2 = LSE * log2(e), (B, Hq, N) fp32 each;
@@ -142,6 +150,7 @@ struct BwdArgs {
   // (B, Hq, N, N) fp32; written where a row meets a key, so the caller
   // zeroes it first. Null: not computed.
   float* dbias = nullptr;
+  int Nkv = 0;                     // as FwdArgs::Nkv (k, v, dk, dv rows)
 };
 
 hipError_t launch_fwd(const FwdArgs& a);
@@ -162,7 +171,8 @@ hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, 
 // work-items in 32-bit fields, and the kernels number their work items with
 // int, so a shape is launchable when these fit in 32 bits (checked by the C
 // ABI before any launch).
+// Nkv: rows of k and v (as FwdArgs::Nkv; 0 = N).
 unsigned long long fwd_launch_items(int B, int Hq, int N, int D);
-unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D);
+unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D, int Nkv = 0);
 
 }  // namespace fa

@@ -287,8 +287,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
               ") must be a multiple of key/value heads (", Hkv, ")");
   TORCH_CHECK(k.sizes() == v.sizes(), "k and v must match");
-  TORCH_CHECK(k.size(0) == B && k.size(1) == N && k.size(3) == D,
-              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(k.size(0) == B && k.size(1) > 0 && k.size(3) == D,
+              "k/v must be (B, Hkv, Nk, D) matching q's B and D");
   TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
               "q, k and v must be on the same device");
   TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type(),
@@ -296,9 +296,11 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  const fa_options op =
+  fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
                 mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+  // key rows that differ from the query rows: bottom-right-aligned causal
+  op.kv_rows = k.size(1) != N ? (int)k.size(1) : 0;
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -323,8 +325,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
-  TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == B && k.size(1) == N && k.size(3) == D,
-              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == B && k.size(1) > 0 && k.size(3) == D,
+              "k/v must be (B, Hkv, Nk, D) matching q's B and D");
   TORCH_CHECK(dO.sizes() == q.sizes() && o.sizes() == q.sizes(), "dO and o must match q");
   TORCH_CHECK(lse.scalar_type() == at::kFloat && lse.dim() == 3 && lse.size(0) == B &&
                   lse.size(1) == H && lse.size(2) == N,
@@ -337,9 +339,11 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  const fa_options op =
+  fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
                 mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+  // key rows that differ from the query rows: bottom-right-aligned causal
+  op.kv_rows = k.size(1) != N ? (int)k.size(1) : 0;
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,
@@ -377,16 +381,18 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
               ") must be a multiple of key/value heads (", Hkv, ")");
   TORCH_CHECK(k.sizes() == v.sizes(), "k and v must match");
-  TORCH_CHECK(k.size(0) == B && k.size(2) == N && k.size(3) == D,
-              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+  TORCH_CHECK(k.size(0) == B && k.size(2) > 0 && k.size(3) == D,
+              "k/v must be (B, Hkv, Nk, D) matching q's B and D");
   TORCH_CHECK(k.device() == q.device() && v.device() == q.device(),
               "q, k and v must be on the same device");
   c10::DeviceGuard guard(q.device());
   auto o = at::empty_like(q);
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
-  const fa_options op =
+  fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
                 mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+  // key rows that differ from the query rows: bottom-right-aligned causal
+  op.kv_rows = k.size(2) != N ? (int)k.size(2) : 0;
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), B, H, Hkv, N, D, causal ? 1 : 0, &op,
                      current_stream(q)),
@@ -418,9 +424,9 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   for (const at::Tensor* t : {&k, &v, &dO, &o})
     TORCH_CHECK(t->scalar_type() == q.scalar_type(), "q, k, v, dO and o must have one dtype");
   TORCH_CHECK(lse.scalar_type() == at::kFloat, "lse must be fp32");
-  TORCH_CHECK(k.sizes() == v.sizes() && k.dim() == 4 && k.size(0) == B && k.size(2) == N &&
+  TORCH_CHECK(k.sizes() == v.sizes() && k.dim() == 4 && k.size(0) == B && k.size(2) > 0 &&
                   k.size(3) == D,
-              "k/v must be (B, Hkv, N, D) matching q's B, N, D");
+              "k/v must be (B, Hkv, Nk, D) matching q's B and D");
   TORCH_CHECK(dO.sizes() == q.sizes() && o.sizes() == q.sizes(), "dO and o must match q");
   TORCH_CHECK(lse.dim() == 3 && lse.size(0) == B && lse.size(1) == H && lse.size(2) == N,
               "lse must be (B, H, N)");
@@ -430,9 +436,11 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto dv = at::empty_like(k);
   const size_t ws_bytes = fa_bwd_workspace_bytes(B, H, Hkv, N, D);
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
-  const fa_options op =
+  fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
                 mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+  // key rows that differ from the query rows: bottom-right-aligned causal
+  op.kv_rows = k.size(2) != N ? (int)k.size(2) : 0;
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
                      lse.data_ptr<float>(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                      ws.data_ptr(), ws_bytes, B, H, Hkv, N, D, causal ? 1 : 0, &op,

@@ -103,7 +103,7 @@ class _FlashAttnP100(torch.autograd.Function):
             return ob.transpose(1, 2)
         if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
                 or segs is not None or scale or mask is not None or drop is not None
-                or bias is not None):
+                or bias is not None or k.size(2) != q.size(2)):
             o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end,
                                      scale, bits, drop=z, drop_scale=z_scale, bias=ctx.bias)
         else:
@@ -140,7 +140,8 @@ class _FlashAttnP100(torch.autograd.Function):
         g = grad_o.contiguous()
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
                 or ctx.alibi is not None or ctx.segs is not None or ctx.scale
-                or ctx.mask is not None or ctx.drop is not None or ctx.bias is not None):
+                or ctx.mask is not None or ctx.drop is not None or ctx.bias is not None
+                or k.size(2) != q.size(2)):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
                                           ctx.alibi, seg_start, seg_end, ctx.scale, bits, bits_t,
                                           z, z_t, z_scale, ctx.bias, dbias)
@@ -168,6 +169,14 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
     and D a multiple of 8 up to 128 (the reference: 64 or 128). scale = 1/sqrt(D).
     Causal masking is top-left aligned (key j is hidden from query i when
     j > i).
+
+    k and v may also hold a different number of rows Nk than q's N (the
+    reference requires N == Nk): KV-cache decoding (N = 1) and chunked
+    prefill (N < Nk). Causal masking then aligns the last query row with the
+    last key row (key j is hidden from query i when j > i + Nk - N; with
+    N > Nk the first N - Nk rows see no key and get o = 0 and zero
+    gradients), and sliding windows and ALiBi count from that diagonal. Not
+    with segment_ids, attn_mask, dropout_p or attn_bias.
 
     Beyond the reference (which raises on anything but fp16 and on padding
     masks, README.md:72-75):
@@ -224,6 +233,11 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         gradient of the scaled scores, summed over the dimensions it
         shares) comes back in its own shape and dtype.
     """
+    if k.size(2) != q.size(2) and (segment_ids is not None or attn_mask is not None
+                                   or dropout_p or attn_bias is not None):
+        raise ValueError(
+            f"q has {q.size(2)} rows and k, v {k.size(2)}: segment_ids, attn_mask, dropout_p "
+            "and attn_bias need q_len == kv_len")
     window = 0
     if sliding_window is not None:
         window = int(sliding_window)

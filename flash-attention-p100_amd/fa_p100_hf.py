@@ -53,12 +53,17 @@ Attention dropout (a layer's `attention_dropout` in training), which the
 reference rejects (fa_p100_hf.py:83-85), runs in the kernels with keep bits
 drawn per call from torch's default generator (fa_p100.dropout_bits).
 
+KV-cache steps (q_len != kv_len: decoding one token, or a chunk of the
+prompt after cached ones), which the reference rejects (fa_p100_hf.py:100-105),
+run in the kernels with the causal diagonal aligned at the bottom right (the
+last query row against the last key), without a padding mask.
+
 Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): output_attentions,
 head_mask, attention sinks (s_aux) and logit soft-capping (softcap), which
 other models pass to the attention interface, a window on non-causal
-attention, a head_dim that is not a multiple of 8 up to 128, q_len != kv_len
-(KV-cache decoding). A scale other than 1/sqrt(D),
+attention, a head_dim that is not a multiple of 8 up to 128, a cached step
+with padding or a mask. A scale other than 1/sqrt(D),
 which the reference rejected, goes to the kernels.
 """
 import warnings
@@ -251,10 +256,11 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
     softmax_scale = None
     if scaling is not None and abs(scaling - head_dim ** -0.5) > 1e-6:
         softmax_scale = float(scaling)
-    if key.size(2) != query.size(2):
-        raise NotImplementedError(
-            f"fa_p100 needs q_len == kv_len (got q={query.size(2)}, kv={key.size(2)}); "
-            "incremental decoding with a KV cache is not supported.")
+    # q_len != kv_len: a KV cache (decoding, chunked prefill). The kernels
+    # align the causal diagonal at the bottom right, the last query row with
+    # the last key row, as the cached positions require (the reference
+    # raised, fa_p100_hf.py:100-105).
+    cached = key.size(2) != query.size(2)
 
     if is_causal is None:
         is_causal = getattr(module, "is_causal", True) and query.size(2) > 1
@@ -267,6 +273,11 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
         # A 4-D mask alone decides which keys each query sees (eager adds it
         # to the logits, sdpa passes it with is_causal=False).
         is_causal, sliding_window, kv_len, segs = mask[2], None, None, _NOT_PACKED
+    if cached and (mask is not None or kv_len is not None
+                   or (segs is not None and segs is not _NOT_PACKED)):
+        raise NotImplementedError(
+            f"fa_p100 serves q_len != kv_len (q={query.size(2)}, kv={key.size(2)}: a KV cache) "
+            "without padding, packing or an attention mask; run the cached steps unpadded.")
     if sliding_window is not None and (not is_causal or sliding_window <= 0):
         raise NotImplementedError(
             f"fa_p100 serves sliding windows on causal attention only; this layer asks for "
@@ -342,17 +353,23 @@ def _set_impl(config, name):
             _set_impl(child, name)
 
 
-def enable_fa_p100(model, full_precision=False):
+def enable_fa_p100(model, full_precision=False, use_cache=False):
     """Switch `model` onto the kernels and guard the paths they cannot serve.
 
     Mirrors fa_p100_hf.py:161-213: registers the implementation, points every
     config at it, records `full_precision` on every module, turns the KV cache
-    off, and wraps `model.forward` once so that use_cache=True raises and the
+    off (unless use_cache=True), and wraps `model.forward` once so that the
     attention mask, which transformers would drop before the attention
     interface, reaches the kernels: a right-padded mask as per-entry key
     lengths, a left-padded one (causal layers) as packed-sequence bounds, any
     other 2-D mask as a key bit mask, and a 4-D mask as a bit mask of its
     own, each prepared once per model call.
+
+    The reference raised on use_cache (its kernels needed q_len == kv_len);
+    here cached steps run with the causal diagonal aligned at the bottom
+    right, so a call may pass use_cache=True (and enable_fa_p100(model,
+    use_cache=True) leaves the model's cache setting alone). Cached steps take
+    no padding mask: a padded batch raises there.
     """
     register()
     _set_impl(model.config, _IMPL_NAME)
@@ -361,10 +378,12 @@ def enable_fa_p100(model, full_precision=False):
             _set_impl(mod.config, _IMPL_NAME)
         mod._fa_p100_full_precision = full_precision
 
-    # q_len must equal kv_len, so a cache could never be used.
-    model.config.use_cache = False
-    if getattr(model, "generation_config", None) is not None:
-        model.generation_config.use_cache = False
+    # As the reference: training needs no cache. Cached steps (q_len !=
+    # kv_len) are served when a caller asks for them.
+    if not use_cache:
+        model.config.use_cache = False
+        if getattr(model, "generation_config", None) is not None:
+            model.generation_config.use_cache = False
 
     if not getattr(model, "_fa_p100_guarded", False):
         inner = model.forward
@@ -391,13 +410,6 @@ def enable_fa_p100(model, full_precision=False):
                     kv_len = end  # keys past the run exist for no row
                     if bool((first > 0).any()):
                         left = first
-            # Rejected up front rather than at the first decode step, after a
-            # prefill that would have succeeded.
-            if use_cache:
-                raise NotImplementedError(
-                    "fa_p100 needs q_len == kv_len, so it cannot serve a KV cache; it "
-                    "is a training kernel. Set generation_config.use_cache = False for "
-                    "cache-free generation.")
             # Packed sequences: restarting position_ids (checked once per call)
             # when the model gets no mask, as transformers' mask creation does.
             # Left padding rides on the same bounds: the pads form a sequence

@@ -58,8 +58,10 @@ enum {
   FA_ERR_MASK = 10014,       /* mask_heads not 1 or Hq, or a backward mask without mask_t */
   FA_ERR_DROPOUT = 10015,    /* dropout p not in [0, 1), a scale not positive and finite, or
                                 a backward with drop but without drop_t */
-  FA_ERR_BIAS = 10016        /* a negative bias stride, dbias without bias, or a bias with
+  FA_ERR_BIAS = 10016,       /* a negative bias stride, dbias without bias, or a bias with
                                 N > 2^22 */
+  FA_ERR_KV_ROWS = 10017     /* kv_rows < 0, or kv_rows != N together with packed sequences,
+                                a mask, dropout or a bias */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -231,7 +233,18 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *     dense). The backward writes the bias's gradient, dS of the scaled
  *     logits, to dbias when it is not NULL: dense (B, Hq, N, N) fp32, only
  *     where a query row meets a key it may attend (the caller zeroes dbias
- *     first; reduce over shared dimensions afterwards).
+ *     first; reduce over shared dimensions afterwards);
+ *   - kv_rows: 0, or the number of key/value rows Nk when it differs from
+ *     the query rows (the N of the call): k, v, dk, dv are then
+ *     (B, Hkv, Nk, D) (or (B, Nk, Hkv, D)), q, o, dO, dq, lse keep N rows.
+ *     Causal masking aligns the last query row with the last key row
+ *     (bottom-right): query i sees key j iff j <= i + Nk - N, as in KV-cache
+ *     decoding (N = 1) and chunked prefill (N < Nk); with N > Nk the first
+ *     N - Nk rows see no key (o = 0, lse = +inf, zero gradients). Windows
+ *     and ALiBi distances count from that diagonal, key lengths clamp to
+ *     [1, Nk]. Not with packed sequences, a mask, dropout or a bias
+ *     (FA_ERR_KV_ROWS); the backward workspace is the one for N rows.
+ *     The reference requires q_len == kv_len (fa_p100_hf.py:100-105).
  */
 typedef struct fa_options {
   int dtype;
@@ -252,6 +265,7 @@ typedef struct fa_options {
   long long bias_stride_b;
   long long bias_stride_h;
   float* dbias;
+  int kv_rows;
 } fa_options;
 
 /*

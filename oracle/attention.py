@@ -82,26 +82,36 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
     attn_mask. With `bias` (a float array broadcastable to (B, Hq, N, N),
     another extension) it is added to the scaled logits before the masks, as
     SDPA reads a float attn_mask.
+
+    K may hold nk rows where Q holds n (another extension: the reference
+    needs q_len == kv_len, fa_p100_hf.py:100-105). The causal diagonal is
+    then bottom-right aligned, key col is masked for row when
+    col > row + nk - n, and the window and ALiBi distances count from that
+    diagonal (row + nk - n against col); key lengths clamp to [1, nk].
+    Segments, masks and biases need nk == n.
     """
     d = q.shape[-1]
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     s = np.matmul(q.astype(dtype), np.swapaxes(k.astype(dtype), -1, -2)) * dtype(scale)
-    n = q.shape[-2]
+    n, nk = q.shape[-2], k.shape[-2]
+    kofs = nk - n
+    if kofs and (segments is not None or mask is not None or bias is not None):
+        raise ValueError("segments, masks and biases need as many key rows as query rows")
     if alibi is not None:
         slopes = np.asarray(alibi, dtype=np.float64).reshape(-1)
         if slopes.size != q.shape[1]:
             raise ValueError("alibi needs one slope per query head")
-        dist = np.abs(np.arange(n)[:, None] - np.arange(n)[None, :]).astype(np.float64)
+        dist = np.abs(np.arange(n)[:, None] + kofs - np.arange(nk)[None, :]).astype(np.float64)
         s = (s - (slopes[:, None, None] * dist[None]).astype(dtype)[None]).astype(dtype)
     if bias is not None:
         s = (s + np.broadcast_to(np.asarray(bias, dtype=np.float64), s.shape)).astype(dtype)
     if causal:
-        above = np.triu(np.ones((n, n), dtype=bool), 1)
+        above = np.triu(np.ones((n, nk), dtype=bool), 1 + kofs)
         s = np.where(above, -np.inf, s).astype(dtype)
     if window is not None:
         if not causal:
             raise ValueError("a sliding window needs causal masking")
-        outside = np.tril(np.ones((n, n), dtype=bool), -int(window))
+        outside = np.tril(np.ones((n, nk), dtype=bool), kofs - int(window))
         s = np.where(outside, -np.inf, s).astype(dtype)
     if segments is not None:
         seg = np.asarray(segments).reshape(q.shape[0], n)
@@ -110,8 +120,8 @@ def _scores(q, k, causal, dtype, kv_len=None, window=None, alibi=None, segments=
         other = run[:, :, None] != run[:, None, :]  # (B, N, N): different sequences
         s = np.where(other[:, None], -np.inf, s).astype(dtype)
     if kv_len is not None:
-        lens = np.clip(np.asarray(kv_len).reshape(-1), 1, n)
-        cols = np.arange(n)[None, :] >= lens[:, None]  # (B, N) masked key columns
+        lens = np.clip(np.asarray(kv_len).reshape(-1), 1, nk)
+        cols = np.arange(nk)[None, :] >= lens[:, None]  # (B, Nk) masked key columns
         s = np.where(cols[:, None, None, :], -np.inf, s).astype(dtype)
     if mask is not None:
         m = np.broadcast_to(np.asarray(mask, dtype=bool), s.shape)

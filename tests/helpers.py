@@ -87,13 +87,14 @@ class FaOptions(ctypes.Structure):
                 ("mask_heads", ctypes.c_int), ("drop", ctypes.c_void_p),
                 ("drop_t", ctypes.c_void_p), ("drop_scale", ctypes.c_float),
                 ("bias", ctypes.c_void_p), ("bias_stride_b", ctypes.c_longlong),
-                ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p)]
+                ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p),
+                ("kv_rows", ctypes.c_int)]
 
 
 def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_start=None,
             seg_end=None, scale=0.0, mask=None, mask_t=None, mask_heads=0, drop=None,
             drop_t=None, drop_scale=0.0, bias=None, bias_stride_b=0, bias_stride_h=0,
-            dbias=None):
+            dbias=None, kv_rows=0):
     """A pointer to an FaOptions; the array fields are device addresses (ints)
     or tensors."""
     def addr(x):
@@ -101,7 +102,7 @@ def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_sta
     o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes), addr(seg_start),
                   addr(seg_end), scale, addr(mask), addr(mask_t), mask_heads, addr(drop),
                   addr(drop_t), drop_scale, addr(bias), bias_stride_b, bias_stride_h,
-                  addr(dbias))
+                  addr(dbias), kv_rows)
     return ctypes.pointer(o)
 
 

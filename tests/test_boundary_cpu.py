@@ -131,6 +131,19 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_pack_mask(one, 1, 8, z, one, s) == 10005
     # BNHD puts every head of a row in one 32-bit buffer range
     assert lib.fa_fwd_ex(*([one] * 5), 1, 1 << 12, 1, 1 << 14, 128, 0, fa_opts(0, 1), s) == 10007
+    # kv_rows (key rows != query rows): negative, or combined with packed
+    # sequences, a mask, dropout or a bias, is refused; too many rows too.
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(kv_rows=-1), s) == 10017
+    for bad in (fa_opts(kv_rows=9, seg_start=1, seg_end=1),
+                fa_opts(kv_rows=9, mask=1, mask_t=1, mask_heads=1),
+                fa_opts(kv_rows=9, drop=1, drop_t=1, drop_scale=1.0),
+                fa_opts(kv_rows=9, bias=1)):
+        assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, bad, s) == 10017
+    assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, fa_opts(kv_rows=1 << 26), s) == 10007
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 1, fa_opts(kv_rows=9), s) == 10005
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 1, fa_opts(kv_rows=8, mask=1,
+                                                                    mask_heads=1), s) == 10005
+    assert b"kv_rows" in lib.fa_error_string(10017)
     assert b"layout" in lib.fa_error_string(10008)
     assert b"format" in lib.fa_error_string(10009)
     assert b"window" in lib.fa_error_string(10010)

@@ -55,9 +55,16 @@ def test_head_dim_scale_and_kv_len_guards():
     # binding's device check); the reference raised here.
     with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         hf.fa_p100_attention_forward(MOD, q, k, v, None, scaling=0.1)
+    # q_len != kv_len (a KV cache) passes to the kernels now (the reference
+    # raised); host tensors stop at the binding's device check. A cached step
+    # with a padding bound raises.
     q, k, v = qkv(n=1, kv_len=9)
-    with pytest.raises(NotImplementedError, match="q_len == kv_len"):
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         hf.fa_p100_attention_forward(MOD, q, k, v, None)
+    with pytest.raises(NotImplementedError, match="KV cache"):
+        hf.fa_p100_attention_forward(MOD, q, k, v, None,
+                                     fa_p100_bounds=(torch.tensor([5], dtype=torch.int32),
+                                                     hf._NOT_PACKED, None))
 
 
 def test_valid_call_reaches_the_kernel_and_casts_with_one_warning():
@@ -92,6 +99,10 @@ def test_register_and_enable():
     assert model.config._attn_implementation == "fa_p100"
     assert model.config.use_cache is False
     assert all(getattr(m, "_fa_p100_full_precision") is True for m in model.modules())
+    other = _tiny_qwen3()
+    other.config.use_cache = True
+    hf.enable_fa_p100(other, use_cache=True)  # leaves the cache setting alone
+    assert other.config.use_cache is True
     inner = model.forward
     hf.enable_fa_p100(model)          # idempotent: the guard wraps once
     assert model.forward is inner
@@ -118,7 +129,9 @@ def test_register_and_enable():
         [0, 0, 1, 1, 1, 1], [1, 1, 1, 1, 1, 1], [0, 1, 1, 1, 1, 1]]
     with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         model(ids, attention_mask=torch.tensor([[1, 1, 1, 1, 0, 0]]))
-    with pytest.raises(NotImplementedError, match="KV cache"):
+    # A cached call is served (the reference raised on use_cache); host
+    # tensors then stop at the binding's device check.
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
         model(ids, use_cache=True)
     # An all-ones mask passes the guard; the attention hook then receives no
     # mask (transformers' early exit) and the call reaches the binding, whose

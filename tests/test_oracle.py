@@ -712,3 +712,99 @@ def test_bias_pins(causal):
         assert abs(fd - ds[idx]) < 1e-6 * max(1.0, abs(fd))
     assert not np.allclose(ora.attention_fwd(q, k, v, causal, bias=np.swapaxes(bias, -1, -2))[0],
                            ora.attention_fwd(q, k, v, causal, bias=bias)[0], atol=1e-6)
+
+
+def _fd_kv(rng, q, k, v, do, grads, loss_kw, probes=4, tol=1e-6):
+    h = 1e-4
+    for which, g in enumerate(grads):
+        for _ in range(probes):
+            base = [q, k, v]
+            idx = int(rng.integers(base[which].size))
+            plus = [t.copy() for t in base]
+            minus = [t.copy() for t in base]
+            plus[which].flat[idx] += h
+            minus[which].flat[idx] -= h
+            fd = (ora.attention_loss(*plus, do, **loss_kw)
+                  - ora.attention_loss(*minus, do, **loss_kw)) / (2 * h)
+            assert abs(fd - g.flat[idx]) < tol * max(1.0, abs(fd)), (which, fd, g.flat[idx])
+
+
+@pytest.mark.parametrize("n,nk", [(1, 37), (5, 37), (19, 40), (37, 37), (40, 19), (3, 1)])
+def test_kv_rows_pins(n, nk):
+    """K/V with nk rows where Q has n (an extension; the reference needs
+    q_len == kv_len): causal masking is aligned at the bottom right, as torch
+    defines it in torch.nn.attention.bias.causal_lower_right (an independent
+    library definition), dense attention ignores the row counts; finite
+    differences pin the backward; rows above the first key (n > nk) see
+    nothing and get O = 0, LSE = +inf and zero gradients; decoding one row
+    is dense attention of that row; a chunk of the last n rows equals those
+    rows of the square causal attention over all nk rows, and so do its dK,
+    dV when the earlier rows carry no output gradient."""
+    from torch.nn.attention.bias import causal_lower_right
+    rng = np.random.default_rng(100 * n + nk)
+    b, hq, hkv, d = 2, 4, 2, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, nk, d), rnd(rng, b, hkv, nk, d)
+    for causal in (False, True):
+        o, lse = ora.attention_fwd(q, k, v, causal)
+        grads = ora.attention_bwd(q, k, v, do, causal)
+        tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+        ke = tk.repeat_interleave(hq // hkv, dim=1)
+        ve = tv.repeat_interleave(hq // hkv, dim=1)
+        if causal:
+            seen = (np.arange(nk)[None, :] <= np.arange(n)[:, None] + nk - n).any(axis=1)
+            mask = causal_lower_right(n, nk)
+        else:
+            seen, mask = np.ones(n, dtype=bool), None
+        to = F.scaled_dot_product_attention(tq, ke, ve, attn_mask=mask)
+        (to[:, :, torch.tensor(seen)] * torch.tensor(do)[:, :, torch.tensor(seen)]).sum().backward()
+        assert np.allclose(o[:, :, seen], to.detach().numpy()[:, :, seen], atol=1e-12)
+        assert not np.any(o[:, :, ~seen]) and np.all(lse[:, :, ~seen] == np.inf)
+        assert not np.any(grads[0][:, :, ~seen])
+        for mine, theirs in zip(grads, (tq.grad, tk.grad, tv.grad)):
+            assert np.allclose(mine, theirs.numpy(), atol=1e-11, rtol=1e-9)
+        _fd_kv(rng, q, k, v, do, grads, {"causal": causal})
+    if n == 1:  # the one row sees every key
+        assert np.allclose(ora.attention_fwd(q, k, v, True)[0], ora.attention_fwd(q, k, v, False)[0],
+                           atol=1e-14)
+    if n <= nk:
+        qf = rnd(rng, b, hq, nk, d)
+        qf[:, :, nk - n:] = q
+        dof = np.zeros((b, hq, nk, d))
+        dof[:, :, nk - n:] = do
+        of, _ = ora.attention_fwd(qf, k, v, True)
+        assert np.allclose(ora.attention_fwd(q, k, v, True)[0], of[:, :, nk - n:], atol=1e-13)
+        _, dkf, dvf = ora.attention_bwd(qf, k, v, dof, True)
+        _, dk, dv = ora.attention_bwd(q, k, v, do, True)
+        assert np.allclose(dk, dkf, atol=1e-12) and np.allclose(dv, dvf, atol=1e-12)
+
+
+@pytest.mark.parametrize("window", [1, 4, 9])
+def test_kv_rows_with_window_alibi_and_key_lengths(window):
+    """With nk != n the window and ALiBi count from the bottom-right diagonal
+    (row i's diagonal key is i + nk - n) and key lengths clamp to [1, nk]:
+    pinned against SDPA with the explicit band and bias built from that
+    diagonal, and by finite differences."""
+    rng = np.random.default_rng(window)
+    b, hq, hkv, n, nk, d = 2, 2, 1, 6, 17, 16
+    q, do = rnd(rng, b, hq, n, d), rnd(rng, b, hq, n, d)
+    k, v = rnd(rng, b, hkv, nk, d), rnd(rng, b, hkv, nk, d)
+    lens, slopes = np.array([nk, 13]), alibi_slopes(hq)
+    kw = dict(causal=True, kv_len=lens, window=window, alibi=slopes)
+    o, _ = ora.attention_fwd(q, k, v, **kw)
+    grads = ora.attention_bwd(q, k, v, do, **kw)
+    i, j = np.arange(n)[:, None] + nk - n, np.arange(nk)[None, :]
+    for e, L in enumerate(lens):
+        band = (j <= i) & (j > i - window) & (j < L)
+        bias = -slopes[:, None, None] * np.abs(i - j)[None]
+        allowed = np.where(band[None], bias, -np.inf)
+        ke = torch.tensor(np.repeat(k[e:e + 1], hq // hkv, axis=1))
+        ve = torch.tensor(np.repeat(v[e:e + 1], hq // hkv, axis=1))
+        ref = F.scaled_dot_product_attention(torch.tensor(q[e:e + 1]), ke, ve,
+                                             attn_mask=torch.tensor(allowed)[None]).numpy()
+        seen = band.any(axis=1)
+        assert np.allclose(o[e][:, seen], ref[0][:, seen], atol=1e-12)
+        assert not np.any(o[e][:, ~seen])
+    _fd_kv(rng, q, k, v, do, grads, kw)
+    with pytest.raises(ValueError):
+        ora.attention_fwd(q, k, v, True, segments=np.zeros((b, n), dtype=np.int64))
