@@ -60,11 +60,25 @@
 namespace fa {
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 128;  // rows a workgroup owns (keys in phase 1, queries in phase 2)
-constexpr int kSub = 64;    // rows per streamed tile (queries in 1, keys in 2)
 static_assert(kTile == kBwdTile, "workspace layout assumes this key tile");
+// Waves per workgroup and rows per streamed tile (queries in phase 1, keys in
+// phase 2) at tile width D. Four row blocks of 32 rows cover kTile; up to
+// width 128 two waves share each row block, one per 32-row half of a 64-row
+// streamed tile (two waves per SIMD). At width 256 one wave's dK^T and dV^T
+// accumulators alone take 256 registers, so each row block has one wave (512
+// registers per lane at one wave per SIMD), the streamed tiles have 32 rows
+// and the K operands come straight from global memory into registers (a
+// resident K tile would not fit in LDS beside V and the staged tiles).
+template <int D>
+struct BwdShape {
+  static constexpr int kWaves = D > 128 ? 4 : 8;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kHalves = kWaves / 4;  // waves per row block
+  static constexpr int kSub = 32 * kHalves;
+  static constexpr bool kKGlobal = D > 128;   // K operands loaded from global memory
+};
+constexpr int kVecStride = 64;  // floats per staged lse2 / dvec run (>= every kSub)
 // Causal split of key tile u (see bwd_kernel): floor((group * (n_tiles-1-2u) *
 // kSplitNum - kSplitBias) / 256) of its phase-1 iterations move to workgroup
 // n_tiles-1-u. Phase-1 steps cost more than phase-2 steps, so the iterations
@@ -85,18 +99,22 @@ constexpr int kSplitBias = 5;
 // next step's direct loads are filling and does not wait for those loads.
 template <int D>
 struct BwdLds {
-  static constexpr int kTileHalves = Stream<D>::template bytes<kSub>() / 2;  // staged tile
-  static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();  // resident K or V
-  // Partial-sum exchange regions (they reuse the tiles once a phase's loop is
-  // done): D/32 accumulators x 16 floats per lane for one wave.
+  using Sh = BwdShape<D>;
+  static constexpr int kTileHalves = Stream<D>::template bytes<Sh::kSub>() / 2;  // staged tile
+  static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();  // resident V
+  static constexpr int kKTileHalves = Sh::kKGlobal ? 512 : kKVTileHalves;  // resident K
+  // Partial-sum exchange regions between the two waves of a row block (they
+  // reuse the tiles once a phase's loop is done): D/32 accumulators x 16
+  // floats per lane for one wave.
   static constexpr int kRegionBytes = (D / 32) * 16 * 64 * 4;
-  static_assert(kRegionBytes <= kTileHalves * 2 && 2 * kRegionBytes <= kKVTileHalves * 2,
+  static_assert(Sh::kHalves == 1 ||
+                    (kRegionBytes <= kTileHalves * 2 && 2 * kRegionBytes <= kKTileHalves * 2),
                 "exchange regions exceed the tiles");
 };
 
 // Lanes per row of the preprocess: D/8 rounded up to a power of two (the
 // row sum is a butterfly over them; lanes past D/8 add zeros).
-constexpr int pre_lanes_per_row(int D) { return D / 8 <= 8 ? 8 : 16; }
+constexpr int pre_lanes_per_row(int D) { return D / 8 <= 8 ? 8 : D / 8 <= 16 ? 16 : 32; }
 
 // ---------------------------------------------------------------------------
 // Preprocess: dvec[row] = sum_d float(O[row,d]) * float(dO[row,d]) from the
@@ -423,7 +441,7 @@ struct QWave {
 // ---------------------------------------------------------------------------
 // FEAT: the optional per-score inputs compiled in (Feat, with BOUNDS).
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
-__global__ __launch_bounds__(kThreads) void bwd_kernel(
+__global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
     const float* __restrict__ Lse2, const float* __restrict__ Dvec,
@@ -439,6 +457,9 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     long long bias_sb, long long bias_sh, float bias_raw, float* __restrict__ dbias, int dr,
     int NK) {
   using L = BwdLds<D>;
+  constexpr int kWaves = BwdShape<D>::kWaves, kHalves = BwdShape<D>::kHalves;
+  constexpr int kSub = BwdShape<D>::kSub;
+  constexpr bool KG = BwdShape<D>::kKGlobal;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
   // The larger alignment makes the compiler place the four staged tiles first,
@@ -446,8 +467,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   // ds_read; each read is then one per-lane offset register plus a constant.
   __shared__ __align__(1024) half_t ta0[L::kTileHalves], tb0[L::kTileHalves];
   __shared__ __align__(1024) half_t ta1[L::kTileHalves], tb1[L::kTileHalves];
-  __shared__ __align__(16) float vec0[2 * kSub], vec1[2 * kSub];
-  __shared__ __align__(16) half_t kres[L::kKVTileHalves], vres[L::kKVTileHalves];
+  __shared__ __align__(16) float vec0[2 * kVecStride], vec1[2 * kVecStride];
+  __shared__ __align__(16) half_t kres[L::kKTileHalves], vres[L::kKVTileHalves];
   __shared__ unsigned xflag;  // a split tile's counter, as one thread read it
 
   const int tid = threadIdx.x;
@@ -455,7 +476,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
   __builtin_assume(wave >= 0 && wave < kWaves);
   const int w4 = wave & 3;     // row block (keys in phase 1, queries in phase 2)
-  const int half = wave >> 2;  // which 32-row half of each streamed tile
+  const int half = wave >> 2;  // which 32-row half of each streamed tile (0 with one wave)
   const int h = lane >> 5;
   const int l32 = lane & 31;
 
@@ -532,13 +553,13 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   typename Stream<D>::Offsets so;          // staged tiles, rows 32*half ..
   so.init(lane, 32 * half);
 
-  StreamPlan<D, kSub, kWaves> plan_q, plan_k;  // staged 64-row tiles of Q/dO (phase 1), K/V (2)
+  StreamPlan<D, kSub, kWaves> plan_q, plan_k;  // staged tiles of Q/dO (phase 1), K/V (2)
   plan_q.init(wave, lane, stq.n, dr);
   plan_k.init(wave, lane, stk.n, dr);
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
-  // 16 KB-class exchange regions: the four staged tiles, then the halves of
-  // the resident ones.
+  // 16 KB-class exchange regions (two waves per row block only): the four
+  // staged tiles, then the halves of the resident ones.
   auto region = [&](int i) -> float* {
     half_t* t = i == 0 ? ta0 : i == 1 ? tb0 : i == 2 ? ta1 : i == 3 ? tb1
               : i == 4 ? kres : i == 5 ? kres + L::kKVTileHalves / 2
@@ -565,6 +586,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
   };
   auto n_iters = [&](int u) { return group * ((q_end(u) - q_start(u) + kSub - 1) / kSub); };
   auto split = [&](int u) {
+    // (not at width 256: a second inlined copy of phase 1 spilled registers)
+    if constexpr (KG) return 0;
     const int m = n_tiles - 1 - 2 * u;
     // windows leave the tiles' work equal; with kofs != 0 the key and query
     // tiles do not pair up
@@ -587,15 +610,21 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     const int it_begin = helping ? n_it - x_help : 0;
     const int it_end = helping ? n_it : n_it - x_own;
     const bool shared = helping || x_own > 0;
-    KVWave<D, CAUSAL, BOUNDS, BF, FEAT == 0> w;
+    KVWave<D, CAUSAL, BOUNDS, BF, FEAT == 0 || KG> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
       plan_kv.init(wave, lane, stk.n, dr);
 #pragma unroll
       for (int u = 0; u < decltype(plan_kv)::TL::kParts; ++u) {
-        plan_kv.part(kres, rk, tp0, wave, u);
+        if constexpr (!KG) plan_kv.part(kres, rk, tp0, wave, u);
         plan_kv.part(vres, rv, tp0, wave, u);
       }
+    }
+    if constexpr (KG) {  // this lane's K row j_col (keys past NK: zeros, all masked)
+      const half_t* krow = K + kv_off + (size_t)min(j_col, NK - 1) * stk.n + h * 8;
+#pragma unroll
+      for (int kk = 0; kk < D / 16; ++kk)
+        w.kb[kk] = as_half8(load16(krow + kk * 16, j_col < NK && kk * 16 + h * 8 < dr));
     }
 #pragma unroll
     for (int k = 0; k < 2 * (D / 32); ++k) w.acc[k] = zero16();
@@ -622,7 +651,8 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
         plan_q.part(to, ro, i0, wave, u);
       }
       if (wave == 0) vec_load64(tv, make_rsrc(Lse2 + bhq * N, (uint32_t)N * 4), i0, lane);
-      if (wave == 1) vec_load64(tv + kSub, make_rsrc(Dvec + bhq * N, (uint32_t)N * 4), i0, lane);
+      if (wave == 1)
+        vec_load64(tv + kVecStride, make_rsrc(Dvec + bhq * N, (uint32_t)N * 4), i0, lane);
     };
     // Bias values of step `it` for this lane's key and its 16 query rows,
     // through a resource over the wave's 32 rows (rows past N read zeros, a
@@ -665,7 +695,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       // the softmax until the whole next stage had landed.
       fetch(it + 1, P ? ta0 : ta1, P ? tb0 : tb1, P ? vec0 : vec1);
       // (j_col - kofs: the ALiBi distance counts from the aligned diagonal)
-      w.step(Qs, Os, lse2s, lse2s + kSub, vres, kres, half, w4 * 32, i0, j_col - kofs, row_lo,
+      w.step(Qs, Os, lse2s, lse2s + kVecStride, vres, kres, half, w4 * 32, i0, j_col - kofs, row_lo,
              row_end,
              alibi_raw, mtw, ztw, zs, bv1, [&] { return bload1(min(it + 1, it_end - 1)); },
              braw, lane, roff, so, scale_log2);
@@ -676,7 +706,7 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
     fetch(it_begin, ta0, tb0, vec0);
     wait_vmem();
     __syncthreads();
-    if constexpr (FEAT == 0) {
+    if constexpr (FEAT == 0 && !KG) {
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) w.kb[kk] = tile_read16<D>(kres, w4 * 32, kk, roff);
     }
@@ -689,14 +719,16 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
 
     // Sum the two halves' partials (dV^T in region 2*w4, dK^T in region
     // 2*w4 + 1) into the waves of the lower half.
-    if (half) {
-      partial_store<D / 32>(region(2 * w4), w.acc, 0, lane);
-      partial_store<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
-    }
-    __syncthreads();
-    if (!half) {
-      partial_add<D / 32>(region(2 * w4), w.acc, 0, lane);
-      partial_add<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
+    if constexpr (kHalves == 2) {
+      if (half) {
+        partial_store<D / 32>(region(2 * w4), w.acc, 0, lane);
+        partial_store<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
+      }
+      __syncthreads();
+      if (!half) {
+        partial_add<D / 32>(region(2 * w4), w.acc, 0, lane);
+        partial_add<D / 32>(region(2 * w4 + 1), w.acc, D / 32, lane);
+      }
     }
     bool finish = true;
     if (shared) {
@@ -889,10 +921,12 @@ __global__ __launch_bounds__(kThreads) void bwd_kernel(
       }
       if (t < n_kt) step(t, P0{});
 
-      if (half) partial_store<D / 32>(region(4 + w4), w.acc, 0, lane);
-      __syncthreads();
+      if constexpr (kHalves == 2) {
+        if (half) partial_store<D / 32>(region(4 + w4), w.acc, 0, lane);
+        __syncthreads();
+      }
       if (!half && row_ok) {
-        partial_add<D / 32>(region(4 + w4), w.acc, 0, lane);
+        if constexpr (kHalves == 2) partial_add<D / 32>(region(4 + w4), w.acc, 0, lane);
         const size_t row_off = q_off(hq) + (size_t)i_row * stq.n;
         if (dQh) {  // fp16 dQ: the fp32 result rounded to nearest even, as .to(fp16)
 #pragma unroll
@@ -939,16 +973,17 @@ hipError_t launch_main_t(const BwdArgs& a) {
   const int NK = key_rows(a.N, a.Nkv);
   const int n_tiles = (max(a.N, NK) + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
+  using Sh = BwdShape<D>;
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D);
-  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((bwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid, dim3(Sh::kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (const half_t*)a.dO, a.lse2, a.dvec, a.dq,
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, a.D),
                      make_strides(a.layout, a.Hkv, NK, a.D), a.counters, a.slots,
-                     a.slots ? kSplitNum : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
+                     a.slots ? kSplitNum * 64 / Sh::kSub : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
                      a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.drop,
                      a.drop_t, a.drop_scale, a.bias, a.bias_sb, a.bias_sh,
                      a.bias ? 1.f / scale : 0.f, a.dbias, a.D, NK);
@@ -958,7 +993,7 @@ hipError_t launch_main_t(const BwdArgs& a) {
 template <int D, bool BF>
 hipError_t launch_main_d(const BwdArgs& a) {
   // Key lengths, windows, packed sequences and ALiBi need the masked
-  // instantiation (kTile is a multiple of kSub); a mask, dropout or a bias
+  // instantiation (kTile is a multiple of every kSub); a mask, dropout or a bias
   // one of its copies with those inputs compiled in (Feat).
   const bool bounds = (a.N % kTile) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr ||
@@ -972,7 +1007,9 @@ hipError_t launch_main_d(const BwdArgs& a) {
     case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
     case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
     case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});
-    case kFeatBias: return with(std::integral_constant<int, kFeatBias>{});
+    case kFeatBias:  // (no bias at width 256: the C ABI refuses it)
+      if constexpr (D > 128) return hipErrorInvalidValue;
+      else return with(std::integral_constant<int, kFeatBias>{});
     default: break;
   }
   if (a.causal)
@@ -991,7 +1028,8 @@ unsigned long long bwd_launch_items(int B, int Hq, int Hkv, int N, int D, int Nk
   const unsigned long long tiles =
       ((unsigned long long)(N > key_rows(N, Nkv) ? N : key_rows(N, Nkv)) + kTile - 1) / kTile;
   const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hkv;
-  const unsigned long long main = (wgs + kXcds - 1) / kXcds * kXcds * kThreads;
+  const unsigned long long threads = padded_head_dim(D) > 128 ? 256 : 512;  // BwdShape
+  const unsigned long long main = (wgs + kXcds - 1) / kXcds * kXcds * threads;
   return pre > main ? pre : main;
 }
 
@@ -999,18 +1037,22 @@ hipError_t launch_bwd_preprocess(const BwdArgs& a) {
   const int w = padded_head_dim(a.D);
   if (a.dtype == kBF16)
     return w == 32 ? launch_pre_d<32, true>(a) : w == 64 ? launch_pre_d<64, true>(a)
-         : w == 96 ? launch_pre_d<96, true>(a) : launch_pre_d<128, true>(a);
+         : w == 96 ? launch_pre_d<96, true>(a) : w == 128 ? launch_pre_d<128, true>(a)
+         : launch_pre_d<256, true>(a);
   return w == 32 ? launch_pre_d<32, false>(a) : w == 64 ? launch_pre_d<64, false>(a)
-       : w == 96 ? launch_pre_d<96, false>(a) : launch_pre_d<128, false>(a);
+       : w == 96 ? launch_pre_d<96, false>(a) : w == 128 ? launch_pre_d<128, false>(a)
+       : launch_pre_d<256, false>(a);
 }
 
 hipError_t launch_bwd_main(const BwdArgs& a) {
   const int w = padded_head_dim(a.D);
   if (a.dtype == kBF16)
     return w == 32 ? launch_main_d<32, true>(a) : w == 64 ? launch_main_d<64, true>(a)
-         : w == 96 ? launch_main_d<96, true>(a) : launch_main_d<128, true>(a);
+         : w == 96 ? launch_main_d<96, true>(a) : w == 128 ? launch_main_d<128, true>(a)
+         : launch_main_d<256, true>(a);
   return w == 32 ? launch_main_d<32, false>(a) : w == 64 ? launch_main_d<64, false>(a)
-       : w == 96 ? launch_main_d<96, false>(a) : launch_main_d<128, false>(a);
+       : w == 96 ? launch_main_d<96, false>(a) : w == 128 ? launch_main_d<128, false>(a)
+       : launch_main_d<256, false>(a);
 }
 
 }  // namespace fa

@@ -91,7 +91,7 @@ extern "C" {
 const char* fa_error_string(int err) {
   switch (err) {
     case FA_OK: return "success";
-    case FA_ERR_HEAD_DIM: return "head dim must be a multiple of 8 from 8 to 128";
+    case FA_ERR_HEAD_DIM: return "head dim must be a multiple of 8 from 8 to 256";
     case FA_ERR_SEQLEN: return "N must be positive";
     case FA_ERR_HEADS: return "query heads (H) must be a multiple of key/value heads (Hkv)";
     case FA_ERR_BATCH: return "B must be positive";
@@ -109,7 +109,9 @@ const char* fa_error_string(int err) {
     case FA_ERR_DROPOUT:
       return "dropout p must lie in [0, 1) and its scale be positive and finite; the backward "
              "needs drop_t with drop";
-    case FA_ERR_BIAS: return "bias strides must not be negative, dbias needs a bias, and a bias needs N <= 2^22";
+    case FA_ERR_BIAS:
+      return "bias strides must not be negative, dbias needs a bias, and a bias needs N <= 2^22 "
+             "and a head dim up to 128";
     case FA_ERR_KV_ROWS:
       return "kv_rows must be >= 0, and key rows that differ from the query rows do not combine "
              "with packed sequences, a mask, dropout or a bias";
@@ -135,7 +137,7 @@ constexpr fa_options kDefaultOpts = {fa::kFP16, fa::kBHND, nullptr, 0,       nul
 // (One N x N fp32 plane at this N is 64 TiB, so no real caller meets it.)
 static constexpr int kMaxBiasN = 1 << 22;
 
-static int check_opts(const fa_options& op, int causal, int Hq, int N, bool backward) {
+static int check_opts(const fa_options& op, int causal, int Hq, int N, int D, bool backward) {
   if (op.dtype != fa::kFP16 && op.dtype != fa::kBF16) return FA_ERR_DTYPE;
   if (op.layout != fa::kBHND && op.layout != fa::kBNHD) return FA_ERR_LAYOUT;
   if (op.window < 0 || (op.window > 0 && !causal)) return FA_ERR_WINDOW;
@@ -152,6 +154,8 @@ static int check_opts(const fa_options& op, int causal, int Hq, int N, bool back
   if (op.bias_stride_b < 0 || op.bias_stride_h < 0) return FA_ERR_BIAS;
   if (op.dbias != nullptr && op.bias == nullptr) return FA_ERR_BIAS;
   if (op.bias != nullptr && N > kMaxBiasN) return FA_ERR_BIAS;
+  // (the width-256 kernels have no registers left for the bias values)
+  if (op.bias != nullptr && fa::padded_head_dim(D) > 128) return FA_ERR_BIAS;
   if (op.kv_rows < 0) return FA_ERR_KV_ROWS;
   if (op.kv_rows > 0 && op.kv_rows != N &&
       (op.seg_start != nullptr || op.mask != nullptr || op.drop != nullptr || op.bias != nullptr))
@@ -177,7 +181,7 @@ static uint32_t dropout_threshold(float p) {
 
 static int fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int Hq,
                int Hkv, int N, int D, int causal, const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal, Hq, N, false);
+  int rc = check_opts(op, causal, Hq, N, D, false);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc == FA_OK) rc = check_kv_rows(op, B, Hq, Hkv, N, D);
@@ -280,7 +284,7 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
                     void* workspace, size_t workspace_bytes, float* dq, void* dq16,
                     void* dk, void* dv, int B, int Hq, int Hkv, int N, int D, int causal,
                     const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal, Hq, N, true);
+  int rc = check_opts(op, causal, Hq, N, D, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK && op.layout == fa::kBNHD) rc = check_bnhd(Hq, N, D);
   if (rc == FA_OK) rc = check_kv_rows(op, B, Hq, Hkv, N, D);
@@ -337,7 +341,7 @@ static int bwd_16(const void* q, const void* k, const void* v, const void* dO, c
                   const float* lse, void* dq, void* dk, void* dv, void* workspace,
                   size_t workspace_bytes, int B, int Hq, int Hkv, int N, int D, int causal,
                   const fa_options& op, void* stream) {
-  int rc = check_opts(op, causal, Hq, N, true);
+  int rc = check_opts(op, causal, Hq, N, D, true);
   if (rc == FA_OK) rc = check_shape(B, Hq, Hkv, N, D);
   if (rc == FA_OK) rc = check_kv_rows(op, B, Hq, Hkv, N, D);
   if (rc != FA_OK) return rc;

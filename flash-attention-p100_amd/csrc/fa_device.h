@@ -230,15 +230,21 @@ __device__ __forceinline__ rsrc_t bias_rows_rsrc(const float* plane, int row0, i
   return make_rsrc(plane + (size_t)min(row0, N) * N, (uint32_t)rows * (uint32_t)N * 4u);
 }
 // Each lane loads `size` bytes (4 or 16) from voff + soff into LDS at
-// lds + size * lane (lds wave-uniform).
+// lds + byte_off + size * lane (lds and byte_off wave-uniform). The offset is
+// added after the conversion to an LDS address: added to the generic
+// pointer, a constant offset makes the compiler fold a generic-to-LDS
+// conversion of a constant address, for which it emits an invalid
+// instruction.
 template <int size>
-__device__ __forceinline__ void lds_direct_buf(void* lds, rsrc_t r, uint32_t voff, uint32_t soff) {
+__device__ __forceinline__ void lds_direct_buf(void* lds, rsrc_t r, uint32_t voff, uint32_t soff,
+                                               uint32_t byte_off = 0) {
   static_assert(size == 4 || size == 16, "LDS direct loads of 4 or 16 bytes per lane");
+  auto* p = (__attribute__((address_space(3))) char*)lds + byte_off;
   if constexpr (size == 16)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)p, 16,
                                              voff, soff, 0, 0);
   else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 4,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)p, 4,
                                              voff, soff, 0, 0);
 }
 
@@ -333,8 +339,8 @@ struct SwzPlan {
   // halves, row_bytes apart) into `tile`; rows past the buffer's end read as
   // zeros.
   __device__ __forceinline__ void part(void* tile, rsrc_t r, int r0, int wave, int u) const {
-    lds_direct_buf<16>(reinterpret_cast<char*>(tile) + (u * NW + wave) * 1024, r, base,
-                       ((uint32_t)r0 + (uint32_t)(u * kPartRows)) * row_bytes);
+    lds_direct_buf<16>(tile, r, base, ((uint32_t)r0 + (uint32_t)(u * kPartRows)) * row_bytes,
+                       (uint32_t)(u * NW + wave) * 1024u);
   }
 };
 
@@ -426,7 +432,7 @@ struct TilePlan {
   __device__ __forceinline__ void part(half_t* tile, rsrc_t r, int r0, int wave, int u) const {
     const int inst = u * NW + wave;
     if (EVEN || TL::kInsts % NW == 0 || inst < TL::kInsts)
-      lds_direct_buf<16>(tile + inst * 512, r, off[u], (uint32_t)r0 * row_bytes);
+      lds_direct_buf<16>(tile, r, off[u], (uint32_t)r0 * row_bytes, (uint32_t)inst * 1024u);
   }
 };
 

@@ -50,19 +50,30 @@
 namespace fa {
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kBR = 64;    // query rows per tile (2 row blocks of 32)
-constexpr int kKV = 128;   // keys staged per step (4 quarters of 32)
 constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold, log2 units
+
+// Waves and staged keys per width. Up to D = 128: 8 waves (two per SIMD) =
+// 2 row blocks x 4 key quarters of a 128-key stage. At D = 256 a wave's Q
+// operands and O accumulators need ~260 registers and a 128-key K or V tile
+// 66 KB of LDS, so 4 waves (one per SIMD, 512 registers each) = 2 row blocks
+// x 2 key halves of a 64-key stage.
+template <int D>
+struct FwdShape {
+  static constexpr int kWaves = D > 128 ? 4 : 8;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kQuarters = kWaves / 2;  // key slices of 32 per stage
+  static constexpr int kKV = 32 * kQuarters;    // keys staged per step
+};
 
 template <int D>
 struct FwdLds {
+  static constexpr int kWaves = FwdShape<D>::kWaves, kKV = FwdShape<D>::kKV;
   static constexpr int kTileHalves = Tile<D>::template halves<kKV>();  // one K or V tile
   static constexpr int kStageHalves = 2 * kTileHalves; // K + V
-  // Merge area (reuses the four tiles, two waves each): per wave, D/32 x 16
-  // floats per lane.
-  static_assert(2 * 64 * D * 2 <= kTileHalves * 2, "merge area exceeds a tile");
+  // Merge area (reuses the four tiles, kWaves / 4 waves each): per wave,
+  // D/32 x 16 floats per lane.
+  static_assert((kWaves / 4) * 64 * D * 2 <= kTileHalves * 2, "merge area exceeds a tile");
   static constexpr int kMLFloat2 = kWaves * 64;  // (m, l) per lane
   // Load instructions per wave and tile that every wave issues inside the
   // step; the remaining kInsts % kWaves go out at the start of the step.
@@ -129,10 +140,24 @@ struct FwdWave {
     floatx16 sn = zero16();
     constexpr int kS = D / 16;  // products of the next S^T
     constexpr int kFront = kS > 2 ? 2 : 1;  // issued before the row max (covers its latency)
+    // At width 256 each product's LDS operand is read one product ahead and
+    // pinned there (scheduling fence): left to the scheduler, a step's 32
+    // operand reads were hoisted to its top and spilled registers. Narrower
+    // widths leave the reads to the scheduler.
+    constexpr bool kPin = D > 128;
+    auto kread = [&](int kk) { return tile_read16<D>(Kn, kq * 32, kk, roff); };
+    half8 kcur = kPin && NEXT ? kread(0) : half8{};
+    auto kop = [&](int kk) {
+      if constexpr (!kPin) return kread(kk);
+      const half8 a = kcur;
+      if (kk + 1 < kS) kcur = kread(kk + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      return a;
+    };
 #pragma unroll
     for (int kk = 0; kk < kFront; ++kk)
       if constexpr (NEXT) {
-        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qop(kk, roff), sn);
+        sn = mfma16<BF>(kop(kk), qop(kk, roff), sn);
         issue(kk);
       }
     // ALiBi (masked instantiation only): -slope |i - j| in raw-score units,
@@ -181,7 +206,7 @@ struct FwdWave {
 #pragma unroll
     for (int kk = kFront; kk < kS; ++kk) {
       if constexpr (NEXT) {
-        sn = mfma16<BF>(tile_read16<D>(Kn, kq * 32, kk, roff), qop(kk, roff), sn);
+        sn = mfma16<BF>(kop(kk), qop(kk, roff), sn);
         issue(kk);
       }
       // 16 exponentials spread over the remaining products.
@@ -199,12 +224,25 @@ struct FwdWave {
       }
     }
     // O^T += V^T P^T; k-step q covers keys 16q .. 16q+15 of this quarter.
+    auto vread = [&](int u) {  // u = q * (D / 32) + cb
+      return tile_tr_operand<D>(Vs, kq * 32 + 16 * (u / (D / 32)), 32 * (u % (D / 32)), troff);
+    };
+    half8 vcur = kPin ? vread(0) : half8{};
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int cb = 0; cb < D / 32; ++cb) {
-        oacc[cb] = mfma16<BF>(tile_tr_operand<D>(Vs, kq * 32 + 16 * q, 32 * cb, troff), pb[q], oacc[cb]);
-        if constexpr (NEXT) issue(kS + q * (D / 32) + cb);
+        const int u = q * (D / 32) + cb;
+        half8 va;
+        if constexpr (kPin) {
+          va = vcur;
+          if (u + 1 < D / 16) vcur = vread(u + 1);
+          __builtin_amdgcn_sched_barrier(0);
+        } else {
+          va = vread(u);
+        }
+        oacc[cb] = mfma16<BF>(va, pb[q], oacc[cb]);
+        if constexpr (NEXT) issue(kS + u);
       }
     if constexpr (NEXT) sc = sn;
   }
@@ -224,6 +262,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml, half_t* qt) {
   using L = FwdLds<D>;
+  constexpr int kWaves = FwdShape<D>::kWaves, kKV = FwdShape<D>::kKV;
+  constexpr int kQuarters = FwdShape<D>::kQuarters;
   constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
@@ -445,11 +485,13 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   else run(j, P0{}, T{}, F{});
   __syncthreads();  // every wave is done reading the tiles (they hold the merge area)
 
-  // Merge the four key quarters of each row block through LDS: each of the
-  // four tiles holds the partials of two waves.
+  // Merge the key slices of each row block through LDS: each of the four
+  // tiles holds the partials of kWaves / 4 waves.
+  constexpr int kPerTile = kWaves / 4;
   auto part_of = [&](int src) {
-    half_t* t = src < 2 ? kt0 : src < 4 ? vt0 : src < 6 ? kt1 : vt1;
-    return reinterpret_cast<float*>(t) + (src & 1) * (D / 8) * 64 * 4;
+    const int t4 = src / kPerTile;
+    half_t* t = t4 == 0 ? kt0 : t4 == 1 ? vt0 : t4 == 2 ? kt1 : vt1;
+    return reinterpret_cast<float*>(t) + (src % kPerTile) * (D / 8) * 64 * 4;
   };
 #pragma unroll
   for (int cb = 0; cb < D / 32; ++cb)
@@ -462,13 +504,16 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   ml[wave * 64 + lane] = make_float2(w.m_raw, w.l);
   __syncthreads();
 
-  // Wave (rb, kq) finishes d-block kq of row block rb (D=64: kq < 2 only).
-  if (kq < D / 32) {
-    const int cb = kq;
-    float mk[4], lk[4];
+  // Wave (rb, kq) finishes d-blocks kq, kq + kQuarters, ... of row block rb
+  // (D = 64: kq < 2 only).
+#pragma unroll
+  for (int ci = 0; ci < (D / 32 + kQuarters - 1) / kQuarters; ++ci) {
+    const int cb = kq + ci * kQuarters;
+    if (cb >= D / 32) continue;
+    float mk[kQuarters], lk[kQuarters];
     float m_star = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kQuarters; ++k) {
       const int src = k * 2 + rb;  // wave index of quarter k in this row block
       const float2 a = ml[src * 64 + lane];
       const float2 bb = ml[src * 64 + (lane ^ 32)];
@@ -476,9 +521,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
       lk[k] = a.y + bb.y;
       m_star = fmaxf(m_star, mk[k]);
     }
-    float wk[4], l_star = 0.f;
+    float wk[kQuarters], l_star = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kQuarters; ++k) {
       wk[k] = (mk[k] == -INFINITY) ? 0.f : fast_exp2((mk[k] - m_star) * c);
       l_star += wk[k] * lk[k];
     }
@@ -491,7 +536,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
       for (int g = 0; g < 4; ++g) {
         floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
+        for (int k = 0; k < kQuarters; ++k) {
           const int src = k * 2 + rb;
           const floatx4 v =
               *reinterpret_cast<const floatx4*>(part_of(src) + ((cb * 4 + g) * 64 + lane) * 4);
@@ -510,7 +555,7 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
 }
 
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
-__global__ __launch_bounds__(kThreads) void fwd_kernel(
+__global__ __launch_bounds__(FwdShape<D>::kThreads) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
@@ -576,7 +621,8 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D));
-  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid, dim3(kThreads), 0,
+  hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid,
+                     dim3(FwdShape<D>::kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
@@ -594,7 +640,7 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
   // Key lengths, windows, packed sequences and ALiBi need the masked
   // instantiation (kKV is a multiple of kBR); a mask, dropout or a bias one
   // of its copies with those inputs compiled in (Feat).
-  const bool bounds = (a.N % kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
+  const bool bounds = (a.N % FwdShape<D>::kKV) != 0 || a.kv_len != nullptr || a.window > 0 ||
                       a.alibi != nullptr || a.seg_start != nullptr ||
                       key_rows(a.N, a.Nkv) != a.N;
   auto with = [&](auto feat) {
@@ -606,7 +652,11 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
     case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
     case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
     case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});
-    case kFeatBias: return with(std::integral_constant<int, kFeatBias>{});
+    case kFeatBias:
+      // (the bias copy stages Q in LDS too, which at D = 256 does not fit
+      // beside the K/V stages; the C ABI refuses a bias there)
+      if constexpr (D > 128) return hipErrorInvalidValue;
+      else return with(std::integral_constant<int, kFeatBias>{});
     default: break;
   }
   if (a.causal)
@@ -622,16 +672,18 @@ unsigned long long fwd_launch_items(int B, int Hq, int N, int D) {
   (void)D;
   const unsigned long long tiles = ((unsigned long long)N + kBR - 1) / kBR;  // non-causal grid
   const unsigned long long wgs = tiles * (unsigned long long)B * (unsigned long long)Hq;
-  return (wgs + kXcds - 1) / kXcds * kXcds * kThreads;
+  return (wgs + kXcds - 1) / kXcds * kXcds * (padded_head_dim(D) > 128 ? 256 : 512);
 }
 
 hipError_t launch_fwd(const FwdArgs& a) {
   const int w = padded_head_dim(a.D);
   if (a.dtype == kBF16)
     return w == 32 ? launch_fwd_d<32, true>(a) : w == 64 ? launch_fwd_d<64, true>(a)
-         : w == 96 ? launch_fwd_d<96, true>(a) : launch_fwd_d<128, true>(a);
+         : w == 96 ? launch_fwd_d<96, true>(a) : w == 128 ? launch_fwd_d<128, true>(a)
+                                                         : launch_fwd_d<256, true>(a);
   return w == 32 ? launch_fwd_d<32, false>(a) : w == 64 ? launch_fwd_d<64, false>(a)
-       : w == 96 ? launch_fwd_d<96, false>(a) : launch_fwd_d<128, false>(a);
+       : w == 96 ? launch_fwd_d<96, false>(a) : w == 128 ? launch_fwd_d<128, false>(a)
+                                                         : launch_fwd_d<256, false>(a);
 }
 
 }  // namespace fa

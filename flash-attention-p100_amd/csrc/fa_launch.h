@@ -77,12 +77,14 @@ inline int key_rows(int N, int Nkv) { return Nkv > 0 ? Nkv : N; }
 //   the preprocess kernel zeroes (sized by Hq, which bounds Hkv, so that the
 //   preprocess needs no Hkv);
 //   two fp32 partial dK/dV slots per such pair and (b, kv head).
-// Head dims: any multiple of 8 from 8 to 128 (the `D` of the argument
+// Head dims: any multiple of 8 from 8 to 256 (the `D` of the argument
 // structs, the row length in memory). The kernels are compiled for the
-// widths 32, 64, 96 and 128 and run a head dim on the smallest that holds
-// it: the extra columns load as zeros and are never stored.
-inline int padded_head_dim(int D) { return D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : 128; }
-inline bool valid_head_dim(int D) { return D >= 8 && D <= 128 && D % 8 == 0; }
+// widths 32, 64, 96, 128 and 256 and run a head dim on the smallest that
+// holds it: the extra columns load as zeros and are never stored.
+inline int padded_head_dim(int D) {
+  return D <= 32 ? 32 : D <= 64 ? 64 : D <= 96 ? 96 : D <= 128 ? 128 : 256;
+}
+inline bool valid_head_dim(int D) { return D >= 8 && D <= 256 && D % 8 == 0; }
 
 constexpr int kBwdTile = 128;  // key rows of one backward workgroup
 struct BwdWorkspace {

@@ -174,7 +174,7 @@ std::vector<at::Tensor> fa_forward(at::Tensor q, at::Tensor k, at::Tensor v, boo
   v = v.contiguous();
   const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   const int Hkv = k.size(1);
-  TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
+  TORCH_CHECK(D >= 8 && D <= 256 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 256, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
               ") must be a multiple of key/value heads (", Hkv, ")");
@@ -209,7 +209,7 @@ static std::vector<at::Tensor> backward_impl(at::Tensor q, at::Tensor k, at::Ten
   lse = lse.contiguous();
   const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   const int Hkv = k.size(1);
-  TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
+  TORCH_CHECK(D >= 8 && D <= 256 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 256, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
   // The reference checks only q and dO here (fa_p100_ext.cu:106); the kernels
@@ -282,7 +282,7 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   check_bnhd(v, "v");
   const int B = q.size(0), N = q.size(1), H = q.size(2), D = q.size(3);
   const int Hkv = k.size(2);
-  TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
+  TORCH_CHECK(D >= 8 && D <= 256 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 256, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
               ") must be a multiple of key/value heads (", Hkv, ")");
@@ -322,7 +322,7 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   lse = lse.contiguous();
   const int B = q.size(0), N = q.size(1), H = q.size(2), D = q.size(3);
   const int Hkv = k.size(2);
-  TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
+  TORCH_CHECK(D >= 8 && D <= 256 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 256, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
   TORCH_CHECK(k.sizes() == v.sizes() && k.size(0) == B && k.size(1) > 0 && k.size(3) == D,
@@ -376,7 +376,7 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   v = v.contiguous();
   const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   const int Hkv = k.size(1);
-  TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
+  TORCH_CHECK(D >= 8 && D <= 256 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 256, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads (", H,
               ") must be a multiple of key/value heads (", Hkv, ")");
@@ -418,7 +418,7 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   lse = lse.contiguous();
   const int B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(3);
   const int Hkv = k.size(1);
-  TORCH_CHECK(D >= 8 && D <= 128 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 128, got ", D);
+  TORCH_CHECK(D >= 8 && D <= 256 && D % 8 == 0, "head dim must be a multiple of 8 from 8 to 256, got ", D);
   TORCH_CHECK(N > 0, "N must be positive");
   TORCH_CHECK(Hkv > 0 && H % Hkv == 0, "query heads must be a multiple of kv heads");
   for (const at::Tensor* t : {&k, &v, &dO, &o})

@@ -7,7 +7,7 @@ names, arguments and return values.
     o = flash_attn(q, k, v, causal=True)   # q: (B, Hq, N, D) fp16 on the GPU
                                            # k, v: (B, Hkv, N, D), Hq % Hkv == 0
 
-D is any multiple of 8 up to 128 (the reference: 64 or 128); N is arbitrary; Hkv == Hq is
+D is any multiple of 8 up to 256 (the reference: 64 or 128); N is arbitrary; Hkv == Hq is
 multi-head, Hkv == 1 multi-query, anything between grouped-query. The kernels
 are hand-written HIP for gfx950 (fp16 MFMA with fp32 accumulation), built
 in-tree by build.py into libfa_mi355x.so, and reached through the
@@ -166,7 +166,8 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
-    and D a multiple of 8 up to 128 (the reference: 64 or 128). scale = 1/sqrt(D).
+    and D a multiple of 8 up to 256 (the reference: 64 or 128; attn_bias only
+    up to 128). scale = 1/sqrt(D).
     Causal masking is top-left aligned (key j is hidden from query i when
     j > i).
 
@@ -238,6 +239,8 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         raise ValueError(
             f"q has {q.size(2)} rows and k, v {k.size(2)}: segment_ids, attn_mask, dropout_p "
             "and attn_bias need q_len == kv_len")
+    if attn_bias is not None and q.size(-1) > 128:
+        raise ValueError(f"attn_bias needs a head dim up to 128, got {q.size(-1)}")
     window = 0
     if sliding_window is not None:
         window = int(sliding_window)

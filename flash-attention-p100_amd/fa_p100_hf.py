@@ -62,7 +62,8 @@ Every other unsupported request raises NotImplementedError instead of
 degrading (fa_p100_hf.py:24-32): output_attentions,
 head_mask, attention sinks (s_aux) and logit soft-capping (softcap), which
 other models pass to the attention interface, a window on non-causal
-attention, a head_dim that is not a multiple of 8 up to 128, a cached step
+attention, a head_dim that is not a multiple of 8 up to 256 (up to 128 with
+an additive float mask, which goes to the kernels as a bias), a cached step
 with padding or a mask. A scale other than 1/sqrt(D),
 which the reference rejected, goes to the kernels.
 """
@@ -248,9 +249,9 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
             "use attn_implementation='eager'.")
 
     head_dim = query.size(-1)
-    if not (8 <= head_dim <= 128 and head_dim % 8 == 0):
+    if not (8 <= head_dim <= 256 and head_dim % 8 == 0):
         raise NotImplementedError(
-            f"fa_p100 supports head_dim multiples of 8 up to 128, got {head_dim}.")
+            f"fa_p100 supports head_dim multiples of 8 up to 256, got {head_dim}.")
     # The reference fixed scale = 1/sqrt(D) and raised on anything else; the
     # kernels take the model's scale (softmax_scale) when it differs.
     softmax_scale = None
@@ -268,6 +269,10 @@ def fa_p100_attention_forward(module, query, key, value, attention_mask, dropout
     kv_len, segs, mask = kwargs.pop(_BOUNDS_KW, None) or (None, None, None)
     if attention_mask is not None and mask is None:  # a 4-D mask, no wrapper
         mask = dense_mask_bits(attention_mask, query.size(0), query.size(1))
+    if mask is not None and mask[3] is not None and head_dim > 128:
+        raise NotImplementedError(
+            f"fa_p100 takes an additive float mask (an attention bias) up to head_dim 128, "
+            f"got {head_dim}; use a boolean mask or attn_implementation='eager'.")
     sliding_window = kwargs.get("sliding_window")
     if mask is not None and mask[2] is not None:
         # A 4-D mask alone decides which keys each query sees (eager adds it

@@ -24,7 +24,7 @@ def test_host_only_helpers():
     lib = load_capi()
     assert lib.fa_version().decode().startswith("fa_mi355x")
     assert lib.fa_error_string(0) == b"success"
-    assert b"multiple of 8 from 8 to 128" in lib.fa_error_string(10001)
+    assert b"multiple of 8 from 8 to 256" in lib.fa_error_string(10001)
     assert b"multiple" in lib.fa_error_string(10003)
     # two (B, Hq, N) float32 vectors, each rounded up to 256 bytes; 0 if invalid.
     # dvec + lse2 (256-aligned), counters per key-tile pair (by Hq), then two
@@ -36,7 +36,11 @@ def test_host_only_helpers():
     assert lib.fa_bwd_workspace_bytes(1, 3, 3, 7, 64) == 512  # one key tile: no pairs
     assert lib.fa_bwd_workspace_bytes(1, 8, 3, 4096, 128) == 0
     assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 100) == 0
-    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 136) == 0
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 264) == 0
+    # head dims 136 .. 256 run at tile width 256 and take its slots
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 256) == (
+        2 * 8 * 4096 * 4 + 8 * 16 * 4 + 8 * 16 * 2 * 128 * 256 * 2 * 4)
+    assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 136) == lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 256)
     # narrower head dims take the slots of the tile width they run on (80 -> 96)
     assert lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 80) == lib.fa_bwd_workspace_bytes(1, 8, 8, 4096, 96)
 
@@ -48,7 +52,9 @@ def test_capi_validation_returns_before_any_launch():
     # head dim, sequence length, heads, batch, null pointers
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 100, 0, 0, s) == 10001
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 4, 0, 0, s) == 10001
-    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 136, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 264, 0, 0, s) == 10001
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 256, 0, 0, s) == 10005
+    assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 8, 136, 0, 0, s) == 10005
     assert lib.fa_fwd(z, z, z, z, z, 1, 2, 2, 0, 64, 0, 0, s) == 10002
     assert lib.fa_fwd(z, z, z, z, z, 1, 4, 3, 8, 64, 0, 0, s) == 10003
     assert lib.fa_fwd(z, z, z, z, z, 0, 2, 2, 8, 64, 0, 0, s) == 10004
@@ -115,6 +121,11 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, 64, 1,
                          fa_opts(bias=1, bias_stride_b=0, bias_stride_h=64), s) == 10005
     assert b"dbias" in lib.fa_error_string(10016)
+    # no bias at the head dims of tile width 256 (136 .. 256)
+    for D in (136, 256):
+        assert lib.fa_fwd_ex(*([one] * 5), 1, 4, 2, 8, D, 0, fa_opts(bias=1), s) == 10016
+        assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, D, 0, fa_opts(), s) == 10005
+    assert b"head dim up to 128" in lib.fa_error_string(10016)
     # the dropout generator: p in [0, 1), shape, pointers; the scale of the drawn rate
     for bad in (-0.1, 1.0, 1.5, float("nan")):
         assert lib.fa_dropout_bits(7, bad, 1, 8, one, one, s) == 10015
@@ -245,11 +256,11 @@ def test_shape_limits_follow_the_one_dimensional_grids():
     # At a tile width (32, 64, 96, 128) a head's rows, with the 256 rows a
     # staged tile may address past them, stay within 2^32 bytes: (N+256)*D
     # <= INT_MAX; narrower head dims keep (N+256)*D <= 2^29.
-    for D in (32, 64, 96, 128):
+    for D in (32, 64, 96, 128, 256):
         n_max = (2**31 - 1) // D - 256
         assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max, D) > 0, D
         assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max + 1, D) == 0, D
-    for D in (8, 40, 120):
+    for D in (8, 40, 120, 136, 248):
         n_max = 2**29 // D - 256
         assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max, D) > 0, D
         assert lib.fa_bwd_workspace_bytes(1, 1, 1, n_max + 1, D) == 0, D

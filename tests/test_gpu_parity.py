@@ -176,7 +176,7 @@ def test_reference_error_messages_on_device():
         fa._ext.forward(h(1, 2, 8, 64).float(), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
     with pytest.raises(RuntimeError, match=r"q must be \(B, H, N, D\)"):
         fa._ext.forward(h(2, 8, 64), h(1, 2, 8, 64), h(1, 2, 8, 64), False, False)
-    with pytest.raises(RuntimeError, match="head dim must be a multiple of 8 from 8 to 128, got 100"):
+    with pytest.raises(RuntimeError, match="head dim must be a multiple of 8 from 8 to 256, got 100"):
         fa._ext.forward(h(1, 2, 8, 100), h(1, 2, 8, 100), h(1, 2, 8, 100), False, False)
     with pytest.raises(RuntimeError, match="N must be positive"):
         fa._ext.forward(h(1, 2, 0, 64), h(1, 2, 0, 64), h(1, 2, 0, 64), False, False)

@@ -48,8 +48,18 @@ def test_dropout_reaches_the_kernel():
 
 def test_head_dim_scale_and_kv_len_guards():
     q, k, v = qkv(d=100)
-    with pytest.raises(NotImplementedError, match="multiples of 8 up to 128, got 100"):
+    with pytest.raises(NotImplementedError, match="multiples of 8 up to 256, got 100"):
         hf.fa_p100_attention_forward(MOD, q, k, v, None)
+    with pytest.raises(NotImplementedError, match="multiples of 8 up to 256, got 264"):
+        hf.fa_p100_attention_forward(MOD, *qkv(d=264), None)
+    # head_dim 256 passes the guards (host tensors stop at the device check),
+    # but not with an additive float mask, which would be a bias
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        hf.fa_p100_attention_forward(MOD, *qkv(d=256), None)
+    soft = torch.zeros(1, 1, 4, 4)
+    soft[..., 0] = -0.5
+    with pytest.raises(NotImplementedError, match="up to head_dim 128, got 256"):
+        hf.fa_p100_attention_forward(MOD, *qkv(d=256), soft)
     q, k, v = qkv(d=128)
     # Another scale passes the guards now (the host tensors then stop at the
     # binding's device check); the reference raised here.
