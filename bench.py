@@ -165,7 +165,8 @@ class FaOptions(ctypes.Structure):
                 ("drop_t", ctypes.c_void_p), ("drop_scale", ctypes.c_float),
                 ("bias", ctypes.c_void_p), ("bias_stride_b", ctypes.c_longlong),
                 ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p),
-                ("kv_rows", ctypes.c_int)]
+                ("kv_rows", ctypes.c_int), ("block_rows", ctypes.c_void_p),
+                ("block_cols", ctypes.c_void_p)]
 
 
 def feature_paths(c, steps, warmup):

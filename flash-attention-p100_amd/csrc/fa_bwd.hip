@@ -455,7 +455,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const uint32_t* __restrict__ mask_t, int mask_heads, const uint32_t* __restrict__ drop,
     const uint32_t* __restrict__ drop_t, float drop_scale, const float* __restrict__ bias,
     long long bias_sb, long long bias_sh, float bias_raw, float* __restrict__ dbias, int dr,
-    int NK) {
+    int NK, const int* __restrict__ block_rows, const int* __restrict__ block_cols) {
   using L = BwdLds<D>;
   constexpr int kWaves = BwdShape<D>::kWaves, kHalves = BwdShape<D>::kHalves;
   constexpr int kSub = BwdShape<D>::kSub;
@@ -533,6 +533,15 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
   // Offset of query head hq's row 0 in Q, dO, dQ.
   auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
   constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
+  // Block-sparse layout (SPARSE instantiations): nb blocks of kSparseBlock
+  // rows (= kTile) per side, kSpb streamed tiles per block. Phase 1 steps
+  // over the (query head, query block) pairs listed for its key block, phase
+  // 2 over the key blocks listed for its query block; the masks below work
+  // on row and key indices, so each step is masked as its position needs.
+  constexpr bool SPARSE = Feat<FEAT>::kBlock;
+  constexpr int kSpb = kSparseBlock / kSub;
+  static_assert(kSparseBlock == kTile, "a workgroup's rows are one block of the layout");
+  const int nb = (N + kSparseBlock - 1) / kSparseBlock;
   // Arbitrary mask (MASKB instantiations): query head hq's bit plane,
   // rows of W32 words, row-major (phase 2: row = query) or transposed (phase
   // 1: row = key). Word indices are clamped (bits past N are masked anyway).
@@ -586,8 +595,9 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
   };
   auto n_iters = [&](int u) { return group * ((q_end(u) - q_start(u) + kSub - 1) / kSub); };
   auto split = [&](int u) {
-    // (not at width 256: a second inlined copy of phase 1 spilled registers)
-    if constexpr (KG) return 0;
+    // (not at width 256: a second inlined copy of phase 1 spilled registers;
+    // not with a block layout, whose key tiles have no common amount of work)
+    if constexpr (KG || SPARSE) return 0;
     const int m = n_tiles - 1 - 2 * u;
     // windows leave the tiles' work equal; with kofs != 0 the key and query
     // tiles do not pair up
@@ -606,7 +616,11 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const int tp0 = tile * kTile;  // first key row of this item
     const int jw = tp0 + w4 * 32;  // this wave's key rows
     const int j_col = jw + l32;
-    const int n_it = n_iters(tile);
+    // Block-sparse: the pairs attending this key block (count first); step
+    // `it` runs streamed tile it % kSpb of the (it / kSpb)-th pair.
+    const int* const clist =
+        SPARSE ? block_cols + ((size_t)bkv * nb + tile) * (group * nb + 1) : nullptr;
+    const int n_it = SPARSE ? clist[0] * kSpb : n_iters(tile);
     const int it_begin = helping ? n_it - x_help : 0;
     const int it_end = helping ? n_it : n_it - x_own;
     const bool shared = helping || x_own > 0;
@@ -634,13 +648,26 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const int n_qt = (q_end(tile) - i_start + kSub - 1) / kSub;
     // Rows this wave's key column reaches (see KVWave::step).
     const int row_end = j_col < Nk ? (narrowed ? upper(j_col) : N) : 0;
+    // Query head (of the group) and first query row of flattened step `it`.
+    auto qpos = [&](int it, int& g, int& i0) {
+      if constexpr (SPARSE) {
+        const int e = it / kSpb;
+        const int f = clist[1 + e];
+        g = f / nb;
+        i0 = (f - g * nb) * kSparseBlock + (it - e * kSpb) * kSub;
+      } else {
+        g = it / n_qt;
+        i0 = i_start + (it % n_qt) * kSub;
+      }
+    };
 
     // Q, dO tiles and lse2, dvec of flattened step `it` (clamped to the last
     // one, so that every step issues the same loads) into one stage.
     auto fetch = [&](int it, half_t* tq, half_t* to, float* tv) {
       it = min(it, it_end - 1);
-      const int g = it / n_qt;
-      const int i0 = i_start + (it % n_qt) * kSub;
+      if constexpr (SPARSE) it = max(it, 0);  // (no pair: a listed padding pair, never run)
+      int g, i0;
+      qpos(it, g, i0);
       const int hq = hkv * group + g;
       const size_t bhq = (size_t)b * Hq + hq;
       const rsrc_t rq = rows_rsrc(Q + q_off(hq), N, stq.n, dr);
@@ -661,8 +688,9 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     auto bload1 = [&](int it) {
       floatx16 v = zero16();
       if (has_bias) {
-        const rsrc_t rb = bias_rows_rsrc(bplane(hkv * group + it / n_qt),
-                                         i_start + (it % n_qt) * kSub + 32 * half, N);
+        int g, i0;
+        qpos(it, g, i0);
+        const rsrc_t rb = bias_rows_rsrc(bplane(hkv * group + g), i0 + 32 * half, N);
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           v[r] = buf_load_f32(rb, bvoff1, (uint32_t)((8 * (r >> 2) + (r & 3)) * N) * 4u);
@@ -677,19 +705,20 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
       const half_t* Qs = P ? ta1 : ta0;
       const half_t* Os = P ? tb1 : tb0;
       const float* lse2s = P ? vec1 : vec0;
-      const int i0 = i_start + (it % n_qt) * kSub;
+      int g, i0;
+      qpos(it, g, i0);
       // Causal tiles wholly above a wave's keys give exact zeros through the
       // mask; they occur only on the diagonal, so they are not skipped.
       const float alibi_raw =
-          BOUNDS && alibi ? alibi[hkv * group + (it / n_qt)] / scale : 0.f;  // step's query head
+          BOUNDS && alibi ? alibi[hkv * group + g] / scale : 0.f;  // step's query head
       // Key j_col's mask word for the step's query rows (clamped: rows past N
       // are masked by row_end, keys past N have row_end = 0).
       const size_t tword =
           (size_t)min(j_col, N - 1) * W32 + min((i0 + 32 * half) >> 5, W32 - 1);
       const uint32_t mtw =
-          MASKB && mask_t ? plane(mask_t, hkv * group + it / n_qt)[tword] : ~0u;
+          MASKB && mask_t ? plane(mask_t, hkv * group + g)[tword] : ~0u;
       const uint32_t ztw =
-          DROPB && drop_t ? zplane(drop_t, hkv * group + it / n_qt)[tword] : ~0u;
+          DROPB && drop_t ? zplane(drop_t, hkv * group + g)[tword] : ~0u;
       // The next stage's loads go out after the step's mask and dropout words:
       // loads complete in issue order, so words loaded after them would hold
       // the softmax until the whole next stage had landed.
@@ -830,6 +859,17 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     for (int g = 0; g < group; ++g) {
       const int hq = hkv * group + g;
       const size_t bhq = (size_t)b * Hq + hq;
+      // Block-sparse: the key blocks this query block attends (count first);
+      // step t runs streamed tile t % kSpb of the (t / kSpb)-th block (an
+      // empty list: one step, whose rows have lse = +inf, so P = 0).
+      const int* const rlist = SPARSE ? block_rows + (bhq * nb + tw) * (nb + 1) : nullptr;
+      const int n_steps = SPARSE ? max(1, rlist[0] * kSpb) : n_kt;
+      const int t_first = SPARSE ? 0 : t_lo;
+      auto stage = [&](int t) {
+        if constexpr (!SPARSE) return t;
+        const int e = t / kSpb;
+        return rlist[1 + e] * kSpb + (t - e * kSpb);
+      };
       const float alibi_raw = BOUNDS && alibi ? alibi[hq] / scale : 0.f;
       const half_t* Qg = Q + q_off(hq);
       const half_t* dOg = dO + q_off(hq);
@@ -868,7 +908,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
         }
         return v;
       };
-      floatx16 bv2 = bload2(t_lo);
+      floatx16 bv2 = bload2(stage(t_first));
       QWave<D, CAUSAL, BOUNDS, BF> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
@@ -883,7 +923,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
 
       // K, V tiles of key step t (clamped to the last one) into a stage.
       auto fetch = [&](int t, half_t* tk, half_t* tv) {
-        const int jn = min(t, n_kt - 1) * kSub;
+        const int jn = stage(min(t, n_steps - 1)) * kSub;
 #pragma unroll
         for (int u = 0; u < decltype(plan_k)::kParts; ++u) {
           plan_k.part(tk, rk, jn, wave, u);
@@ -893,7 +933,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
       auto step = [&](int t, auto par) {
         constexpr int P = decltype(par)::value;
         // The next stage's loads go out between this step's products.
-        const int jn = min(t + 1, n_kt - 1) * kSub;
+        const int jn = stage(min(t + 1, n_steps - 1)) * kSub;
         auto issue = [&](int q) {
           constexpr int kParts = decltype(plan_k)::kParts;
           static_assert(2 * kParts <= D / 16, "every load needs an issue point");
@@ -902,24 +942,26 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
             else plan_k.part(P ? ta0 : ta1, rk, jn, wave, q >> 1);
           }
         };
-        const int word = min(t * (kSub / 32) + half, W32 - 1);  // keys t*kSub + 32*half ..
+        const int ts = stage(t);
+        const int word = min(ts * (kSub / 32) + half, W32 - 1);  // keys ts*kSub + 32*half ..
         const uint32_t mw = mrow ? mrow[word] : ~0u;
         const uint32_t zw = zrow ? zrow[word] : ~0u;
-        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, t * kSub, i_row + kofs, lane_hi, key_lo, alibi_raw, mw,
-               zw, zs, bv2, [&] { return bload2(min(t + 1, n_kt - 1)); }, braw, dbrow, db_x4,
+        w.step(P ? ta1 : ta0, P ? tb1 : tb0, half, ts * kSub, i_row + kofs, lane_hi, key_lo,
+               alibi_raw, mw, zw, zs, bv2,
+               [&] { return bload2(stage(min(t + 1, n_steps - 1))); }, braw, dbrow, db_x4,
                lane, so, scale_log2, issue);
         wait_vmem();
         __syncthreads();
       };
-      fetch(t_lo, ta0, tb0);
+      fetch(t_first, ta0, tb0);
       wait_vmem();
       __syncthreads();
-      int t = t_lo;  // buffer parity counts from t_lo
-      for (; t + 2 <= n_kt; t += 2) {
+      int t = t_first;  // buffer parity counts from t_first
+      for (; t + 2 <= n_steps; t += 2) {
         step(t, P0{});
         step(t + 1, P1{});
       }
-      if (t < n_kt) step(t, P0{});
+      if (t < n_steps) step(t, P0{});
 
       if constexpr (kHalves == 2) {
         if (half) partial_store<D / 32>(region(4 + w4), w.acc, 0, lane);
@@ -986,7 +1028,7 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      a.slots ? kSplitNum * 64 / Sh::kSub : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
                      a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.drop,
                      a.drop_t, a.drop_scale, a.bias, a.bias_sb, a.bias_sh,
-                     a.bias ? 1.f / scale : 0.f, a.dbias, a.D, NK);
+                     a.bias ? 1.f / scale : 0.f, a.dbias, a.D, NK, a.block_rows, a.block_cols);
   return hipGetLastError();
 }
 
@@ -1003,7 +1045,11 @@ hipError_t launch_main_d(const BwdArgs& a) {
     return a.causal ? launch_main_t<D, true, true, F, BF>(a)
                     : launch_main_t<D, false, true, F, BF>(a);
   };
-  switch (feat_of(a.mask != nullptr, a.drop != nullptr, a.bias != nullptr)) {
+  switch (feat_of(a.mask != nullptr, a.drop != nullptr, a.bias != nullptr,
+                  a.block_rows != nullptr)) {
+    case kFeatBlock: return with(std::integral_constant<int, kFeatBlock>{});
+    case kFeatBlock | kFeatDrop:
+      return with(std::integral_constant<int, kFeatBlock | kFeatDrop>{});
     case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
     case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
     case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});

@@ -115,6 +115,9 @@ const char* fa_error_string(int err) {
     case FA_ERR_KV_ROWS:
       return "kv_rows must be >= 0, and key rows that differ from the query rows do not combine "
              "with packed sequences, a mask, dropout or a bias";
+    case FA_ERR_BLOCKS:
+      return "a block-sparse layout does not combine with a mask, a bias or key rows that differ "
+             "from the query rows, and the backward needs block_cols with block_rows";
     case FA_ERR_SCRATCH:
       return "fa_bwd_noalloc: 2 * B*Hq*N floats exceed the built-in scratch "
              "(FA_BWD_NOALLOC_SCRATCH_BYTES); use fa_bwd with a workspace";
@@ -160,6 +163,13 @@ static int check_opts(const fa_options& op, int causal, int Hq, int N, int D, bo
   if (op.kv_rows > 0 && op.kv_rows != N &&
       (op.seg_start != nullptr || op.mask != nullptr || op.drop != nullptr || op.bias != nullptr))
     return FA_ERR_KV_ROWS;
+  if (op.block_rows != nullptr) {
+    if (op.mask != nullptr || op.bias != nullptr || (op.kv_rows > 0 && op.kv_rows != N))
+      return FA_ERR_BLOCKS;
+    if (backward && op.block_cols == nullptr) return FA_ERR_BLOCKS;
+  } else if (op.block_cols != nullptr) {
+    return FA_ERR_BLOCKS;
+  }
   return FA_OK;
 }
 
@@ -216,6 +226,7 @@ static int fwd(const void* q, const void* k, const void* v, void* o, float* lse,
   a.bias_sb = op.bias_stride_b;
   a.bias_sh = op.bias_stride_h;
   a.Nkv = op.kv_rows;
+  a.block_rows = op.block_rows;
   return to_code(fa::launch_fwd(a));
 }
 
@@ -333,6 +344,8 @@ static int bwd_main(const void* q, const void* k, const void* v, const void* dO,
   a.bias_sh = op.bias_stride_h;
   a.dbias = op.dbias;
   a.Nkv = op.kv_rows;
+  a.block_rows = op.block_rows;
+  a.block_cols = op.block_cols;
   return to_code(fa::launch_bwd_main(a));
 }
 
@@ -416,6 +429,18 @@ int fa_dropout_bits(uint64_t seed, float p, int P, int N, uint32_t* bits, uint32
   if (P <= 0) return FA_ERR_BATCH;
   if (!bits) return FA_ERR_NULL;
   return to_code(fa::launch_dropout_bits(seed, dropout_threshold(p), P, N, bits, bits_t, stream));
+}
+
+int fa_pack_blocks(const uint8_t* layout, int layout_b, int layout_h, int B, int Hq, int Hkv,
+                   int N, int causal, int* block_rows, int* block_cols, void* stream) {
+  if (N <= 0) return FA_ERR_SEQLEN;
+  if (Hkv <= 0 || Hq <= 0 || Hq % Hkv != 0) return FA_ERR_HEADS;
+  if (B <= 0) return FA_ERR_BATCH;
+  if ((layout_b != 1 && layout_b != B) || (layout_h != 1 && layout_h != Hq)) return FA_ERR_BLOCKS;
+  if (!layout || !block_rows) return FA_ERR_NULL;
+  const int nb = (N + fa::kSparseBlock - 1) / fa::kSparseBlock;
+  return to_code(fa::launch_pack_blocks(layout, layout_b, layout_h, B, Hq, Hkv, nb, causal != 0,
+                                        block_rows, block_cols, stream));
 }
 
 float fa_dropout_scale(float p) {

@@ -201,17 +201,22 @@ constexpr uint32_t kOutOfRange = 0x80000000u;
 // step of the D = 128 copies (the mask or the dropout bits alone ~90 bytes of
 // spills per lane, both ~180), so each set the launchers meet has its own
 // copy: FEAT = kFeatMask, kFeatDrop, both, or kFeatBias (a bias, with a mask
-// and dropout as run-time options).
-enum : int { kFeatMask = 1, kFeatDrop = 2, kFeatBias = 4 };
+// and dropout as run-time options). kFeatBlock: a block-sparse layout (steps
+// over its visible blocks only), alone or with dropout.
+enum : int { kFeatMask = 1, kFeatDrop = 2, kFeatBias = 4, kFeatBlock = 8 };
 template <int FEAT>
 struct Feat {
   static constexpr bool kMask = (FEAT & (kFeatMask | kFeatBias)) != 0;
   static constexpr bool kDrop = (FEAT & (kFeatDrop | kFeatBias)) != 0;
   static constexpr bool kBias = (FEAT & kFeatBias) != 0;
+  static constexpr bool kBlock = (FEAT & kFeatBlock) != 0;
 };
-// The instantiation serving a set of options (mask, dropout, bias present).
-__host__ __device__ constexpr int feat_of(bool mask, bool drop, bool bias) {
-  return bias ? kFeatBias : (mask ? kFeatMask : 0) | (drop ? kFeatDrop : 0);
+// The instantiation serving a set of options (mask, dropout, bias, block
+// layout present; the C ABI refuses a block layout with a mask or a bias).
+__host__ __device__ constexpr int feat_of(bool mask, bool drop, bool bias, bool block = false) {
+  return block ? kFeatBlock | (drop ? kFeatDrop : 0)
+       : bias  ? kFeatBias
+               : (mask ? kFeatMask : 0) | (drop ? kFeatDrop : 0);
 }
 // One and four fp32 values at voff + soff of a resource (zeros past its size).
 __device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t voff, uint32_t soff) {

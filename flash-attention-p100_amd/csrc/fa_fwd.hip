@@ -260,11 +260,13 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          int W32, int sq, int sk, int dr, int kofs,
                                          int qtile, float c, float thr_raw, half_t* kt0,
                                          half_t* vt0,
-                                         half_t* kt1, half_t* vt1, float2* ml, half_t* qt) {
+                                         half_t* kt1, half_t* vt1, float2* ml, half_t* qt,
+                                         const int* __restrict__ blist) {
   using L = FwdLds<D>;
   constexpr int kWaves = FwdShape<D>::kWaves, kKV = FwdShape<D>::kKV;
   constexpr int kQuarters = FwdShape<D>::kQuarters;
   constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
+  constexpr bool SPARSE = Feat<FEAT>::kBlock;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar M0 bases
   __builtin_assume(wave >= 0 && wave < kWaves);
@@ -303,9 +305,21 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     return packed_nc ? min(Nk, max(sen[i], i + 1)) : Nk;
   };
   const int kv_end = CAUSAL ? min(Nk, q0 + kBR + kofs) : row_hi(q0 + kBR - 1);
+  // Block-sparse layout (SPARSE instantiations): blist lists the key blocks
+  // of this tile's block row (count first). Step v then runs stage(v), stage
+  // v % kSpb of the (v / kSpb)-th listed block; the masks below work in
+  // stages (key offsets / kKV), so each step is masked as its stage needs. A
+  // block row with no visible block runs one step with every key masked.
+  constexpr int kSpb = kSparseBlock / kKV;  // stages per block
+  const int n_blk = SPARSE ? blist[0] : 0;
+  auto stage = [&](int v) {
+    if constexpr (!SPARSE) return v;
+    const int e = v / kSpb;
+    return blist[1 + e] * kSpb + (v - e * kSpb);
+  };
   // (at least one step: a tile whose rows all lie above the first key, when
   // there are more query rows than key rows, masks every key)
-  const int n_it = max(1, (kv_end + kKV - 1) / kKV);
+  const int n_it = SPARSE ? max(1, n_blk * kSpb) : max(1, (kv_end + kKV - 1) / kKV);
   // Leading steps in which this wave's 32x32 block needs no mask. The later
   // ones run masked; blocks wholly past the diagonal or past N give exact
   // zeros there (their few products are not skipped, so every wave issues its
@@ -326,18 +340,21 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     if (sst) lo = max(lo, min(sst[i], i));
     return max(lo, 0);
   };
-  const int j_lo = narrowed ? lower(q0) / kKV : 0;
+  const int j_first = narrowed ? lower(q0) / kKV : 0;  // first stage any row reaches
+  const int j_lo = SPARSE ? 0 : j_first;                 // first step
   const int win_last = narrowed ? lower(i_base + 31) - 1 - kq * 32 : -1;  // last masked block start
-  const int n_head = win_last >= 0 ? max(j_lo, win_last / kKV + 1) : j_lo;
+  const int n_head = win_last >= 0 ? max(j_first, win_last / kKV + 1) : j_first;
   const int w_lo = narrowed ? lower(i_row) - 1 : INT_MIN;
-  int n_full = n_it;
+  int n_full = SPARSE ? INT_MAX : n_it;  // (in stages)
   if (CAUSAL) {
     const int e = i_base + kofs - 31 - kq * 32;  // the wave's blocks stay unmasked up to key e
     n_full = min(n_full, e >= 0 ? e / kKV + 1 : 0);
   }
-  const int k_hi = row_hi(i_base);  // smallest key bound of this wave's rows
+  // (an empty block row: no key for any row)
+  const bool no_keys = SPARSE && n_blk == 0;
+  const int k_hi = no_keys ? 0 : row_hi(i_base);  // smallest key bound of this wave's rows
   if (BOUNDS) n_full = min(n_full, k_hi - 32 - kq * 32 >= 0 ? (k_hi - 32 - kq * 32) / kKV + 1 : 0);
-  const int lane_hi = row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
+  const int lane_hi = no_keys ? 0 : row_hi(i_row);  // this lane's row: keys from lane_hi on are masked
   // Arbitrary mask (MASKB instantiations): this row's bit words; every step
   // then takes the mask. Word w covers keys 32w .. 32w+31, and a wave's 32
   // keys of step j are word (kKV / 32) j + kq (clamped: keys past N are
@@ -392,11 +409,11 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   TilePlan<D, kKV, kWaves, false> plan;
   plan.init(wave, lane, sk, dr);
   const rsrc_t rk = rows_rsrc(K, Nk, sk, dr), rv = rows_rsrc(V, Nk, sk, dr);
-  const int k1 = min(j_lo + 1, n_it - 1) * kKV;
+  const int k0 = stage(j_lo) * kKV, k1 = stage(min(j_lo + 1, n_it - 1)) * kKV;
 #pragma unroll
   for (int u = 0; u < TL::kParts; ++u) {
-    plan.part(kt0, rk, j_lo * kKV, wave, u);
-    plan.part(vt0, rv, j_lo * kKV, wave, u);
+    plan.part(kt0, rk, k0, wave, u);
+    plan.part(vt0, rv, k0, wave, u);
     plan.part(kt1, rk, k1, wave, u);
   }
   if constexpr (BIAS) {  // the tile's 64 query rows (rows past N read zeros)
@@ -414,22 +431,23 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   // Step j with buffer parity P = j % 2 (a compile-time constant, so the
   // compiler sees that the step's reads never touch the buffers its direct
   // loads fill and does not wait for those loads before them).
-  uint32_t mw = mword(j_lo);  // mask bits of the next step to run
-  uint32_t zw = zword(j_lo);  // its dropout keep bits
-  floatx16 bv = bload(j_lo);  // its bias values
+  uint32_t mw = mword(stage(j_lo));  // mask bits of the next step to run
+  uint32_t zw = zword(stage(j_lo));  // its dropout keep bits
+  floatx16 bv = bload(stage(j_lo));  // its bias values
   auto run = [&](int j, auto par_tag, auto mask_tag, auto next_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     constexpr bool NEXT = decltype(next_tag)::value;
     constexpr int P = decltype(par_tag)::value;
     const uint32_t mw_now = mw, zw_now = zw;
+    const int js = stage(j), jn = NEXT ? stage(j + 1) : js;  // this and the next step's stage
     if ((MASKB || DROPB) && NEXT) {
-      mw = mword(j + 1);
-      zw = zword(j + 1);
+      mw = mword(jn);
+      zw = zword(jn);
     }
     half_t* lk = P ? kt1 : kt0;  // receives K_{j+2}
     half_t* lv = P ? vt0 : vt1;  // receives V_{j+1}
-    const int jk = min(j + 2, n_it - 1) * kKV;
-    const int jv = min(j + 1, n_it - 1) * kKV;
+    const int jk = stage(min(j + 2, n_it - 1)) * kKV;
+    const int jv = jn * kKV;
     if (NEXT && L::kEvenParts < TL::kParts && wave < TL::kInsts % kWaves) {
       plan.part(lk, rk, jk, wave, L::kEvenParts);
       plan.part(lv, rv, jv, wave, L::kEvenParts);
@@ -444,9 +462,9 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     const half_t* Vs = P ? vt1 : vt0;  // V_j
     // (every lane takes the ballot: without a mask mw_now is all ones)
     const bool hidden = MASKB && __builtin_amdgcn_ballot_w64(mw_now != ~0u) != 0;
-    w.template step<MASK, NEXT>(Kn, Vs, kq, j * kKV + kq * 32,
-                                j < n_head || j >= n_full || hidden, i_row + kofs,
-                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv, [&] { return bload(j + 1); },
+    w.template step<MASK, NEXT>(Kn, Vs, kq, js * kKV + kq * 32,
+                                js < n_head || js >= n_full || hidden, i_row + kofs,
+                                lane_hi, w_lo, alibi_raw, mw_now, zw_now, bv, [&] { return bload(jn); },
                                 BIAS ? bias_raw : 0.f, lane,
                                 roff, troff, c, thr_raw, issue);
     if (NEXT) {
@@ -458,11 +476,12 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
   using P1 = std::integral_constant<int, 1>;
   using T = std::true_type;
   using F = std::false_type;
-  const int n_plain = MASKB ? 0 : min(n_full, n_it - 1);  // unmasked steps with a next step
+  // unmasked steps with a next step (block-sparse: each step's stage decides)
+  const int n_plain = MASKB || SPARSE ? 0 : min(n_full, n_it - 1);
   // Buffer parity counts from j_lo. Every wave runs steps j_lo .. n_it-1, one
   // barrier each; only which of them are masked differs between waves.
   int j = j_lo;
-  if (narrowed) {  // masked steps at the rows' left bounds
+  if (narrowed && !SPARSE) {  // masked steps at the rows' left bounds
     for (; j < min(n_head, n_it - 1); ++j) {
       if ((j - j_lo) & 1) run(j, P1{}, T{}, T{});
       else run(j, P0{}, T{}, T{});
@@ -563,7 +582,7 @@ __global__ __launch_bounds__(FwdShape<D>::kThreads) void fwd_kernel(
     const int* __restrict__ seg_start, const int* __restrict__ seg_end,
     const uint32_t* __restrict__ mask, int mask_heads, const uint32_t* __restrict__ drop,
     float drop_scale, const float* __restrict__ bias, long long bias_sb, long long bias_sh,
-    float bias_raw, int dr, int NK) {
+    float bias_raw, int dr, int NK, const int* __restrict__ block_rows) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
   __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
@@ -600,6 +619,10 @@ __global__ __launch_bounds__(FwdShape<D>::kThreads) void fwd_kernel(
   // Causal: tile `first`, then its partner n_qtiles-1-first (one code copy).
   const int second = n_qtiles - 1 - first;
   const int n_tiles = (CAUSAL && second > first) ? 2 : 1;
+  // Block-sparse layout: the lists of this head's block rows.
+  const int nb = (N + kSparseBlock - 1) / kSparseBlock;
+  const int* const brows =
+      Feat<FEAT>::kBlock ? block_rows + (size_t)bh * nb * (nb + 1) : nullptr;
   for (int t = 0; t < n_tiles; ++t)
     fwd_tile<D, CAUSAL, BOUNDS, FEAT, BF>(Q + q_off, K + kv_off, V + kv_off, O + q_off,
                                 Lse + (size_t)bh * N, N, Nk, window,
@@ -609,7 +632,10 @@ __global__ __launch_bounds__(FwdShape<D>::kThreads) void fwd_kernel(
                                 stk.n, dr, NK - N,
                                 t ? second : first,
                                 scale_log2, thr_raw,
-                                kt0, vt0, kt1, vt1, ml, qt);
+                                kt0, vt0, kt1, vt1, ml, qt,
+                                brows ? brows + (size_t)((t ? second : first) * kBR /
+                                                         kSparseBlock) * (nb + 1)
+                                      : nullptr);
 }
 
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
@@ -631,7 +657,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
                      a.seg_start, a.seg_end, a.mask, a.mask_heads, a.drop, a.drop_scale, a.bias,
                      a.bias_sb, a.bias_sh,
                      a.bias ? 1.f / (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D)) : 0.f, a.D,
-                     key_rows(a.N, a.Nkv));
+                     key_rows(a.N, a.Nkv), a.block_rows);
   return hipGetLastError();
 }
 
@@ -648,7 +674,11 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
     return a.causal ? launch_fwd_t<D, true, true, F, BF>(a)
                     : launch_fwd_t<D, false, true, F, BF>(a);
   };
-  switch (feat_of(a.mask != nullptr, a.drop != nullptr, a.bias != nullptr)) {
+  switch (feat_of(a.mask != nullptr, a.drop != nullptr, a.bias != nullptr,
+                  a.block_rows != nullptr)) {
+    case kFeatBlock: return with(std::integral_constant<int, kFeatBlock>{});
+    case kFeatBlock | kFeatDrop:
+      return with(std::integral_constant<int, kFeatBlock | kFeatDrop>{});
     case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
     case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
     case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});

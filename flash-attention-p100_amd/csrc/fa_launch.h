@@ -66,7 +66,17 @@ struct FwdArgs {
   // j <= i + Nkv - N, and windows and ALiBi distances count from that
   // diagonal. Only without packed sequences, a mask, dropout or a bias.
   int Nkv = 0;
+  // Block-sparse layout (kSparseBlock x kSparseBlock blocks, nb = ceil(N /
+  // kSparseBlock) per side), device int32: for plane p = b * Hq + h and query
+  // block r, entry ((p * nb + r) * (nb + 1)) holds the count c of the key
+  // blocks row block r may attend, followed by those blocks' indices in
+  // ascending order (then padding, each a valid index). Keys outside them
+  // are masked; the kernels step over the listed blocks only.
+  const int* block_rows = nullptr;
 };
+
+// Rows and keys per block of a block-sparse layout.
+constexpr int kSparseBlock = 128;
 
 // Key rows of a launch: Nkv, or N when Nkv is 0.
 inline int key_rows(int N, int Nkv) { return Nkv > 0 ? Nkv : N; }
@@ -153,6 +163,13 @@ struct BwdArgs {
   // zeroes it first. Null: not computed.
   float* dbias = nullptr;
   int Nkv = 0;                     // as FwdArgs::Nkv (k, v, dk, dv rows)
+  const int* block_rows = nullptr;  // as FwdArgs::block_rows (required with block_cols)
+  // The layout by key block: for plane p = b * Hkv + hkv and key block c,
+  // entry ((p * nb + c) * (G * nb + 1)) holds the count of (query head,
+  // query block) pairs that attend key block c, followed by those pairs as
+  // g * nb + r (query head hkv * G + g, G = Hq / Hkv) in ascending order
+  // (then padding, each a valid pair).
+  const int* block_cols = nullptr;
 };
 
 hipError_t launch_fwd(const FwdArgs& a);
@@ -167,6 +184,12 @@ hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, 
 // draw is at least `threshold` (see fa_dropout_bits).
 hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, uint32_t* bits,
                                uint32_t* bits_t, void* stream);
+// A dense block-sparse layout (Bl x Hl planes of nb x nb bytes, nonzero =
+// visible; Bl in {1, B} and Hl in {1, Hq} broadcast) to the lists of
+// FwdArgs::block_rows and BwdArgs::block_cols (skipped when null). causal:
+// blocks wholly above the diagonal (key block > query block) are left out.
+hipError_t launch_pack_blocks(const uint8_t* layout, int Bl, int Hl, int B, int Hq, int Hkv,
+                              int nb, bool causal, int* rows, int* cols, void* stream);
 
 // Work-items (workgroups x threads) of the largest launch each pass makes for
 // a shape (either masking). An AMD dispatch packet counts its grid in

@@ -144,6 +144,62 @@ __global__ __launch_bounds__(kPackThreads) void dropout_bits_kernel(
   }
 }
 
+// Block-sparse lists (FwdArgs::block_rows, BwdArgs::block_cols) from a dense
+// layout of Bl x Hl planes of nb x nb bytes (a plane index broadcasts when
+// its count is 1). One thread per list scans its row (query block r of query
+// head h) or its column (key block c over the group's query heads) in order,
+// so the entries come out ascending; the unused tail repeats the last entry
+// (0 for an empty list), so every entry is a valid index. The lists are
+// small (nb + 1 ints per block row) next to the attention that reads them.
+__device__ __forceinline__ const uint8_t* layout_plane(const uint8_t* layout, int Bl, int Hl,
+                                                       int b, int h, int nb) {
+  return layout + ((size_t)(Bl == 1 ? 0 : b) * Hl + (Hl == 1 ? 0 : h)) * nb * nb;
+}
+
+__global__ __launch_bounds__(kPackThreads) void block_rows_kernel(
+    const uint8_t* __restrict__ layout, int Bl, int Hl, int B, int Hq, int nb, bool causal,
+    int* __restrict__ rows) {
+  const long long t = (long long)blockIdx.x * kPackThreads + threadIdx.x;  // (b, h, r)
+  if (t >= (long long)B * Hq * nb) return;
+  const int r = (int)(t % nb);
+  const long long p = t / nb;
+  const int h = (int)(p % Hq), b = (int)(p / Hq);
+  const uint8_t* src = layout_plane(layout, Bl, Hl, b, h, nb) + (size_t)r * nb;
+  int* out = rows + t * (nb + 1);
+  const int end = causal ? r + 1 : nb;  // (causal: key blocks past the query block are hidden)
+  int c = 0, last = 0;
+  for (int k = 0; k < end; ++k)
+    if (src[k]) {
+      out[1 + c++] = k;
+      last = k;
+    }
+  for (int k = c; k < nb; ++k) out[1 + k] = last;
+  out[0] = c;
+}
+
+__global__ __launch_bounds__(kPackThreads) void block_cols_kernel(
+    const uint8_t* __restrict__ layout, int Bl, int Hl, int B, int Hq, int Hkv, int nb,
+    bool causal, int* __restrict__ cols) {
+  const long long t = (long long)blockIdx.x * kPackThreads + threadIdx.x;  // (b, hkv, c)
+  if (t >= (long long)B * Hkv * nb) return;
+  const int c = (int)(t % nb);
+  const long long p = t / nb;
+  const int hkv = (int)(p % Hkv), b = (int)(p / Hkv);
+  const int G = Hq / Hkv;
+  int* out = cols + t * ((long long)G * nb + 1);
+  int n = 0, last = 0;
+  for (int g = 0; g < G; ++g) {
+    const uint8_t* src = layout_plane(layout, Bl, Hl, b, hkv * G + g, nb) + c;
+    for (int r = causal ? c : 0; r < nb; ++r)
+      if (src[(size_t)r * nb]) {
+        last = g * nb + r;
+        out[1 + n++] = last;
+      }
+  }
+  for (int k = n; k < G * nb; ++k) out[1 + k] = last;
+  out[0] = n;
+}
+
 unsigned blocks_for(long long items) {
   const long long b = (items + kPackThreads - 1) / kPackThreads;
   return (unsigned)(b < kPackMaxBlocks ? (b > 0 ? b : 1) : kPackMaxBlocks);
@@ -170,6 +226,21 @@ hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, 
   if (blocks > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL(pack_cols_kernel, dim3((unsigned)blocks), dim3(kPackThreads), 0,
                      (hipStream_t)stream, bits, bits_t, N, W, row_blocks, word_chunks);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_blocks(const uint8_t* layout, int Bl, int Hl, int B, int Hq, int Hkv,
+                              int nb, bool causal, int* rows, int* cols, void* stream) {
+  const long long n_rows = (long long)B * Hq * nb, n_cols = (long long)B * Hkv * nb;
+  if ((n_rows + kPackThreads - 1) / kPackThreads > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(block_rows_kernel, dim3((unsigned)((n_rows + kPackThreads - 1) / kPackThreads)),
+                     dim3(kPackThreads), 0, (hipStream_t)stream, layout, Bl, Hl, B, Hq, nb, causal,
+                     rows);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || cols == nullptr) return e;
+  hipLaunchKernelGGL(block_cols_kernel, dim3((unsigned)((n_cols + kPackThreads - 1) / kPackThreads)),
+                     dim3(kPackThreads), 0, (hipStream_t)stream, layout, Bl, Hl, B, Hq, Hkv, nb,
+                     causal, cols);
   return hipGetLastError();
 }
 

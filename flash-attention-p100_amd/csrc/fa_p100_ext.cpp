@@ -108,7 +108,9 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
                      const c10::optional<at::Tensor>& drop,
                      const c10::optional<at::Tensor>& drop_t, double drop_scale,
                      const c10::optional<at::Tensor>& bias,
-                     const c10::optional<at::Tensor>& dbias, int B, int H, int N) {
+                     const c10::optional<at::Tensor>& dbias,
+                     const c10::optional<at::Tensor>& block_rows,
+                     const c10::optional<at::Tensor>& block_cols, int B, int H, int Hkv, int N) {
   fa_options op{};
   op.dtype = dtype_code(q);
   op.layout = layout;
@@ -151,6 +153,19 @@ fa_options make_opts(const at::Tensor& q, int layout, const c10::optional<at::Te
                 "dbias must be fp32 (B, Hq, N, N), contiguous");
     op.dbias = t.data_ptr<float>();
   }
+  // Block-sparse lists (pack_blocks): int32 on q's device, of the sizes the
+  // shape gives.
+  const int64_t nb = (N + FA_SPARSE_BLOCK - 1) / FA_SPARSE_BLOCK;
+  auto blocks_ptr = [&](const c10::optional<at::Tensor>& t, int64_t numel, const char* name) {
+    if (!t.has_value()) return (const int*)nullptr;
+    TORCH_CHECK(t->is_cuda() && t->device() == q.device(), name, " must be on q's device");
+    TORCH_CHECK(t->scalar_type() == at::kInt && t->is_contiguous() && t->numel() == numel, name,
+                " must be pack_blocks' contiguous int32 list for this shape");
+    return (const int*)t->data_ptr<int>();
+  };
+  op.block_rows = blocks_ptr(block_rows, (int64_t)B * H * nb * (nb + 1), "block_rows");
+  op.block_cols =
+      blocks_ptr(block_cols, (int64_t)B * Hkv * nb * ((H / Hkv) * nb + 1), "block_cols");
   return op;
 }
 
@@ -276,7 +291,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
     c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
-    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias,
+    c10::optional<at::Tensor> block_rows, c10::optional<at::Tensor> block_cols) {
   check_bnhd(q, "q");
   check_bnhd(k, "k");
   check_bnhd(v, "v");
@@ -298,7 +314,8 @@ std::vector<at::Tensor> fa_forward_bnhd(at::Tensor q, at::Tensor k, at::Tensor v
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, block_rows, block_cols,
+                B, H, Hkv, N);
   // key rows that differ from the query rows: bottom-right-aligned causal
   op.kv_rows = k.size(1) != N ? (int)k.size(1) : 0;
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
@@ -315,7 +332,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
     c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
-    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias,
+    c10::optional<at::Tensor> block_rows, c10::optional<at::Tensor> block_cols) {
   for (auto& tn : {std::make_pair(&q, "q"), std::make_pair(&k, "k"), std::make_pair(&v, "v"),
                    std::make_pair(&dO, "dO"), std::make_pair(&o, "o")})
     check_bnhd(*tn.first, tn.second);
@@ -341,7 +359,8 @@ std::vector<at::Tensor> fa_backward_bnhd(at::Tensor q, at::Tensor k, at::Tensor 
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   fa_options op =
       make_opts(q, FA_LAYOUT_BNHD, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, block_rows, block_cols,
+                B, H, Hkv, N);
   // key rows that differ from the query rows: bottom-right-aligned causal
   op.kv_rows = k.size(1) != N ? (int)k.size(1) : 0;
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
@@ -365,7 +384,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
     c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
-    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias,
+    c10::optional<at::Tensor> block_rows, c10::optional<at::Tensor> block_cols) {
   check_in16(q, "q");
   check_in16(k, "k");
   check_in16(v, "v");
@@ -390,7 +410,8 @@ std::vector<at::Tensor> fa_forward_dt(at::Tensor q, at::Tensor k, at::Tensor v, 
   auto lse = at::empty({B, H, N}, q.options().dtype(at::kFloat));
   fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, block_rows, block_cols,
+                B, H, Hkv, N);
   // key rows that differ from the query rows: bottom-right-aligned causal
   op.kv_rows = k.size(2) != N ? (int)k.size(2) : 0;
   check_rc(fa_fwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
@@ -407,7 +428,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
     c10::optional<at::Tensor> seg_start, c10::optional<at::Tensor> seg_end,
     double scale, c10::optional<at::Tensor> mask, c10::optional<at::Tensor> mask_t,
     c10::optional<at::Tensor> drop, c10::optional<at::Tensor> drop_t, double drop_scale,
-    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias) {
+    c10::optional<at::Tensor> bias, c10::optional<at::Tensor> dbias,
+    c10::optional<at::Tensor> block_rows, c10::optional<at::Tensor> block_cols) {
   check_in16(q, "q");
   check_in16(dO, "dO");
   q = q.contiguous();
@@ -438,7 +460,8 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
   auto ws = at::empty({(int64_t)(ws_bytes / sizeof(float))}, q.options().dtype(at::kFloat));
   fa_options op =
       make_opts(q, FA_LAYOUT_BHND, kv_len, window, alibi_slopes, seg_start, seg_end, scale,
-                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, B, H, N);
+                mask, mask_t, drop, drop_t, drop_scale, bias, dbias, block_rows, block_cols,
+                B, H, Hkv, N);
   // key rows that differ from the query rows: bottom-right-aligned causal
   op.kv_rows = k.size(2) != N ? (int)k.size(2) : 0;
   check_rc(fa_bwd_ex(q.data_ptr(), k.data_ptr(), v.data_ptr(), dO.data_ptr(), o.data_ptr(),
@@ -447,6 +470,35 @@ std::vector<at::Tensor> fa_backward_dt(at::Tensor q, at::Tensor k, at::Tensor v,
                      current_stream(q)),
            "fa_bwd_ex");
   return {dq, dk, dv};
+}
+
+// Block layout (Bl, Hl, nb, nb) (bool or uint8; Bl in {1, B}, Hl in {1, Hq};
+// nonzero = visible) to the lists the kernels step over (see fa_pack_blocks):
+// [block_rows (B, Hq, nb, nb + 1) int32, block_cols (B, Hkv, nb, G*nb + 1)].
+std::vector<at::Tensor> fa_pack_blocks_t(at::Tensor layout, int64_t B, int64_t Hq, int64_t Hkv,
+                                         int64_t N, bool causal) {
+  TORCH_CHECK(layout.is_cuda(), "block layout must be a CUDA tensor");
+  TORCH_CHECK(layout.scalar_type() == at::kBool || layout.scalar_type() == at::kByte,
+              "block layout must be bool or uint8");
+  TORCH_CHECK(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && N > 0 && N <= INT32_MAX,
+              "B, Hq, Hkv and N must be positive, Hq a multiple of Hkv");
+  const int64_t nb = (N + FA_SPARSE_BLOCK - 1) / FA_SPARSE_BLOCK;
+  TORCH_CHECK(layout.dim() == 4 && (layout.size(0) == 1 || layout.size(0) == B) &&
+                  (layout.size(1) == 1 || layout.size(1) == Hq) && layout.size(2) == nb &&
+                  layout.size(3) == nb,
+              "block layout must be (B or 1, Hq or 1, nb, nb) with nb = ceil(N / ",
+              FA_SPARSE_BLOCK, ") = ", nb);
+  layout = layout.contiguous();
+  c10::DeviceGuard guard(layout.device());
+  auto opts = layout.options().dtype(at::kInt);
+  auto rows = at::empty({B, Hq, nb, nb + 1}, opts);
+  auto cols = at::empty({B, Hkv, nb, (Hq / Hkv) * nb + 1}, opts);
+  check_rc(fa_pack_blocks(reinterpret_cast<const uint8_t*>(layout.data_ptr()),
+                          (int)layout.size(0), (int)layout.size(1), (int)B, (int)Hq, (int)Hkv,
+                          (int)N, causal ? 1 : 0, rows.data_ptr<int>(), cols.data_ptr<int>(),
+                          current_stream(layout)),
+           "fa_pack_blocks");
+  return {rows, cols};
 }
 
 // Dense boolean mask (..., N, N) (nonzero = may attend) to the packed words
@@ -511,6 +563,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dropout_scale", [](double p) { return (double)fa_dropout_scale((float)p); },
         "Scale of the kept probabilities for dropout_bits(p): 1 / (1 - the drawn rate)",
         py::arg("p"));
+  m.def("pack_blocks", &fa_pack_blocks_t,
+        "block-sparse layout (B|1, Hq|1, nb, nb) to the kernels' block lists",
+        py::arg("layout"), py::arg("B"), py::arg("Hq"), py::arg("Hkv"), py::arg("N"),
+        py::arg("causal"));
   m.def("pack_mask", &fa_pack_mask_t,
         "Bit-packs a dense boolean (..., N, N) mask for the mask / mask_t arguments",
         py::arg("mask"), py::arg("transposed") = true);
@@ -525,7 +581,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
         py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
-        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none(),
+        py::arg("block_rows") = py::none(), py::arg("block_cols") = py::none());
   m.def("backward_bnhd", &fa_backward_bnhd,
         "FlashAttention backward (gfx950) on dense (B, N, H, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
@@ -534,7 +591,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
         py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
-        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none(),
+        py::arg("block_rows") = py::none(), py::arg("block_cols") = py::none());
   m.def("forward_dt", &fa_forward_dt,
         "FlashAttention forward (gfx950) on fp16 or bf16 (B, H, N, D) tensors", py::arg("q"),
         py::arg("k"), py::arg("v"), py::arg("causal"), py::arg("kv_len") = py::none(), py::arg("window") = 0,
@@ -542,7 +600,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
         py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
-        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none(),
+        py::arg("block_rows") = py::none(), py::arg("block_cols") = py::none());
   m.def("backward_dt", &fa_backward_dt,
         "FlashAttention backward (gfx950) on fp16 or bf16 (B, H, N, D) tensors, dq in q's dtype",
         py::arg("q"), py::arg("k"), py::arg("v"), py::arg("dO"), py::arg("o"), py::arg("lse"),
@@ -551,5 +610,6 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("seg_end") = py::none(), py::arg("scale") = 0.0,
         py::arg("mask") = py::none(), py::arg("mask_t") = py::none(),
         py::arg("drop") = py::none(), py::arg("drop_t") = py::none(), py::arg("drop_scale") = 1.0,
-        py::arg("bias") = py::none(), py::arg("dbias") = py::none());
+        py::arg("bias") = py::none(), py::arg("dbias") = py::none(),
+        py::arg("block_rows") = py::none(), py::arg("block_cols") = py::none());
 }

@@ -48,6 +48,9 @@ def _load_ext():
 
 _ext = _load_ext()
 
+# Rows and keys per block of a block-sparse layout (flash_attn's block_mask).
+BLOCK_SIZE = 128
+
 
 def _bnhd_storage(t):
     """The dense (B, N, H, D) tensor a (B, H, N, D) view `t` is a transpose of,
@@ -68,7 +71,7 @@ class _FlashAttnP100(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, causal, full_precision, kv_len=None, window=0, alibi=None,
-                segs=None, scale=0.0, mask=None, drop=None, bias=None):
+                segs=None, scale=0.0, mask=None, drop=None, bias=None, blocks=None):
         # (B, N, H, D) path when q is not dense (B, H, N, D) but is dense
         # (B, N, H, D), and k, v are dense (B, N, H, D) too (with one kv head
         # they are dense in both layouts).
@@ -88,6 +91,9 @@ class _FlashAttnP100(torch.autograd.Function):
         ctx.drop = drop
         # bias: fp32 (B|1, Hq|1, N, N) view with dense rows (see flash_attn).
         ctx.bias = bias.detach() if bias is not None else None
+        # blocks: the block-sparse lists (block_rows, block_cols) of pack_blocks.
+        ctx.blocks = blocks
+        b_rows, b_cols = blocks if blocks is not None else (None, None)
         seg_start, seg_end = segs if segs is not None else (None, None)
         bits, bits_t = mask if mask is not None else (None, None)
         z, z_scale = None, 1.0
@@ -98,14 +104,15 @@ class _FlashAttnP100(torch.autograd.Function):
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
                                         seg_end, scale, bits, drop=z, drop_scale=z_scale,
-                                        bias=ctx.bias)
+                                        bias=ctx.bias, block_rows=b_rows)
             ctx.save_for_backward(qb, kb, vb, ob, lse)
             return ob.transpose(1, 2)
         if (q.dtype == torch.bfloat16 or kv_len is not None or window or alibi is not None
                 or segs is not None or scale or mask is not None or drop is not None
-                or bias is not None or k.size(2) != q.size(2)):
+                or bias is not None or blocks is not None or k.size(2) != q.size(2)):
             o, lse = _ext.forward_dt(q, k, v, causal, kv_len, window, alibi, seg_start, seg_end,
-                                     scale, bits, drop=z, drop_scale=z_scale, bias=ctx.bias)
+                                     scale, bits, drop=z, drop_scale=z_scale, bias=ctx.bias,
+                                     block_rows=b_rows)
         else:
             o, lse = _ext.forward(q, k, v, causal, full_precision)
         ctx.save_for_backward(q, k, v, o, lse)
@@ -115,6 +122,7 @@ class _FlashAttnP100(torch.autograd.Function):
     def backward(ctx, grad_o):
         seg_start, seg_end = ctx.segs if ctx.segs is not None else (None, None)
         bits, bits_t = ctx.mask if ctx.mask is not None else (None, None)
+        b_rows, b_cols = ctx.blocks if ctx.blocks is not None else (None, None)
         z, z_t, z_scale = None, None, 1.0
         if ctx.drop is not None:  # the forward's keep bits, drawn again from its seed
             z, z_t, z_scale = dropout_bits(ctx.drop[0], ctx.drop[1], grad_o.size(0),
@@ -128,10 +136,11 @@ class _FlashAttnP100(torch.autograd.Function):
             gb = grad_o.transpose(1, 2).contiguous()
             dq, dk, dv = _ext.backward_bnhd(qb, kb, vb, gb, ob, lse, ctx.causal, ctx.kv_len,
                                             ctx.window, ctx.alibi, seg_start, seg_end, ctx.scale,
-                                            bits, bits_t, z, z_t, z_scale, ctx.bias, dbias)
+                                            bits, bits_t, z, z_t, z_scale, ctx.bias, dbias,
+                                            b_rows, b_cols)
             return (dq.transpose(1, 2), dk.transpose(1, 2), dv.transpose(1, 2),
                     None, None, None, None, None, None, None, None, None,
-                    _reduce_bias_grad(dbias, ctx.bias))
+                    _reduce_bias_grad(dbias, ctx.bias), None)
         q, k, v, o, lse = ctx.saved_tensors
         # dq is accumulated in fp32 and handed back in q's dtype (fa_p100.py:45);
         # backward_half_dq rounds it to fp16 in the kernel (bit-identical to
@@ -141,14 +150,14 @@ class _FlashAttnP100(torch.autograd.Function):
         if (q.dtype == torch.bfloat16 or ctx.kv_len is not None or ctx.window
                 or ctx.alibi is not None or ctx.segs is not None or ctx.scale
                 or ctx.mask is not None or ctx.drop is not None or ctx.bias is not None
-                or k.size(2) != q.size(2)):
+                or ctx.blocks is not None or k.size(2) != q.size(2)):
             dq, dk, dv = _ext.backward_dt(q, k, v, g, o, lse, ctx.causal, ctx.kv_len, ctx.window,
                                           ctx.alibi, seg_start, seg_end, ctx.scale, bits, bits_t,
-                                          z, z_t, z_scale, ctx.bias, dbias)
+                                          z, z_t, z_scale, ctx.bias, dbias, b_rows, b_cols)
         else:
             dq, dk, dv = _ext.backward_half_dq(q, k, v, g, o, lse, ctx.causal)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
-                None, None, None, None, _reduce_bias_grad(dbias, ctx.bias))
+                None, None, None, None, _reduce_bias_grad(dbias, ctx.bias), None)
 
 
 def _reduce_bias_grad(dbias, bias):
@@ -162,7 +171,7 @@ def _reduce_bias_grad(dbias, bias):
 
 def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding_window=None,
                alibi_slopes=None, segment_ids=None, softmax_scale=None, attn_mask=None,
-               dropout_p=None, dropout_seed=None, attn_bias=None):
+               dropout_p=None, dropout_seed=None, attn_bias=None, block_mask=None):
     """Attention over fp16 GPU tensors (fa_p100.py:48-55).
 
     q is (B, Hq, N, D); k and v are (B, Hkv, N, D) with Hq a multiple of Hkv
@@ -177,7 +186,7 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
     last key row (key j is hidden from query i when j > i + Nk - N; with
     N > Nk the first N - Nk rows see no key and get o = 0 and zero
     gradients), and sliding windows and ALiBi count from that diagonal. Not
-    with segment_ids, attn_mask, dropout_p or attn_bias.
+    with segment_ids, attn_mask, dropout_p, attn_bias or block_mask.
 
     Beyond the reference (which raises on anything but fp16 and on padding
     masks, README.md:72-75):
@@ -232,13 +241,25 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         the masks and the softmax (torch scaled_dot_product_attention's
         float attn_mask), in fp32. When it requires grad its gradient (the
         gradient of the scaled scores, summed over the dimensions it
-        shares) comes back in its own shape and dtype.
+        shares) comes back in its own shape and dtype;
+      * block_mask, a boolean block-sparse layout on q's device of shape
+        (nb, nb), (B, nb, nb) or (B or 1, Hq or 1, nb, nb), nb =
+        ceil(N / BLOCK_SIZE): query i may attend key j only if block
+        (i // BLOCK_SIZE, j // BLOCK_SIZE) is True, on top of the causal and
+        other masks. The kernels step over the visible blocks only, so the
+        time scales with their number. A row with no visible key gets o = 0
+        and zero gradients. Also accepted: the (block_rows, block_cols) pair
+        pack_blocks() makes, for callers that reuse one layout across calls.
+        Not with attn_mask or attn_bias.
     """
     if k.size(2) != q.size(2) and (segment_ids is not None or attn_mask is not None
-                                   or dropout_p or attn_bias is not None):
+                                   or dropout_p or attn_bias is not None
+                                   or block_mask is not None):
         raise ValueError(
-            f"q has {q.size(2)} rows and k, v {k.size(2)}: segment_ids, attn_mask, dropout_p "
-            "and attn_bias need q_len == kv_len")
+            f"q has {q.size(2)} rows and k, v {k.size(2)}: segment_ids, attn_mask, dropout_p, "
+            "attn_bias and block_mask need q_len == kv_len")
+    if block_mask is not None and (attn_mask is not None or attn_bias is not None):
+        raise ValueError("block_mask does not combine with attn_mask or attn_bias")
     if attn_bias is not None and q.size(-1) > 128:
         raise ValueError(f"attn_bias needs a head dim up to 128, got {q.size(-1)}")
     window = 0
@@ -308,8 +329,21 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
         bias = bias.float()
         if bias.stride(-1) != 1 or bias.stride(-2) != n:
             bias = bias.contiguous()
+    blocks = None
+    if block_mask is not None:
+        if isinstance(block_mask, (tuple, list)):
+            blocks = tuple(block_mask)
+            nb = (q.size(2) + BLOCK_SIZE - 1) // BLOCK_SIZE
+            want = [(q.size(0), q.size(1), nb, nb + 1),
+                    (q.size(0), k.size(1), nb, (q.size(1) // k.size(1)) * nb + 1)]
+            if len(blocks) != 2 or [tuple(t.shape) for t in blocks] != want:
+                raise ValueError(f"packed block_mask must be the two int32 tensors of "
+                                 f"pack_blocks, shaped {want}, got "
+                                 f"{[tuple(t.shape) for t in blocks]}")
+        else:
+            blocks = pack_blocks(block_mask, q.size(0), q.size(1), k.size(1), q.size(2), causal)
     return _FlashAttnP100.apply(q, k, v, causal, full_precision, kv_len, window, alibi_slopes,
-                                segs, scale, mask, drop, bias)
+                                segs, scale, mask, drop, bias, blocks)
 
 
 def dropout_bits(seed, p, batch, heads, n, device, transposed=True):
@@ -328,6 +362,35 @@ def dropout_bits(seed, p, batch, heads, n, device, transposed=True):
         seed -= 1 << 64
     bits, bits_t = _ext.dropout_bits(seed, float(p), batch, heads, n, index, bool(transposed))
     return bits, bits_t, _ext.dropout_scale(float(p))
+
+
+def pack_blocks(block_mask, batch, heads, kv_heads, n, causal=False):
+    """(block_rows, block_cols) of a block-sparse layout: the int32 lists the
+    kernels step over (fa_options.block_rows / block_cols in the C ABI), built
+    by one HIP kernel on the layout's device.
+
+    block_mask is boolean, (nb, nb), (B, nb, nb) or (B or 1, heads or 1, nb,
+    nb) with nb = ceil(n / BLOCK_SIZE): query row i may attend key j only if
+    block_mask[..., i // BLOCK_SIZE, j // BLOCK_SIZE] is True. With causal,
+    blocks above the diagonal are left out (a causal call never reads them).
+    Packing once and passing the pair as flash_attn's block_mask saves the
+    packing in every call with the same layout.
+    """
+    m = block_mask
+    if m.dtype != torch.bool:
+        raise ValueError(f"block_mask must be a boolean tensor (True = visible), got {m.dtype}")
+    if m.dim() == 2:
+        m = m[None, None]
+    elif m.dim() == 3:
+        m = m[:, None]
+    nb = (n + BLOCK_SIZE - 1) // BLOCK_SIZE
+    if m.dim() != 4 or tuple(m.shape[2:]) != (nb, nb) or m.size(0) not in (1, batch) \
+            or m.size(1) not in (1, heads):
+        raise ValueError(f"block_mask must be ({nb}, {nb}), ({batch}, {nb}, {nb}) or ({batch} "
+                         f"or 1, {heads} or 1, {nb}, {nb}) for N = {n} (blocks of "
+                         f"{BLOCK_SIZE}), got {tuple(block_mask.shape)}")
+    rows, cols = _ext.pack_blocks(m, batch, heads, kv_heads, n, bool(causal))
+    return rows, cols
 
 
 def pack_mask(attn_mask, batch, heads):

@@ -38,16 +38,19 @@
 extern "C" {
 #endif
 
+/* Rows and keys per block of a block-sparse layout (fa_options.block_rows). */
+#define FA_SPARSE_BLOCK 128
+
 enum {
   FA_OK = 0,
-  FA_ERR_HEAD_DIM = 10001,   /* D not a multiple of 8 in [8, 128] (fa_p100_ext.cu:59, 111: {64, 128}) */
+  FA_ERR_HEAD_DIM = 10001,   /* D not a multiple of 8 in [8, 256] (fa_p100_ext.cu:59, 111: {64, 128}) */
   FA_ERR_SEQLEN = 10002,     /* N <= 0 (fa_p100_ext.cu:60, 112) */
   FA_ERR_HEADS = 10003,      /* Hkv <= 0 or Hq % Hkv != 0 (fa_p100_ext.cu:61, 113) */
   FA_ERR_BATCH = 10004,      /* B <= 0 */
   FA_ERR_NULL = 10005,       /* a required pointer is NULL */
   FA_ERR_WORKSPACE = 10006,  /* workspace smaller than fa_bwd_workspace_bytes() */
   FA_ERR_TOO_LARGE = 10007,  /* (N+256)*D (BNHD: (N+256)*H*D) over 2^31-1, or over 2^29 for a
-                                head dim that is not 32, 64, 96 or 128; or a launch's work
+                                head dim that is not 32, 64, 96, 128 or 256; or a launch's work
                                 items over 2^32 */
   FA_ERR_LAYOUT = 10008,     /* layout not FA_LAYOUT_BHND or FA_LAYOUT_BNHD */
   FA_ERR_DTYPE = 10009,      /* element format not supported */
@@ -59,9 +62,12 @@ enum {
   FA_ERR_DROPOUT = 10015,    /* dropout p not in [0, 1), a scale not positive and finite, or
                                 a backward with drop but without drop_t */
   FA_ERR_BIAS = 10016,       /* a negative bias stride, dbias without bias, or a bias with
-                                N > 2^22 */
-  FA_ERR_KV_ROWS = 10017     /* kv_rows < 0, or kv_rows != N together with packed sequences,
+                                N > 2^22 or a head dim above 128 */
+  FA_ERR_KV_ROWS = 10017,    /* kv_rows < 0, or kv_rows != N together with packed sequences,
                                 a mask, dropout or a bias */
+  FA_ERR_BLOCKS = 10018      /* a block-sparse layout with a mask, a bias or kv_rows != N, a
+                                backward without block_cols, block_cols without block_rows,
+                                or (fa_pack_blocks) layout planes not 1 or B by 1 or Hq */
 };
 
 /* Memory layouts of the 16-bit tensors, for the entry points that take one:
@@ -245,6 +251,26 @@ int fa_bwd_main(const void* q, const void* k, const void* v, const void* dO,
  *     [1, Nk]. Not with packed sequences, a mask, dropout or a bias
  *     (FA_ERR_KV_ROWS); the backward workspace is the one for N rows.
  *     The reference requires q_len == kv_len (fa_p100_hf.py:100-105).
+ *   - block_rows, block_cols: a block-sparse layout (block_rows = NULL:
+ *     none). With nb = ceil(N / FA_SPARSE_BLOCK) blocks of FA_SPARSE_BLOCK
+ *     query rows and as many of keys, query row i may attend key j only if
+ *     block (i / FA_SPARSE_BLOCK, j / FA_SPARSE_BLOCK) is visible for its
+ *     query head, on top of every other mask; the kernels step over the
+ *     visible blocks only, so the work scales with their number. A row with
+ *     no visible key gets o = 0, lse = +inf and zero gradients. The lists
+ *     fa_pack_blocks writes from a boolean layout: block_rows for query
+ *     head h of entry b (plane p = b * Hq + h) and query block r, at
+ *     block_rows[(p * nb + r) * (nb + 1)], the count of visible key blocks
+ *     and then their indices in ascending order; block_cols for kv head g of
+ *     entry b (plane p = b * Hkv + g) and key block c, at
+ *     block_cols[(p * nb + c) * (G * nb + 1)] (G = Hq / Hkv), the count of
+ *     (query head, query block) pairs that see it and then those pairs as
+ *     hg * nb + r (query head g * G + hg) in ascending order. Every entry
+ *     past a count must still be a valid index. The forward reads
+ *     block_rows, the backward both. Not with a mask, a bias or kv_rows != N
+ *     (FA_ERR_BLOCKS); with dropout, causal masking, key lengths, windows,
+ *     ALiBi, packed sequences and a scale. No counterpart in the reference,
+ *     which raises on block-sparse patterns (README.md:72-75).
  */
 typedef struct fa_options {
   int dtype;
@@ -266,6 +292,8 @@ typedef struct fa_options {
   long long bias_stride_h;
   float* dbias;
   int kv_rows;
+  const int* block_rows;
+  const int* block_cols;
 } fa_options;
 
 /*
@@ -314,6 +342,23 @@ int fa_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* b
 int fa_dropout_bits(uint64_t seed, float p, int P, int N, uint32_t* bits, uint32_t* bits_t,
                     void* stream);
 float fa_dropout_scale(float p);
+
+/*
+ * The lists of fa_options.block_rows / block_cols from a boolean block
+ * layout. No counterpart in the reference (README.md:72-75: no block-sparse
+ * patterns). `layout` is layout_b x layout_h planes of nb x nb bytes
+ * (nb = ceil(N / FA_SPARSE_BLOCK); plane (b, h), query block r, key block c
+ * at ((b * layout_h + h) * nb + r) * nb + c; nonzero = visible), with
+ * layout_b 1 or B and layout_h 1 or Hq (1 shares one plane). Writes
+ * B * Hq * nb * (nb + 1) int32 to block_rows and, when block_cols is not
+ * NULL, B * Hkv * nb * ((Hq / Hkv) * nb + 1) int32 to block_cols. With
+ * causal != 0 the blocks above the diagonal (key block > query block) are
+ * left out of both lists, as a causal call never needs them (lists packed
+ * without it still give the same results, with more work). Asynchronous on
+ * `stream`.
+ */
+int fa_pack_blocks(const uint8_t* layout, int layout_b, int layout_h, int B, int Hq, int Hkv,
+                   int N, int causal, int* block_rows, int* block_cols, void* stream);
 
 /*
  * fa_bwd without a workspace argument and without any allocation. No

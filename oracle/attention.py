@@ -30,6 +30,12 @@ independent library routine); closed forms (N=1 gives O=V, causal row 0 gives
 V_0, Q=0 gives the (prefix) mean of V and LSE=log(count)); GQA equals MHA on
 repeat_interleave'd K/V with group-summed dK/dV; permutation equivariance over
 heads and key-permutation invariance (dense); causal tail independence.
+
+Block-sparse layouts (an extension; the reference raises on them,
+README.md:72-75) are element masks: block_layout_mask expands one into the
+`mask` argument, and block_lists restates the int32 lists the kernels step
+over (pinned in tests/test_oracle.py against per-element loops and the
+lists' own invariants).
 """
 import math
 
@@ -39,6 +45,7 @@ __all__ = [
     "expand_kv", "attention_fwd", "bwd_preprocess", "attention_bwd",
     "attention_loss", "rel_max_rms", "rel_l2", "max_abs", "fwd_flops",
     "bwd_flops", "lowbias32", "dropout_threshold", "dropout_keep",
+    "block_layout_mask", "block_lists", "SPARSE_BLOCK",
 ]
 
 
@@ -290,3 +297,44 @@ def fwd_flops(b, hq, n, d, causal):
 def bwd_flops(b, hq, n, d, causal):
     """Backward FLOPs = 2.5x the forward (bwd.cu:246)."""
     return 2.5 * fwd_flops(b, hq, n, d, causal)
+
+
+SPARSE_BLOCK = 128  # rows and keys per block of a block-sparse layout
+
+
+def block_layout_mask(layout, n, block=SPARSE_BLOCK):
+    """Element mask (..., n, n) of a block layout (..., nb, nb): query row i
+    may attend key j iff layout[..., i // block, j // block] (flash_attn's
+    block_mask; pass the result as `mask`)."""
+    lay = np.asarray(layout, dtype=bool)
+    idx = np.arange(n) // block
+    return lay[..., idx[:, None], idx[None, :]]
+
+
+def block_lists(layout, batch, heads, kv_heads, n, causal=False, block=SPARSE_BLOCK):
+    """(rows, cols) of a block layout (B|1, H|1, nb, nb), as int32 arrays
+    (batch, heads, nb, nb + 1) and (batch, kv_heads, nb, G*nb + 1), G =
+    heads // kv_heads. rows[b, h, r] = [count, visible key blocks of query
+    block r ascending, then the last of them repeated (0 if none)];
+    cols[b, g, c] = [count, the (query head, query block) pairs that see key
+    block c as hg * nb + r (query head g * G + hg) ascending, then the last
+    repeated]. causal drops blocks above the diagonal (key block >
+    query block) from both."""
+    nb = (n + block - 1) // block
+    lay = np.broadcast_to(np.asarray(layout, dtype=bool), (batch, heads, nb, nb))
+    G = heads // kv_heads
+    rows = np.zeros((batch, heads, nb, nb + 1), dtype=np.int32)
+    cols = np.zeros((batch, kv_heads, nb, G * nb + 1), dtype=np.int32)
+    for b in range(batch):
+        for h in range(heads):
+            for r in range(nb):
+                vis = [c for c in range(nb) if lay[b, h, r, c] and (not causal or c <= r)]
+                rows[b, h, r, 0] = len(vis)
+                rows[b, h, r, 1:] = (vis + [vis[-1] if vis else 0] * nb)[:nb]
+        for g in range(kv_heads):
+            for c in range(nb):
+                vis = [hg * nb + r for hg in range(G) for r in range(nb)
+                       if lay[b, g * G + hg, r, c] and (not causal or c <= r)]
+                cols[b, g, c, 0] = len(vis)
+                cols[b, g, c, 1:] = (vis + [vis[-1] if vis else 0] * (G * nb))[:G * nb]
+    return rows, cols

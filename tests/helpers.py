@@ -71,6 +71,8 @@ def load_capi():
     lib.fa_dropout_bits.restype = i
     lib.fa_dropout_scale.argtypes = [ctypes.c_float]
     lib.fa_dropout_scale.restype = ctypes.c_float
+    lib.fa_pack_blocks.argtypes = [vp] + [i] * 7 + [vp] * 3
+    lib.fa_pack_blocks.restype = i
     if hasattr(lib, "fa_bwd_noalloc"):
         lib.fa_bwd_noalloc.argtypes = [vp] * 9 + [i] * 6 + [vp]
         lib.fa_bwd_noalloc.restype = i
@@ -88,13 +90,14 @@ class FaOptions(ctypes.Structure):
                 ("drop_t", ctypes.c_void_p), ("drop_scale", ctypes.c_float),
                 ("bias", ctypes.c_void_p), ("bias_stride_b", ctypes.c_longlong),
                 ("bias_stride_h", ctypes.c_longlong), ("dbias", ctypes.c_void_p),
-                ("kv_rows", ctypes.c_int)]
+                ("kv_rows", ctypes.c_int), ("block_rows", ctypes.c_void_p),
+                ("block_cols", ctypes.c_void_p)]
 
 
 def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_start=None,
             seg_end=None, scale=0.0, mask=None, mask_t=None, mask_heads=0, drop=None,
             drop_t=None, drop_scale=0.0, bias=None, bias_stride_b=0, bias_stride_h=0,
-            dbias=None, kv_rows=0):
+            dbias=None, kv_rows=0, block_rows=None, block_cols=None):
     """A pointer to an FaOptions; the array fields are device addresses (ints)
     or tensors."""
     def addr(x):
@@ -102,7 +105,7 @@ def fa_opts(dtype=0, layout=0, kv_len=None, window=0, alibi_slopes=None, seg_sta
     o = FaOptions(dtype, layout, addr(kv_len), window, addr(alibi_slopes), addr(seg_start),
                   addr(seg_end), scale, addr(mask), addr(mask_t), mask_heads, addr(drop),
                   addr(drop_t), drop_scale, addr(bias), bias_stride_b, bias_stride_h,
-                  addr(dbias), kv_rows)
+                  addr(dbias), kv_rows, addr(block_rows), addr(block_cols))
     return ctypes.pointer(o)
 
 

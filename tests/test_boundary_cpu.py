@@ -155,6 +155,26 @@ def test_capi_validation_returns_before_any_launch():
     assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 1, fa_opts(kv_rows=8, mask=1,
                                                                     mask_heads=1), s) == 10005
     assert b"kv_rows" in lib.fa_error_string(10017)
+    # block-sparse lists: not with a mask, a bias or kv_rows != N; the
+    # backward needs block_cols; block_cols alone is refused
+    for bad in (fa_opts(block_rows=1, mask=1, mask_heads=1), fa_opts(block_rows=1, bias=1),
+                fa_opts(block_rows=1, kv_rows=9), fa_opts(block_cols=1)):
+        assert lib.fa_fwd_ex(*([one] * 5), 1, 2, 2, 8, 64, 1, bad, s) == 10018
+    assert lib.fa_fwd_ex(z, z, z, z, z, 1, 2, 2, 8, 64, 1, fa_opts(block_rows=1), s) == 10005
+    assert lib.fa_bwd_ex(*([one] * 10), 1 << 30, 1, 2, 2, 8, 64, 0, fa_opts(block_rows=1),
+                         s) == 10018
+    assert lib.fa_bwd_ex(*([z] * 10), 1 << 30, 1, 2, 2, 8, 64, 0,
+                         fa_opts(block_rows=1, block_cols=1, drop=1, drop_t=1, drop_scale=1.25),
+                         s) == 10005
+    assert b"block-sparse" in lib.fa_error_string(10018)
+    # the block packer: shape, layout planes, pointers
+    assert lib.fa_pack_blocks(one, 1, 1, 1, 2, 2, 0, 0, one, one, s) == 10002
+    assert lib.fa_pack_blocks(one, 1, 1, 1, 3, 2, 8, 0, one, one, s) == 10003
+    assert lib.fa_pack_blocks(one, 1, 1, 0, 2, 2, 8, 0, one, one, s) == 10004
+    assert lib.fa_pack_blocks(one, 2, 1, 3, 2, 2, 8, 0, one, one, s) == 10018
+    assert lib.fa_pack_blocks(one, 1, 3, 1, 2, 2, 8, 0, one, one, s) == 10018
+    assert lib.fa_pack_blocks(z, 1, 1, 1, 2, 2, 8, 0, one, one, s) == 10005
+    assert lib.fa_pack_blocks(one, 1, 1, 1, 2, 2, 8, 0, z, one, s) == 10005
     assert b"layout" in lib.fa_error_string(10008)
     assert b"format" in lib.fa_error_string(10009)
     assert b"window" in lib.fa_error_string(10010)
@@ -178,6 +198,11 @@ def test_binding_rejects_host_tensors_with_reference_messages():
         fa_p100.flash_attn(x, x, x, True, attn_mask=torch.ones(3, 8, 8, dtype=torch.bool))
     with pytest.raises(ValueError, match="packed attn_mask"):
         fa_p100.flash_attn(x, x, x, True, attn_mask=(torch.zeros(1, 2, 8, 2, dtype=torch.int32),) * 2)
+    with pytest.raises(ValueError, match="does not combine"):
+        fa_p100.flash_attn(x, x, x, True, block_mask=torch.ones(1, 1, dtype=torch.bool),
+                           attn_mask=torch.ones(8, 8, dtype=torch.bool))
+    with pytest.raises(ValueError, match="block_mask must be"):
+        fa_p100.pack_blocks(torch.ones(2, 2, dtype=torch.bool), 1, 2, 2, 8)
 
 
 def test_public_api_surface_matches_reference():
@@ -190,7 +215,7 @@ def test_public_api_surface_matches_reference():
     # (key lengths, sliding window, ALiBi slopes, packing, scale, mask) come
     # after them and default to None, so every reference call binds the same way.
     extensions = ["kv_len", "sliding_window", "alibi_slopes", "segment_ids", "softmax_scale",
-                  "attn_mask", "dropout_p", "dropout_seed", "attn_bias"]
+                  "attn_mask", "dropout_p", "dropout_seed", "attn_bias", "block_mask"]
     assert list(sig.parameters)[:5] == ["q", "k", "v", "causal", "full_precision"]
     assert sig.parameters["causal"].default is False
     assert sig.parameters["full_precision"].default is False

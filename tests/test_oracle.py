@@ -808,3 +808,82 @@ def test_kv_rows_with_window_alibi_and_key_lengths(window):
     _fd_kv(rng, q, k, v, do, grads, kw)
     with pytest.raises(ValueError):
         ora.attention_fwd(q, k, v, True, segments=np.zeros((b, n), dtype=np.int64))
+
+
+# ---------------------------------------------------------------------------
+# Block-sparse layouts (an extension; the reference raises on them,
+# README.md:72-75).
+
+def test_block_layout_mask_is_the_per_element_rule():
+    """Element (i, j) of the expanded mask is the layout's block
+    (i // 128, j // 128), checked element by element on a ragged N."""
+    rng = np.random.default_rng(5)
+    n = 300
+    nb = (n + 127) // 128
+    lay = rng.random((2, 3, nb, nb)) < 0.5
+    m = ora.block_layout_mask(lay, n)
+    assert m.shape == (2, 3, n, n)
+    for i in range(0, n, 7):
+        for j in range(0, n, 5):
+            assert (m[:, :, i, j] == lay[:, :, i // 128, j // 128]).all()
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lb,lh", [(1, 1), (2, 1), (2, 4)])
+def test_block_lists_invariants(lb, lh, causal):
+    """The lists hold exactly the visible blocks (np.flatnonzero of the
+    layout, cut at the diagonal when causal), ascending, padded with valid
+    indices; the by-key lists are the transpose of the by-row ones."""
+    rng = np.random.default_rng(lb * 10 + lh + causal)
+    B, H, Hkv, n = 2, 4, 2, 700
+    nb = (n + 127) // 128
+    lay = rng.random((lb, lh, nb, nb)) < 0.4
+    lay[..., 2, :] = False  # an empty block row
+    rows, cols = ora.block_lists(lay, B, H, Hkv, n, causal)
+    full = np.broadcast_to(lay, (B, H, nb, nb)) & (
+        np.tril(np.ones((nb, nb), dtype=bool)) if causal else True)
+    G = H // Hkv
+    for b in range(B):
+        for h in range(H):
+            for r in range(nb):
+                want = np.flatnonzero(full[b, h, r])
+                c = rows[b, h, r, 0]
+                assert c == len(want) and np.array_equal(rows[b, h, r, 1:1 + c], want)
+                assert ((rows[b, h, r, 1:] >= 0) & (rows[b, h, r, 1:] < nb)).all()
+        for g in range(Hkv):
+            for c in range(nb):
+                cnt = cols[b, g, c, 0]
+                got = cols[b, g, c, 1:1 + cnt]
+                assert (np.diff(got) > 0).all()
+                pairs = {(f // nb, f % nb) for f in got}
+                want = {(hg, r) for hg in range(G) for r in range(nb)
+                        if c in rows[b, g * G + hg, r, 1:1 + rows[b, g * G + hg, r, 0]]}
+                assert pairs == want
+                assert ((cols[b, g, c, 1:] >= 0) & (cols[b, g, c, 1:] < G * nb)).all()
+    assert rows[:, :, 2, 0].sum() == 0
+
+
+def test_block_sparse_attention_is_softmax_over_visible_keys():
+    """Forward with an expanded layout equals a per-row softmax over the keys
+    the block rule leaves (computed row by row); a row whose block row is
+    empty gets o = 0 and lse = +inf."""
+    rng = np.random.default_rng(11)
+    b, h, n, d = 1, 2, 260, 8
+    nb = (n + 127) // 128
+    lay = np.array([[[[True, False, True], [False, False, False], [True, True, False]],
+                     [[False, True, False], [True, False, True], [False, False, True]]]])
+    assert lay.shape == (b, h, nb, nb)
+    q, k, v = rnd(rng, b, h, n, d), rnd(rng, b, h, n, d), rnd(rng, b, h, n, d)
+    for causal in (False, True):
+        o, lse = ora.attention_fwd(q, k, v, causal, mask=ora.block_layout_mask(lay, n))
+        for hh in range(h):
+            for i in range(0, n, 3):
+                keys = [j for j in range(n)
+                        if lay[0, hh, i // 128, j // 128] and (not causal or j <= i)]
+                if not keys:
+                    assert not o[0, hh, i].any() and np.isinf(lse[0, hh, i])
+                    continue
+                s = q[0, hh, i] @ k[0, hh, keys].T / math.sqrt(d)
+                w = np.exp(s - s.max())
+                assert np.allclose(o[0, hh, i], (w / w.sum()) @ v[0, hh, keys], atol=1e-12)
+                assert math.isclose(lse[0, hh, i], s.max() + math.log(w.sum()), abs_tol=1e-12)
