@@ -230,7 +230,11 @@ __device__ __forceinline__ void slot_add(rsrc_t r, floatx16 (&acc)[n], int w4, i
 // read K from LDS: with it in registers they spill half of kb at D = 128,
 // and each reload's wait (loads complete in issue order) also waits for the
 // next stage's loads.
-template <int D, bool CAUSAL, bool BOUNDS, bool BF, bool KREG = true>
+// SPLIT (masked instantiations with a boolean mask or a block layout): the
+// per-score tests run in a softmax copy of their own, taken only by steps that
+// hide a score. (The block-layout copies split too, so that a layout and the
+// equivalent element mask run the same arithmetic on visible blocks.)
+template <int D, bool CAUSAL, bool BOUNDS, bool BF, bool KREG = true, bool SPLIT = false>
 struct KVWave {
   floatx16 acc[2 * (D / 32)];
   half8 kb[KREG ? D / 16 : 1];  // this wave's 32 key rows of K as B operands (loop-invariant)
@@ -298,7 +302,16 @@ struct KVWave {
     // At D <= 64 the causal test runs only where some lane's rows start above
     // its key (lo > 0), in a copy a wave ballot picks (measured 2% faster at
     // D = 64); at D = 128 a second copy spilled registers and ran 4% slower.
-    const bool edge = BOUNDS || D > 64 || (CAUSAL && __builtin_amdgcn_ballot_w64(lo > 0) != 0);
+    // With a mask (SPLIT) the per-score tests run only where some lane has a
+    // hidden row (before its left bound, from its row end on, or a clear mask
+    // bit; idx runs over 0..3, 8..11, 16..19, 24..27), in a copy the same kind
+    // of ballot picks: most steps of a mask hide nothing (C3 shape with an
+    // all-true mask: 19% -> 7% over the plain backward). The other masked
+    // instantiations keep one copy: a second one spilled registers at D = 128.
+    const bool open = lo <= 0 && hi >= 28 && (mth & 0x0F0F0F0Fu) == 0x0F0F0F0Fu;
+    const bool edge = SPLIT    ? __builtin_amdgcn_ballot_w64(!open) != 0
+                      : BOUNDS ? true
+                               : D > 64 || (CAUSAL && __builtin_amdgcn_ballot_w64(lo > 0) != 0);
     auto softmax = [&](auto edge_tag) {
       constexpr bool EDGE = decltype(edge_tag)::value;
 #pragma unroll
@@ -310,7 +323,7 @@ struct KVWave {
           const int r = 4 * g4 + e, idx = 8 * g4 + e;
           float p = fast_exp2(fmaf(sacc[r], c, -l4[e]));
           if (EDGE && (CAUSAL || BOUNDS)) p = (idx >= lo) ? p : 0.f;
-          if (BOUNDS) p = (idx < hi && ((mth >> idx) & 1u)) ? p : 0.f;
+          if (EDGE && BOUNDS) p = (idx < hi && ((mth >> idx) & 1u)) ? p : 0.f;
           // Dropout (keep bits ztw, scale zs): dV sees the kept P, and the
           // gradient of P is the kept dP scaled.
           const bool keep = (zth >> idx) & 1u;
@@ -333,7 +346,7 @@ struct KVWave {
 };
 
 // ------------------------------- phase 2 -----------------------------------
-template <int D, bool CAUSAL, bool BOUNDS, bool BF>
+template <int D, bool CAUSAL, bool BOUNDS, bool BF, bool SPLIT = false>
 struct QWave {
   half8 qb[D / 16], ob[D / 16];  // this wave's Q, dO rows as B operands
   floatx16 acc[D / 32];          // dQ^T blocks
@@ -393,8 +406,14 @@ struct QWave {
     // The causal test changes nothing unless one of some lane's 16 keys lies
     // past its row (lo < 27, the largest idx): only the diagonal steps take
     // it, in a copy a wave ballot picks (measured 1.6% faster at D = 64 and
-    // at N = 8192, neutral at B=1 H=8 N=4096 D=128).
-    const bool edge = CAUSAL && __builtin_amdgcn_ballot_w64(lo < 27) != 0;
+    // at N = 8192, neutral at B=1 H=8 N=4096 D=128). With a mask (SPLIT) all
+    // per-score tests run in that copy, picked where some lane has a hidden
+    // key (as in KVWave::step); the other masked instantiations always test.
+    const bool open = (!CAUSAL || lo >= 27) && hi >= 28 && lw <= 0 &&
+                      (mwh & 0x0F0F0F0Fu) == 0x0F0F0F0Fu;
+    const bool edge = SPLIT    ? __builtin_amdgcn_ballot_w64(!open) != 0
+                      : BOUNDS ? true
+                               : CAUSAL && __builtin_amdgcn_ballot_w64(lo < 27) != 0;
     auto softmax = [&](auto edge_tag) {
       constexpr bool EDGE = decltype(edge_tag)::value;
 #pragma unroll
@@ -402,7 +421,7 @@ struct QWave {
         const int idx = 8 * (r >> 2) + (r & 3);
         float p = fast_exp2(fmaf(st[r], c, -lse2));
         if (CAUSAL && EDGE) p = (idx <= lo) ? p : 0.f;
-        if (BOUNDS) p = (idx < hi && idx >= lw && ((mwh >> idx) & 1u)) ? p : 0.f;
+        if (BOUNDS && EDGE) p = (idx < hi && idx >= lw && ((mwh >> idx) & 1u)) ? p : 0.f;
         // Dropout: the gradient of P is the kept dP scaled by zs.
         const bool keep = (zwh >> idx) & 1u;
         const float ds = p * ((keep ? pt[r] * zs : 0.f) - dvv);
@@ -539,6 +558,11 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
   // 2 over the key blocks listed for its query block; the masks below work
   // on row and key indices, so each step is masked as its position needs.
   constexpr bool SPARSE = Feat<FEAT>::kBlock;
+  // Masked instantiations whose per-score tests run in a softmax copy of
+  // their own (KVWave, QWave): all but the bias copy at the causal shapes and
+  // the narrow widths; at D = 128 without causal masking only the mask and
+  // block-layout copies (the others spilled registers with a second copy).
+  constexpr bool kSplit = BOUNDS && !BIAS && (MASKB || SPARSE || CAUSAL || D <= 96);
   constexpr int kSpb = kSparseBlock / kSub;
   static_assert(kSparseBlock == kTile, "a workgroup's rows are one block of the layout");
   const int nb = (N + kSparseBlock - 1) / kSparseBlock;
@@ -624,7 +648,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const int it_begin = helping ? n_it - x_help : 0;
     const int it_end = helping ? n_it : n_it - x_own;
     const bool shared = helping || x_own > 0;
-    KVWave<D, CAUSAL, BOUNDS, BF, FEAT == 0 || KG> w;
+    KVWave<D, CAUSAL, BOUNDS, BF, FEAT == 0 || KG, kSplit> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
       plan_kv.init(wave, lane, stk.n, dr);
@@ -909,7 +933,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
         return v;
       };
       floatx16 bv2 = bload2(stage(t_first));
-      QWave<D, CAUSAL, BOUNDS, BF> w;
+      QWave<D, CAUSAL, BOUNDS, BF, kSplit> w;
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) {
         const bool col_ok = row_ok && kk * 16 + h * 8 < dr;

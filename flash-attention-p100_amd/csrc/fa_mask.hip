@@ -55,18 +55,35 @@ __global__ __launch_bounds__(kPackThreads) void pack_rows_kernel(const uint8_t* 
 }
 
 // Transpose of one 64-row x 32-key block of bit words: lane l holds row
-// i0 + l's word w (bits = keys 32w ..); 32 ballots give lane j < 32 key
+// i0 + l's word w (bits = keys 32w ..); afterwards lane j < 32 holds key
 // 32w + j's bits of rows i0 .. i0+31 and lane 32 + j those of rows i0+32 ..
 // i0+63, which it stores as that key's transposed word (rows i0/32 and
 // i0/32 + 1). Keys past N and words past W are not stored.
+//
+// Each half-wave transposes its 32 x 32 bit matrix (lane r = row r) in five
+// butterfly stages s = 16, 8, 4, 2, 1: lanes r and r ^ s exchange words, and
+// the lane with (r & s) == 0 keeps its bits b with (b & s) == 0 and takes the
+// partner's such bits shifted up by s, the other lane keeps its bits with
+// (b & s) != 0 and takes the partner's shifted down by s, which swaps the
+// off-diagonal s x s blocks of every 2s x 2s block (Hacker's Delight 7-3).
+// Five exchanges and a few bit operations replace 32 ballots.
+__device__ __forceinline__ uint32_t transpose32(uint32_t x, int lane) {
+  constexpr uint32_t kKeep[5] = {0x0000FFFFu, 0x00FF00FFu, 0x0F0F0F0Fu, 0x33333333u, 0x55555555u};
+#pragma unroll
+  for (int t = 0; t < 5; ++t) {
+    const int s = 16 >> t;
+    const uint32_t y = (uint32_t)__shfl_xor((int)x, s);
+    const bool lower = (lane & s) == 0;
+    const uint32_t m = lower ? kKeep[t] : ~kKeep[t];  // the bits this lane keeps
+    const uint32_t moved = lower ? (y << s) : (y >> s);
+    x = (x & m) | (moved & ~m);
+  }
+  return x;
+}
+
 __device__ __forceinline__ void store_transposed(uint32_t word, int lane, int w, int i0, int N,
                                                  int W, uint32_t* __restrict__ plane_t) {
-  uint32_t mine = 0u;
-#pragma unroll
-  for (int j = 0; j < 32; ++j) {
-    const unsigned long long b = __ballot((word >> j) & 1u);
-    if ((lane & 31) == j) mine = lane < 32 ? (uint32_t)b : (uint32_t)(b >> 32);
-  }
+  const uint32_t mine = transpose32(word, lane);
   const int kj = 32 * w + (lane & 31);  // this lane's key
   const int rw = (i0 >> 5) + (lane >> 5);  // its word of query rows
   if (kj < N && rw < W) plane_t[(size_t)kj * W + rw] = mine;
