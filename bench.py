@@ -13,7 +13,9 @@ preallocated buffers. K steps are timed between two device synchronisations;
 HIP events recorded on the same stream between the launches give each
 kernel's average duration. The same step through the public autograd op
 (`flash_attn(...).backward(g)`, which adds output and workspace allocation;
-its backward writes dQ as fp16) is timed as `api_ms_per_step`, and torch's own GPU
+its backward writes dQ as fp16) is timed as `api_ms_per_step`, in short runs
+alternating with the C-ABI step (`abi_interleaved_ms_per_step`), so that the
+two compare at one clock state; torch's own GPU
 scaled_dot_product_attention (flash and memory-efficient backends, fp16,
 same inputs) as `torch_sdpa_gpu`, for comparison.
 
@@ -177,11 +179,10 @@ def feature_paths(c, steps, warmup):
     dropout 0.1 with its keep bits drawn in every step (fa_dropout_bits, as
     in training), both, and an fp32 (1, Hq, N, N) bias with and without its
     gradient (dbias zeroed in every step). Back-to-back steps on one stream,
-    wall clock over `steps` after `warmup`. The block runs after the headline
-    and D=64 measurements, whose load lowers the clock a little, so its own
-    plain_ex, measured in the same state, is what the others compare to (in
-    a fresh process fa_fwd_ex + fa_bwd_ex without options take the same time
-    as the headline step)."""
+    wall clock. The block runs after the headline and D=64 measurements,
+    whose load lowers the clock a little, so the cases run in rounds (each
+    case a short run per round) and `vs_plain` gives each case's time over
+    plain_ex's, measured in the same rounds."""
     import torch
     lib = load_capi()
     vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -238,7 +239,7 @@ def feature_paths(c, steps, warmup):
     fwd_args = (P(q), P(k), P(v), P(o), P(lse), B, Hq, Hkv, N, D, causal)
     bwd_args = (P(q), P(k), P(v), P(do), P(o), P(lse), P(dq), P(dk), P(dv), P(ws), ws_bytes,
                 B, Hq, Hkv, N, D, causal)
-    for name, f in cases.items():
+    def make_step(f):
         fp = ctypes.pointer(f)
         draw, zero = bool(f.drop), bool(f.dbias)
 
@@ -249,15 +250,32 @@ def feature_paths(c, steps, warmup):
                 dbias.zero_()
             check(lib.fa_fwd_ex(*fwd_args, fp, s), "fa_fwd_ex")
             check(lib.fa_bwd_ex(*bwd_args, fp, s), "fa_bwd_ex")
+        return step
 
+    runs = {name: make_step(f) for name, f in cases.items()}
+    for name, step in runs.items():
         for n in range(warmup):
             step(n)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for n in range(steps):
-            step(warmup + n)
-        torch.cuda.synchronize()
-        out[name + "_ms"] = round((time.perf_counter() - t0) * 1e3 / steps, 4)
+    # Every case runs once per round, in short runs, so that clock drift over
+    # the block reaches all cases alike; each case's time is its total over
+    # the rounds, and `vs_plain` its ratio to plain_ex's.
+    rounds = 5
+    per = max(1, steps // rounds)
+    tot = {name: 0.0 for name in runs}
+    seed = warmup
+    for _ in range(rounds):
+        for name, step in runs.items():
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(per):
+                step(seed)
+                seed += 1
+            torch.cuda.synchronize()
+            tot[name] += time.perf_counter() - t0
+    for name in runs:
+        out[name + "_ms"] = round(tot[name] * 1e3 / (rounds * per), 4)
+    out["vs_plain"] = {name: round(tot[name] / tot["plain_ex"], 3)
+                       for name in runs if name != "plain_ex"}
     return out
 
 
@@ -348,13 +366,28 @@ def gpu_bench(c, steps, warmup, copy_mib=0, compare=True):
 
     for _ in range(warmup):
         api_step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        api_step()
-    torch.cuda.synchronize()
-    api_ms = (time.perf_counter() - t0) * 1e3 / steps
-    out.update(api_ms=api_ms, sdpa=gpu_sdpa(c, q, k, v, do, steps, warmup))
+    # Interleaved with the C-ABI step in short alternating runs, so that both
+    # see the same clock state (run after the headline, a block of either
+    # alone would read the GPU at a different clock).
+    rounds = 4
+    per = max(1, steps // rounds)
+    t_api = t_abi = 0.0
+    for _ in range(rounds):
+        for fn, is_api in ((step, False), (api_step, True)):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(per):
+                fn()
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+            if is_api:
+                t_api += dt
+            else:
+                t_abi += dt
+    api_ms = t_api * 1e3 / (rounds * per)
+    abi_ms = t_abi * 1e3 / (rounds * per)
+    out.update(api_ms=api_ms, abi_interleaved_ms=abi_ms,
+               sdpa=gpu_sdpa(c, q, k, v, do, steps, warmup))
     return out
 
 
@@ -555,6 +588,7 @@ def main():
         "kernel_ms": {"fwd": round(r["fwd_ms"], 4), "bwd_preprocess": round(r["pre_ms"], 4),
                       "bwd_main": round(r["main_ms"], 4)},
         "api_ms_per_step": round(r["api_ms"], 4),
+        "abi_interleaved_ms_per_step": round(r["abi_interleaved_ms"], 4),
         "torch_sdpa_gpu": r["sdpa"],
         "device": r["device"],
         "roofline": {"kernel": "bwd_main (fa_bwd_main)", "bound": "mfma",

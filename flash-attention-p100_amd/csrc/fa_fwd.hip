@@ -142,13 +142,18 @@ struct FwdWave {
     constexpr int kFront = kS > 2 ? 2 : 1;  // issued before the row max (covers its latency)
     // At width 256 each product's LDS operand is read one product ahead and
     // pinned there (scheduling fence): left to the scheduler, a step's 32
-    // operand reads were hoisted to its top and spilled registers. Narrower
-    // widths leave the reads to the scheduler.
+    // operand reads were hoisted to its top and spilled registers. At width
+    // 128 the unmasked instantiations pin K's operands the same way: the
+    // scheduler had left the step's last four S^T products each waiting for
+    // its own read (same-box A/B: forward -2% at B=1 H=8 N=4096 causal, -1%
+    // at B=2 H=32/8 N=3001, bit-identical; in the masked instantiations it
+    // added spills). Narrower widths leave the reads to the scheduler.
     constexpr bool kPin = D > 128;
+    constexpr bool kPinK = D > 128 || (D == 128 && !BOUNDS);
     auto kread = [&](int kk) { return tile_read16<D>(Kn, kq * 32, kk, roff); };
-    half8 kcur = kPin && NEXT ? kread(0) : half8{};
+    half8 kcur = kPinK && NEXT ? kread(0) : half8{};
     auto kop = [&](int kk) {
-      if constexpr (!kPin) return kread(kk);
+      if constexpr (!kPinK) return kread(kk);
       const half8 a = kcur;
       if (kk + 1 < kS) kcur = kread(kk + 1);
       __builtin_amdgcn_sched_barrier(0);
