@@ -497,6 +497,20 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
     run(j, P0{}, F{}, T{});
     run(j + 1, P1{}, F{}, T{});
   }
+  // With a mask or a block layout every step runs masked: unrolled by buffer
+  // parity like the plain loop. (Through the loop below, whose one step copy
+  // takes either parity, every step copied the previous step's S^T and all O
+  // accumulators between registers: 40 64-bit moves per step.)
+  if constexpr (MASKB || SPARSE) {
+    if (((j - j_lo) & 1) && j < n_it - 1) {
+      run(j, P1{}, T{}, T{});
+      ++j;
+    }
+    for (; j + 2 <= n_it - 1; j += 2) {
+      run(j, P0{}, T{}, T{});
+      run(j + 1, P1{}, T{}, T{});
+    }
+  }
   // The remaining steps (the masked ones, usually one or two) take the mask
   // at run time: fewer inlined copies of the step keep the accumulators in
   // one set of registers.
