@@ -105,6 +105,7 @@ __device__ __forceinline__ half4 lds_read_tr(const half_t* p) {
 // workgroups when `total` is not a multiple of 8. Only locality depends on the
 // dispatch order; correctness does not.
 constexpr int kXcds = 8;
+constexpr int kCUs = 256;  // 8 XCDs x 32 CUs
 __host__ __device__ __forceinline__ int xcd_grid(int total) {
   return ((total + kXcds - 1) / kXcds) * kXcds;
 }

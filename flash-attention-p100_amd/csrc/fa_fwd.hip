@@ -58,17 +58,27 @@ constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold, log2 units
 // operands and O accumulators need ~260 registers and a 128-key K or V tile
 // 66 KB of LDS, so 4 waves (one per SIMD, 512 registers each) = 2 row blocks
 // x 2 key halves of a 64-key stage.
-template <int D>
+// W4 (width 128, plain instantiations, grids of at least two workgroups per
+// CU): the 4-wave shape at width 128 too, with at most 256 registers per wave
+// so that two workgroups share a CU. Their waves then keep no common step
+// barrier, so one workgroup's softmax runs beside the other's products:
+// same-box A/B, forward -7% at B=2 H=32/8 N=3001 D=128, -4% at H=8 N=4096
+// D=128 (dense), -5% at H=16/8 N=8192 D=128 causal; +5% at the causal
+// B=1 H=8 N=4096 D=128, whose 256 tile pairs leave one 4-wave workgroup per
+// CU, so the launcher takes it only where the grid fills both slots.
+template <int D, bool W4 = false>
 struct FwdShape {
-  static constexpr int kWaves = D > 128 ? 4 : 8;
+  static constexpr int kWaves = D > 128 || W4 ? 4 : 8;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kQuarters = kWaves / 2;  // key slices of 32 per stage
   static constexpr int kKV = 32 * kQuarters;    // keys staged per step
 };
+// The FEAT bit that selects W4 (kept clear of the per-score input bits).
+constexpr int kFwdW4 = 16;
 
-template <int D>
+template <int D, bool W4 = false>
 struct FwdLds {
-  static constexpr int kWaves = FwdShape<D>::kWaves, kKV = FwdShape<D>::kKV;
+  static constexpr int kWaves = FwdShape<D, W4>::kWaves, kKV = FwdShape<D, W4>::kKV;
   static constexpr int kTileHalves = Tile<D>::template halves<kKV>();  // one K or V tile
   static constexpr int kStageHalves = 2 * kTileHalves; // K + V
   // Merge area (reuses the four tiles, kWaves / 4 waves each): per wave,
@@ -267,9 +277,10 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
                                          half_t* vt0,
                                          half_t* kt1, half_t* vt1, float2* ml, half_t* qt,
                                          const int* __restrict__ blist) {
-  using L = FwdLds<D>;
-  constexpr int kWaves = FwdShape<D>::kWaves, kKV = FwdShape<D>::kKV;
-  constexpr int kQuarters = FwdShape<D>::kQuarters;
+  constexpr bool W4 = (FEAT & kFwdW4) != 0;
+  using L = FwdLds<D, W4>;
+  constexpr int kWaves = FwdShape<D, W4>::kWaves, kKV = FwdShape<D, W4>::kKV;
+  constexpr int kQuarters = FwdShape<D, W4>::kQuarters;
   constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
   constexpr bool SPARSE = Feat<FEAT>::kBlock;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -593,7 +604,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
 }
 
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
-__global__ __launch_bounds__(FwdShape<D>::kThreads) void fwd_kernel(
+__global__ __launch_bounds__((FwdShape<D, (FEAT & kFwdW4) != 0>::kThreads))
+__attribute__((amdgpu_waves_per_eu((FEAT & kFwdW4) != 0 ? 2 : 1))) void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
@@ -604,11 +616,12 @@ __global__ __launch_bounds__(FwdShape<D>::kThreads) void fwd_kernel(
     float bias_raw, int dr, int NK, const int* __restrict__ block_rows) {
   // K and V tiles of two stages as distinct LDS objects (see fwd_tile), plus
   // (m, l).
-  __shared__ __align__(16) half_t kt0[FwdLds<D>::kTileHalves];
-  __shared__ __align__(16) half_t vt0[FwdLds<D>::kTileHalves];
-  __shared__ __align__(16) half_t kt1[FwdLds<D>::kTileHalves];
-  __shared__ __align__(16) half_t vt1[FwdLds<D>::kTileHalves];
-  __shared__ float2 ml[FwdLds<D>::kMLFloat2];
+  using L = FwdLds<D, (FEAT & kFwdW4) != 0>;
+  __shared__ __align__(16) half_t kt0[L::kTileHalves];
+  __shared__ __align__(16) half_t vt0[L::kTileHalves];
+  __shared__ __align__(16) half_t kt1[L::kTileHalves];
+  __shared__ __align__(16) half_t vt1[L::kTileHalves];
+  __shared__ float2 ml[L::kMLFloat2];
   // The bias copy's staged Q tile (64 rows; a placeholder elsewhere).
   __shared__ __align__(16) half_t qt[Feat<FEAT>::kBias ? Tile<D>::template halves<kBR>() : 8];
   const int w = xcd_work_index(gx * BH);
@@ -667,7 +680,7 @@ hipError_t launch_fwd_t(const FwdArgs& a) {
   // scale and the strides.
   const float scale_log2 = kLog2e * (a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D));
   hipLaunchKernelGGL((fwd_kernel<D, CAUSAL, BOUNDS, FEAT, BF>), grid,
-                     dim3(FwdShape<D>::kThreads), 0,
+                     dim3(FwdShape<D, (FEAT & kFwdW4) != 0>::kThreads), 0,
                      (hipStream_t)a.stream, (const half_t*)a.q, (const half_t*)a.k,
                      (const half_t*)a.v, (half_t*)a.o, a.lse, a.N, a.Hq, a.Hq / a.Hkv,
                      n_qtiles, gx, BH, scale_log2, make_strides(a.layout, a.Hq, a.N, a.D),
@@ -707,6 +720,21 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
       if constexpr (D > 128) return hipErrorInvalidValue;
       else return with(std::integral_constant<int, kFeatBias>{});
     default: break;
+  }
+  if constexpr (D == 128) {
+    // W4 where the grid gives every CU two workgroups (FwdShape).
+    const long long n_qt = (a.N + kBR - 1) / kBR;
+    const long long wgs = (a.causal ? (n_qt + 1) / 2 : n_qt) * a.B * a.Hq;
+    if (wgs >= 2LL * kCUs) {
+      const bool bounds4 = (a.N % FwdShape<D, true>::kKV) != 0 || a.kv_len != nullptr ||
+                           a.window > 0 || a.alibi != nullptr || a.seg_start != nullptr ||
+                           key_rows(a.N, a.Nkv) != a.N;
+      // (not the causal masked copy, which spills 23 registers at this shape)
+      if (a.causal && !bounds4) return launch_fwd_t<D, true, false, kFwdW4, BF>(a);
+      if (!a.causal)
+        return bounds4 ? launch_fwd_t<D, false, true, kFwdW4, BF>(a)
+                       : launch_fwd_t<D, false, false, kFwdW4, BF>(a);
+    }
   }
   if (a.causal)
     return bounds ? launch_fwd_t<D, true, true, 0, BF>(a)
