@@ -58,12 +58,13 @@ constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold, log2 units
 // operands and O accumulators need ~260 registers and a 128-key K or V tile
 // 66 KB of LDS, so 4 waves (one per SIMD, 512 registers each) = 2 row blocks
 // x 2 key halves of a 64-key stage.
-// W4 (width 128, plain instantiations, grids of at least two workgroups per
-// CU): the 4-wave shape at width 128 too, with at most 256 registers per wave
-// so that two workgroups share a CU. Their waves then keep no common step
-// barrier, so one workgroup's softmax runs beside the other's products:
-// same-box A/B, forward -7% at B=2 H=32/8 N=3001 D=128, -4% at H=8 N=4096
-// D=128 (dense), -5% at H=16/8 N=8192 D=128 causal; +5% at the causal
+// W4 (widths 64 and 128, grids of at least two workgroups per CU): the
+// 4-wave shape there too, with at most 256 registers per wave so that two
+// workgroups share a CU. Their waves then keep no common step barrier, so
+// one workgroup's softmax runs beside the other's products: same-box A/B,
+// forward -7% at B=2 H=32/8 N=3001 D=128, -4% at H=8 N=4096 D=128 (dense),
+// -5% at H=16/8 N=8192 D=128 causal, -9% at H=16 N=4096 D=64 causal, -4% at
+// H=16 N=4096 D=64 dense and at H=16/8 N=8192 D=64 causal; +5% at the causal
 // B=1 H=8 N=4096 D=128, whose 256 tile pairs leave one 4-wave workgroup per
 // CU, so the launcher takes it only where the grid fills both slots.
 template <int D, bool W4 = false>
@@ -721,7 +722,7 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
       else return with(std::integral_constant<int, kFeatBias>{});
     default: break;
   }
-  if constexpr (D == 128) {
+  if constexpr (D == 128 || D == 64) {
     // W4 where the grid gives every CU two workgroups (FwdShape).
     const long long n_qt = (a.N + kBR - 1) / kBR;
     const long long wgs = (a.causal ? (n_qt + 1) / 2 : n_qt) * a.B * a.Hq;
