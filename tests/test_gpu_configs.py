@@ -29,6 +29,10 @@ CONFIGS = {
     # CU (C2 and C3 run its 8-wave shape, C4 the 4-wave one).
     "D64": dict(B=1, Hq=16, Hkv=16, N=4096, D=64, causal=True, s=1.0),
     "C5L": dict(B=1, Hq=16, Hkv=8, N=8192, D=128, causal=True, s=1.0),
+    # N a multiple of that shape's 64-key stage but not of the 8-wave shape's
+    # 128: the two-workgroup forward's unmasked copy serves them.
+    "W4C64": dict(B=1, Hq=16, Hkv=16, N=4160, D=64, causal=True, s=1.0),
+    "W4D128": dict(B=1, Hq=8, Hkv=4, N=4160, D=128, causal=False, s=1.0),
 }
 
 
