@@ -105,3 +105,30 @@ def test_baseline_config(name):
     assert ora.max_abs(np64(o[:1, h:h + 1]), ref_o) <= FWD_MAX_ABS
     dq64, _, _ = ora.attention_bwd(qs, ks, vs, dos, c["causal"])
     assert ora.rel_l2(np64(qg.grad[:1, h:h + 1]), dq64) <= GRAD_REL_L2
+
+
+@pytest.mark.parametrize("D, causal", [(64, True), (128, False)])
+def test_two_workgroup_forward_bf16_and_bnhd(D, causal):
+    """The forward's two-workgroup shape (a grid of at least two workgroups
+    per CU) in bf16 against the fp32 restatement, and on (B, N, H, D)-stored
+    views bit-identical to dense tensors."""
+    import fa_p100
+    from test_gpu_bf16 import BF_FWD_MAX_ABS, BF_GRAD_REL_L2, bf16_inputs
+    B, Hq, Hkv, N = 1, 16, 8, 4096
+    q, k, v, do = (t.cuda() for t in bf16_inputs(B, Hq, Hkv, N, D, seed=23))
+    as_bnhd = lambda t: t.transpose(1, 2).contiguous().transpose(1, 2)
+    dense = [t.clone().requires_grad_(True) for t in (q, k, v)]
+    views = [as_bnhd(t).detach().requires_grad_(True) for t in (q, k, v)]
+    o1 = fa_p100.flash_attn(*dense, causal)
+    o2 = fa_p100.flash_attn(*views, causal)
+    o1.backward(do)
+    o2.backward(as_bnhd(do))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    for x, y in zip(dense, views):
+        assert torch.equal(x.grad, y.grad)
+    ro, rdq, rdk, rdv = fp32_reference(q, k, v, do, causal)
+    assert (o1.float() - ro).abs().max().item() <= BF_FWD_MAX_ABS
+    for g, r, n in ((dense[0].grad, rdq, "dQ"), (dense[1].grad, rdk, "dK"),
+                    (dense[2].grad, rdv, "dV")):
+        assert rel_l2(g, r) <= BF_GRAD_REL_L2, n
