@@ -105,28 +105,39 @@ def test_qwen3_0p6b_shaped_training_step_through_hook():
 
 def test_hook_runs_bf16_under_bf16_autocast():
     """Under bf16 autocast the hook runs the bf16 kernels (the reference cast
-    to fp16): no cast warning, logits within twice the eager-vs-sdpa envelope
-    of eager in bf16, and a training step's loss and attention gradients
-    against eager within max(5e-2, twice sdpa's distance from eager)."""
+    to fp16): no cast warning; logits, and a training step's loss and
+    attention gradients, against the same model in float32 (eager attention)
+    within twice the distance of sdpa's fused bf16 kernels from it.
+
+    No attention runs as bf16 torch matmuls: torch's batched bf16 products
+    with a transposed operand (eager attention's Q K^T, and the backward of
+    its products) have faulted the GPU on these machines, so the reference
+    is the float32 model and sdpa is held to its fused backends (no math
+    fallback), which do not call them."""
     import warnings
+    from torch.nn.attention import SDPBackend, sdpa_kernel
     import fa_p100_hf
     ids = torch.randint(0, 1000, (2, 300), device="cuda",
                         generator=torch.Generator("cuda").manual_seed(2))
+    fused = [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]
 
     def logits(m, impl):
         m.config._attn_implementation = impl
-        with torch.no_grad(), torch.autocast("cuda", torch.bfloat16):
-            return m(ids).logits.float()
+        with torch.no_grad():
+            if impl == "eager":  # the float32 reference
+                return m(ids).logits.float()
+            with torch.autocast("cuda", torch.bfloat16), sdpa_kernel(fused):
+                return m(ids).logits.float()
 
     model = qwen3(2, 512, 8, 2, 128, 1024, 1000).eval()
-    eager, sdpa = logits(model, "eager"), logits(model, "sdpa")
+    ref, sdpa = logits(model, "eager"), logits(model, "sdpa")
     fa_p100_hf.enable_fa_p100(model)
     fa_p100_hf._warned_cast = False
     with warnings.catch_warnings(record=True) as w:
         warnings.simplefilter("always")
         fa = logits(model, "fa_p100")
     assert not [x for x in w if "casts" in str(x.message)]
-    env, gap = (sdpa - eager).abs(), (fa - eager).abs()
+    env, gap = (sdpa - ref).abs(), (fa - ref).abs()
     assert gap.mean() <= 2 * env.mean() + 1e-4, (gap.mean().item(), env.mean().item())
 
     losses, grads = {}, {}
@@ -136,13 +147,18 @@ def test_hook_runs_bf16_under_bf16_autocast():
             fa_p100_hf.enable_fa_p100(m)
         else:
             m.config._attn_implementation = impl
-        with torch.autocast("cuda", torch.bfloat16):
+        if impl == "eager":
             out = m(ids, labels=ids)
+        else:
+            with torch.autocast("cuda", torch.bfloat16), sdpa_kernel(fused):
+                out = m(ids, labels=ids)
         out.loss.backward()
         losses[impl] = out.loss.item()
         grads[impl] = {n: p.grad.float().clone() for n, p in m.named_parameters()
                        if "self_attn" in n and p.grad is not None}
-    assert abs(losses["fa_p100"] - losses["eager"]) <= 2e-3 * abs(losses["eager"])
+    env_l = abs(losses["sdpa"] - losses["eager"])
+    assert abs(losses["fa_p100"] - losses["eager"]) <= max(2e-3 * abs(losses["eager"]),
+                                                           2 * env_l), (losses, env_l)
     for n, g in grads["eager"].items():
         rel = ((grads["fa_p100"][n] - g).norm() / g.norm()).item()
         env_g = ((grads["sdpa"][n] - g).norm() / g.norm()).item()
