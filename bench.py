@@ -176,13 +176,14 @@ def feature_paths(c, steps, warmup):
     the same inputs, with each optional input the reference lacks: the step
     as timed above but with options (plain, for comparison), an all-true
     boolean mask packed once (the packing is per model call, not per layer),
-    dropout 0.1 with its keep bits drawn in every step (fa_dropout_bits, as
-    in training), both, and an fp32 (1, Hq, N, N) bias with and without its
-    gradient (dbias zeroed in every step). Back-to-back steps on one stream,
-    wall clock. The block runs after the headline and D=64 measurements,
-    whose load lowers the clock a little, so the cases run in rounds (each
-    case a short run per round) and `vs_plain` gives each case's time over
-    plain_ex's, measured in the same rounds."""
+    dropout 0.1 with its keep bits drawn in every step (as in training:
+    fa_dropout_bits_causal for a causal workload, as flash_attn draws them
+    there, else fa_dropout_bits), both, and an fp32 (1, Hq, N, N) bias with
+    and without its gradient (dbias zeroed in every step). Back-to-back
+    steps on one stream, wall clock. The block runs after the headline and
+    D=64 measurements, whose load lowers the clock a little, so the cases run
+    in rounds (each case a short run per round) and `vs_plain` gives each
+    case's time over plain_ex's, measured in the same rounds."""
     import torch
     lib = load_capi()
     vp, i, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
@@ -191,6 +192,7 @@ def feature_paths(c, steps, warmup):
     lib.fa_bwd_ex.argtypes = [vp] * 10 + [sz] + [i] * 6 + [opts_t, vp]
     lib.fa_pack_mask.argtypes = [vp, i, i, vp, vp, vp]
     lib.fa_dropout_bits.argtypes = [ctypes.c_uint64, ctypes.c_float, i, i, vp, vp, vp]
+    lib.fa_dropout_bits_causal.argtypes = lib.fa_dropout_bits.argtypes
     lib.fa_dropout_scale.argtypes = [ctypes.c_float]
     lib.fa_dropout_scale.restype = ctypes.c_float
     dev = torch.device("cuda:0")
@@ -239,13 +241,15 @@ def feature_paths(c, steps, warmup):
     fwd_args = (P(q), P(k), P(v), P(o), P(lse), B, Hq, Hkv, N, D, causal)
     bwd_args = (P(q), P(k), P(v), P(do), P(o), P(lse), P(dq), P(dk), P(dv), P(ws), ws_bytes,
                 B, Hq, Hkv, N, D, causal)
+    drawer = lib.fa_dropout_bits_causal if causal else lib.fa_dropout_bits
+
     def make_step(f):
         fp = ctypes.pointer(f)
         draw, zero = bool(f.drop), bool(f.dbias)
 
         def step(seed):
             if draw:
-                check(lib.fa_dropout_bits(seed, 0.1, B * Hq, N, pz, pzt, s), "fa_dropout_bits")
+                check(drawer(seed, 0.1, B * Hq, N, pz, pzt, s), "dropout draw")
             if zero:
                 dbias.zero_()
             check(lib.fa_fwd_ex(*fwd_args, fp, s), "fa_fwd_ex")

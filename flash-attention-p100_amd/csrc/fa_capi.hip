@@ -428,7 +428,18 @@ int fa_dropout_bits(uint64_t seed, float p, int P, int N, uint32_t* bits, uint32
   if (N <= 0) return FA_ERR_SEQLEN;
   if (P <= 0) return FA_ERR_BATCH;
   if (!bits) return FA_ERR_NULL;
-  return to_code(fa::launch_dropout_bits(seed, dropout_threshold(p), P, N, bits, bits_t, stream));
+  return to_code(
+      fa::launch_dropout_bits(seed, dropout_threshold(p), P, N, false, bits, bits_t, stream));
+}
+
+int fa_dropout_bits_causal(uint64_t seed, float p, int P, int N, uint32_t* bits,
+                           uint32_t* bits_t, void* stream) {
+  if (!(p >= 0.f && p < 1.f)) return FA_ERR_DROPOUT;
+  if (N <= 0) return FA_ERR_SEQLEN;
+  if (P <= 0) return FA_ERR_BATCH;
+  if (!bits) return FA_ERR_NULL;
+  return to_code(
+      fa::launch_dropout_bits(seed, dropout_threshold(p), P, N, true, bits, bits_t, stream));
 }
 
 int fa_pack_blocks(const uint8_t* layout, int layout_b, int layout_h, int B, int Hq, int Hkv,

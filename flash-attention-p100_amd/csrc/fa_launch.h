@@ -181,9 +181,9 @@ hipError_t launch_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, 
                             void* stream);
 // Dropout keep bits for P planes of N x N (bits and, when not null, bits_t;
 // layouts as the mask's): key j of row i in plane p is kept iff its 16-bit
-// draw is at least `threshold` (see fa_dropout_bits).
-hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, uint32_t* bits,
-                               uint32_t* bits_t, void* stream);
+// draw is at least `threshold` (see fa_dropout_bits); causal: and j <= i.
+hipError_t launch_dropout_bits(uint64_t seed, uint32_t threshold, int P, int N, bool causal,
+                               uint32_t* bits, uint32_t* bits_t, void* stream);
 // A dense block-sparse layout (Bl x Hl planes of nb x nb bytes, nonzero =
 // visible; Bl in {1, B} and Hl in {1, Hq} broadcast) to the lists of
 // FwdArgs::block_rows and BwdArgs::block_cols (skipped when null). causal:

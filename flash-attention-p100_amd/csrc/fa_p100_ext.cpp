@@ -534,8 +534,10 @@ std::vector<at::Tensor> fa_pack_mask_t(at::Tensor dense, bool transposed) {
 // the given device, drawn from `seed` with drop probability p (see
 // fa_dropout_bits). Without `transposed` only `drop` is drawn (the forward
 // reads no other) and the second tensor is undefined (None in Python).
+// causal: the bits of keys past each row's diagonal are cleared and not drawn
+// (fa_dropout_bits_causal), for causal attention over N keys.
 std::vector<at::Tensor> fa_dropout_bits_t(int64_t seed, double p, int64_t B, int64_t H, int64_t N,
-                                          int64_t device, bool transposed) {
+                                          int64_t device, bool transposed, bool causal) {
   TORCH_CHECK(p >= 0.0 && p < 1.0, "dropout p must lie in [0, 1), got ", p);
   TORCH_CHECK(B > 0 && H > 0 && N > 0 && B * H <= INT32_MAX && N <= INT32_MAX,
               "dropout bits need positive B, H, N");
@@ -546,12 +548,12 @@ std::vector<at::Tensor> fa_dropout_bits_t(int64_t seed, double p, int64_t B, int
   auto bits = at::empty({B, H, N, W}, opts);
   at::Tensor bits_t;
   if (transposed) bits_t = at::empty({B, H, N, W}, opts);
-  check_rc(fa_dropout_bits((uint64_t)seed, (float)p, (int)(B * H), (int)N,
-                           reinterpret_cast<uint32_t*>(bits.data_ptr<int>()),
-                           transposed ? reinterpret_cast<uint32_t*>(bits_t.data_ptr<int>())
-                                      : nullptr,
-                           current_stream(bits)),
-           "fa_dropout_bits");
+  check_rc((causal ? fa_dropout_bits_causal : fa_dropout_bits)(
+               (uint64_t)seed, (float)p, (int)(B * H), (int)N,
+               reinterpret_cast<uint32_t*>(bits.data_ptr<int>()),
+               transposed ? reinterpret_cast<uint32_t*>(bits_t.data_ptr<int>()) : nullptr,
+               current_stream(bits)),
+           causal ? "fa_dropout_bits_causal" : "fa_dropout_bits");
   return {bits, bits_t};
 }
 
@@ -559,7 +561,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("dropout_bits", &fa_dropout_bits_t,
         "Dropout keep bits (B, H, N, ceil(N/32)) and their transpose for drop / drop_t",
         py::arg("seed"), py::arg("p"), py::arg("B"), py::arg("H"), py::arg("N"),
-        py::arg("device"), py::arg("transposed") = true);
+        py::arg("device"), py::arg("transposed") = true, py::arg("causal") = false);
   m.def("dropout_scale", [](double p) { return (double)fa_dropout_scale((float)p); },
         "Scale of the kept probabilities for dropout_bits(p): 1 / (1 - the drawn rate)",
         py::arg("p"));

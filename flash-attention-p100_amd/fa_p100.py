@@ -99,7 +99,7 @@ class _FlashAttnP100(torch.autograd.Function):
         z, z_scale = None, 1.0
         if drop is not None:
             z, _, z_scale = dropout_bits(drop[0], drop[1], q.size(0), q.size(1), q.size(2),
-                                         q.device, transposed=False)
+                                         q.device, transposed=False, causal=causal)
         ctx.bnhd = qb is not None and kb is not None and vb is not None
         if ctx.bnhd:
             ob, lse = _ext.forward_bnhd(qb, kb, vb, causal, kv_len, window, alibi, seg_start,
@@ -126,7 +126,8 @@ class _FlashAttnP100(torch.autograd.Function):
         z, z_t, z_scale = None, None, 1.0
         if ctx.drop is not None:  # the forward's keep bits, drawn again from its seed
             z, z_t, z_scale = dropout_bits(ctx.drop[0], ctx.drop[1], grad_o.size(0),
-                                           grad_o.size(1), grad_o.size(2), grad_o.device)
+                                           grad_o.size(1), grad_o.size(2), grad_o.device,
+                                           causal=ctx.causal)
         dbias = None
         if ctx.bias is not None and ctx.needs_input_grad[12]:  # bias is input 12
             B, H, N = grad_o.size(0), grad_o.size(1), grad_o.size(2)
@@ -346,13 +347,16 @@ def flash_attn(q, k, v, causal=False, full_precision=False, kv_len=None, sliding
                                 segs, scale, mask, drop, bias, blocks)
 
 
-def dropout_bits(seed, p, batch, heads, n, device, transposed=True):
+def dropout_bits(seed, p, batch, heads, n, device, transposed=True, causal=False):
     """(bits, bits_t, scale) of attention dropout: int32 keep bits
     (batch, heads, n, ceil(n/32)) in the mask layout and its transpose (bit
     set = keep; None when `transposed` is False), drawn by one HIP kernel from
     the 64-bit `seed` with drop probability p (fa_dropout_bits in the C ABI
     states the draw), and the scale 1 / (1 - drawn rate) of the kept
-    probabilities."""
+    probabilities. With `causal` the bits of keys j > i (row i) are cleared
+    and not drawn (fa_dropout_bits_causal): causal attention over n keys
+    never reads them, so its results do not change, and the draw does about
+    half the work."""
     device = torch.device(device)
     if device.type != "cuda":
         raise ValueError(f"dropout bits are drawn on the GPU, got device {device}")
@@ -360,7 +364,8 @@ def dropout_bits(seed, p, batch, heads, n, device, transposed=True):
     seed = int(seed) % (1 << 64)
     if seed >= 1 << 63:  # the binding takes a signed 64-bit value with the same bits
         seed -= 1 << 64
-    bits, bits_t = _ext.dropout_bits(seed, float(p), batch, heads, n, index, bool(transposed))
+    bits, bits_t = _ext.dropout_bits(seed, float(p), batch, heads, n, index, bool(transposed),
+                                     bool(causal))
     return bits, bits_t, _ext.dropout_scale(float(p))
 
 

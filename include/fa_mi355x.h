@@ -341,6 +341,16 @@ int fa_pack_mask(const uint8_t* dense, int P, int N, uint32_t* bits, uint32_t* b
  */
 int fa_dropout_bits(uint64_t seed, float p, int P, int N, uint32_t* bits, uint32_t* bits_t,
                     void* stream);
+/*
+ * fa_dropout_bits for causal attention with as many key rows as query rows:
+ * the same draw with every bit of a key j > i (row i) cleared, in both
+ * layouts. Causal masking never reads those bits, so attention results are
+ * the same as with fa_dropout_bits' planes; the draw skips the hashes of
+ * words wholly past the diagonal (about half of them). No counterpart in the
+ * reference. Errors as fa_dropout_bits.
+ */
+int fa_dropout_bits_causal(uint64_t seed, float p, int P, int N, uint32_t* bits,
+                           uint32_t* bits_t, void* stream);
 float fa_dropout_scale(float p);
 
 /*

@@ -155,13 +155,14 @@ def dropout_threshold(p):
     return int(min(max(t, 0.0), 65535.0))
 
 
-def dropout_keep(seed, p, planes, n):
+def dropout_keep(seed, p, planes, n, causal=False):
     """Keep mask (planes, n, n) of attention dropout, restating the draw that
     include/fa_mi355x.h states for fa_dropout_bits (an extension: the
     reference has no dropout, fa_p100_hf.py:83-85): row key
     r = h(h(h(h(lo) ^ hi) ^ plane) ^ row) of the seed's 32-bit halves, key j
     draws the low (j even) or high (j odd) 16 bits of h(r ^ (j // 2)), and
-    is kept iff the draw >= dropout_threshold(p). Returns (keep, scale), the
+    is kept iff the draw >= dropout_threshold(p). causal: fa_dropout_bits_causal,
+    the same draw with keys j > i of row i cleared. Returns (keep, scale), the
     scale 65536 / (65536 - t) of the kept probabilities."""
     t = dropout_threshold(p)
     seed = int(seed) % (1 << 64)
@@ -170,7 +171,10 @@ def dropout_keep(seed, p, planes, n):
     rows = lowbias32(base[:, None] ^ np.arange(n, dtype=np.uint32)[None, :])
     u = lowbias32(rows[:, :, None] ^ np.arange((n + 1) // 2, dtype=np.uint32)[None, None, :])
     draws = np.stack([u & np.uint32(0xFFFF), u >> np.uint32(16)], axis=-1).reshape(planes, n, -1)
-    return draws[:, :, :n] >= t, 65536.0 / (65536 - t)
+    keep = draws[:, :, :n] >= t
+    if causal:
+        keep &= np.tril(np.ones((n, n), dtype=bool))
+    return keep, 65536.0 / (65536 - t)
 
 
 def _drop_factor(dropout, shape):

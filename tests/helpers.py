@@ -69,6 +69,8 @@ def load_capi():
     lib.fa_pack_mask.restype = i
     lib.fa_dropout_bits.argtypes = [ctypes.c_uint64, ctypes.c_float, i, i, vp, vp, vp]
     lib.fa_dropout_bits.restype = i
+    lib.fa_dropout_bits_causal.argtypes = [ctypes.c_uint64, ctypes.c_float, i, i, vp, vp, vp]
+    lib.fa_dropout_bits_causal.restype = i
     lib.fa_dropout_scale.argtypes = [ctypes.c_float]
     lib.fa_dropout_scale.restype = ctypes.c_float
     lib.fa_pack_blocks.argtypes = [vp] + [i] * 7 + [vp] * 3

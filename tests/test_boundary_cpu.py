@@ -127,12 +127,14 @@ def test_capi_validation_returns_before_any_launch():
         assert lib.fa_fwd_ex(z, z, z, z, z, 1, 4, 2, 8, D, 0, fa_opts(), s) == 10005
     assert b"head dim up to 128" in lib.fa_error_string(10016)
     # the dropout generator: p in [0, 1), shape, pointers; the scale of the drawn rate
+    for draw in (lib.fa_dropout_bits, lib.fa_dropout_bits_causal):
+        for bad in (-0.1, 1.0, 1.5, float("nan")):
+            assert draw(7, bad, 1, 8, one, one, s) == 10015
+        assert draw(7, 0.1, 1, 0, one, one, s) == 10002
+        assert draw(7, 0.1, 0, 8, one, one, s) == 10004
+        assert draw(7, 0.1, 1, 8, z, one, s) == 10005
     for bad in (-0.1, 1.0, 1.5, float("nan")):
-        assert lib.fa_dropout_bits(7, bad, 1, 8, one, one, s) == 10015
         assert lib.fa_dropout_scale(bad) == 0.0
-    assert lib.fa_dropout_bits(7, 0.1, 1, 0, one, one, s) == 10002
-    assert lib.fa_dropout_bits(7, 0.1, 0, 8, one, one, s) == 10004
-    assert lib.fa_dropout_bits(7, 0.1, 1, 8, z, one, s) == 10005
     for p, t in ((0.0, 0), (0.1, 6554), (0.5, 32768), (0.999999, 65535)):
         assert abs(lib.fa_dropout_scale(p) - 65536.0 / (65536 - t)) < 1e-6 * 65536 / (65536 - t)
     # the packer: N, planes, pointers

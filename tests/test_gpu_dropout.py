@@ -51,6 +51,63 @@ def test_dropout_bits_match_the_oracle_draw_on_long_rows():
         assert np.array_equal(as_u32(bits_t[0]), host_words(np.swapaxes(keep, -1, -2))), (planes, n)
 
 
+@pytest.mark.parametrize("planes,N", [(1, 1), (3, 31), (2, 33), (1, 100), (4, 1000), (1, 4095),
+                                      (2, 4096)])
+def test_causal_dropout_bits_match_the_oracle_draw(planes, N):
+    """fa_dropout_bits_causal (what causal flash_attn draws): the full draw
+    with the bits of keys j > i cleared, both layouts bit for bit, from one
+    word per row to 128, ragged last words, and rows on both sides of the
+    draw's 64-row waves; the forward's draw without the transpose gives the
+    same words."""
+    import fa_p100
+    tril = np.tril(np.ones((N, N), dtype=bool))
+    for seed, p in ((3, 0.1), ((1 << 64) - 9, 0.5)):
+        bits, bits_t, _ = fa_p100.dropout_bits(seed, p, 1, planes, N, DEV, causal=True)
+        keep, _ = ora.dropout_keep(seed, p, planes, N, causal=True)
+        full, _ = ora.dropout_keep(seed, p, planes, N)
+        assert not (keep & ~tril).any() and np.array_equal(keep, full & tril)
+        assert np.array_equal(as_u32(bits[0]), host_words(keep)), (planes, N, seed)
+        assert np.array_equal(as_u32(bits_t[0]), host_words(np.swapaxes(keep, -1, -2)))
+        fwd_only, none, _ = fa_p100.dropout_bits(seed, p, 1, planes, N, DEV, transposed=False,
+                                                 causal=True)
+        assert none is None and torch.equal(fwd_only, bits)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D", [(1, 8, 8, 4096, 128), (2, 4, 2, 1000, 64)])
+def test_causal_draw_leaves_causal_attention_bit_identical(B, Hq, Hkv, N, D):
+    """Causal attention reads no bit of a key past the diagonal, so the
+    forward and backward through the C ABI give bit-identical O, LSE, dQ, dK
+    and dV with fa_dropout_bits_causal's planes and with fa_dropout_bits'
+    (the headline shape and a ragged GQA one)."""
+    lib = load_capi()
+    q, k, v, do = (t.to(DEV) for t in make_inputs(B, Hq, Hkv, N, D, seed=N + D))
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    W = (N + 31) // 32
+    p = 0.1
+    scale = lib.fa_dropout_scale(p)
+    ws_bytes = lib.fa_bwd_workspace_bytes(B, Hq, Hkv, N, D)
+    ws = torch.empty(ws_bytes, device=DEV, dtype=torch.uint8)
+    outs = []
+    for draw in (lib.fa_dropout_bits, lib.fa_dropout_bits_causal):
+        z = torch.empty(B, Hq, N, W, dtype=torch.int32, device=DEV)
+        z_t = torch.empty_like(z)
+        assert draw(99, p, B * Hq, N, ptr(z), ptr(z_t), s) == 0
+        opts = fa_opts(drop=z, drop_t=z_t, drop_scale=scale)
+        o, lse = torch.empty_like(q), torch.empty(B, Hq, N, device=DEV)
+        assert lib.fa_fwd_ex(ptr(q), ptr(k), ptr(v), ptr(o), ptr(lse), B, Hq, Hkv, N, D, 1, opts,
+                             s) == 0
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        rc = lib.fa_bwd_ex(ptr(q), ptr(k), ptr(v), ptr(do), ptr(o), ptr(lse), ptr(dq), ptr(dk),
+                           ptr(dv), ptr(ws), ws_bytes, B, Hq, Hkv, N, D, 1, opts, s)
+        assert rc == 0, lib.fa_error_string(rc)
+        torch.cuda.synchronize()
+        outs.append((o, lse, dq, dk, dv))
+    for name, a, b in zip(("O", "LSE", "dQ", "dK", "dV"), *outs):
+        assert torch.equal(a, b), name
+    assert (outs[0][2] != 0).any()
+
+
 def run(q, k, v, do, causal, p, seed, **kw):
     import fa_p100
     qg, kg, vg = (t.to(DEV).requires_grad_(True) for t in (q, k, v))

@@ -604,6 +604,14 @@ def test_dropout_draw_pins():
         u = _h32(r ^ (j // 2))
         draw = (u >> 16) if j % 2 else (u & 0xFFFF)
         assert keep[plane, i, j] == (draw >= t)
+    # The causal draw (fa_dropout_bits_causal): keys at or left of the
+    # diagonal draw as above, keys past it are cleared.
+    kc, _ = ora.dropout_keep(seed, p, planes, n, causal=True)
+    for plane, i, j in [(0, 0, 0), (2, 36, 36), (1, 17, 5), (2, 11, 2), (1, 5, 17), (0, 0, 36)]:
+        r = _h32(_h32(_h32(_h32(seed & 0xFFFFFFFF) ^ (seed >> 32)) ^ plane) ^ i)
+        u = _h32(r ^ (j // 2))
+        draw = (u >> 16) if j % 2 else (u & 0xFFFF)
+        assert kc[plane, i, j] == (j <= i and draw >= t)
     assert ora.dropout_threshold(0.0) == 0 and ora.dropout_threshold(0.9999999) == 65535
     # Statistics over ~1M draws per rate.
     for p in (0.1, 0.5, 0.9):
