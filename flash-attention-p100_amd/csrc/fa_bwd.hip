@@ -70,9 +70,19 @@ static_assert(kTile == kBwdTile, "workspace layout assumes this key tile");
 // registers per lane at one wave per SIMD), the streamed tiles have 32 rows
 // and the K operands come straight from global memory into registers (a
 // resident K tile would not fit in LDS beside V and the staged tiles).
-template <int D>
+// W4 (width 64, grids of at least two workgroups per CU): one wave per row
+// block and 32-row streamed tiles as at width 256, but K resident in LDS and
+// at most 256 registers per wave (the kernel needs ~170), so two workgroups
+// (54 KB of LDS each) share a CU on separate barriers and one's softmax runs
+// beside the other's products. Same-box A/B, bwd_main at H=16 N=4096 D=64
+// causal: -4% (minimum) and -7% (median of five rounds); within 0.6% at
+// H=16 N=4096 D=64 dense and at H=16/8 N=8192 D=64 causal; +17% at H=16
+// N=2048 D=64 causal, whose 256 workgroups leave one per CU, so the launcher
+// takes it only where the grid fills both slots. (At width 128 two such
+// workgroups do not fit in LDS.)
+template <int D, bool W4 = false>
 struct BwdShape {
-  static constexpr int kWaves = D > 128 ? 4 : 8;
+  static constexpr int kWaves = D > 128 || W4 ? 4 : 8;
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int kHalves = kWaves / 4;  // waves per row block
   static constexpr int kSub = 32 * kHalves;
@@ -93,13 +103,15 @@ constexpr int kVecStride = 64;  // floats per staged lse2 / dvec run (>= every k
 // D=64, H=16 N=8192 D=128 and H=16 N=2048 D=64.
 constexpr int kSplitNum = 86;
 constexpr int kSplitBias = 5;
+// The FEAT bit that selects W4 (kept clear of the per-score input bits).
+constexpr int kBwdW4 = 16;
 
 // LDS: every tile is its own __shared__ object (declared in bwd_kernel), so
 // the compiler can tell that a step's reads never touch the tiles that the
 // next step's direct loads are filling and does not wait for those loads.
-template <int D>
+template <int D, bool W4 = false>
 struct BwdLds {
-  using Sh = BwdShape<D>;
+  using Sh = BwdShape<D, W4>;
   static constexpr int kTileHalves = Stream<D>::template bytes<Sh::kSub>() / 2;  // staged tile
   static constexpr int kKVTileHalves = Tile<D>::template halves<kTile>();  // resident V
   static constexpr int kKTileHalves = Sh::kKGlobal ? 512 : kKVTileHalves;  // resident K
@@ -460,7 +472,8 @@ struct QWave {
 // ---------------------------------------------------------------------------
 // FEAT: the optional per-score inputs compiled in (Feat, with BOUNDS).
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
-__global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
+__global__ __launch_bounds__((BwdShape<D, (FEAT & kBwdW4) != 0>::kThreads))
+__attribute__((amdgpu_waves_per_eu((FEAT & kBwdW4) != 0 ? 2 : 1))) void bwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, const half_t* __restrict__ dO,
     const float* __restrict__ Lse2, const float* __restrict__ Dvec,
@@ -475,10 +488,13 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const uint32_t* __restrict__ drop_t, float drop_scale, const float* __restrict__ bias,
     long long bias_sb, long long bias_sh, float bias_raw, float* __restrict__ dbias, int dr,
     int NK, const int* __restrict__ block_rows, const int* __restrict__ block_cols) {
-  using L = BwdLds<D>;
-  constexpr int kWaves = BwdShape<D>::kWaves, kHalves = BwdShape<D>::kHalves;
-  constexpr int kSub = BwdShape<D>::kSub;
-  constexpr bool KG = BwdShape<D>::kKGlobal;
+  constexpr bool W4 = (FEAT & kBwdW4) != 0;
+  constexpr int FI = FEAT & ~kBwdW4;  // the per-score inputs
+  using Sh = BwdShape<D, W4>;
+  using L = BwdLds<D, W4>;
+  constexpr int kWaves = Sh::kWaves, kHalves = Sh::kHalves;
+  constexpr int kSub = Sh::kSub;
+  constexpr bool KG = Sh::kKGlobal;
   constexpr int kSlotFloats = kTile * D * 2;  // one workgroup's dK^T and dV^T
   // Two stages of (first tile, second tile, lse2 | dvec), and the resident K, V.
   // The larger alignment makes the compiler place the four staged tiles first,
@@ -551,13 +567,13 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
   const rsrc_t rk = rows_rsrc(K + kv_off, NK, stk.n, dr), rv = rows_rsrc(V + kv_off, NK, stk.n, dr);
   // Offset of query head hq's row 0 in Q, dO, dQ.
   auto q_off = [&](int hq) { return (size_t)(b * stq.b + hq * stq.h); };
-  constexpr bool MASKB = Feat<FEAT>::kMask, DROPB = Feat<FEAT>::kDrop, BIAS = Feat<FEAT>::kBias;
+  constexpr bool MASKB = Feat<FI>::kMask, DROPB = Feat<FI>::kDrop, BIAS = Feat<FI>::kBias;
   // Block-sparse layout (SPARSE instantiations): nb blocks of kSparseBlock
   // rows (= kTile) per side, kSpb streamed tiles per block. Phase 1 steps
   // over the (query head, query block) pairs listed for its key block, phase
   // 2 over the key blocks listed for its query block; the masks below work
   // on row and key indices, so each step is masked as its position needs.
-  constexpr bool SPARSE = Feat<FEAT>::kBlock;
+  constexpr bool SPARSE = Feat<FI>::kBlock;
   // Masked instantiations whose per-score tests run in a softmax copy of
   // their own (KVWave, QWave): all but the bias copy at the causal shapes and
   // the narrow widths; at D = 128 without causal masking only the mask and
@@ -648,7 +664,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     const int it_begin = helping ? n_it - x_help : 0;
     const int it_end = helping ? n_it : n_it - x_own;
     const bool shared = helping || x_own > 0;
-    KVWave<D, CAUSAL, BOUNDS, BF, FEAT == 0 || KG, kSplit> w;
+    KVWave<D, CAUSAL, BOUNDS, BF, FI == 0 || KG, kSplit> w;
     {
       TilePlan<D, kTile, kWaves, false> plan_kv;  // resident K, V rows tp0 .. tp0+kTile-1
       plan_kv.init(wave, lane, stk.n, dr);
@@ -759,7 +775,7 @@ __global__ __launch_bounds__(BwdShape<D>::kThreads) void bwd_kernel(
     fetch(it_begin, ta0, tb0, vec0);
     wait_vmem();
     __syncthreads();
-    if constexpr (FEAT == 0 && !KG) {
+    if constexpr (FI == 0 && !KG) {
 #pragma unroll
       for (int kk = 0; kk < D / 16; ++kk) w.kb[kk] = tile_read16<D>(kres, w4 * 32, kk, roff);
     }
@@ -1039,7 +1055,7 @@ hipError_t launch_main_t(const BwdArgs& a) {
   const int NK = key_rows(a.N, a.Nkv);
   const int n_tiles = (max(a.N, NK) + kTile - 1) / kTile;
   const dim3 grid(xcd_grid(n_tiles * a.B * a.Hkv));
-  using Sh = BwdShape<D>;
+  using Sh = BwdShape<D, (FEAT & kBwdW4) != 0>;
   // D is the tile width; a.D the head dim in memory, which sets the default
   // scale and the strides.
   const float scale = a.scale > 0.f ? a.scale : 1.f / sqrtf((float)a.D);
@@ -1081,6 +1097,17 @@ hipError_t launch_main_d(const BwdArgs& a) {
       if constexpr (D > 128) return hipErrorInvalidValue;
       else return with(std::integral_constant<int, kFeatBias>{});
     default: break;
+  }
+  if constexpr (D == 64) {  // W4 where the grid gives every CU two workgroups (BwdShape)
+    const long long wgs =
+        (long long)((max(a.N, key_rows(a.N, a.Nkv)) + kTile - 1) / kTile) * a.B * a.Hkv;
+    if (wgs >= 2LL * kCUs) {
+      if (a.causal)
+        return bounds ? launch_main_t<D, true, true, kBwdW4, BF>(a)
+                      : launch_main_t<D, true, false, kBwdW4, BF>(a);
+      return bounds ? launch_main_t<D, false, true, kBwdW4, BF>(a)
+                    : launch_main_t<D, false, false, kBwdW4, BF>(a);
+    }
   }
   if (a.causal)
     return bounds ? launch_main_t<D, true, true, 0, BF>(a)

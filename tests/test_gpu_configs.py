@@ -26,7 +26,8 @@ CONFIGS = {
     "C4": dict(B=2, Hq=32, Hkv=8, N=3001, D=128, causal=False, s=0.5),
     # The metric's D=64 leg and a C5 layer's attention: grids of two or more
     # workgroups per CU, which the forward runs as two 4-wave workgroups per
-    # CU (C2 and C3 run its 8-wave shape, C4 the 4-wave one).
+    # CU (C2 and C3 run its 8-wave shape, C4 the 4-wave one), and the
+    # backward too at width 64 (D64, W4C64).
     "D64": dict(B=1, Hq=16, Hkv=16, N=4096, D=64, causal=True, s=1.0),
     "C5L": dict(B=1, Hq=16, Hkv=8, N=8192, D=128, causal=True, s=1.0),
     # N a multiple of that shape's 64-key stage but not of the 8-wave shape's
@@ -132,3 +133,40 @@ def test_two_workgroup_forward_bf16_and_bnhd(D, causal):
     for g, r, n in ((dense[0].grad, rdq, "dQ"), (dense[1].grad, rdk, "dK"),
                     (dense[2].grad, rdv, "dV")):
         assert rel_l2(g, r) <= BF_GRAD_REL_L2, n
+
+
+@pytest.mark.parametrize("N, causal, bf16", [(4096, False, False), (4160, False, True),
+                                             (4160, True, False)])
+def test_two_workgroup_backward_width_64(N, causal, bf16):
+    """The backward's two-workgroup shape at width 64 (B=2, Hkv=8: 2 * 8 *
+    ceil(N/128) >= 512 workgroups, two per CU): the unmasked (N = 4096) and
+    masked (N = 4160) copies, dense and causal, fp16 and bf16, against the
+    fp32 restatement; (B, N, H, D)-stored views bit-identical to dense
+    tensors; a second run bit-identical to the first."""
+    import fa_p100
+    from test_gpu_bf16 import BF_FWD_MAX_ABS, BF_GRAD_REL_L2, bf16_inputs
+    B, Hq, Hkv, D = 2, 16, 8, 64
+    if bf16:
+        q, k, v, do = (t.cuda() for t in bf16_inputs(B, Hq, Hkv, N, D, seed=31))
+        fwd_bar, grad_bar = BF_FWD_MAX_ABS, BF_GRAD_REL_L2
+    else:
+        q, k, v, do = (t.cuda() for t in make_inputs(B, Hq, Hkv, N, D, seed=31))
+        fwd_bar, grad_bar = FWD_MAX_ABS, GRAD_REL_L2
+    as_bnhd = lambda t: t.transpose(1, 2).contiguous().transpose(1, 2)
+    runs = []
+    for make in (lambda t: t.clone(), lambda t: t.clone(), as_bnhd):
+        xs = [make(t).detach().requires_grad_(True) for t in (q, k, v)]
+        o = fa_p100.flash_attn(*xs, causal)
+        o.backward(make(do))
+        torch.cuda.synchronize()
+        runs.append((o, *(x.grad for x in xs)))
+    for a, b, c in zip(*runs):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    ro, rdq, rdk, rdv = fp32_reference(q, k, v, do, causal)
+    o, dq, dk, dv = runs[0]
+    assert (o.float() - ro).abs().max().item() <= fwd_bar
+    for g, r, n in ((dq, rdq, "dQ"), (dk, rdk, "dK"), (dv, rdv, "dV")):
+        assert torch.isfinite(g).all(), n
+        assert rel_l2(g, r) <= grad_bar, (n, rel_l2(g, r))
+        if not bf16:
+            assert rel_rms(g, r) < REF_REL, (n, rel_rms(g, r))
