@@ -103,6 +103,10 @@ constexpr int kVecStride = 64;  // floats per staged lse2 / dvec run (>= every k
 // D=64, H=16 N=8192 D=128 and H=16 N=2048 D=64.
 constexpr int kSplitNum = 86;
 constexpr int kSplitBias = 5;
+// The same rate for the W4 shape (below): swept 65..130 at H=16 N=4096 D=64
+// causal (two boxes): 100 beat 86 by 1.4%, 115 and 130 lost; at H=16/8
+// N=8192 D=64 within 0.7%.
+constexpr int kSplitNumW4 = 100;
 // The FEAT bit that selects W4 (kept clear of the per-score input bits).
 constexpr int kBwdW4 = 16;
 
@@ -1065,7 +1069,8 @@ hipError_t launch_main_t(const BwdArgs& a) {
                      (half_t*)a.dq16, (half_t*)a.dk, (half_t*)a.dv, a.N, a.Hq, a.Hq / a.Hkv, n_tiles,
                      a.B * a.Hkv, scale, scale * kLog2e, make_strides(a.layout, a.Hq, a.N, a.D),
                      make_strides(a.layout, a.Hkv, NK, a.D), a.counters, a.slots,
-                     a.slots ? kSplitNum * 64 / Sh::kSub : 0, a.slots ? kSplitBias : 0, a.kv_len, a.window,
+                     a.slots ? ((FEAT & kBwdW4) ? kSplitNumW4 : kSplitNum) * 64 / Sh::kSub : 0,
+                     a.slots ? kSplitBias : 0, a.kv_len, a.window,
                      a.alibi, a.seg_start, a.seg_end, a.mask, a.mask_t, a.mask_heads, a.drop,
                      a.drop_t, a.drop_scale, a.bias, a.bias_sb, a.bias_sh,
                      a.bias ? 1.f / scale : 0.f, a.dbias, a.D, NK, a.block_rows, a.block_cols);
