@@ -66,7 +66,10 @@ constexpr float kRescaleLog2 = 8.f;  // lazy-rescale threshold, log2 units
 // -5% at H=16/8 N=8192 D=128 causal, -9% at H=16 N=4096 D=64 causal, -4% at
 // H=16 N=4096 D=64 dense and at H=16/8 N=8192 D=64 causal; +5% at the causal
 // B=1 H=8 N=4096 D=128, whose 256 tile pairs leave one 4-wave workgroup per
-// CU, so the launcher takes it only where the grid fills both slots.
+// CU, so the launcher takes it only where the grid fills both slots. Without
+// causal masking the width-64 copies fit 168 registers without spills, so
+// three workgroups share a CU: -2.1% at H=16 N=4096 D=64 dense (bit-identical;
+// the causal copy then spills 3 registers and ran 2% slower, so it keeps two).
 template <int D, bool W4 = false>
 struct FwdShape {
   static constexpr int kWaves = D > 128 || W4 ? 4 : 8;
@@ -606,7 +609,8 @@ __device__ __forceinline__ void fwd_tile(const half_t* __restrict__ Q, const hal
 
 template <int D, bool CAUSAL, bool BOUNDS, int FEAT, bool BF>
 __global__ __launch_bounds__((FwdShape<D, (FEAT & kFwdW4) != 0>::kThreads))
-__attribute__((amdgpu_waves_per_eu((FEAT & kFwdW4) != 0 ? 2 : 1))) void fwd_kernel(
+__attribute__((amdgpu_waves_per_eu((FEAT & kFwdW4) != 0 ? (D == 64 && !CAUSAL ? 3 : 2) : 1)))
+void fwd_kernel(
     const half_t* __restrict__ Q, const half_t* __restrict__ K,
     const half_t* __restrict__ V, half_t* __restrict__ O, float* __restrict__ Lse,
     int N, int Hq, int group, int n_qtiles, int gx, int BH, float scale_log2, Strides stq,
