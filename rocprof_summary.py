@@ -100,10 +100,11 @@ def main():
                 sq[k][n] = sum(vals) / len(vals)
 
     os.makedirs(a.out, exist_ok=True)
-    cmd_bench = "python3 bench.py --no-cpu --no-d64 --no-features"
-    cmd_cnt = ("python3 bench.py --no-cpu --no-d64 --no-features --steps 3 --warmup 1 --copy-calibration %d"
-               % a.copy_mib)
-    cmd_sq = "python3 bench.py --no-cpu --no-d64 --no-features --steps 3 --warmup 1"
+    # (the headline C3 is bench.py's default configuration)
+    cfg = "" if a.workload == "C3" else f" --config {a.workload}"
+    cmd_bench = f"python3 bench.py{cfg} --no-cpu --no-d64 --no-features"
+    cmd_cnt = f"{cmd_bench} --steps 3 --warmup 1 --copy-calibration {a.copy_mib}"
+    cmd_sq = f"{cmd_bench} --steps 3 --warmup 1"
     sq_sets = [
         "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS "
         "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE",
