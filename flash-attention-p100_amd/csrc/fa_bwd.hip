@@ -1096,7 +1096,15 @@ hipError_t launch_main_d(const BwdArgs& a) {
     case kFeatBlock | kFeatDrop:
       return with(std::integral_constant<int, kFeatBlock | kFeatDrop>{});
     case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
-    case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
+    case kFeatDrop:
+      // Keep bits need no bounds: where nothing else does, the unmasked
+      // instantiations (not at width 256, where they spill).
+      if constexpr (D <= 128) {
+        if (!bounds)
+          return a.causal ? launch_main_t<D, true, false, kFeatDrop, BF>(a)
+                          : launch_main_t<D, false, false, kFeatDrop, BF>(a);
+      }
+      return with(std::integral_constant<int, kFeatDrop>{});
     case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});
     case kFeatBias:  // (no bias at width 256: the C ABI refuses it)
       if constexpr (D > 128) return hipErrorInvalidValue;

@@ -717,7 +717,15 @@ hipError_t launch_fwd_d(const FwdArgs& a) {
     case kFeatBlock | kFeatDrop:
       return with(std::integral_constant<int, kFeatBlock | kFeatDrop>{});
     case kFeatMask: return with(std::integral_constant<int, kFeatMask>{});
-    case kFeatDrop: return with(std::integral_constant<int, kFeatDrop>{});
+    case kFeatDrop:
+      // Keep bits need no bounds: where nothing else does, the unmasked
+      // instantiations (not at width 256, where they spill).
+      if constexpr (D <= 128) {
+        if (!bounds)
+          return a.causal ? launch_fwd_t<D, true, false, kFeatDrop, BF>(a)
+                          : launch_fwd_t<D, false, false, kFeatDrop, BF>(a);
+      }
+      return with(std::integral_constant<int, kFeatDrop>{});
     case kFeatMask | kFeatDrop: return with(std::integral_constant<int, kFeatMask | kFeatDrop>{});
     case kFeatBias:
       // (the bias copy stages Q in LDS too, which at D = 256 does not fit
