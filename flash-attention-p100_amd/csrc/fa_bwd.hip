@@ -637,7 +637,11 @@ __attribute__((amdgpu_waves_per_eu((FEAT & kBwdW4) != 0 ? 2 : 1))) void bwd_kern
   auto q_start = [&](int u) {
     return CAUSAL ? max(0, u * kTile - kofs) / kSub * kSub : col_lo(u * kTile) / kSub * kSub;
   };
-  auto n_iters = [&](int u) { return group * ((q_end(u) - q_start(u) + kSub - 1) / kSub); };
+  // (none when no query row reaches the tile: with more key rows than query
+  // rows and a window, or more query rows than key rows, q_end < q_start)
+  auto n_iters = [&](int u) {
+    return group * max(0, (q_end(u) - q_start(u) + kSub - 1) / kSub);
+  };
   auto split = [&](int u) {
     // (not at width 256: a second inlined copy of phase 1 spilled registers;
     // not with a block layout, whose key tiles have no common amount of work)
@@ -689,7 +693,7 @@ __attribute__((amdgpu_waves_per_eu((FEAT & kBwdW4) != 0 ? 2 : 1))) void bwd_kern
 
     const int i_start = q_start(tile);
     const int row_lo = CAUSAL ? j_col - kofs : packed_nc ? col_lo(j_col) : -(1 << 30);
-    const int n_qt = (q_end(tile) - i_start + kSub - 1) / kSub;
+    const int n_qt = max(1, (q_end(tile) - i_start + kSub - 1) / kSub);  // (a divisor)
     // Rows this wave's key column reaches (see KVWave::step).
     const int row_end = j_col < Nk ? (narrowed ? upper(j_col) : N) : 0;
     // Query head (of the group) and first query row of flattened step `it`.
@@ -707,9 +711,12 @@ __attribute__((amdgpu_waves_per_eu((FEAT & kBwdW4) != 0 ? 2 : 1))) void bwd_kern
 
     // Q, dO tiles and lse2, dvec of flattened step `it` (clamped to the last
     // one, so that every step issues the same loads) into one stage.
+    // Without any step (it_end <= 0) this is step 0, loaded but never run: a
+    // valid query head whose rows past N read as zeros. (Clamped only from
+    // above, a negative index would name a query head past the last one,
+    // whose loads' resources start past the tensors' ends.)
     auto fetch = [&](int it, half_t* tq, half_t* to, float* tv) {
-      it = min(it, it_end - 1);
-      if constexpr (SPARSE) it = max(it, 0);  // (no pair: a listed padding pair, never run)
+      it = max(0, min(it, it_end - 1));
       int g, i0;
       qpos(it, g, i0);
       const int hq = hkv * group + g;
