@@ -162,8 +162,9 @@ struct FwdWave {
     // its own read (same-box A/B: forward -2% at B=1 H=8 N=4096 causal, -1%
     // at B=2 H=32/8 N=3001, bit-identical; in the masked instantiations it
     // added spills). At width 64 the same: -2% on the forward at H=16 N=4096
-    // causal, -1.6% at H=16/8 N=8192, -1% dense, bit-identical. Widths 32 and
-    // 96 leave the reads to the scheduler.
+    // causal, -1.6% at H=16/8 N=8192, -1% dense, bit-identical (V's operands
+    // pinned too: 1-2% slower). Widths 32 and 96 leave the reads to the
+    // scheduler.
     constexpr bool kPin = D > 128;
     constexpr bool kPinK = D > 128 || ((D == 128 || D == 64) && !BOUNDS);
     auto kread = [&](int kk) { return tile_read16<D>(Kn, kq * 32, kk, roff); };
